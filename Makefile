@@ -1,0 +1,59 @@
+# EdgeCore MI355X build.  Everything lands in-tree so it travels with the
+# repository snapshot:
+#   edgecore_amd/lib/libedgecore_hip.so   the C-ABI library (HIP, gfx950)
+#   edgecore_amd/bin/edgecore-runtime     the command-line driver
+#   edgecore_amd/bin/ecm_synth            seeded synthetic .ecm / prompt generator
+#   oracle/liboracle.so                   CPU oracle (test infrastructure)
+#   oracle/_ref/*                         reference CPU runtime built from its sources,
+#                                         only where the reference tree exists
+ROCM    ?= /opt/rocm
+HIPCC   ?= $(ROCM)/bin/hipcc
+CC      ?= gcc
+ARCH    ?= gfx950
+REF     ?= /root/reference
+
+PKG     := edgecore_amd
+SRC     := $(PKG)/csrc
+OBJ     := build/obj
+LIB     := $(PKG)/lib/libedgecore_hip.so
+RUNTIME := $(PKG)/bin/edgecore-runtime
+SYNTH   := $(PKG)/bin/ecm_synth
+
+# -ffp-contract=off keeps every a*b+c a rounded multiply and a rounded add, as
+# in the reference's -std=c11 build; packed fp32 instructions are disabled.
+HIPFLAGS := --offload-arch=$(ARCH) -O3 -std=c++17 -fPIC -ffp-contract=off \
+            -Xclang -target-feature -Xclang -packed-fp32-ops -Iinclude -I$(SRC) -Wall
+CFLAGS   := -O2 -std=c11 -Wall -Wextra -fPIC -Iinclude -ffp-contract=off
+
+HIPSRC := $(SRC)/kernels.hip $(SRC)/runtime.hip
+HIPOBJ := $(HIPSRC:$(SRC)/%.hip=$(OBJ)/%.o)
+
+all: $(LIB) $(RUNTIME) $(SYNTH) oracle
+
+$(OBJ) $(PKG)/lib $(PKG)/bin:
+	mkdir -p $@
+
+$(OBJ)/%.o: $(SRC)/%.hip $(SRC)/ec_device.h $(SRC)/ec_kernels.h include/edgecore.h | $(OBJ)
+	$(HIPCC) $(HIPFLAGS) -c $< -o $@
+
+$(OBJ)/ecm.o: $(SRC)/ecm.c include/edgecore.h | $(OBJ)
+	$(CC) $(CFLAGS) -c $< -o $@
+
+$(LIB): $(HIPOBJ) $(OBJ)/ecm.o | $(PKG)/lib
+	$(HIPCC) --offload-arch=$(ARCH) -shared -fPIC $^ -o $@
+
+$(RUNTIME): $(SRC)/runtime_main.c include/edgecore.h $(LIB) | $(PKG)/bin
+	$(CC) $(CFLAGS) $< -o $@ -L$(PKG)/lib -ledgecore_hip -Wl,-rpath,'$$ORIGIN/../lib' -lm
+
+$(SYNTH): $(SRC)/ecm_synth.c $(SRC)/ecm.c include/edgecore.h | $(PKG)/bin
+	$(CC) -O2 -std=c11 -Wall -Wextra -fopenmp -Iinclude $(SRC)/ecm_synth.c $(SRC)/ecm.c -o $@ -lm
+
+oracle:
+	$(MAKE) -C oracle
+	@if [ -d "$(REF)/src" ]; then $(MAKE) -C oracle ref REF=$(REF); fi
+
+clean:
+	rm -rf build $(PKG)/lib $(PKG)/bin
+	$(MAKE) -C oracle clean
+
+.PHONY: all oracle clean

@@ -1,0 +1,905 @@
+// Host runtime of libedgecore_hip.so: the C ABI of include/edgecore.h.
+//
+// One GPU per process (device 0 or $EDGECORE_DEVICE), one non-blocking HIP
+// stream at the default priority.  gpt2_load reads the .ecm file once, packs
+// every tensor into one HBM arena (Qwen2 q/k/v back to back so one GEMV
+// produces all three), builds the RoPE table on the host with the same libm
+// calls as the reference and allocates the fp16 KV cache and workspaces.
+// A forward call copies tokens/positions/slots in, enqueues the layer kernels
+// and copies logits (or greedy ids) out.
+#include "edgecore.h"
+#include "ec_kernels.h"
+
+#include <hip/hip_runtime.h>
+
+#include <errno.h>
+#include <fcntl.h>
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <string>
+#include <vector>
+
+using namespace ec;
+
+// ---------------------------------------------------------------------------
+// errors, device, stream
+// ---------------------------------------------------------------------------
+
+static thread_local char g_err[512];
+static int g_inited = 0;
+static int g_device = 0;
+static hipStream_t g_stream = nullptr;
+static hipDeviceProp_t g_prop;
+static int g_max_lds = 65536;
+
+static int set_err(int code, const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+#define EC_HIP(call)                                                                        \
+  do {                                                                                      \
+    hipError_t e_ = (call);                                                                 \
+    if (e_ != hipSuccess)                                                                   \
+      return set_err(-3, "%s failed: %s (%s:%d)", #call, hipGetErrorString(e_), __FILE__,   \
+                     __LINE__);                                                             \
+  } while (0)
+
+extern "C" const char *ec_last_error(void) { return g_err; }
+
+extern "C" size_t ec_gpt2_sizeof(void) { return sizeof(GPT2); }
+
+extern "C" int ec_init(void) {
+  if (g_inited) return 0;
+  const char *d = getenv("EDGECORE_DEVICE");
+  g_device = d ? atoi(d) : 0;
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n <= 0)
+    return set_err(-2, "no HIP device available");
+  if (g_device < 0 || g_device >= n)
+    return set_err(-2, "EDGECORE_DEVICE=%d out of range (%d devices)", g_device, n);
+  EC_HIP(hipSetDevice(g_device));
+  EC_HIP(hipGetDeviceProperties(&g_prop, g_device));
+  int lds = 0;
+  if (hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, g_device) == hipSuccess &&
+      lds > 0)
+    g_max_lds = lds;
+  EC_HIP(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
+  g_inited = 1;
+  return 0;
+}
+
+#define EC_INIT()                      \
+  do {                                 \
+    int r_ = ec_init();                \
+    if (r_) return r_;                 \
+  } while (0)
+
+extern "C" void *ec_stream(void) {
+  if (ec_init()) return nullptr;
+  return (void *)g_stream;
+}
+
+extern "C" int ec_sync(void) {
+  EC_INIT();
+  EC_HIP(hipStreamSynchronize(g_stream));
+  return 0;
+}
+
+extern "C" int ec_device_info(char *buf, int len) {
+  EC_INIT();
+  int n = snprintf(buf, (size_t)len,
+                   "{\"device\": %d, \"name\": \"%s\", \"arch\": \"%s\", \"cus\": %d, "
+                   "\"hbm_bytes\": %zu, \"max_lds_per_block\": %d, \"clock_khz\": %d}",
+                   g_device, g_prop.name, g_prop.gcnArchName, g_prop.multiProcessorCount,
+                   (size_t)g_prop.totalGlobalMem, g_max_lds, g_prop.clockRate);
+  return n;
+}
+
+extern "C" void *ec_dev_alloc(size_t bytes) {
+  if (ec_init()) return nullptr;
+  void *p = nullptr;
+  if (hipMalloc(&p, bytes ? bytes : 1) != hipSuccess) {
+    set_err(-3, "hipMalloc(%zu) failed", bytes);
+    return nullptr;
+  }
+  return p;
+}
+
+extern "C" int ec_dev_free(void *p) {
+  EC_INIT();
+  if (p) EC_HIP(hipFree(p));
+  return 0;
+}
+
+extern "C" int ec_memcpy_h2d(void *dst, const void *src, size_t bytes) {
+  EC_INIT();
+  EC_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, g_stream));
+  EC_HIP(hipStreamSynchronize(g_stream));
+  return 0;
+}
+
+extern "C" int ec_memcpy_d2h(void *dst, const void *src, size_t bytes) {
+  EC_INIT();
+  EC_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, g_stream));
+  EC_HIP(hipStreamSynchronize(g_stream));
+  return 0;
+}
+
+extern "C" int ec_memset_dev(void *dst, int value, size_t bytes) {
+  EC_INIT();
+  EC_HIP(hipMemsetAsync(dst, value, bytes, g_stream));
+  EC_HIP(hipStreamSynchronize(g_stream));
+  return 0;
+}
+
+// ---------------------------------------------------------------------------
+// per-kernel timing
+// ---------------------------------------------------------------------------
+
+struct ProfRec {
+  const char *fam;
+  int ev;  // index of the first of two pooled events
+  double bytes;
+};
+static bool g_prof_on = false;
+static std::string g_prof_filter;
+static std::vector<hipEvent_t> g_ev_pool;
+static size_t g_ev_used = 0;
+static std::vector<ProfRec> g_prof;
+
+static int prof_begin(const char *fam, double bytes) {
+  if (!g_prof_on) return -1;
+  if (!g_prof_filter.empty() && !strstr(fam, g_prof_filter.c_str())) return -1;
+  while (g_ev_pool.size() < g_ev_used + 2) {
+    hipEvent_t e;
+    if (hipEventCreate(&e) != hipSuccess) return -1;
+    g_ev_pool.push_back(e);
+  }
+  const int ev = (int)g_ev_used;
+  g_ev_used += 2;
+  (void)hipEventRecord(g_ev_pool[ev], g_stream);
+  g_prof.push_back({fam, ev, bytes});
+  return (int)g_prof.size() - 1;
+}
+
+static void prof_end(int rec) {
+  if (rec < 0) return;
+  (void)hipEventRecord(g_ev_pool[g_prof[rec].ev + 1], g_stream);
+}
+
+extern "C" int ec_prof_start(const char *filter) {
+  EC_INIT();
+  g_prof_filter = filter ? filter : "";
+  g_prof.clear();
+  g_ev_used = 0;
+  g_prof_on = true;
+  return 0;
+}
+
+extern "C" int ec_prof_stop(char *buf, int len) {
+  EC_INIT();
+  g_prof_on = false;
+  EC_HIP(hipStreamSynchronize(g_stream));
+  struct Agg {
+    const char *fam;
+    int n;
+    double us, bytes;
+  };
+  std::vector<Agg> agg;
+  for (const ProfRec &r : g_prof) {
+    float ms = 0.0f;
+    EC_HIP(hipEventElapsedTime(&ms, g_ev_pool[r.ev], g_ev_pool[r.ev + 1]));
+    size_t i = 0;
+    for (; i < agg.size(); i++)
+      if (!strcmp(agg[i].fam, r.fam)) break;
+    if (i == agg.size()) agg.push_back({r.fam, 0, 0.0, 0.0});
+    agg[i].n++;
+    agg[i].us += ms * 1000.0;
+    agg[i].bytes += r.bytes;
+  }
+  std::string s = "[";
+  for (size_t i = 0; i < agg.size(); i++) {
+    char tmp[512];
+    const double avg = agg[i].us / agg[i].n, bpl = agg[i].bytes / agg[i].n;
+    snprintf(tmp, sizeof tmp,
+             "%s{\"kernel\": \"%s\", \"launches\": %d, \"total_us\": %.3f, \"avg_us\": %.4f, "
+             "\"bytes_per_launch\": %.0f, \"gbps\": %.2f}",
+             i ? ", " : "", agg[i].fam, agg[i].n, agg[i].us, avg, bpl,
+             avg > 0 ? bpl / (avg * 1e3) : 0.0);
+    s += tmp;
+  }
+  s += "]";
+  g_prof.clear();
+  g_ev_used = 0;
+  if ((int)s.size() + 1 > len) return set_err(-1, "ec_prof_stop: buffer too small (%zu)", s.size() + 1);
+  memcpy(buf, s.c_str(), s.size() + 1);
+  return (int)s.size();
+}
+
+#define EC_LAUNCH(fam, bytes, call)                                                        \
+  do {                                                                                     \
+    const int p_ = prof_begin(fam, (double)(bytes));                                      \
+    const hipError_t e_ = (call);                                                          \
+    prof_end(p_);                                                                          \
+    if (e_ != hipSuccess) return set_err(-3, "%s launch failed: %s", fam, hipGetErrorString(e_)); \
+  } while (0)
+
+// ---------------------------------------------------------------------------
+// kernel ABI
+// ---------------------------------------------------------------------------
+
+static double gemv_i8_bytes(int M, int K, int N, bool scales, bool bias, int epi) {
+  double b = (double)N * K + (scales ? 4.0 * N : 0) + (bias ? 4.0 * N : 0) + (double)M * K + 4.0 * M;
+  b += 4.0 * M * N * (epi == EPI_RESID ? 2 : 1);
+  return b;
+}
+
+static double gemv_w16_bytes(int M, int K, int N, bool bias, int epi) {
+  double b = 2.0 * N * K + (bias ? 4.0 * N : 0) + 4.0 * M * K;
+  b += 4.0 * M * N * ((epi == EPI_RESID || epi == EPI_BIAS_RESID) ? 2 : 1);
+  return b;
+}
+
+extern "C" int ec_gemm_int8_dev(float *C, const int8_t *A, const float *a_scale, const int8_t *B,
+                                const float *b_scale, const float *bias, int M, int K, int N) {
+  EC_INIT();
+  if (M < 0 || N < 0 || K < 0) return set_err(-1, "gemm_int8: negative shape M=%d K=%d N=%d", M, K, N);
+  if (M == 0 || N == 0) return 0;
+  if (!C || !a_scale || (K > 0 && (!A || !B))) return set_err(-1, "gemm_int8: null pointer");
+  GemvI8Args a{A, K, a_scale, B, b_scale, bias, nullptr, nullptr, C, N, M, K, N};
+  EC_LAUNCH("gemv_i8", gemv_i8_bytes(M, K, N, b_scale, bias, EPI_STORE), gemv_i8(a, EPI_STORE, g_stream));
+  return 0;
+}
+
+static int gemm_w16_dev(float *C, const float *A, const uint16_t *B, int M, int K, int N, bool bf16) {
+  EC_INIT();
+  if (M < 0 || N < 0 || K < 0) return set_err(-1, "gemm: negative shape M=%d K=%d N=%d", M, K, N);
+  if (M == 0 || N == 0) return 0;
+  if (!C || (K > 0 && (!A || !B))) return set_err(-1, "gemm: null pointer");
+  GemvW16Args a{A, K, B, nullptr, nullptr, C, N, M, K, N};
+  EC_LAUNCH("gemv_w16", gemv_w16_bytes(M, K, N, false, EPI_STORE), gemv_w16(a, EPI_STORE, bf16, g_stream));
+  return 0;
+}
+
+extern "C" int ec_gemm_fp16_fp32_dev(float *C, const float *A, const uint16_t *B, int M, int K, int N) {
+  return gemm_w16_dev(C, A, B, M, K, N, false);
+}
+
+extern "C" int ec_gemm_bf16_fp32_dev(float *C, const float *A, const uint16_t *B, int M, int K, int N) {
+  return gemm_w16_dev(C, A, B, M, K, N, true);
+}
+
+extern "C" int ec_quantize_rows_dev(const float *in, int M, int K, int8_t *q, float *s) {
+  EC_INIT();
+  if (M < 0 || K < 0) return set_err(-1, "quantize_rows: negative shape");
+  if (M == 0) return 0;
+  if (!in || !q || !s) return set_err(-1, "quantize_rows: null pointer");
+  EC_LAUNCH("quant", 5.0 * M * K + 4.0 * M, quant_rows(in, K, M, K, q, K, s, g_stream));
+  return 0;
+}
+
+// grow-only device staging for the host-pointer ABI
+struct Staging {
+  void *p = nullptr;
+  size_t n = 0;
+};
+static Staging g_st[6];
+
+static int stage(int i, size_t bytes, void **out) {
+  if (g_st[i].n < bytes) {
+    if (g_st[i].p) EC_HIP(hipFree(g_st[i].p));
+    g_st[i].p = nullptr;
+    g_st[i].n = 0;
+    EC_HIP(hipMalloc(&g_st[i].p, bytes));
+    g_st[i].n = bytes;
+  }
+  *out = g_st[i].p;
+  return 0;
+}
+
+static void abi_die(const char *fn) {
+  fprintf(stderr, "%s: %s\n", fn, g_err);
+  exit(1);
+}
+
+static int gemm_int8_host(float *C, const int8_t *A, const float *a_scale, const int8_t *B,
+                          const float *b_scale, const float *bias, int M, int K, int N) {
+  EC_INIT();
+  if (M <= 0 || N <= 0) return 0;
+  if (K < 0) K = 0;
+  void *dA, *das, *dB, *dbs = nullptr, *dbias = nullptr, *dC;
+  int r;
+  if ((r = stage(0, (size_t)M * K + 16, &dA)) || (r = stage(1, (size_t)M * 4, &das)) ||
+      (r = stage(2, (size_t)N * K + 16, &dB)) || (r = stage(4, (size_t)M * N * 4, &dC)))
+    return r;
+  if (K) EC_HIP(hipMemcpyAsync(dA, A, (size_t)M * K, hipMemcpyHostToDevice, g_stream));
+  EC_HIP(hipMemcpyAsync(das, a_scale, (size_t)M * 4, hipMemcpyHostToDevice, g_stream));
+  if (K) EC_HIP(hipMemcpyAsync(dB, B, (size_t)N * K, hipMemcpyHostToDevice, g_stream));
+  if (b_scale || bias) {
+    if ((r = stage(3, (size_t)N * 8, &dbs))) return r;
+    if (b_scale) EC_HIP(hipMemcpyAsync(dbs, b_scale, (size_t)N * 4, hipMemcpyHostToDevice, g_stream));
+    dbias = (char *)dbs + (size_t)N * 4;
+    if (bias) EC_HIP(hipMemcpyAsync(dbias, bias, (size_t)N * 4, hipMemcpyHostToDevice, g_stream));
+  }
+  if ((r = ec_gemm_int8_dev((float *)dC, (const int8_t *)dA, (const float *)das, (const int8_t *)dB,
+                            b_scale ? (const float *)dbs : nullptr,
+                            bias ? (const float *)dbias : nullptr, M, K, N)))
+    return r;
+  EC_HIP(hipMemcpyAsync(C, dC, (size_t)M * N * 4, hipMemcpyDeviceToHost, g_stream));
+  EC_HIP(hipStreamSynchronize(g_stream));
+  return 0;
+}
+
+static int gemm_w16_host(float *C, const float *A, const uint16_t *B, int M, int K, int N, bool bf16) {
+  EC_INIT();
+  if (M <= 0 || N <= 0) return 0;
+  if (K < 0) K = 0;
+  void *dA, *dB, *dC;
+  int r;
+  if ((r = stage(0, (size_t)M * K * 4 + 16, &dA)) || (r = stage(2, (size_t)N * K * 2 + 16, &dB)) ||
+      (r = stage(4, (size_t)M * N * 4, &dC)))
+    return r;
+  if (K) {
+    EC_HIP(hipMemcpyAsync(dA, A, (size_t)M * K * 4, hipMemcpyHostToDevice, g_stream));
+    EC_HIP(hipMemcpyAsync(dB, B, (size_t)N * K * 2, hipMemcpyHostToDevice, g_stream));
+  }
+  if ((r = gemm_w16_dev((float *)dC, (const float *)dA, (const uint16_t *)dB, M, K, N, bf16))) return r;
+  EC_HIP(hipMemcpyAsync(C, dC, (size_t)M * N * 4, hipMemcpyDeviceToHost, g_stream));
+  EC_HIP(hipStreamSynchronize(g_stream));
+  return 0;
+}
+
+extern "C" void gemm_int8(float *C, const int8_t *A, const float *a_scale, const int8_t *B,
+                          const float *b_scale, const float *bias, int M, int K, int N) {
+  if (gemm_int8_host(C, A, a_scale, B, b_scale, bias, M, K, N)) abi_die("gemm_int8");
+}
+
+extern "C" void gemm_fp16_fp32(float *C, const float *A, const uint16_t *B, int M, int K, int N) {
+  if (gemm_w16_host(C, A, B, M, K, N, false)) abi_die("gemm_fp16_fp32");
+}
+
+extern "C" void gemm_bf16_fp32(float *C, const float *A, const uint16_t *B, int M, int K, int N) {
+  if (gemm_w16_host(C, A, B, M, K, N, true)) abi_die("gemm_bf16_fp32");
+}
+
+// ---------------------------------------------------------------------------
+// model
+// ---------------------------------------------------------------------------
+
+struct LayerDev {
+  const float *ln1_g, *ln1_b, *ln2_g, *ln2_b;
+  const void *wqkv;
+  const float *sqkv, *bqkv;
+  const void *wo;
+  const float *so, *bo;
+  const void *wg, *wu;
+  const float *sg, *su;
+  const void *wfc;
+  const float *sfc, *bfc;
+  const void *wd;
+  const float *sd, *bd;
+};
+
+struct DevModel {
+  char *arena = nullptr;
+  size_t arena_bytes = 0;
+  std::vector<LayerDev> L;
+  double2 *rope = nullptr;
+  int half = 0;
+  int eff_ctx = 0, mmax = 0, lm_rows = 0;
+  int qkv_ld = 0, aq_ld = 0, F = 0;
+  int *d_tok = nullptr, *d_pos = nullptr, *d_slot = nullptr, *d_amax = nullptr;
+  int *h_stage = nullptr;  // pinned: tokens | positions | slots
+  float *x = nullptr, *h = nullptr, *qkv = nullptr, *att = nullptr, *ff = nullptr;
+  int8_t *aq = nullptr;
+  float *as = nullptr;
+  float *logits = nullptr;
+  uint16_t *kc = nullptr, *vc = nullptr;
+  size_t kv_layer = 0;  // elements per layer of one cache
+  const uint16_t *lm = nullptr;
+};
+
+namespace {
+
+struct Place {
+  const EcmTensor *t;
+  size_t off;
+};
+
+struct Loader {
+  GPT2 *g;
+  const char *base;
+  EcmTensor *tens;
+  int n;
+  std::vector<Place> places;
+  size_t cursor = 0;
+  char err[256] = {0};
+
+  const EcmTensor *find(const char *name) const {
+    for (int i = 0; i < n; i++)
+      if (!strcmp(tens[i].name, name)) return &tens[i];
+    return nullptr;
+  }
+  // reserve an aligned arena slot (or, with `glue`, the bytes right after the
+  // previous tensor) and return its offset; -1 on a size mismatch
+  long place(const EcmTensor *t, size_t want_bytes, int want_dtype, bool glue = false) {
+    if (!t) return -1;
+    if (t->bytes != want_bytes || (want_dtype >= 0 && t->dtype != want_dtype)) {
+      snprintf(err, sizeof err, "ecm: tensor %s has %zu bytes of dtype %d, expected %zu of dtype %d",
+               t->name, t->bytes, t->dtype, want_bytes, want_dtype);
+      return -2;
+    }
+    if (!glue) cursor = (cursor + 255) & ~(size_t)255;
+    places.push_back({t, cursor});
+    const size_t off = cursor;
+    cursor += t->bytes;
+    return (long)off;
+  }
+};
+
+}  // namespace
+
+static void free_dev(DevModel *d) {
+  if (!d) return;
+  void *ps[] = {d->arena, d->rope, d->d_tok, d->d_pos, d->d_slot, d->d_amax, d->x, d->h, d->qkv,
+                d->att, d->ff, d->aq, d->as, d->logits, d->kc, d->vc};
+  for (void *p : ps)
+    if (p) (void)hipFree(p);
+  if (d->h_stage) (void)hipHostFree(d->h_stage);
+  delete d;
+}
+
+static int load_impl(GPT2 *g, const char *path, int batch_cap, int max_ctx) {
+  memset(g, 0, sizeof *g);
+  g->batch_cap = batch_cap < 1 ? 1 : batch_cap;
+  g->max_ctx = max_ctx > 0 ? max_ctx : 0;
+  g->eps = 1e-5;
+  EC_INIT();
+
+  const int fd = open(path, O_RDONLY);
+  if (fd < 0) return set_err(-1, "open model %s: %s", path, strerror(errno));
+  struct stat st;
+  if (fstat(fd, &st) != 0 || st.st_size <= 0) {
+    close(fd);
+    return set_err(-1, "model %s is empty", path);
+  }
+  void *map = mmap(nullptr, (size_t)st.st_size, PROT_READ, MAP_PRIVATE, fd, 0);
+  close(fd);
+  if (map == MAP_FAILED) return set_err(-1, "mmap model: %s", strerror(errno));
+  g->file_data = map;
+  g->file_size = (size_t)st.st_size;
+  g->file_mapped = 1;
+
+  std::vector<EcmTensor> tens(4096);
+  const int n = ecm_parse(map, g->file_size, tens.data(), (int)tens.size(), g);
+  if (n < 0) return set_err(-1, "ecm: cannot parse %s", path);
+  for (int i = 0; i < n; i++)
+    if (tens[i].offset + tens[i].bytes > g->file_size)
+      return set_err(-1, "ecm: tensor %s extends past the end of the file (truncated?)", tens[i].name);
+
+  Loader ld{g, (const char *)map, tens.data(), n};
+  const bool qwen = g->arch == ARCH_QWEN2;
+  const EcmTensor *t0 = ld.find(qwen ? "blocks.0.q.w" : "blocks.0.attn.w");
+  if (!ld.find("wte") || !ld.find("ln_f.g")) return set_err(-1, "ecm: missing core tensors (wte, ln_f.g)");
+  if (!t0) return set_err(-1, "ecm: missing %s", qwen ? "blocks.0.q.w" : "blocks.0.attn.w");
+  if (t0->dtype == 1) g->precision = 1;
+  else if (t0->dtype == 2) g->precision = 0;
+  else if (t0->dtype == 4) g->precision = 2;
+  else return set_err(-1, "ecm: unexpected linear weight dtype");
+
+  const int E = g->n_embd, H = g->n_head, V = g->vocab, Lc = g->n_layer;
+  if (E <= 0 || H <= 0 || V <= 0 || Lc <= 0 || g->n_ctx <= 0 || E % H)
+    return set_err(-1, "ecm: bad shape meta (n_embd %d, n_head %d, vocab %d, n_layer %d, n_ctx %d)", E, H,
+                   V, Lc, g->n_ctx);
+  if (qwen) {  // set_qwen2_defaults, src/gpt2.c:149-159
+    if (g->n_kv_head <= 0) g->n_kv_head = g->n_head;
+    g->head_dim = E / H;
+    g->n_kv_embd = g->n_kv_head * g->head_dim;
+    if (g->intermediate <= 0) g->intermediate = 4 * E;
+    if (g->rope_theta <= 0) g->rope_theta = 10000.0;
+    if (g->yarn_orig_max <= 0) g->yarn_orig_max = g->n_ctx;
+    if (g->yarn_factor <= 0) g->yarn_factor = 1.0;
+    if (g->yarn_attention_factor <= 0) g->yarn_attention_factor = 1.0;
+  } else {
+    g->n_kv_embd = E;
+    g->n_kv_head = H;
+    g->intermediate = 4 * E;
+    g->head_dim = E / H;
+  }
+  const int kv = g->n_kv_embd, F = g->intermediate, hd = g->head_dim;
+  const int wdt = g->precision == 0 ? 2 : g->precision == 1 ? 1 : 4;  // linear weight dtype
+  const int edt = g->precision == 2 ? 4 : 1;                          // embedding dtype
+  const size_t wb = g->precision == 0 ? 1 : 2;
+  const int eff = gpt2_eff_ctx(g);
+
+  DevModel *d = new DevModel();
+  g->dev = d;
+  d->eff_ctx = eff;
+  d->F = F;
+  d->L.resize(Lc);
+
+  long o_wte = ld.place(ld.find("wte"), (size_t)V * E * 2, edt), o_wpe = -1, o_lm = -1;
+  long o_lnf = ld.place(ld.find("ln_f.g"), (size_t)E * 4, 0), o_lnfb = -1;
+  if (!qwen) {
+    if (!ld.find("wpe") || !ld.find("ln_f.b")) return set_err(-1, "ecm: missing wpe / ln_f.b");
+    o_wpe = ld.place(ld.find("wpe"), (size_t)g->n_ctx * E * 2, edt);
+    o_lnfb = ld.place(ld.find("ln_f.b"), (size_t)E * 4, 0);
+  } else {
+    const EcmTensor *lmh = ld.find("lm_head.w");
+    if (lmh && !g->tie_word_embeddings) o_lm = ld.place(lmh, (size_t)V * E * 2, edt);
+    if (g->tie_word_embeddings || !lmh) g->tie_word_embeddings = 1;
+  }
+  if (o_wte < 0 || o_lnf < 0 || (!qwen && (o_wpe < 0 || o_lnfb < 0)) || o_lm == -2)
+    return set_err(-1, "%s", ld.err[0] ? ld.err : "ecm: bad core tensor");
+
+  struct LOff {
+    long ln1, ln1b, ln2, ln2b, w[7], s[7], b[7];
+  };
+  std::vector<LOff> lo(Lc);
+  char nm[256];
+  for (int l = 0; l < Lc; l++) {
+    LOff &o = lo[l];
+    for (int i = 0; i < 7; i++) o.w[i] = o.s[i] = o.b[i] = -1;
+    auto vec = [&](const char *suf, bool need) -> long {
+      snprintf(nm, sizeof nm, "blocks.%d.%s", l, suf);
+      const EcmTensor *t = ld.find(nm);
+      if (!t) return need ? -3 : -1;
+      return ld.place(t, (size_t)E * 4, 0);
+    };
+    o.ln1 = vec("ln_1.g", true);
+    o.ln2 = vec("ln_2.g", true);
+    o.ln1b = qwen ? -1 : vec("ln_1.b", true);
+    o.ln2b = qwen ? -1 : vec("ln_2.b", true);
+    if (o.ln1 < 0 || o.ln2 < 0 || (!qwen && (o.ln1b < 0 || o.ln2b < 0)))
+      return set_err(-1, "%s", ld.err[0] ? ld.err : "ecm: missing layer norm tensors");
+    // linear list: name, out, in; qwen q/k/v are glued back to back
+    const char *qn[7] = {"q", "k", "v", "o", "gate", "up", "down"};
+    const int qo[7] = {E, kv, kv, E, F, F, E}, qi[7] = {E, E, E, E, E, E, F};
+    const char *gn[4] = {"attn", "proj", "fc", "fc2"};
+    const int go[4] = {3 * E, E, 4 * E, E}, gi[4] = {E, E, E, 4 * E};
+    const int cnt = qwen ? 7 : 4;
+    for (int i = 0; i < cnt; i++) {
+      const char *suf = qwen ? qn[i] : gn[i];
+      const int out = qwen ? qo[i] : go[i], in = qwen ? qi[i] : gi[i];
+      snprintf(nm, sizeof nm, "blocks.%d.%s.w", l, suf);
+      o.w[i] = ld.place(ld.find(nm), (size_t)out * in * wb, wdt, qwen && (i == 1 || i == 2));
+      if (o.w[i] < 0) return set_err(-1, "%s", ld.err[0] ? ld.err : "ecm: missing linear weight");
+    }
+    if (g->precision == 0) {
+      for (int i = 0; i < cnt; i++) {
+        const char *suf = qwen ? qn[i] : gn[i];
+        const int out = qwen ? qo[i] : go[i];
+        snprintf(nm, sizeof nm, "blocks.%d.%s.s", l, suf);
+        o.s[i] = ld.place(ld.find(nm), (size_t)out * 4, 0, qwen && (i == 1 || i == 2));
+        if (o.s[i] < 0) return set_err(-1, "%s", ld.err[0] ? ld.err : "ecm: missing int8 scale");
+      }
+    }
+    if (!qwen) {  // GPT-2 linears carry biases (src/gpt2.c:289-305); Qwen2 biases are ignored
+      for (int i = 0; i < 4; i++) {
+        snprintf(nm, sizeof nm, "blocks.%d.%s.b", l, gn[i]);
+        o.b[i] = ld.place(ld.find(nm), (size_t)go[i] * 4, 0);
+        if (o.b[i] < 0) return set_err(-1, "%s", ld.err[0] ? ld.err : "ecm: missing bias");
+      }
+    }
+  }
+  const EcmTensor *tv = ld.find("tokenizer.vocab"), *tm = ld.find("tokenizer.merges");
+  if (!tv || !tm) return set_err(-1, "ecm: tokenizer blobs missing");
+  if (tokenizer_load(&g->tok, ld.base + tv->offset, tv->bytes, ld.base + tm->offset, tm->bytes, V,
+                     qwen ? 1 : 0) != 0)
+    return set_err(-1, "ecm: tokenizer blobs unreadable");
+
+  // upload the arena
+  d->arena_bytes = (ld.cursor + 255) & ~(size_t)255;
+  EC_HIP(hipMalloc(&d->arena, d->arena_bytes));
+  for (const Place &p : ld.places)
+    EC_HIP(hipMemcpy(d->arena + p.off, ld.base + p.t->offset, p.t->bytes, hipMemcpyHostToDevice));
+  char *A = d->arena;
+  auto F32 = [&](long off) -> const float * { return off >= 0 ? (const float *)(A + off) : nullptr; };
+  g->wte = (const uint16_t *)(A + o_wte);
+  g->wpe = o_wpe >= 0 ? (const uint16_t *)(A + o_wpe) : nullptr;
+  g->lm_head = o_lm >= 0 ? (const uint16_t *)(A + o_lm) : nullptr;
+  g->lnf_g = F32(o_lnf);
+  g->lnf_b = F32(o_lnfb);
+  d->lm = g->lm_head ? g->lm_head : g->wte;
+  g->lw = (struct LayerW *)calloc((size_t)Lc, sizeof *g->lw);
+  for (int l = 0; l < Lc; l++) {
+    const LOff &o = lo[l];
+    struct LayerW *W = &g->lw[l];
+    LayerDev &D = d->L[l];
+    W->ln1_g = D.ln1_g = F32(o.ln1);
+    W->ln1_b = D.ln1_b = F32(o.ln1b);
+    W->ln2_g = D.ln2_g = F32(o.ln2);
+    W->ln2_b = D.ln2_b = F32(o.ln2b);
+    if (qwen) {
+      const void *w[7];
+      for (int i = 0; i < 7; i++) w[i] = A + o.w[i];
+      W->q_w = w[0]; W->k_w = w[1]; W->v_w = w[2]; W->o_w = w[3];
+      W->gate_w = w[4]; W->up_w = w[5]; W->down_w = w[6];
+      W->q_s = F32(o.s[0]); W->k_s = F32(o.s[1]); W->v_s = F32(o.s[2]); W->o_s = F32(o.s[3]);
+      W->gate_s = F32(o.s[4]); W->up_s = F32(o.s[5]); W->down_s = F32(o.s[6]);
+      D.wqkv = w[0]; D.sqkv = W->q_s; D.bqkv = nullptr;
+      D.wo = w[3]; D.so = W->o_s; D.bo = nullptr;
+      D.wg = w[4]; D.sg = W->gate_s; D.wu = w[5]; D.su = W->up_s;
+      D.wd = w[6]; D.sd = W->down_s; D.bd = nullptr;
+    } else {
+      W->attn_w = A + o.w[0]; W->proj_w = A + o.w[1]; W->fc_w = A + o.w[2]; W->fc2_w = A + o.w[3];
+      W->attn_s = F32(o.s[0]); W->proj_s = F32(o.s[1]); W->fc_s = F32(o.s[2]); W->fc2_s = F32(o.s[3]);
+      W->attn_b = F32(o.b[0]); W->proj_b = F32(o.b[1]); W->fc_b = F32(o.b[2]); W->fc2_b = F32(o.b[3]);
+      D.wqkv = W->attn_w; D.sqkv = W->attn_s; D.bqkv = W->attn_b;
+      D.wo = W->proj_w; D.so = W->proj_s; D.bo = W->proj_b;
+      D.wfc = W->fc_w; D.sfc = W->fc_s; D.bfc = W->fc_b;
+      D.wd = W->fc2_w; D.sd = W->fc2_s; D.bd = W->fc2_b;
+    }
+  }
+
+  // RoPE table: the reference's qwen_inv_freq / qwen_rope_cos_sin
+  // (src/gpt2.c:608-654) evaluated once per position with the same libm calls
+  if (qwen) {
+    int half = hd / 2;
+    if (half > 512) half = 512;
+    d->half = half;
+    std::vector<double> invf(half);
+    const int dim = 2 * half;
+    const double inv_base = 1.0 / g->rope_theta;
+    for (int i = 0; i < half; i++) invf[i] = pow(inv_base, (double)(2 * i) / (double)dim);
+    if (g->rope_type == ROPE_YARN) {
+      const double pi2 = 6.28318530717958647692, logbase = log(g->rope_theta);
+      double lo_ = floor((double)dim * log(g->yarn_orig_max / (32.0 * pi2)) / (2.0 * logbase));
+      double hi_ = ceil((double)dim * log(g->yarn_orig_max / (1.0 * pi2)) / (2.0 * logbase));
+      if (lo_ < 0.0) lo_ = 0.0;
+      if (hi_ > (double)(dim - 1)) hi_ = (double)(dim - 1);
+      double span = hi_ - lo_;
+      if (span < 1.0) span = 1.0;
+      for (int i = 0; i < half; i++) {
+        double ramp = ((double)i - lo_) / span;
+        if (ramp < 0.0) ramp = 0.0;
+        if (ramp > 1.0) ramp = 1.0;
+        const double extrap = invf[i], interp = invf[i] / g->yarn_factor;
+        invf[i] = interp * ramp + extrap * (1.0 - ramp);
+      }
+    }
+    std::vector<double2> tab((size_t)eff * half);
+    const double scale = g->yarn_attention_factor;
+    for (int p = 0; p < eff; p++)
+      for (int i = 0; i < half; i++) {
+        const double f = (double)p * invf[i];
+        tab[(size_t)p * half + i] = make_double2(cos(f) * scale, sin(f) * scale);
+      }
+    EC_HIP(hipMalloc(&d->rope, tab.size() * sizeof(double2)));
+    EC_HIP(hipMemcpy(d->rope, tab.data(), tab.size() * sizeof(double2), hipMemcpyHostToDevice));
+  }
+
+  // KV cache [L][B][eff_ctx][kv] fp16, zeroed
+  d->kv_layer = (size_t)g->batch_cap * eff * kv;
+  const size_t kvb = d->kv_layer * Lc * sizeof(uint16_t);
+  EC_HIP(hipMalloc(&d->kc, kvb));
+  EC_HIP(hipMalloc(&d->vc, kvb));
+  EC_HIP(hipMemset(d->kc, 0, kvb));
+  EC_HIP(hipMemset(d->vc, 0, kvb));
+  g->k_cache = d->kc;
+  g->v_cache = d->vc;
+
+  // workspaces for M up to max(eff_ctx, batch_cap) (src/gpt2.c:319-348)
+  const int mmax = eff > g->batch_cap ? eff : g->batch_cap;
+  d->mmax = mmax;
+  d->qkv_ld = qwen ? E + 2 * kv : 3 * E;
+  const int qmax = E > F ? E : F;
+  d->aq_ld = (qmax + 15) & ~15;
+  d->lm_rows = mmax < 64 ? mmax : 64;
+  if (d->lm_rows < g->batch_cap) d->lm_rows = g->batch_cap;
+  EC_HIP(hipMalloc(&d->x, (size_t)mmax * E * 4));
+  EC_HIP(hipMalloc(&d->h, (size_t)mmax * E * 4));
+  EC_HIP(hipMalloc(&d->qkv, (size_t)mmax * d->qkv_ld * 4));
+  EC_HIP(hipMalloc(&d->att, (size_t)mmax * E * 4));
+  EC_HIP(hipMalloc(&d->ff, (size_t)mmax * F * 4));
+  EC_HIP(hipMalloc(&d->aq, (size_t)mmax * d->aq_ld));
+  EC_HIP(hipMalloc(&d->as, (size_t)mmax * 4));
+  EC_HIP(hipMalloc(&d->logits, (size_t)d->lm_rows * V * 4));
+  EC_HIP(hipMalloc(&d->d_tok, (size_t)mmax * 4));
+  EC_HIP(hipMalloc(&d->d_pos, (size_t)mmax * 4));
+  EC_HIP(hipMalloc(&d->d_slot, (size_t)mmax * 4));
+  EC_HIP(hipMalloc(&d->d_amax, (size_t)mmax * 4));
+  EC_HIP(hipHostMalloc((void **)&d->h_stage, (size_t)mmax * 3 * 4, hipHostMallocDefault));
+  g->ws_x = d->x;
+  g->ws_tmp = d->h;
+  g->ws_qkv = d->qkv;
+  g->ws_attn = d->att;
+  g->ws_scores = nullptr;  // attention scores live in LDS
+  g->ws_q = d->aq;
+  g->ws_qs = d->as;
+  g->ws_q_cols = (size_t)d->aq_ld;
+
+  munmap(g->file_data, g->file_size);
+  g->file_data = nullptr;
+  g->file_size = 0;
+  g->file_mapped = 0;
+  return 0;
+}
+
+extern "C" int gpt2_load(GPT2 *g, const char *path, int batch_cap, int max_ctx) {
+  const int r = load_impl(g, path, batch_cap, max_ctx);
+  if (r) {
+    fprintf(stderr, "%s\n", g_err);
+    gpt2_free(g);
+    return -1;
+  }
+  return 0;
+}
+
+extern "C" void gpt2_free(GPT2 *g) {
+  if (!g) return;
+  tokenizer_free(&g->tok);
+  free(g->lw);
+  free_dev((DevModel *)g->dev);
+  if (g->file_data && g->file_mapped) munmap(g->file_data, g->file_size);
+  memset(g, 0, sizeof *g);
+}
+
+extern "C" int gpt2_kv_reset(GPT2 *g) {
+  EC_INIT();
+  DevModel *d = (DevModel *)g->dev;
+  if (!d) return set_err(-1, "gpt2_kv_reset: model not loaded");
+  const size_t b = d->kv_layer * g->n_layer * sizeof(uint16_t);
+  EC_HIP(hipMemsetAsync(d->kc, 0, b, g_stream));
+  EC_HIP(hipMemsetAsync(d->vc, 0, b, g_stream));
+  EC_HIP(hipStreamSynchronize(g_stream));
+  return 0;
+}
+
+static int forward_impl(GPT2 *g, const int *tokens, const int *positions, const int *seqs, int M,
+                        int lm_from, float *logits, int *argmax) {
+  EC_INIT();
+  DevModel *d = (DevModel *)g->dev;
+  if (!d) return set_err(-1, "model not loaded");
+  if (M < 1 || M > d->mmax) return set_err(-1, "M=%d outside [1, %d]", M, d->mmax);
+  if (lm_from < 0 || lm_from > M) return set_err(-1, "lm_from=%d outside [0, %d]", lm_from, M);
+  if (!tokens || !positions) return set_err(-1, "null tokens/positions");
+  const int E = g->n_embd, H = g->n_head, V = g->vocab, kv = g->n_kv_embd, hd = g->head_dim;
+  const bool qwen = g->arch == ARCH_QWEN2, i8 = g->precision == 0, bf16 = g->precision == 2;
+  int *st = d->h_stage;
+  int max_npos = 0;
+  for (int m = 0; m < M; m++) {
+    if (tokens[m] < 0 || tokens[m] >= V) return set_err(-1, "token %d at row %d outside [0, %d)", tokens[m], m, V);
+    if (positions[m] < 0 || positions[m] >= d->eff_ctx)
+      return set_err(-1, "position %d at row %d outside [0, %d)", positions[m], m, d->eff_ctx);
+    int slot = seqs ? seqs[m] : m;
+    if (slot < 0) return set_err(-1, "negative slot %d at row %d", slot, m);
+    if (slot >= g->batch_cap) slot = g->batch_cap - 1;  // src/gpt2.c:512-513
+    st[m] = tokens[m];
+    st[d->mmax + m] = positions[m];
+    st[2 * d->mmax + m] = slot;
+    if (positions[m] + 1 > max_npos) max_npos = positions[m] + 1;
+  }
+  const size_t lds = attention_lds_bytes(max_npos, hd);
+  if (lds > (size_t)g_max_lds)
+    return set_err(-1, "position %d needs %zu bytes of LDS for attention scores (limit %d)", max_npos - 1,
+                   lds, g_max_lds);
+  hipStream_t s = g_stream;
+  EC_HIP(hipMemcpyAsync(d->d_tok, st, (size_t)M * 4, hipMemcpyHostToDevice, s));
+  EC_HIP(hipMemcpyAsync(d->d_pos, st + d->mmax, (size_t)M * 4, hipMemcpyHostToDevice, s));
+  EC_HIP(hipMemcpyAsync(d->d_slot, st + 2 * d->mmax, (size_t)M * 4, hipMemcpyHostToDevice, s));
+
+  EC_LAUNCH("embed", (double)M * E * (g->wpe ? 8 : 6), embed(g->wte, g->wpe, bf16, d->d_tok, d->d_pos, M, E, d->x, s));
+
+  const int F = d->F, ldq = d->qkv_ld, aql = d->aq_ld;
+  const int nqkv = qwen ? E + 2 * kv : 3 * E;
+  for (int l = 0; l < g->n_layer; l++) {
+    const LayerDev &W = d->L[l];
+    uint16_t *kcl = d->kc + d->kv_layer * l, *vcl = d->vc + d->kv_layer * l;
+    // norm -> qkv projection
+    if (i8) {
+      EC_LAUNCH("norm_quant", (double)M * E * 5 + 8.0 * E,
+                norm_rows(d->x, M, E, W.ln1_g, W.ln1_b, g->eps, nullptr, 0, d->aq, aql, d->as, s));
+      GemvI8Args a{d->aq, aql, d->as, (const int8_t *)W.wqkv, W.sqkv, W.bqkv, nullptr, nullptr, d->qkv, ldq, M, E, nqkv};
+      EC_LAUNCH("gemv_i8_qkv", gemv_i8_bytes(M, E, nqkv, true, W.bqkv, EPI_STORE), gemv_i8(a, EPI_STORE, s));
+    } else {
+      EC_LAUNCH("norm", (double)M * E * 8 + 8.0 * E,
+                norm_rows(d->x, M, E, W.ln1_g, W.ln1_b, g->eps, d->h, E, nullptr, 0, nullptr, s));
+      GemvW16Args a{d->h, E, (const uint16_t *)W.wqkv, W.bqkv, nullptr, d->qkv, ldq, M, E, nqkv};
+      const int epi = W.bqkv ? EPI_BIAS : EPI_STORE;
+      EC_LAUNCH("gemv_w16_qkv", gemv_w16_bytes(M, E, nqkv, W.bqkv, epi), gemv_w16(a, epi, bf16, s));
+    }
+    // RoPE (Qwen2) + fp16 KV append
+    KvArgs ka{d->qkv, d->qkv + E, d->qkv + E + (qwen ? kv : E), ldq, ldq, H, g->n_kv_head, hd, kv,
+              qwen ? d->rope : nullptr, d->half, d->d_pos, d->d_slot, kcl, vcl, d->eff_ctx, M};
+    EC_LAUNCH("rope_kv", (double)M * (qwen ? (E + kv) * 8 + kv * 8 : kv * 12), rope_kv_append(ka, s));
+    // attention
+    AttnArgs aa{d->qkv, ldq, kcl, vcl, d->att, E, d->d_pos, d->d_slot, H, g->n_kv_head, hd, kv,
+                d->eff_ctx, qwen ? g->sliding_window : 0, 1.0 / sqrt((double)hd), M, max_npos};
+    double abytes = 0;
+    for (int m = 0; m < M; m++) abytes += (double)(positions[m] + 1) * kv * 4 + 8.0 * E;
+    EC_LAUNCH("attention", abytes, attention(aa, s));
+    // output projection + residual
+    if (i8) {
+      EC_LAUNCH("quant", (double)M * E * 5, quant_rows(d->att, E, M, E, d->aq, aql, d->as, s));
+      GemvI8Args a{d->aq, aql, d->as, (const int8_t *)W.wo, W.so, W.bo, nullptr, nullptr, d->x, E, M, E, E};
+      EC_LAUNCH("gemv_i8_o", gemv_i8_bytes(M, E, E, true, W.bo, EPI_RESID), gemv_i8(a, EPI_RESID, s));
+    } else {
+      GemvW16Args a{d->att, E, (const uint16_t *)W.wo, W.bo, nullptr, d->x, E, M, E, E};
+      const int epi = W.bo ? EPI_BIAS_RESID : EPI_RESID;
+      EC_LAUNCH("gemv_w16_o", gemv_w16_bytes(M, E, E, W.bo, epi), gemv_w16(a, epi, bf16, s));
+    }
+    // MLP
+    if (i8) {
+      EC_LAUNCH("norm_quant", (double)M * E * 5 + 8.0 * E,
+                norm_rows(d->x, M, E, W.ln2_g, W.ln2_b, g->eps, nullptr, 0, d->aq, aql, d->as, s));
+      if (qwen) {
+        GemvI8Args a{d->aq, aql, d->as, (const int8_t *)W.wg, W.sg, nullptr, (const int8_t *)W.wu, W.su, d->ff, F, M, E, F};
+        EC_LAUNCH("gemv_i8_gateup", 2 * gemv_i8_bytes(M, E, F, true, false, EPI_STORE) - (double)M * E - 4.0 * M - 4.0 * M * F,
+                  gemv_i8(a, EPI_SWIGLU, s));
+      } else {
+        GemvI8Args a{d->aq, aql, d->as, (const int8_t *)W.wfc, W.sfc, W.bfc, nullptr, nullptr, d->ff, F, M, E, F};
+        EC_LAUNCH("gemv_i8_fc", gemv_i8_bytes(M, E, F, true, true, EPI_GELU), gemv_i8(a, EPI_GELU, s));
+      }
+      EC_LAUNCH("quant", (double)M * F * 5, quant_rows(d->ff, F, M, F, d->aq, aql, d->as, s));
+      GemvI8Args a{d->aq, aql, d->as, (const int8_t *)W.wd, W.sd, W.bd, nullptr, nullptr, d->x, E, M, F, E};
+      EC_LAUNCH("gemv_i8_down", gemv_i8_bytes(M, F, E, true, W.bd, EPI_RESID), gemv_i8(a, EPI_RESID, s));
+    } else {
+      EC_LAUNCH("norm", (double)M * E * 8 + 8.0 * E,
+                norm_rows(d->x, M, E, W.ln2_g, W.ln2_b, g->eps, d->h, E, nullptr, 0, nullptr, s));
+      if (qwen) {
+        GemvW16Args a{d->h, E, (const uint16_t *)W.wg, nullptr, (const uint16_t *)W.wu, d->ff, F, M, E, F};
+        EC_LAUNCH("gemv_w16_gateup", 2 * gemv_w16_bytes(M, E, F, false, EPI_STORE) - 4.0 * M * E - 4.0 * M * F,
+                  gemv_w16(a, EPI_SWIGLU, bf16, s));
+      } else {
+        GemvW16Args a{d->h, E, (const uint16_t *)W.wfc, W.bfc, nullptr, d->ff, F, M, E, F};
+        EC_LAUNCH("gemv_w16_fc", gemv_w16_bytes(M, E, F, true, EPI_BIAS_GELU), gemv_w16(a, EPI_BIAS_GELU, bf16, s));
+      }
+      GemvW16Args a{d->ff, F, (const uint16_t *)W.wd, W.bd, nullptr, d->x, E, M, F, E};
+      const int epi = W.bd ? EPI_BIAS_RESID : EPI_RESID;
+      EC_LAUNCH("gemv_w16_down", gemv_w16_bytes(M, F, E, W.bd, epi), gemv_w16(a, epi, bf16, s));
+    }
+  }
+  // final norm + LM head (always fp16/bf16, src/gpt2.c:576-580 / 799-804)
+  if (lm_from < M) {
+    EC_LAUNCH("norm", (double)M * E * 8 + 8.0 * E,
+              norm_rows(d->x, M, E, g->lnf_g, g->lnf_b, g->eps, d->h, E, nullptr, 0, nullptr, s));
+    for (int r0 = lm_from; r0 < M; r0 += d->lm_rows) {
+      const int rows = M - r0 < d->lm_rows ? M - r0 : d->lm_rows;
+      GemvW16Args a{d->h + (size_t)r0 * E, E, d->lm, nullptr, nullptr, d->logits, V, rows, E, V};
+      EC_LAUNCH("gemv_w16_lmhead", gemv_w16_bytes(rows, E, V, false, EPI_STORE), gemv_w16(a, EPI_STORE, bf16, s));
+      if (argmax)
+        EC_LAUNCH("argmax", 4.0 * rows * V, argmax_rows(d->logits, rows, V, d->d_amax + (r0 - lm_from), s));
+      if (logits)
+        EC_HIP(hipMemcpyAsync(logits + (size_t)(r0 - lm_from) * V, d->logits, (size_t)rows * V * 4,
+                              hipMemcpyDeviceToHost, s));
+    }
+    if (argmax)
+      EC_HIP(hipMemcpyAsync(argmax, d->d_amax, (size_t)(M - lm_from) * 4, hipMemcpyDeviceToHost, s));
+  }
+  EC_HIP(hipStreamSynchronize(s));
+  return 0;
+}
+
+extern "C" int gpt2_forward_ex(GPT2 *g, const int *tokens, const int *positions, const int *seqs, int M,
+                               int lm_from, float *logits, int *argmax) {
+  return forward_impl(g, tokens, positions, seqs, M, lm_from, logits, argmax);
+}
+
+extern "C" void gpt2_forward(GPT2 *g, const int *tokens, const int *positions, const int *seqs, int M,
+                             float *logits) {
+  if (forward_impl(g, tokens, positions, seqs, M, 0, logits, nullptr)) {
+    fprintf(stderr, "gpt2_forward: %s\n", g_err);
+    exit(1);
+  }
+}
+
+extern "C" void qwen2_forward(GPT2 *g, const int *tokens, const int *positions, const int *seqs, int M,
+                              float *logits) {
+  if (g->arch != ARCH_QWEN2) {
+    fprintf(stderr, "qwen2_forward: model is not a qwen2 model\n");
+    exit(1);
+  }
+  gpt2_forward(g, tokens, positions, seqs, M, logits);
+}

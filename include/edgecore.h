@@ -1,0 +1,342 @@
+/*
+ * edgecore.h -- C ABI of the MI355X (gfx950) EdgeCore library,
+ * libedgecore_hip.so.
+ *
+ * The kernel and forward entry points keep the names, argument order,
+ * layouts and meaning of the reference CPU runtime header (src/edgecore.h of
+ * MaheshJakkala/EdgeCore), so a host written against that header links
+ * against this library unchanged.  Each declaration names the reference
+ * declaration it replaces.  Differences from the reference are listed at the
+ * declaration they concern; the two that matter to callers are:
+ *
+ *   1. GPT2's weight, KV-cache and workspace pointers are DEVICE pointers
+ *      (HBM on the GPU the library opened).  A host must not dereference or
+ *      memset them; gpt2_kv_reset() replaces the reference driver's memset of
+ *      k_cache/v_cache (src/runtime_main.c:312-316).
+ *   2. The kernel ABI (gemm_*) takes host pointers exactly like the reference
+ *      and stages through device memory; the ec_*_dev variants take device
+ *      pointers and run on ec_stream().
+ *
+ * Everything runs on one GPU (device 0, or $EDGECORE_DEVICE) and one HIP
+ * stream per process.  Like the reference, nothing here is re-entrant.
+ */
+#ifndef EDGECORE_H
+#define EDGECORE_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <string.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ECM_MAGIC "ECM1\n"
+
+/* architecture ids of the .ecm meta `arch` field (src/edgecore.h:22-24) */
+#define ARCH_GPT2 0
+#define ARCH_QWEN2 1
+
+/* rope scaling variants, meta `rope_type` (src/edgecore.h:27-28) */
+#define ROPE_DEFAULT 0
+#define ROPE_YARN 1
+
+/* ------------------------------------------------------------------ */
+/* host conversions (src/edgecore.h:34-109)                             */
+/* ------------------------------------------------------------------ */
+
+/* binary16 -> binary32, exact (replaces fp16_to_f32, src/edgecore.h:34) */
+static inline float fp16_to_f32(uint16_t h)
+{
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16, e = (h >> 10) & 0x1fu, m = h & 0x3ffu, bits;
+    if (e == 0) {
+        if (m == 0) {
+            bits = sign;
+        } else {
+            int sh = 0;
+            while ((m & 0x400u) == 0) { m <<= 1; sh++; }
+            bits = sign | ((uint32_t)(113 - sh) << 23) | ((m & 0x3ffu) << 13);
+        }
+    } else if (e == 31) {
+        bits = sign | 0x7f800000u | (m << 13) | (m ? 0x400000u : 0u);
+    } else {
+        bits = sign | ((e + 112u) << 23) | (m << 13);
+    }
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+/* binary32 -> binary16, round to nearest even, as the F16C path of the
+ * reference (replaces f32_to_fp16, src/edgecore.h:64) */
+static inline uint16_t f32_to_fp16(float f)
+{
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    uint32_t sign = (x >> 16) & 0x8000u, ax = x & 0x7fffffffu;
+    if (ax > 0x7f800000u) return (uint16_t)(sign | 0x7e00u | ((ax >> 13) & 0x3ffu));
+    if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);
+    if (ax >= 0x38800000u) {
+        uint32_t r = ax - 0x38000000u, h = r >> 13, rem = r & 0x1fffu;
+        if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h++;
+        return (uint16_t)(sign | h);
+    }
+    uint32_t e = ax >> 23;
+    if (e < 102) return (uint16_t)sign;
+    uint32_t mant = (ax & 0x7fffffu) | 0x800000u, shift = 126u - e;
+    uint32_t h = mant >> shift, rem = mant & ((1u << shift) - 1u), half = 1u << (shift - 1u);
+    if (rem > half || (rem == half && (h & 1u))) h++;
+    return (uint16_t)(sign | h);
+}
+
+/* bfloat16 -> fp32 (src/edgecore.h:103) */
+static inline float bf16_to_f32(uint16_t b)
+{
+    uint32_t bits = (uint32_t)b << 16;
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+/* ------------------------------------------------------------------ */
+/* kernel ABI (src/edgecore.h:115-136, semantics of src/kernels.c:129-168)*/
+/* ------------------------------------------------------------------ */
+
+/* C[M][N] = A[M][K] (fp32) . B[N][K]^T (fp16 weights, row-major [out][in]).
+ * C is overwritten.  Host pointers.  Replaces gemm_fp16_fp32,
+ * src/edgecore.h:119.  fp32 accumulation; the summation order differs from
+ * the reference's 8-lane AVX2 order (results agree to fp32 rounding). */
+void gemm_fp16_fp32(float *C, const float *A, const uint16_t *B, int M, int K, int N);
+
+/* Same with bfloat16 weights.  Replaces gemm_bf16_fp32, src/edgecore.h:126. */
+void gemm_bf16_fp32(float *C, const float *A, const uint16_t *B, int M, int K, int N);
+
+/* C[m][n] = bias[n] + ((float)sum_k A[m][k]*B[n][k] * a_scale[m]) * b_scale[n]
+ * with an exact int32 dot.  A int8 [M][K], B int8 [N][K]; b_scale and bias
+ * may be NULL (1 and 0), a_scale may not.  Bit-exact with the reference.
+ * Replaces gemm_int8, src/edgecore.h:134. */
+void gemm_int8(float *C, const int8_t *A, const float *a_scale, const int8_t *B,
+               const float *b_scale, const float *bias, int M, int K, int N);
+
+/* Device-pointer variants (additions).  Enqueue on ec_stream() and return 0,
+ * or a negative error code (message in ec_last_error()) without launching
+ * anything when a shape or pointer is invalid. */
+int ec_gemm_fp16_fp32_dev(float *C, const float *A, const uint16_t *B, int M, int K, int N);
+int ec_gemm_bf16_fp32_dev(float *C, const float *A, const uint16_t *B, int M, int K, int N);
+int ec_gemm_int8_dev(float *C, const int8_t *A, const float *a_scale, const int8_t *B,
+                     const float *b_scale, const float *bias, int M, int K, int N);
+/* Activation quantizer of the reference linear() (src/gpt2.c:446-461):
+ * per row s = max|a|/127 (1 for an all-zero row), q = clamp(rint(a/s)). */
+int ec_quantize_rows_dev(const float *in, int M, int K, int8_t *q, float *s);
+
+/* ------------------------------------------------------------------ */
+/* tokenizer (src/edgecore.h:142-164)                                   */
+/* ------------------------------------------------------------------ */
+
+/* Byte-level only: the library reads the .ecm vocab blob and maps each input
+ * byte to its single-byte token (the raw byte value when the vocab has none),
+ * which is what the reference BPE produces for byte vocabularies without
+ * merges.  A vocabulary with merges is rejected by tokenizer_encode (-1). */
+typedef struct {
+    char **id_to_token;
+    int32_t *byte_to_id;
+    int32_t *cp_to_byte;
+    uint32_t *merge_l, *merge_r, *merge_m;
+    int n_merges;
+    int vocab_size;
+    int variant;
+    int eos_id;
+    char **sp_tok;
+    uint32_t *sp_len;
+    int32_t *sp_id;
+    int n_sp;
+} Tokenizer;
+
+int tokenizer_load(Tokenizer *t, const void *vocab_blob, size_t vocab_bytes,
+                   const void *merges_blob, size_t merges_bytes, int vocab_size, int variant);
+void tokenizer_free(Tokenizer *t);
+int tokenizer_encode(const Tokenizer *t, const char *text, int *out, int max_out);
+char *tokenizer_decode(const Tokenizer *t, const int *ids, int n);
+
+/* ------------------------------------------------------------------ */
+/* model (src/edgecore.h:170-273)                                       */
+/* ------------------------------------------------------------------ */
+
+/* Per-layer weights (src/edgecore.h:192-211): device pointers. */
+struct LayerW {
+    const float *ln1_g, *ln1_b;
+    const void *attn_w;
+    const float *attn_s, *attn_b;
+    const void *proj_w;
+    const float *proj_s, *proj_b;
+    const float *ln2_g, *ln2_b;
+    const void *fc_w;
+    const float *fc_s, *fc_b;
+    const void *fc2_w;
+    const float *fc2_s, *fc2_b;
+
+    const void *q_w, *k_w, *v_w, *o_w;
+    const float *q_s, *k_s, *v_s, *o_s;
+    const float *q_b, *k_b, *v_b, *o_b;
+    const void *gate_w, *up_w, *down_w;
+    const float *gate_s, *up_s, *down_s;
+    const float *gate_b, *up_b, *down_b;
+};
+
+/* Field names and meaning follow src/edgecore.h:170-234.  All pointers below
+ * `eos_token_id` point into device memory.  Qwen2 q/k/v weights (and scales)
+ * are stored back to back, so q_w, k_w and v_w are each still a row-major
+ * [out][in] matrix. */
+typedef struct {
+    char model_name[64];
+    int n_layer, n_head, n_embd, n_ctx, vocab;
+    int n_kv_head;
+    int n_kv_embd;
+    int intermediate;
+    int head_dim;
+    int arch;
+    size_t n_params;
+    double eps;
+
+    double rope_theta;
+    int rope_type;
+    double yarn_factor, yarn_orig_max, yarn_attention_factor;
+    int sliding_window;
+    int tie_word_embeddings;
+    int eos_token_id;
+
+    const uint16_t *wte;
+    const uint16_t *wpe;
+
+    struct LayerW *lw; /* host array (n_layer) of device pointers */
+
+    const float *lnf_g, *lnf_b;
+    const uint16_t *lm_head;
+
+    int precision; /* 0 = int8, 1 = fp16, 2 = bf16 (from the .ecm weight dtype) */
+
+    uint16_t *k_cache, *v_cache; /* device, [n_layer][batch_cap][eff_ctx][n_kv_embd] fp16 */
+    int batch_cap;
+    int max_ctx;
+
+    float *ws_x, *ws_tmp, *ws_qkv, *ws_attn, *ws_scores; /* device workspaces */
+    int8_t *ws_q;
+    float *ws_qs;
+    size_t ws_q_cols;
+
+    Tokenizer tok;
+
+    void *file_data; /* host mapping of the .ecm file while loading, else NULL */
+    size_t file_size;
+    int file_mapped;
+
+    void *dev; /* addition: the library's device state for this model */
+} GPT2;
+
+typedef struct {
+    char name[128];
+    int dtype; /* 0 fp32, 1 fp16, 2 int8, 3 text, 4 bf16 */
+    size_t nelems;
+    size_t bytes;
+    size_t offset;
+    size_t dims[4];
+    int ndims;
+} EcmTensor;
+
+/* Load an .ecm file, upload weights to HBM once and allocate the device KV
+ * cache and workspaces for M up to max(eff_ctx, batch_cap).  0 ok, -1 fail
+ * (message on stderr).  Replaces gpt2_load, src/edgecore.h:246. */
+int gpt2_load(GPT2 *g, const char *path, int batch_cap, int max_ctx);
+
+/* Replaces gpt2_free, src/edgecore.h:247. */
+void gpt2_free(GPT2 *g);
+
+/* Forward for M tokens (host tokens/positions/seqs, host logits [M][vocab]);
+ * seqs NULL means token m goes to KV slot m.  Replaces gpt2_forward,
+ * src/edgecore.h:259 (dispatches to the Qwen2 forward for arch qwen2).
+ * Unlike the reference it checks its inputs: a token outside [0, vocab), a
+ * position outside [0, eff_ctx) or M above the workspace prints a message
+ * and exits with status 1, as the reference does on workspace overflow
+ * (src/gpt2.c:442-445). */
+void gpt2_forward(GPT2 *g, const int *tokens, const int *positions, const int *seqs,
+                  int M, float *logits);
+
+/* Replaces qwen2_forward, src/edgecore.h:263. */
+void qwen2_forward(GPT2 *g, const int *tokens, const int *positions, const int *seqs,
+                   int M, float *logits);
+
+/* src/edgecore.h:267-269 */
+static inline int gpt2_eff_ctx(const GPT2 *g)
+{
+    return (g->max_ctx > 0 && g->max_ctx < g->n_ctx) ? g->max_ctx : g->n_ctx;
+}
+
+/* Parse the .ecm text header and tensor table.  Returns the tensor count, or
+ * -1.  Like the reference it fails once the table reaches `max` entries.
+ * Replaces ecm_parse, src/edgecore.h:272. */
+int ecm_parse(const void *data, size_t size, EcmTensor *out, int max, GPT2 *meta_out);
+
+/* src/edgecore.h:279-280 (defined in the library rather than the driver) */
+float peak_rss_gb(void);
+double now_sec(void);
+
+/* ------------------------------------------------------------------ */
+/* additions                                                            */
+/* ------------------------------------------------------------------ */
+
+/* Zero the device KV cache (replaces the driver's memset of k_cache/v_cache,
+ * src/runtime_main.c:312-316).  0 ok, <0 error. */
+int gpt2_kv_reset(GPT2 *g);
+
+/* Checked forward.  Computes the LM head only for rows [lm_from, M) (lm_from
+ * = M skips it; every other result is the same as gpt2_forward).  If logits
+ * is non-NULL it receives those rows ([M - lm_from][vocab], host).  If argmax
+ * is non-NULL it receives, per row, the greedy token of src/runtime_main.c:
+ * 215-218 (first maximum wins), computed on the GPU.  Returns 0 or a negative
+ * error code (ec_last_error() has the message); nothing is launched when the
+ * inputs are invalid. */
+int gpt2_forward_ex(GPT2 *g, const int *tokens, const int *positions, const int *seqs,
+                    int M, int lm_from, float *logits, int *argmax);
+
+/* sizeof(GPT2) as compiled into the library (lets foreign-function hosts
+ * check their mirror of the struct). */
+size_t ec_gpt2_sizeof(void);
+
+/* Error message of the last failing call on this thread ("" if none). */
+const char *ec_last_error(void);
+
+/* Opens the GPU on first use; 0 ok.  Every other entry point calls it. */
+int ec_init(void);
+
+/* One-line JSON description of the GPU: name, gcnArchName, CUs, HBM bytes. */
+int ec_device_info(char *buf, int len);
+
+/* The library's HIP stream (hipStream_t) and a blocking wait on it. */
+void *ec_stream(void);
+int ec_sync(void);
+
+/* Device memory helpers for hosts without a HIP runtime of their own. */
+void *ec_dev_alloc(size_t bytes);
+int ec_dev_free(void *p);
+int ec_memcpy_h2d(void *dst, const void *src, size_t bytes);
+int ec_memcpy_d2h(void *dst, const void *src, size_t bytes);
+int ec_memset_dev(void *dst, int value, size_t bytes);
+
+/* Per-kernel timing.  While enabled, every launch of a kernel whose family
+ * name contains `filter` ("" = all) is bracketed by HIP events recorded on
+ * the stream the kernel runs on.  ec_prof_stop synchronises and writes a JSON
+ * array of {"kernel", "launches", "total_us", "avg_us", "bytes_per_launch",
+ * "gbps"} (bytes are the algorithmic bytes of each launch) into buf and
+ * returns its length, or a negative error code. */
+int ec_prof_start(const char *filter);
+int ec_prof_stop(char *buf, int len);
+
+/* int8 weight packing of edgecore/ecm.py:50-59 (float64 max|w|/127, zero row
+ * -> scale 1, round half to even, clip), used by the synthetic generator. */
+void ec_quantize_int8_symmetric(const float *w, int rows, int cols, int8_t *q, float *scales);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EDGECORE_H */

@@ -1,0 +1,121 @@
+"""GPU parity of the kernel ABI (src/kernels.c:129-168, src/gpt2.c:446-461)
+against the CPU oracle, through the C ABI of libedgecore_hip.so.
+
+int8: bit-exact (exact int32 dot, same epilogue rounding sequence).
+fp16/bf16: fp32 accumulation in a different order than the reference's
+8-lane AVX2 order; bounded by |gpu - ref| <= 2 * K * 2^-24 * sum_k |a_k b_k|
+(+1e-30), and checked against a float64 brute force with the same bound.
+"""
+import numpy as np
+import pytest
+
+import edgecore_amd as ec
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+I8_SHAPES = [
+    (1, 896, 1152), (1, 896, 896), (1, 4864, 896), (1, 896, 4864),  # Qwen2-0.5B decode
+    (1, 1536, 256), (1, 8960, 1536),                                  # Qwen2.5-1.5B
+    (3, 896, 896), (8, 4864, 896), (16, 1536, 1536), (37, 896, 1152),  # batched / prefill
+    (1, 64, 192), (2, 256, 64),                                       # tiny GPT-2
+    (5, 40, 7), (2, 1, 3), (3, 17, 33),                               # odd K: generic path
+]
+
+
+def _rand_i8(rng, shape):
+    return rng.integers(-128, 128, size=shape, dtype=np.int16).astype(np.int8)
+
+
+@pytest.mark.parametrize("M,K,N", I8_SHAPES)
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_gemm_int8_bit_exact(M, K, N, with_bias):
+    rng = np.random.default_rng(M * 7 + K * 13 + N)
+    A = _rand_i8(rng, (M, K))
+    B = _rand_i8(rng, (N, K))
+    a_s = rng.uniform(1e-4, 1e-1, M).astype(np.float32)
+    b_s = rng.uniform(1e-4, 1e-2, N).astype(np.float32)
+    bias = rng.normal(0, 0.02, N).astype(np.float32) if with_bias else None
+    got = ec.gemm_int8(A, a_s, B, b_s, bias)
+    want = oracle.gemm_int8(A, a_s, B, b_s, bias)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_gemm_int8_null_scale_and_adversarial():
+    K = 4864
+    A = np.full((2, K), -128, np.int8)
+    A[1] = 127
+    B = np.full((3, K), -128, np.int8)
+    B[1] = 127
+    B[2, ::2] = 127
+    a_s = np.array([1.0, 0.5], np.float32)
+    got = ec.gemm_int8(A, a_s, B, None, None)
+    want = oracle.gemm_int8(A, a_s, B, None, None)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    # the exact dots: (-128)(-128)K, (-128)(127)K, 127*127*K ...
+    assert got[0, 0] == np.float32(float(128 * 128 * K))
+    assert got[1, 1] == np.float32(float(127 * 127 * K) * 0.5)
+
+
+def _f16_bits(x):
+    return np.asarray(x, np.float16).view(np.uint16)
+
+
+def _bf16_bits(x):
+    u = np.asarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+W16_SHAPES = [(1, 896, 151936), (1, 768, 2304), (1, 3072, 768), (4, 896, 4864), (9, 64, 50257),
+              (2, 37, 5), (1, 8, 3)]
+
+
+@pytest.mark.parametrize("M,K,N", W16_SHAPES)
+@pytest.mark.parametrize("bf16", [False, True])
+def test_gemm_w16_within_bound(M, K, N, bf16):
+    rng = np.random.default_rng(M + K + N + bf16)
+    A = rng.normal(0, 1, (M, K)).astype(np.float32)
+    Wf = rng.normal(0, 0.02, (N, K)).astype(np.float32)
+    B = _bf16_bits(Wf) if bf16 else _f16_bits(Wf)
+    got = (ec.gemm_bf16_fp32 if bf16 else ec.gemm_fp16_fp32)(A, B)
+    want = oracle.gemm_w16(A, B, bf16=bf16)
+    Bf = (B.astype(np.uint32) << 16).view(np.float32) if bf16 else B.view(np.float16).astype(np.float32)
+    exact = A.astype(np.float64) @ Bf.astype(np.float64).T
+    bound = 2.0 * K * 2.0 ** -24 * (np.abs(A).astype(np.float64) @ np.abs(Bf).astype(np.float64).T) + 1e-30
+    assert np.all(np.abs(got - exact) <= bound)
+    assert np.all(np.abs(want - exact) <= bound)
+
+
+def test_quantize_rows_bit_exact_with_ties():
+    rng = np.random.default_rng(5)
+    x = rng.normal(0, 1, (6, 896)).astype(np.float32)
+    # row 1: exact .5 ties after division by s = 127/127 = 1 -> maxabs 127
+    x[1, :] = np.linspace(-127, 127, 896).astype(np.float32)
+    x[1, :8] = [0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 127.0, -126.5]
+    x[2, :] = 0.0  # all-zero row: scale 1, codes 0
+    x[3, 5] = np.inf
+    x[4, 7] = np.nan
+    src = ec.DeviceBuffer.from_array(x)
+    q = ec.DeviceBuffer(x.size)
+    s = ec.DeviceBuffer(4 * x.shape[0])
+    try:
+        rc = ec.lib().ec_quantize_rows_dev(src.ptr, x.shape[0], x.shape[1], q.ptr, s.ptr)
+        assert rc == 0, ec.last_error()
+        gq = q.to_array(np.int8, x.shape)
+        gs = s.to_array(np.float32, x.shape[0])
+    finally:
+        for b in (src, q, s):
+            b.close()
+    oq, os_ = oracle.quantize_rows(x)
+    assert np.array_equal(gq, oq)
+    assert np.array_equal(gs.view(np.uint32), os_.view(np.uint32))
+    assert list(gq[1, :6]) == [0, 2, 2, 0, -2, -2]
+    assert gs[2] == 1.0 and not gq[2].any()
+
+
+def test_dev_entry_points_reject_bad_shapes():
+    L = ec.lib()
+    assert L.ec_gemm_int8_dev(None, None, None, None, None, None, -1, 4, 4) < 0
+    assert "negative" in ec.last_error()
+    assert L.ec_gemm_fp16_fp32_dev(None, None, None, 2, 16, 4) < 0
+    assert L.ec_gemm_int8_dev(None, None, None, None, None, None, 0, 4, 4) == 0

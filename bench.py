@@ -1,0 +1,222 @@
+#!/usr/bin/env python3
+"""Decode benchmark of the EdgeCore MI355X path on the Qwen2-0.5B int8 shape.
+
+Workload (bs=1): Qwen2-0.5B architecture (24 layers, d_model 896, 14/2 heads,
+head_dim 64, SwiGLU 4864, vocab 151936 tied), int8 per-output-channel weights
+N(0, 0.02) from seed 0 (synthetic, bin/ecm_synth), a 256-token prompt of ids
+uniform in [0, 151936) from seed 1, greedy decoding.  One step is one decode
+token: the forward at M=1 plus the GPU argmax and the copy of the id back to
+the host.  The prompt is prefilled first (reported as prefill tok/s, untimed),
+then W warmup steps, then K timed steps bracketed by stream synchronisation.
+
+Per-kernel durations come from HIP events recorded on the library's stream
+around every kernel launch of the timed region (ec_prof_*), and the roofline
+object is computed for the kernel family with the largest total time.  The
+CPU baseline is the reference runtime built from its own sources
+(oracle/_ref/edgecore-runtime) on the same model file and prompt, timed on
+the host cores.
+
+Prints one JSON line.
+"""
+import argparse
+import json
+import os
+import subprocess
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO))
+
+METRIC = "decode tok/s + int8 GEMV HBM GB/s (% of peak), Qwen2-0.5B-shape int8 bs=1"
+HBM_PEAK_GBPS = 8000.0
+PROMPT = 256
+
+
+def ensure_inputs(cache: Path):
+    import edgecore_amd as ec
+
+    cache.mkdir(parents=True, exist_ok=True)
+    model = cache / "qwen2-0.5b-int8.ecm"
+    prompt = cache / "prompt256.txt"
+    if not model.exists():
+        tmp = cache / "qwen2-0.5b-int8.ecm.tmp"
+        ec.synth(tmp, preset="qwen2-0.5b")
+        tmp.rename(model)
+    if not prompt.exists():
+        ec.synth(None, prompt_out=prompt, prompt_len=PROMPT, prompt_seed=1, vocab=151936)
+    return model, prompt
+
+
+def physical_cores() -> int:
+    try:
+        out = subprocess.run(["lscpu", "-p=CORE,SOCKET"], capture_output=True, text=True).stdout
+        cores = {tuple(l.split(",")) for l in out.splitlines() if l and not l.startswith("#")}
+        socket0 = [c for c in cores if c[1] == "0"]
+        return max(1, len(socket0) or len(cores))
+    except Exception:
+        return os.cpu_count() or 1
+
+
+def cpu_baseline(model: Path, prompt: Path, n_tokens: int):
+    """The reference CPU runtime (built from its sources) on a bounded sample:
+    the same 256-token prefill, then n_tokens greedy decode steps."""
+    sys.path.insert(0, str(REPO))
+    import oracle
+
+    threads = min(16, physical_cores(), len(os.sched_getaffinity(0)))
+    if oracle.REF_RUNTIME.exists():
+        cmd = [str(oracle.REF_RUNTIME), "--model", str(model), "--mode", "bench", "--tokens-file",
+               str(prompt), "--n-tokens", str(n_tokens), "--warmup", "0", "--iters", "1",
+               "--threads", str(threads), "--affinity", "physical", "--max-ctx",
+               str(PROMPT + n_tokens + 8), "--no-print"]
+        p = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
+        if p.returncode == 0:
+            d = json.loads(p.stdout)
+            return {"value": d["tokens_per_sec"], "unit": "tok/s", "cores": threads, "kind": "reference",
+                    "sample": f"reference runtime_main.c/gpt2.c/kernels.c built with gcc -O3 "
+                              f"-mavx2 -mfma -mf16c; same model and 256-token prompt; "
+                              f"{n_tokens} greedy decode steps after the prefill; "
+                              f"--threads {threads} --affinity physical",
+                    "ttft_ms": d.get("ttft_avg_ms"), "avg_token_ms": d.get("avg_token_ms")}
+    # the C restatement (oracle port) when the reference build is absent
+    import numpy as np
+
+    om = oracle.OracleModel(model, 1, PROMPT + n_tokens + 8)
+    ids = [int(x) for x in Path(prompt).read_text().split()]
+    om.kv_reset()
+    om.forward(ids, list(range(PROMPT)), [0] * PROMPT)
+    cur, pos, t = ids[-1], PROMPT, 0.0
+    for _ in range(n_tokens):
+        t0 = time.perf_counter()
+        lg = om.forward([cur], [pos], None)
+        t += time.perf_counter() - t0
+        cur, pos = int(np.argmax(lg[0])), pos + 1
+    om.close()
+    return {"value": n_tokens / t, "unit": "tok/s", "cores": int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+            or (os.cpu_count() or 1), "kind": "port",
+            "sample": f"oracle/ec_oracle.c; same model and prompt; {n_tokens} greedy decode steps"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=248)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--cache", default=os.environ.get("EDGECORE_BENCH_DIR", "/tmp/edgecore_bench"))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-tokens", type=int, default=16)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              f"(independent sequences would shard as pure data parallelism, see DESIGN.md)",
+              file=sys.stderr)
+        return 2
+
+    import numpy as np
+
+    import edgecore_amd as ec
+
+    model, prompt_file = ensure_inputs(Path(args.cache))
+    prompt = ec.read_ids(prompt_file)
+    K, W = args.steps, args.warmup
+    max_ctx = PROMPT + W + K + 8
+    m = ec.Model(model, 1, max_ctx)
+    L = ec.lib()
+
+    def prefill():
+        m.kv_reset()
+        t0 = time.perf_counter()
+        _, am = m.forward(prompt, np.arange(PROMPT), np.zeros(PROMPT, np.int32), lm_from=PROMPT - 1,
+                          want_logits=False, want_argmax=True)
+        return time.perf_counter() - t0
+
+    prefill()  # first call warms code paths
+    ttft = prefill()
+    cur, pos = int(prompt[-1]), PROMPT
+    for _ in range(W):
+        _, am = m.forward([cur], [pos], None, want_logits=False, want_argmax=True)
+        cur, pos = int(am[0]), pos + 1
+    L.ec_sync()
+
+    # timed region: K decode steps, per-kernel HIP events on the library stream
+    L.ec_prof_start(b"")
+    L.ec_sync()
+    t0 = time.perf_counter()
+    ids = []
+    for _ in range(K):
+        _, am = m.forward([cur], [pos], None, want_logits=False, want_argmax=True)
+        cur, pos = int(am[0]), pos + 1
+        ids.append(cur)
+    L.ec_sync()
+    elapsed = time.perf_counter() - t0
+    buf = __import__("ctypes").create_string_buffer(1 << 16)
+    n = L.ec_prof_stop(buf, len(buf))
+    kernels = json.loads(buf.value.decode()) if n > 0 else []
+
+    # the same steps again without events, to state the instrumentation cost
+    m.kv_reset()
+    m.forward(prompt, np.arange(PROMPT), np.zeros(PROMPT, np.int32), lm_from=PROMPT, want_logits=False)
+    cur2, pos2 = int(prompt[-1]), PROMPT
+    for _ in range(W):
+        _, am = m.forward([cur2], [pos2], None, want_logits=False, want_argmax=True)
+        cur2, pos2 = int(am[0]), pos2 + 1
+    L.ec_sync()
+    t1 = time.perf_counter()
+    for _ in range(K):
+        _, am = m.forward([cur2], [pos2], None, want_logits=False, want_argmax=True)
+        cur2, pos2 = int(am[0]), pos2 + 1
+    L.ec_sync()
+    elapsed_clean = time.perf_counter() - t1
+    m.close()
+
+    tot = sum(k["total_us"] for k in kernels) or 1.0
+    for k in kernels:
+        k["share"] = round(k["total_us"] / tot, 4)
+    dom = max(kernels, key=lambda k: k["total_us"]) if kernels else None
+    int8 = [k for k in kernels if k["kernel"].startswith("gemv_i8")]
+    dom_i8 = max(int8, key=lambda k: k["total_us"]) if int8 else None
+
+    def roof(k):
+        if not k:
+            return None
+        ach = k["bytes_per_launch"] / (k["avg_us"] * 1e3)
+        return {"kernel": k["kernel"], "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBPS,
+                "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBPS, 4), "traffic": None,
+                "bytes_per_launch": k["bytes_per_launch"], "avg_us": k["avg_us"]}
+
+    # algorithmic bytes of one decode step (weights once + fp16 KV read), mean position
+    E, F, kv, V, Lyr = 896, 4864, 128, 151936, 24
+    lin = E * E * 2 + 2 * kv * E + 3 * F * E
+    mean_pos = PROMPT + W + (K - 1) / 2.0
+    step_bytes = Lyr * (lin + 4 * (lin // E) + (mean_pos + 1) * kv * 4) + V * E * 2
+    value = K / elapsed
+    out = {
+        "metric": METRIC, "value": round(value, 2), "unit": "tok/s", "n_gpus": 1, "steps": K,
+        "warmup": W, "ms_per_step": round(elapsed / K * 1e3, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+        "config": {"workload": "Qwen2-0.5B-shape int8 bs1 greedy decode after a 256-token prompt",
+                   "layers": Lyr, "d_model": E, "heads": 14, "kv_heads": 2, "ffn": F, "vocab": V,
+                   "prompt_tokens": PROMPT, "decode_positions": [PROMPT + W, PROMPT + W + K - 1],
+                   "batch": 1},
+        "roofline": roof(dom),
+        "roofline_int8_gemv": roof(dom_i8),
+        "decode_bytes_per_step": int(step_bytes),
+        "decode_effective_gbps": round(step_bytes * value / 1e9, 1),
+        "ms_per_step_without_events": round(elapsed_clean / K * 1e3, 4),
+        "prefill_tok_s": round(PROMPT / ttft, 1), "ttft_ms": round(ttft * 1e3, 3),
+        "kernels": kernels,
+        "device": ec.device_info(),
+    }
+    if not args.no_cpu_baseline:
+        try:
+            out["cpu_baseline"] = cpu_baseline(model, prompt_file, args.cpu_tokens)
+        except Exception as e:  # the GPU figure stands on its own
+            out["cpu_baseline"] = {"error": str(e)}
+    print(json.dumps(out))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -105,6 +105,7 @@ _SIG = {
     "ec_prof_stop": (_I, [C.c_char_p, _I]),
     "ec_quantize_int8_symmetric": (None, [_P, _I, _I, _P, _P]),
     "ec_gpt2_sizeof": (C.c_size_t, []),
+    "ec_device_math": (_I, [_I, _P, _P, C.c_size_t]),
     "tokenizer_encode": (_I, [_P, C.c_char_p, _P, _I]),
     "now_sec": (C.c_double, []),
     "peak_rss_gb": (C.c_float, []),

@@ -10,6 +10,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "ec_expf.h"
+
 namespace ec {
 
 constexpr int kWave = 64;
@@ -35,16 +37,9 @@ __device__ __forceinline__ float w2f(uint16_t w) {
   if constexpr (BF16) return b2f(w); else return h2f(w);
 }
 
-// exp of a float computed in double and rounded once: the correctly rounded
-// expf except within ~2^-29 of a rounding midpoint.  glibc's expf (what the
-// reference calls) agrees with it on all but ~8e-5 of inputs.
-__device__ __forceinline__ float expf_d(float x) {
-  return (float)exp((double)x);
-}
-
-// src/gpt2.c:587-590
+// src/gpt2.c:587-590, with the reference's expf (ec_expf.h)
 __device__ __forceinline__ float silu(float x) {
-  float e = expf_d(-x);
+  float e = ec_expf_ref(-x);
   float den = 1.0f + e;
   return x / den;
 }
@@ -93,13 +88,13 @@ __device__ __forceinline__ float block_max256(float v, float *red) {
 }
 
 // int8 quantization of one activation with the row scale s
-// (src/gpt2.c:456-459: lrintf(a / s) clamped to [-128, 127]; lrintf of NaN is
-// LONG_MIN on x86-64, which clamps to -128)
+// (src/gpt2.c:456-459: lrintf(a / s) clamped to [-128, 127]).  On x86-64,
+// lrintf of NaN or of a magnitude >= 2^63 returns LONG_MIN, which clamps to
+// -128; every other value rounds half to even and clamps.
 __device__ __forceinline__ int8_t quant1(float a, float s) {
-  float r = __builtin_rintf(a / s);
-  if (r != r) return (int8_t)-128;
-  r = fminf(fmaxf(r, -128.0f), 127.0f);
-  return (int8_t)(int)r;
+  const float r = __builtin_rintf(a / s);
+  if (!(fabsf(r) < 9.2233720368547758e18f)) return (int8_t)-128;
+  return (int8_t)(int)fminf(fmaxf(r, -128.0f), 127.0f);
 }
 
 // row scale of src/gpt2.c:453

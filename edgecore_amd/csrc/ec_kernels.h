@@ -1,57 +1,71 @@
-// Host-side launch interface of the gfx950 kernels (kernels.hip).  Every
-// launcher checks nothing: callers (runtime.hip) validate shapes first.
+// Host-side launch interface of the gfx950 kernels.  Launchers check
+// nothing: callers (runtime.hip) validate shapes and pointers first.
 #pragma once
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace ec {
 
 // GEMV/GEMM epilogues.  `out` has row stride ldo.
 enum Epi {
-  EPI_STORE = 0,       // out = v
-  EPI_RESID = 1,       // out = out + v            (residual add, src/gpt2.c:782-784)
-  EPI_GELU = 2,        // out = gelu_new(v)        (src/gpt2.c:568)
+  EPI_STORE = 0,       // out = v                   (+ optional argmax candidates)
+  EPI_RESID = 1,       // out = out + v             (residual add, src/gpt2.c:782-784)
+  EPI_GELU = 2,        // out = gelu_new(v)         (src/gpt2.c:568)
   EPI_SWIGLU = 3,      // out = silu(v_gate) * v_up (src/gpt2.c:790-791)
-  EPI_BIAS = 4,        // out = v + bias            (fp16/bf16 linear bias pass, src/gpt2.c:425-429)
+  EPI_BIAS = 4,        // out = v + bias            (16-bit linear bias pass, src/gpt2.c:425-429)
   EPI_BIAS_RESID = 5,  // out = out + (v + bias)
   EPI_BIAS_GELU = 6,   // out = gelu_new(v + bias)
 };
 
-struct GemvI8Args {
-  const int8_t *A;  // [M][lda] int8 activations
+// Activation prologues of the GEMV kernels (see gemv_impl.h).
+enum Pro {
+  PRO_I8 = 0,     // int8 rows + per-row scales
+  PRO_F32 = 1,    // fp32 rows (16-bit weights)
+  PRO_QUANT = 2,  // fp32 rows, quantized per row to int8
+  PRO_RMS = 3,    // RMSNorm of fp32 rows (then quantized for int8 weights)
+  PRO_LN = 4,     // LayerNorm of fp32 rows (then quantized for int8 weights)
+};
+
+struct GemvArgs {
+  const void *A;  // [M][lda] int8 (PRO_I8) or fp32
   int lda;
-  const float *as;  // [M] activation scales
-  const int8_t *W;  // [N][K]
-  const float *ws;  // [N] or null (1.0)
-  const float *bias;  // [N] or null (0.0)
-  const int8_t *W2;  // up weights for EPI_SWIGLU
-  const float *ws2;
+  const float *as;  // PRO_I8 scales [M]
+  const float *gamma, *beta;  // norm weights (PRO_RMS / PRO_LN)
+  double eps;
+  const void *W;   // [N][K] int8 / fp16 / bf16
+  const void *W2;  // up weights (EPI_SWIGLU)
+  const float *ws, *ws2;  // int8 per-row weight scales or null (1.0)
+  const float *bias;      // [N] or null
   float *out;
   int ldo;
   int M, K, N;
+  unsigned long long *cand;  // EPI_STORE: [M][gridDim.x] argmax candidate keys, or null
 };
 
-struct GemvW16Args {
-  const float *A;  // [M][lda] fp32 activations
-  int lda;
-  const uint16_t *W;  // [N][K] fp16 or bf16
-  const float *bias;  // [N] or null
-  const uint16_t *W2;  // up weights for EPI_SWIGLU
-  float *out;
-  int ldo;
-  int M, K, N;
-};
+// Weight types
+enum { WT_I8 = 0, WT_F16 = 1, WT_BF16 = 2 };
 
-// The vector kernels need K % 16 == 0 (int8) / K % 8 == 0 (16-bit) and
-// 16-byte aligned rows; gemv_i8 / gemv_w16 fall back to the one-thread-per-
-// output gemm_*_generic kernels (same epilogues) for anything else.
-bool gemv_i8_vector_ok(const GemvI8Args &a);
-bool gemv_w16_vector_ok(const GemvW16Args &a);
-hipError_t gemv_i8(const GemvI8Args &a, int epi, hipStream_t s);
-hipError_t gemv_w16(const GemvW16Args &a, int epi, bool bf16, hipStream_t s);
-hipError_t gemm_i8_generic(const GemvI8Args &a, int epi, hipStream_t s);
-hipError_t gemm_w16_generic(const GemvW16Args &a, int epi, bool bf16, hipStream_t s);
+// Fused vector kernels; return hipErrorInvalidValue for an (epi, pro) pair
+// that is not instantiated.  gemv_vector_ok tells whether a shape can use
+// them (16-byte rows, LDS budget); gemv_generic runs any shape with PRO_I8 /
+// PRO_F32 and every epilogue, one thread per output.
+bool gemv_vector_ok(const GemvArgs &a, int wt, int pro);
+hipError_t gemv(const GemvArgs &a, int wt, int epi, int pro, hipStream_t s);
+hipError_t gemv_i8_fused(const GemvArgs &a, int epi, int pro, hipStream_t s);
+hipError_t gemv_f16_fused(const GemvArgs &a, int epi, int pro, hipStream_t s);
+hipError_t gemv_bf16_fused(const GemvArgs &a, int epi, int pro, hipStream_t s);
+hipError_t gemv_generic(const GemvArgs &a, int wt, int epi, hipStream_t s);
+// grid-size cap of the grid-stride GEMV (set from the CU count at init)
+void gemv_set_max_blocks(int n);
+int gemv_max_blocks();
+// LDS budget per block (device limit), checked by gemv_vector_ok
+void gemv_set_max_lds(int bytes);
+size_t gemv_lds_bytes(int wt, int pro, int MT, int K);
+// number of x-blocks a gemv launch of this shape uses (sizes argmax candidates)
+int gemv_grid_x(const GemvArgs &a, int wt, int epi);
 
 // per-row activation quantizer: q[m][k], s[m]
 hipError_t quant_rows(const float *in, int ldi, int M, int K, int8_t *q, int ldq, float *s,
@@ -85,7 +99,8 @@ struct KvArgs {
 };
 hipError_t rope_kv_append(const KvArgs &a, hipStream_t st);
 
-// causal attention over the fp16 cache for every (head, token)
+// causal attention over the fp16 cache for every (head, token), in the
+// reference's arithmetic order (see kernels.hip)
 struct AttnArgs {
   const float *q;
   int ldq;
@@ -96,12 +111,20 @@ struct AttnArgs {
   int H, KVH, hd, kv, C, window;
   double inv_hd;
   int M;
-  int max_npos;  // upper bound of pos+1 over the batch (sizes LDS)
+  int max_npos;  // upper bound of pos+1 over the batch (sizes the LDS score array)
+  int vtile;     // V positions staged in LDS per tile (multiple of 8)
 };
 hipError_t attention(const AttnArgs &a, hipStream_t st);
-size_t attention_lds_bytes(int max_npos, int hd);
+size_t attention_lds_bytes(int max_npos, int hd, int vtile);
 
 // greedy argmax per row (src/runtime_main.c:215-218 semantics)
 hipError_t argmax_rows(const float *logits, int rows, int V, int *out, hipStream_t st);
+// final reduction of the LM head's per-block argmax candidates
+hipError_t argmax_finalize(const unsigned long long *cand, int ncand, const float *logits,
+                           int ldl, int rows, int *out, hipStream_t st);
+
+// elementwise device math (ec_device_math)
+enum { MATH_EXPF = 0, MATH_SILU = 1, MATH_GELU = 2, MATH_F32_TO_F16 = 3, MATH_F16_TO_F32 = 4, MATH_QUANT1 = 5 };
+hipError_t device_math(int op, const void *in, void *out, size_t n, hipStream_t st);
 
 }  // namespace ec

@@ -8,244 +8,50 @@
 // widened to fp32 and accumulated with FMA.  The LPR partial sums are combined
 // with a wave64 xor-shuffle tree and the epilogue (scales, bias, residual,
 // GELU or SwiGLU) is applied in registers before the single store.
-#include "ec_device.h"
-#include "ec_kernels.h"
+#include "gemv_impl.h"
 
 #include <float.h>
 
 namespace ec {
 
 // ---------------------------------------------------------------------------
-// int8 GEMV
+// generic GEMV (any K, any alignment, every epilogue): one thread per output
+// element, activations given as int8 rows + scales (PRO_I8) or fp32 rows
+// (PRO_F32).  Used for shapes the vector kernels cannot read with 16-byte loads.
 // ---------------------------------------------------------------------------
 
-template <int LPR, int MT, int EPI>
-__global__ __launch_bounds__(256) void gemv_i8_kernel(GemvI8Args a) {
-  constexpr int RPW = kWave / LPR;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int grp = lane / LPR, sub = lane % LPR;
-  int n, part = 0, rib;
-  if constexpr (EPI == EPI_SWIGLU) {
-    rib = (wave & 1) * RPW + grp;  // waves 0-1: gate rows, waves 2-3: up rows
-    part = wave >> 1;
-    n = blockIdx.x * (2 * RPW) + rib;
-  } else {
-    rib = wave * RPW + grp;
-    n = blockIdx.x * (4 * RPW) + rib;
-  }
-  const int m0 = blockIdx.y * MT;
-  const int mc = min(MT, a.M - m0);
-  const bool valid = n < a.N;
-  const int8_t *W = (EPI == EPI_SWIGLU && part) ? a.W2 : a.W;
-  const int nch = a.K >> 4;
-
-  int acc[MT];
-#pragma unroll
-  for (int m = 0; m < MT; m++) acc[m] = 0;
-  if (valid) {
-    const v4i *wrow = reinterpret_cast<const v4i *>(W + (size_t)n * a.K);
-#pragma unroll 4
-    for (int c = sub; c < nch; c += LPR) {
-      v4i w = __builtin_nontemporal_load(wrow + c);
-#pragma unroll
-      for (int m = 0; m < MT; m++) {
-        if (m < mc) {
-          v4i x = reinterpret_cast<const v4i *>(a.A + (size_t)(m0 + m) * a.lda)[c];
-          int t = acc[m];
-          t = __builtin_amdgcn_sdot4(x.x, w.x, t, false);
-          t = __builtin_amdgcn_sdot4(x.y, w.y, t, false);
-          t = __builtin_amdgcn_sdot4(x.z, w.z, t, false);
-          t = __builtin_amdgcn_sdot4(x.w, w.w, t, false);
-          acc[m] = t;
-        }
-      }
-    }
-  }
-#pragma unroll
-  for (int m = 0; m < MT; m++) {
-#pragma unroll
-    for (int o = LPR / 2; o > 0; o >>= 1) acc[m] += __shfl_xor(acc[m], o, kWave);
-  }
-
-  if constexpr (EPI == EPI_SWIGLU) {
-    __shared__ float up[MT][2 * RPW];
-    if (sub == 0 && valid && part == 1) {
-      const float bs = a.ws2 ? a.ws2[n] : 1.0f;
-#pragma unroll
-      for (int m = 0; m < MT; m++)
-        if (m < mc) up[m][rib] = i8_epilogue(acc[m], a.as[m0 + m], bs, 0.0f);
-    }
-    __syncthreads();
-    if (sub == 0 && valid && part == 0) {
-      const float bs = a.ws ? a.ws[n] : 1.0f;
-#pragma unroll
-      for (int m = 0; m < MT; m++) {
-        if (m < mc) {
-          float g = i8_epilogue(acc[m], a.as[m0 + m], bs, 0.0f);
-          float r = silu(g) * up[m][rib];
-          a.out[(size_t)(m0 + m) * a.ldo + n] = r;
-        }
-      }
-    }
-  } else {
-    if (sub == 0 && valid) {
-      const float bs = a.ws ? a.ws[n] : 1.0f;
-      const float bv = a.bias ? a.bias[n] : 0.0f;
-#pragma unroll
-      for (int m = 0; m < MT; m++) {
-        if (m < mc) {
-          float v = i8_epilogue(acc[m], a.as[m0 + m], bs, bv);
-          float *o = a.out + (size_t)(m0 + m) * a.ldo + n;
-          if constexpr (EPI == EPI_RESID) v = *o + v;
-          if constexpr (EPI == EPI_GELU) v = gelu_new(v);
-          *o = v;
-        }
-      }
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------
-// fp16 / bf16 GEMV with fp32 activations
-// ---------------------------------------------------------------------------
-
-template <int LPR, int MT, int EPI, bool BF16>
-__global__ __launch_bounds__(256) void gemv_w16_kernel(GemvW16Args a) {
-  constexpr int RPW = kWave / LPR;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int grp = lane / LPR, sub = lane % LPR;
-  int n, part = 0, rib;
-  if constexpr (EPI == EPI_SWIGLU) {
-    rib = (wave & 1) * RPW + grp;
-    part = wave >> 1;
-    n = blockIdx.x * (2 * RPW) + rib;
-  } else {
-    rib = wave * RPW + grp;
-    n = blockIdx.x * (4 * RPW) + rib;
-  }
-  const int m0 = blockIdx.y * MT;
-  const int mc = min(MT, a.M - m0);
-  const bool valid = n < a.N;
-  const uint16_t *W = (EPI == EPI_SWIGLU && part) ? a.W2 : a.W;
-  const int nch = a.K >> 3;
-
-  float acc[MT];
-#pragma unroll
-  for (int m = 0; m < MT; m++) acc[m] = 0.0f;
-  if (valid) {
-    const v4u *wrow = reinterpret_cast<const v4u *>(W + (size_t)n * a.K);
-#pragma unroll 4
-    for (int c = sub; c < nch; c += LPR) {
-      v4u w = __builtin_nontemporal_load(wrow + c);
-      float wf[8];
-      wf[0] = w2f<BF16>((uint16_t)(w.x & 0xffffu));
-      wf[1] = w2f<BF16>((uint16_t)(w.x >> 16));
-      wf[2] = w2f<BF16>((uint16_t)(w.y & 0xffffu));
-      wf[3] = w2f<BF16>((uint16_t)(w.y >> 16));
-      wf[4] = w2f<BF16>((uint16_t)(w.z & 0xffffu));
-      wf[5] = w2f<BF16>((uint16_t)(w.z >> 16));
-      wf[6] = w2f<BF16>((uint16_t)(w.w & 0xffffu));
-      wf[7] = w2f<BF16>((uint16_t)(w.w >> 16));
-#pragma unroll
-      for (int m = 0; m < MT; m++) {
-        if (m < mc) {
-          const float4 *ap = reinterpret_cast<const float4 *>(a.A + (size_t)(m0 + m) * a.lda) + 2 * c;
-          float4 x0 = ap[0], x1 = ap[1];
-          float t = acc[m];
-          t = __builtin_fmaf(x0.x, wf[0], t);
-          t = __builtin_fmaf(x0.y, wf[1], t);
-          t = __builtin_fmaf(x0.z, wf[2], t);
-          t = __builtin_fmaf(x0.w, wf[3], t);
-          t = __builtin_fmaf(x1.x, wf[4], t);
-          t = __builtin_fmaf(x1.y, wf[5], t);
-          t = __builtin_fmaf(x1.z, wf[6], t);
-          t = __builtin_fmaf(x1.w, wf[7], t);
-          acc[m] = t;
-        }
-      }
-    }
-  }
-#pragma unroll
-  for (int m = 0; m < MT; m++) {
-#pragma unroll
-    for (int o = LPR / 2; o > 0; o >>= 1) acc[m] += __shfl_xor(acc[m], o, kWave);
-  }
-
-  if constexpr (EPI == EPI_SWIGLU) {
-    __shared__ float up[MT][2 * RPW];
-    if (sub == 0 && valid && part == 1) {
-#pragma unroll
-      for (int m = 0; m < MT; m++)
-        if (m < mc) up[m][rib] = acc[m];
-    }
-    __syncthreads();
-    if (sub == 0 && valid && part == 0) {
-#pragma unroll
-      for (int m = 0; m < MT; m++)
-        if (m < mc) a.out[(size_t)(m0 + m) * a.ldo + n] = silu(acc[m]) * up[m][rib];
-    }
-  } else {
-    if (sub == 0 && valid) {
-      const float bv = a.bias ? a.bias[n] : 0.0f;
-#pragma unroll
-      for (int m = 0; m < MT; m++) {
-        if (m < mc) {
-          float v = acc[m];
-          float *o = a.out + (size_t)(m0 + m) * a.ldo + n;
-          if constexpr (EPI == EPI_BIAS || EPI == EPI_BIAS_RESID || EPI == EPI_BIAS_GELU) v = v + bv;
-          if constexpr (EPI == EPI_RESID || EPI == EPI_BIAS_RESID) v = *o + v;
-          if constexpr (EPI == EPI_GELU || EPI == EPI_BIAS_GELU) v = gelu_new(v);
-          *o = v;
-        }
-      }
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------
-// generic GEMMs (any K, any alignment, every epilogue): one thread per output
-// element.  Used for shapes the vector kernels cannot read with 16-byte loads.
-// ---------------------------------------------------------------------------
-
-template <int EPI>
-__global__ __launch_bounds__(256) void gemm_i8_generic_kernel(GemvI8Args a) {
+template <int WT, int EPI>
+__global__ __launch_bounds__(256) void gemv_generic_kernel(GemvArgs a) {
   const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
   if (idx >= (size_t)a.M * a.N) return;
   const int m = (int)(idx / a.N), n = (int)(idx % a.N);
-  const int8_t *x = a.A + (size_t)m * a.lda, *w = a.W + (size_t)n * a.K;
-  int dot = 0;
-  for (int k = 0; k < a.K; k++) dot += (int)x[k] * (int)w[k];
-  float v = i8_epilogue(dot, a.as[m], a.ws ? a.ws[n] : 1.0f, a.bias ? a.bias[n] : 0.0f);
-  float *o = a.out + (size_t)m * a.ldo + n;
-  if constexpr (EPI == EPI_SWIGLU) {
-    const int8_t *w2 = a.W2 + (size_t)n * a.K;
-    int d2 = 0;
-    for (int k = 0; k < a.K; k++) d2 += (int)x[k] * (int)w2[k];
-    const float u = i8_epilogue(d2, a.as[m], a.ws2 ? a.ws2[n] : 1.0f, 0.0f);
-    v = silu(v) * u;
+  float v, u = 0.0f;
+  if constexpr (WT == WT_I8) {
+    const int8_t *x = reinterpret_cast<const int8_t *>(a.A) + (size_t)m * a.lda;
+    const int8_t *w = reinterpret_cast<const int8_t *>(a.W) + (size_t)n * a.K;
+    int dot = 0;
+    for (int k = 0; k < a.K; k++) dot += (int)x[k] * (int)w[k];
+    v = i8_epilogue(dot, a.as[m], a.ws ? a.ws[n] : 1.0f,
+                    (a.bias && EPI != EPI_SWIGLU) ? a.bias[n] : 0.0f);
+    if constexpr (EPI == EPI_SWIGLU) {
+      const int8_t *w2 = reinterpret_cast<const int8_t *>(a.W2) + (size_t)n * a.K;
+      int d2 = 0;
+      for (int k = 0; k < a.K; k++) d2 += (int)x[k] * (int)w2[k];
+      u = i8_epilogue(d2, a.as[m], a.ws2 ? a.ws2[n] : 1.0f, 0.0f);
+    }
+  } else {
+    const float *x = reinterpret_cast<const float *>(a.A) + (size_t)m * a.lda;
+    const uint16_t *w = reinterpret_cast<const uint16_t *>(a.W) + (size_t)n * a.K;
+    v = 0.0f;
+    for (int k = 0; k < a.K; k++) v = __builtin_fmaf(x[k], w2f<WT == WT_BF16>(w[k]), v);
+    if constexpr (EPI == EPI_SWIGLU) {
+      const uint16_t *w2 = reinterpret_cast<const uint16_t *>(a.W2) + (size_t)n * a.K;
+      for (int k = 0; k < a.K; k++) u = __builtin_fmaf(x[k], w2f<WT == WT_BF16>(w2[k]), u);
+    }
+    if constexpr (EPI == EPI_BIAS || EPI == EPI_BIAS_RESID || EPI == EPI_BIAS_GELU) v = v + a.bias[n];
   }
-  if constexpr (EPI == EPI_RESID) v = *o + v;
-  if constexpr (EPI == EPI_GELU) v = gelu_new(v);
-  *o = v;
-}
-
-template <int EPI, bool BF16>
-__global__ __launch_bounds__(256) void gemm_w16_generic_kernel(GemvW16Args a) {
-  const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
-  if (idx >= (size_t)a.M * a.N) return;
-  const int m = (int)(idx / a.N), n = (int)(idx % a.N);
-  const float *x = a.A + (size_t)m * a.lda;
-  const uint16_t *w = a.W + (size_t)n * a.K;
-  float v = 0.0f;
-  for (int k = 0; k < a.K; k++) v = __builtin_fmaf(x[k], w2f<BF16>(w[k]), v);
   float *o = a.out + (size_t)m * a.ldo + n;
-  if constexpr (EPI == EPI_SWIGLU) {
-    const uint16_t *w2 = a.W2 + (size_t)n * a.K;
-    float u = 0.0f;
-    for (int k = 0; k < a.K; k++) u = __builtin_fmaf(x[k], w2f<BF16>(w2[k]), u);
-    v = silu(v) * u;
-  }
-  if constexpr (EPI == EPI_BIAS || EPI == EPI_BIAS_RESID || EPI == EPI_BIAS_GELU) v = v + a.bias[n];
+  if constexpr (EPI == EPI_SWIGLU) v = silu(v) * u;
   if constexpr (EPI == EPI_RESID || EPI == EPI_BIAS_RESID) v = *o + v;
   if constexpr (EPI == EPI_GELU || EPI == EPI_BIAS_GELU) v = gelu_new(v);
   *o = v;
@@ -370,13 +176,17 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(KvArgs a) {
 // attention (src/gpt2.c:527-557 and 744-777)
 // ---------------------------------------------------------------------------
 
-// One block per (head, token).  Each score is one thread's sequential fp32
-// dot over head_dim in the reference order; max, exp (in double, rounded
-// once), double sum and the normalisation follow the reference; each output
-// element is one thread's sequential sum over positions in the reference
-// order.  Scores live in LDS.
+// One block per (head, token), reproducing the reference's arithmetic in its
+// order: each score is one thread's sequential fp32 dot over head_dim, scaled
+// in double; max; e = expf(s - max) with the reference's expf; double sum;
+// p = (float)(e * (1/sum)); each output element is one thread's sequential
+// fp32 sum over positions.  The int8 path turns any last-bit difference here
+// into different activation codes downstream, so the order is kept exactly.
+// The V rows of the attended positions are staged into LDS (tiles of vtile
+// positions) with loads issued before the scores, so the sequential sums read
+// LDS instead of waiting on memory latency.
 __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
-  extern __shared__ float lds[];
+  extern __shared__ __attribute__((aligned(16))) float lds[];
   __shared__ float redf[4];
   __shared__ double redd[4];
   const int h = blockIdx.x, m = blockIdx.y;
@@ -388,18 +198,38 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     if (lo < 0) lo = 0;
   }
   const int n = pos + 1 - lo;
-  const int hd = a.hd;
+  const int hd = a.hd, T = a.vtile;
   float *qs = lds;
   float *sc = lds + ((hd + 3) & ~3);
+  uint16_t *vt = reinterpret_cast<uint16_t *>(sc + ((a.max_npos + 3) & ~3));
   const float *q = a.q + (size_t)m * a.ldq + (size_t)h * hd;
-  for (int d = threadIdx.x; d < hd; d += 256) qs[d] = q[d];
-  __syncthreads();
   const size_t cbase = (size_t)slot * a.C * a.kv + (size_t)kvh * hd;
   const uint16_t *K = a.kc + cbase + (size_t)lo * a.kv;
   const uint16_t *V = a.vc + cbase + (size_t)lo * a.kv;
+  const bool vec = (hd & 7) == 0 && (a.kv & 7) == 0;
+
+  auto stage_v = [&](int t0) {  // V rows [t0, t0 + T) of the attended range -> vt
+    const int cnt = min(T, n - t0);
+    if (vec) {
+      const int cpr = hd >> 3;
+      for (int c = threadIdx.x; c < cnt * cpr; c += 256) {
+        const int i = c / cpr, j = (c - i * cpr) << 3;
+        *reinterpret_cast<v4u *>(vt + i * hd + j) =
+            *reinterpret_cast<const v4u *>(V + (size_t)(t0 + i) * a.kv + j);
+      }
+    } else {
+      for (int c = threadIdx.x; c < cnt * hd; c += 256) {
+        const int i = c / hd, j = c - i * hd;
+        vt[i * hd + j] = V[(size_t)(t0 + i) * a.kv + j];
+      }
+    }
+  };
+
+  for (int d = threadIdx.x; d < hd; d += 256) qs[d] = q[d];
+  stage_v(0);
+  __syncthreads();
 
   float mx = -FLT_MAX;
-  const bool vec = (hd & 7) == 0 && (a.kv & 7) == 0;
   for (int i = threadIdx.x; i < n; i += 256) {
     const uint16_t *kp = K + (size_t)i * a.kv;
     float s = 0.0f;
@@ -409,15 +239,15 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         const uint32_t wv[4] = {kk.x, kk.y, kk.z, kk.w};
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-          float p0 = qs[d + 2 * j] * h2f((uint16_t)(wv[j] & 0xffffu));
+          const float p0 = qs[d + 2 * j] * h2f((uint16_t)(wv[j] & 0xffffu));
           s = s + p0;
-          float p1 = qs[d + 2 * j + 1] * h2f((uint16_t)(wv[j] >> 16));
+          const float p1 = qs[d + 2 * j + 1] * h2f((uint16_t)(wv[j] >> 16));
           s = s + p1;
         }
       }
     } else {
       for (int d = 0; d < hd; d++) {
-        float p0 = qs[d] * h2f(kp[d]);
+        const float p0 = qs[d] * h2f(kp[d]);
         s = s + p0;
       }
     }
@@ -428,7 +258,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   mx = block_max256(mx, redf);
   double sum = 0.0;
   for (int i = threadIdx.x; i < n; i += 256) {
-    const float e = expf_d(sc[i] - mx);
+    const float e = ec_expf_ref(sc[i] - mx);
     sc[i] = e;
     sum += (double)e;
   }
@@ -436,26 +266,39 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   const double isum = 1.0 / sum;
   for (int i = threadIdx.x; i < n; i += 256) sc[i] = (float)((double)sc[i] * isum);
   __syncthreads();
-  for (int d = threadIdx.x; d < hd; d += 256) {
-    const uint16_t *vp = V + d;
-    float o = 0.0f;
-    int i = 0;
-    for (; i + 8 <= n; i += 8) {
-      float vv[8];
+
+  float o = 0.0f;
+  for (int t0 = 0; t0 < n; t0 += T) {
+    if (t0) {
+      __syncthreads();
+      stage_v(t0);
+      __syncthreads();
+    }
+    if ((int)threadIdx.x < hd) {
+      const int cnt = min(T, n - t0);
+      const uint16_t *vc = vt + threadIdx.x;
+      const float *pp = sc + t0;
+      int i = 0;
+      for (; i + 8 <= cnt; i += 8) {
+        float vv[8], pw[8];
 #pragma unroll
-      for (int j = 0; j < 8; j++) vv[j] = h2f(vp[(size_t)(i + j) * a.kv]);
+        for (int j = 0; j < 8; j++) {
+          vv[j] = h2f(vc[(i + j) * hd]);
+          pw[j] = pp[i + j];
+        }
 #pragma unroll
-      for (int j = 0; j < 8; j++) {
-        float p = sc[i + j] * vv[j];
-        o = o + p;
+        for (int j = 0; j < 8; j++) {
+          const float pr = pw[j] * vv[j];
+          o = o + pr;
+        }
+      }
+      for (; i < cnt; i++) {
+        const float pr = pp[i] * h2f(vc[i * hd]);
+        o = o + pr;
       }
     }
-    for (; i < n; i++) {
-      float p = sc[i] * h2f(vp[(size_t)i * a.kv]);
-      o = o + p;
-    }
-    a.out[(size_t)m * a.ldo + (size_t)h * hd + d] = o;
   }
+  if ((int)threadIdx.x < hd) a.out[(size_t)m * a.ldo + (size_t)h * hd + threadIdx.x] = o;
 }
 
 // ---------------------------------------------------------------------------
@@ -495,145 +338,141 @@ __global__ __launch_bounds__(256) void argmax_kernel(const float *L, int V, int 
   }
 }
 
+// argmax over the LM head's per-block candidates; logits[0] NaN -> 0 and no
+// non-NaN logit -> 0, like the reference's strict '>' scan from index 0
+__global__ __launch_bounds__(256) void argmax_finalize_kernel(const unsigned long long *cand, int ncand,
+                                                              const float *logits, int ldl, int *out) {
+  __shared__ unsigned long long red[4];
+  const int r = blockIdx.x;
+  unsigned long long b = 0ull;
+  for (int i = threadIdx.x; i < ncand; i += 256) {
+    const unsigned long long c = cand[(size_t)r * ncand + i];
+    b = c > b ? c : b;
+  }
+  b = wave_max_u64(b);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = b;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < 4; w++) b = red[w] > b ? red[w] : b;
+    const float l0 = logits[(size_t)r * ldl];
+    out[r] = (l0 != l0 || b == 0ull) ? 0 : (int)(0xFFFFFFFFu - (uint32_t)(b & 0xFFFFFFFFull));
+  }
+}
+
+// ---------------------------------------------------------------------------
+// elementwise device math, for checking the device arithmetic from tests
+// ---------------------------------------------------------------------------
+
+__global__ __launch_bounds__(256) void math_kernel(int op, const void *in, void *out, size_t n) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  if (op == MATH_F16_TO_F32) {
+    reinterpret_cast<float *>(out)[i] = h2f(reinterpret_cast<const uint16_t *>(in)[i]);
+    return;
+  }
+  const float x = reinterpret_cast<const float *>(in)[i];
+  switch (op) {
+  case MATH_EXPF: reinterpret_cast<float *>(out)[i] = ec_expf_ref(x); break;
+  case MATH_SILU: reinterpret_cast<float *>(out)[i] = silu(x); break;
+  case MATH_GELU: reinterpret_cast<float *>(out)[i] = gelu_new(x); break;
+  case MATH_F32_TO_F16: reinterpret_cast<uint16_t *>(out)[i] = f2h(x); break;
+  case MATH_QUANT1: reinterpret_cast<int8_t *>(out)[i] = quant1(x, 1.0f); break;
+  default: break;
+  }
+}
+
+hipError_t device_math(int op, const void *in, void *out, size_t n, hipStream_t st) {
+  if (op < 0 || op > MATH_QUANT1) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(math_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, op, in, out, n);
+  return hipGetLastError();
+}
+
 // ---------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------
 
 static inline bool al16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
-bool gemv_i8_vector_ok(const GemvI8Args &a) {
-  return a.K % 16 == 0 && a.lda % 16 == 0 && al16(a.A) && al16(a.W) && (!a.W2 || al16(a.W2));
+static int g_gemv_max_blocks = 1024;
+void gemv_set_max_blocks(int n) { g_gemv_max_blocks = n > 0 ? n : 1024; }
+int gemv_max_blocks() { return g_gemv_max_blocks; }
+
+int gemv_pick_mt(int M) { return M >= 5 ? 8 : M >= 3 ? 4 : M == 2 ? 2 : 1; }
+
+// lanes per row: the narrow variant (4 or 2 rows per wave) when the whole
+// row fits its register block and there are enough row groups to fill the
+// chip, else one row per wave
+int gemv_pick_lpr(int wt, int epi, int K, int N) {
+  const int chb = wt == WT_I8 ? 16 : 8;
+  const int narrow = wt == WT_I8 ? 16 : 32;
+  const int nch = K / chb;
+  const int rpb = (epi == EPI_SWIGLU ? 2 : 4) * (64 / narrow);
+  if (nch <= narrow * lpr_cpl(narrow) && (N + rpb - 1) / rpb >= 256) return narrow;
+  return 64;
 }
 
-bool gemv_w16_vector_ok(const GemvW16Args &a) {
-  return a.K % 8 == 0 && a.lda % 4 == 0 && al16(a.A) && al16(a.W) && (!a.W2 || al16(a.W2));
+int gemv_grid_x(const GemvArgs &a, int wt, int epi) {
+  const int lpr = gemv_pick_lpr(wt, epi, a.K, a.N);
+  const int rpb = (epi == EPI_SWIGLU ? 2 : 4) * (64 / lpr);
+  const int ng = (a.N + rpb - 1) / rpb;
+  return ng < g_gemv_max_blocks ? ng : g_gemv_max_blocks;
 }
 
-static int pick_mt(int M) { return M >= 5 ? 8 : M >= 3 ? 4 : M == 2 ? 2 : 1; }
-static int pick_lpr(int chunks) { return chunks >= 48 ? 64 : chunks >= 24 ? 32 : 16; }
-
-template <int LPR, int MT, int EPI>
-static hipError_t launch_i8(const GemvI8Args &a, hipStream_t s) {
-  const int rpb = (EPI == EPI_SWIGLU ? 2 : 4) * (kWave / LPR);
-  dim3 grid((a.N + rpb - 1) / rpb, (a.M + MT - 1) / MT);
-  hipLaunchKernelGGL((gemv_i8_kernel<LPR, MT, EPI>), grid, dim3(256), 0, s, a);
-  return hipGetLastError();
-}
-
-template <int LPR, int EPI>
-static hipError_t launch_i8_mt(const GemvI8Args &a, hipStream_t s) {
-  switch (pick_mt(a.M)) {
-  case 1: return launch_i8<LPR, 1, EPI>(a, s);
-  case 2: return launch_i8<LPR, 2, EPI>(a, s);
-  case 4: return launch_i8<LPR, 4, EPI>(a, s);
-  default: return launch_i8<LPR, 8, EPI>(a, s);
+size_t gemv_lds_bytes(int wt, int pro, int MT, int K) {
+  if (pro == PRO_F32) return 0;
+  if (wt == WT_I8) {
+    const size_t kp = (size_t)(K + 15) / 16 * 16;
+    return (MT * kp + 4 * MT + 15) / 16 * 16;
   }
+  const size_t kp = (size_t)(K + 7) / 8 * 8;
+  return MT * kp * 4;
 }
 
-template <int EPI>
-static hipError_t launch_i8_lpr(const GemvI8Args &a, hipStream_t s) {
-  switch (pick_lpr(a.K >> 4)) {
-  case 64: return launch_i8_mt<64, EPI>(a, s);
-  case 32: return launch_i8_mt<32, EPI>(a, s);
-  default: return launch_i8_mt<16, EPI>(a, s);
-  }
+static int g_max_lds_bytes = 65536;
+
+bool gemv_vector_ok(const GemvArgs &a, int wt, int pro) {
+  const int chb = wt == WT_I8 ? 16 : 8;
+  if (a.K <= 0 || a.K % chb || !al16(a.W) || (a.W2 && !al16(a.W2))) return false;
+  if (pro == PRO_I8 && (a.lda % 16 || !al16(a.A))) return false;
+  if (pro == PRO_F32 && (a.lda % 4 || !al16(a.A))) return false;
+  if (wt == WT_I8 && pro == PRO_F32) return false;
+  if (wt != WT_I8 && (pro == PRO_I8 || pro == PRO_QUANT)) return false;
+  return gemv_lds_bytes(wt, pro, gemv_pick_mt(a.M), a.K) <= (size_t)g_max_lds_bytes;
 }
 
-template <int EPI>
-static hipError_t launch_i8_generic(const GemvI8Args &a, hipStream_t s) {
+void gemv_set_max_lds(int bytes) { g_max_lds_bytes = bytes; }
+
+hipError_t gemv(const GemvArgs &a, int wt, int epi, int pro, hipStream_t s) {
+  if (wt == WT_I8) return gemv_i8_fused(a, epi, pro, s);
+  if (wt == WT_BF16) return gemv_bf16_fused(a, epi, pro, s);
+  return gemv_f16_fused(a, epi, pro, s);
+}
+
+template <int WT, int EPI>
+static hipError_t launch_generic(const GemvArgs &a, hipStream_t s) {
   const size_t tot = (size_t)a.M * a.N;
-  hipLaunchKernelGGL(gemm_i8_generic_kernel<EPI>, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s, a);
+  hipLaunchKernelGGL((gemv_generic_kernel<WT, EPI>), dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
-hipError_t gemm_i8_generic(const GemvI8Args &a, int epi, hipStream_t s) {
+template <int WT>
+static hipError_t generic_epi(const GemvArgs &a, int epi, hipStream_t s) {
   switch (epi) {
-  case EPI_STORE: return launch_i8_generic<EPI_STORE>(a, s);
-  case EPI_RESID: return launch_i8_generic<EPI_RESID>(a, s);
-  case EPI_GELU: return launch_i8_generic<EPI_GELU>(a, s);
-  case EPI_SWIGLU: return launch_i8_generic<EPI_SWIGLU>(a, s);
+  case EPI_STORE: return launch_generic<WT, EPI_STORE>(a, s);
+  case EPI_RESID: return launch_generic<WT, EPI_RESID>(a, s);
+  case EPI_GELU: return launch_generic<WT, EPI_GELU>(a, s);
+  case EPI_SWIGLU: return launch_generic<WT, EPI_SWIGLU>(a, s);
+  case EPI_BIAS: return launch_generic<WT, EPI_BIAS>(a, s);
+  case EPI_BIAS_RESID: return launch_generic<WT, EPI_BIAS_RESID>(a, s);
+  case EPI_BIAS_GELU: return launch_generic<WT, EPI_BIAS_GELU>(a, s);
   default: return hipErrorInvalidValue;
   }
 }
 
-hipError_t gemv_i8(const GemvI8Args &a, int epi, hipStream_t s) {
-  if (a.K == 0 || !gemv_i8_vector_ok(a)) return gemm_i8_generic(a, epi, s);
-  switch (epi) {
-  case EPI_STORE: return launch_i8_lpr<EPI_STORE>(a, s);
-  case EPI_RESID: return launch_i8_lpr<EPI_RESID>(a, s);
-  case EPI_GELU: return launch_i8_lpr<EPI_GELU>(a, s);
-  case EPI_SWIGLU: return launch_i8_lpr<EPI_SWIGLU>(a, s);
-  default: return hipErrorInvalidValue;
-  }
-}
-
-template <int LPR, int MT, int EPI, bool BF16>
-static hipError_t launch_w16(const GemvW16Args &a, hipStream_t s) {
-  const int rpb = (EPI == EPI_SWIGLU ? 2 : 4) * (kWave / LPR);
-  dim3 grid((a.N + rpb - 1) / rpb, (a.M + MT - 1) / MT);
-  hipLaunchKernelGGL((gemv_w16_kernel<LPR, MT, EPI, BF16>), grid, dim3(256), 0, s, a);
-  return hipGetLastError();
-}
-
-template <int LPR, int EPI, bool BF16>
-static hipError_t launch_w16_mt(const GemvW16Args &a, hipStream_t s) {
-  switch (pick_mt(a.M)) {
-  case 1: return launch_w16<LPR, 1, EPI, BF16>(a, s);
-  case 2: return launch_w16<LPR, 2, EPI, BF16>(a, s);
-  case 4: return launch_w16<LPR, 4, EPI, BF16>(a, s);
-  default: return launch_w16<LPR, 8, EPI, BF16>(a, s);
-  }
-}
-
-template <int EPI, bool BF16>
-static hipError_t launch_w16_lpr(const GemvW16Args &a, hipStream_t s) {
-  switch (pick_lpr(a.K >> 3)) {
-  case 64: return launch_w16_mt<64, EPI, BF16>(a, s);
-  case 32: return launch_w16_mt<32, EPI, BF16>(a, s);
-  default: return launch_w16_mt<16, EPI, BF16>(a, s);
-  }
-}
-
-template <bool BF16>
-static hipError_t gemv_w16_t(const GemvW16Args &a, int epi, hipStream_t s) {
-  switch (epi) {
-  case EPI_STORE: return launch_w16_lpr<EPI_STORE, BF16>(a, s);
-  case EPI_RESID: return launch_w16_lpr<EPI_RESID, BF16>(a, s);
-  case EPI_SWIGLU: return launch_w16_lpr<EPI_SWIGLU, BF16>(a, s);
-  case EPI_BIAS: return launch_w16_lpr<EPI_BIAS, BF16>(a, s);
-  case EPI_BIAS_RESID: return launch_w16_lpr<EPI_BIAS_RESID, BF16>(a, s);
-  case EPI_BIAS_GELU: return launch_w16_lpr<EPI_BIAS_GELU, BF16>(a, s);
-  default: return hipErrorInvalidValue;
-  }
-}
-
-template <int EPI, bool BF16>
-static hipError_t launch_w16_generic(const GemvW16Args &a, hipStream_t s) {
-  const size_t tot = (size_t)a.M * a.N;
-  hipLaunchKernelGGL((gemm_w16_generic_kernel<EPI, BF16>), dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s, a);
-  return hipGetLastError();
-}
-
-template <bool BF16>
-static hipError_t gemm_w16_generic_t(const GemvW16Args &a, int epi, hipStream_t s) {
-  switch (epi) {
-  case EPI_STORE: return launch_w16_generic<EPI_STORE, BF16>(a, s);
-  case EPI_RESID: return launch_w16_generic<EPI_RESID, BF16>(a, s);
-  case EPI_SWIGLU: return launch_w16_generic<EPI_SWIGLU, BF16>(a, s);
-  case EPI_BIAS: return launch_w16_generic<EPI_BIAS, BF16>(a, s);
-  case EPI_BIAS_RESID: return launch_w16_generic<EPI_BIAS_RESID, BF16>(a, s);
-  case EPI_BIAS_GELU: return launch_w16_generic<EPI_BIAS_GELU, BF16>(a, s);
-  default: return hipErrorInvalidValue;
-  }
-}
-
-hipError_t gemm_w16_generic(const GemvW16Args &a, int epi, bool bf16, hipStream_t s) {
-  return bf16 ? gemm_w16_generic_t<true>(a, epi, s) : gemm_w16_generic_t<false>(a, epi, s);
-}
-
-hipError_t gemv_w16(const GemvW16Args &a, int epi, bool bf16, hipStream_t s) {
-  if (a.K == 0 || !gemv_w16_vector_ok(a)) return gemm_w16_generic(a, epi, bf16, s);
-  return bf16 ? gemv_w16_t<true>(a, epi, s) : gemv_w16_t<false>(a, epi, s);
+hipError_t gemv_generic(const GemvArgs &a, int wt, int epi, hipStream_t s) {
+  if (wt == WT_I8) return generic_epi<WT_I8>(a, epi, s);
+  if (wt == WT_BF16) return generic_epi<WT_BF16>(a, epi, s);
+  return generic_epi<WT_F16>(a, epi, s);
 }
 
 hipError_t quant_rows(const float *in, int ldi, int M, int K, int8_t *q, int ldq, float *s,
@@ -668,13 +507,20 @@ hipError_t rope_kv_append(const KvArgs &a, hipStream_t st) {
   return hipGetLastError();
 }
 
-size_t attention_lds_bytes(int max_npos, int hd) {
-  return ((size_t)((hd + 3) & ~3) + (size_t)max_npos) * sizeof(float);
+size_t attention_lds_bytes(int max_npos, int hd, int vtile) {
+  return ((size_t)((hd + 3) & ~3) + (size_t)((max_npos + 3) & ~3)) * sizeof(float) +
+         (size_t)vtile * hd * sizeof(uint16_t);
 }
 
 hipError_t attention(const AttnArgs &a, hipStream_t st) {
-  const size_t lds = attention_lds_bytes(a.max_npos, a.hd);
+  const size_t lds = attention_lds_bytes(a.max_npos, a.hd, a.vtile);
   hipLaunchKernelGGL(attn_kernel, dim3(a.H, a.M), dim3(256), lds, st, a);
+  return hipGetLastError();
+}
+
+hipError_t argmax_finalize(const unsigned long long *cand, int ncand, const float *logits, int ldl, int rows,
+                           int *out, hipStream_t st) {
+  hipLaunchKernelGGL(argmax_finalize_kernel, dim3(rows), dim3(256), 0, st, cand, ncand, logits, ldl, out);
   return hipGetLastError();
 }
 

@@ -75,6 +75,8 @@ extern "C" int ec_init(void) {
       lds > 0)
     g_max_lds = lds;
   EC_HIP(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
+  gemv_set_max_blocks(4 * g_prop.multiProcessorCount);
+  gemv_set_max_lds(g_max_lds);
   g_inited = 1;
   return 0;
 }
@@ -239,16 +241,21 @@ extern "C" int ec_prof_stop(char *buf, int len) {
 // kernel ABI
 // ---------------------------------------------------------------------------
 
-static double gemv_i8_bytes(int M, int K, int N, bool scales, bool bias, int epi) {
-  double b = (double)N * K + (scales ? 4.0 * N : 0) + (bias ? 4.0 * N : 0) + (double)M * K + 4.0 * M;
-  b += 4.0 * M * N * (epi == EPI_RESID ? 2 : 1);
+// algorithmic bytes of one GEMV launch: weights (twice for gate+up), weight
+// scales and bias, the activation rows read, the output rows written (read
+// too for a residual add)
+static double gemv_bytes(int wt, int pro, int epi, int M, int K, int N, bool scales, bool bias) {
+  const double wb = wt == WT_I8 ? 1.0 : 2.0, mats = epi == EPI_SWIGLU ? 2.0 : 1.0;
+  double b = mats * ((double)N * K * wb + (scales ? 4.0 * N : 0.0)) + (bias ? 4.0 * N : 0.0);
+  b += (double)M * K * (pro == PRO_I8 ? 1.0 : 4.0);
+  b += 4.0 * M * N * ((epi == EPI_RESID || epi == EPI_BIAS_RESID) ? 2.0 : 1.0);
   return b;
 }
 
-static double gemv_w16_bytes(int M, int K, int N, bool bias, int epi) {
-  double b = 2.0 * N * K + (bias ? 4.0 * N : 0) + 4.0 * M * K;
-  b += 4.0 * M * N * ((epi == EPI_RESID || epi == EPI_BIAS_RESID) ? 2 : 1);
-  return b;
+// the fused vector kernel when the shape allows it, else the generic kernel
+static hipError_t gemv_any(const GemvArgs &a, int wt, int epi, int pro, hipStream_t s) {
+  if (gemv_vector_ok(a, wt, pro)) return gemv(a, wt, epi, pro, s);
+  return gemv_generic(a, wt, epi, s);
 }
 
 extern "C" int ec_gemm_int8_dev(float *C, const int8_t *A, const float *a_scale, const int8_t *B,
@@ -257,8 +264,9 @@ extern "C" int ec_gemm_int8_dev(float *C, const int8_t *A, const float *a_scale,
   if (M < 0 || N < 0 || K < 0) return set_err(-1, "gemm_int8: negative shape M=%d K=%d N=%d", M, K, N);
   if (M == 0 || N == 0) return 0;
   if (!C || !a_scale || (K > 0 && (!A || !B))) return set_err(-1, "gemm_int8: null pointer");
-  GemvI8Args a{A, K, a_scale, B, b_scale, bias, nullptr, nullptr, C, N, M, K, N};
-  EC_LAUNCH("gemv_i8", gemv_i8_bytes(M, K, N, b_scale, bias, EPI_STORE), gemv_i8(a, EPI_STORE, g_stream));
+  GemvArgs a{A, K, a_scale, nullptr, nullptr, 0.0, B, nullptr, b_scale, nullptr, bias, C, N, M, K, N, nullptr};
+  EC_LAUNCH("gemv_i8", gemv_bytes(WT_I8, PRO_I8, EPI_STORE, M, K, N, b_scale, bias),
+            gemv_any(a, WT_I8, EPI_STORE, PRO_I8, g_stream));
   return 0;
 }
 
@@ -267,8 +275,10 @@ static int gemm_w16_dev(float *C, const float *A, const uint16_t *B, int M, int 
   if (M < 0 || N < 0 || K < 0) return set_err(-1, "gemm: negative shape M=%d K=%d N=%d", M, K, N);
   if (M == 0 || N == 0) return 0;
   if (!C || (K > 0 && (!A || !B))) return set_err(-1, "gemm: null pointer");
-  GemvW16Args a{A, K, B, nullptr, nullptr, C, N, M, K, N};
-  EC_LAUNCH("gemv_w16", gemv_w16_bytes(M, K, N, false, EPI_STORE), gemv_w16(a, EPI_STORE, bf16, g_stream));
+  const int wt = bf16 ? WT_BF16 : WT_F16;
+  GemvArgs a{A, K, nullptr, nullptr, nullptr, 0.0, B, nullptr, nullptr, nullptr, nullptr, C, N, M, K, N, nullptr};
+  EC_LAUNCH("gemv_w16", gemv_bytes(wt, PRO_F32, EPI_STORE, M, K, N, false, false),
+            gemv_any(a, wt, EPI_STORE, PRO_F32, g_stream));
   return 0;
 }
 
@@ -286,6 +296,15 @@ extern "C" int ec_quantize_rows_dev(const float *in, int M, int K, int8_t *q, fl
   if (M == 0) return 0;
   if (!in || !q || !s) return set_err(-1, "quantize_rows: null pointer");
   EC_LAUNCH("quant", 5.0 * M * K + 4.0 * M, quant_rows(in, K, M, K, q, K, s, g_stream));
+  return 0;
+}
+
+extern "C" int ec_device_math(int op, const void *in, void *out, size_t n) {
+  EC_INIT();
+  if (!in || !out) return set_err(-1, "ec_device_math: null pointer");
+  if (n == 0) return 0;
+  EC_LAUNCH("math", 8.0 * n, device_math(op, in, out, n, g_stream));
+  EC_HIP(hipStreamSynchronize(g_stream));
   return 0;
 }
 
@@ -408,7 +427,12 @@ struct DevModel {
   uint16_t *kc = nullptr, *vc = nullptr;
   size_t kv_layer = 0;  // elements per layer of one cache
   const uint16_t *lm = nullptr;
+  unsigned long long *cand = nullptr;  // LM-head argmax candidates [lm_rows][gemv blocks]
+  int ncand = 0;
 };
+
+// V positions staged per attention tile (LDS: 64 KB at head_dim 64)
+static constexpr int kAttnVTile = 512;
 
 namespace {
 
@@ -453,7 +477,7 @@ struct Loader {
 static void free_dev(DevModel *d) {
   if (!d) return;
   void *ps[] = {d->arena, d->rope, d->d_tok, d->d_pos, d->d_slot, d->d_amax, d->x, d->h, d->qkv,
-                d->att, d->ff, d->aq, d->as, d->logits, d->kc, d->vc};
+                d->att, d->ff, d->aq, d->as, d->logits, d->kc, d->vc, d->cand};
   for (void *p : ps)
     if (p) (void)hipFree(p);
   if (d->h_stage) (void)hipHostFree(d->h_stage);
@@ -711,6 +735,8 @@ static int load_impl(GPT2 *g, const char *path, int batch_cap, int max_ctx) {
   EC_HIP(hipMalloc(&d->d_slot, (size_t)mmax * 4));
   EC_HIP(hipMalloc(&d->d_amax, (size_t)mmax * 4));
   EC_HIP(hipHostMalloc((void **)&d->h_stage, (size_t)mmax * 3 * 4, hipHostMallocDefault));
+  d->ncand = gemv_max_blocks();
+  EC_HIP(hipMalloc(&d->cand, (size_t)d->lm_rows * d->ncand * sizeof(unsigned long long)));
   g->ws_x = d->x;
   g->ws_tmp = d->h;
   g->ws_qkv = d->qkv;
@@ -757,6 +783,36 @@ extern "C" int gpt2_kv_reset(GPT2 *g) {
   return 0;
 }
 
+// One linear layer: the fused GEMV when the shape allows it; otherwise the
+// prologue runs as its own kernel (norm / quantize into the aq or h
+// workspace) and the generic kernel does the product.
+static int linear(GPT2 *g, DevModel *d, const char *fam, GemvArgs a, int wt, int epi, int pro, hipStream_t s) {
+  const double bytes = gemv_bytes(wt, pro, epi, a.M, a.K, a.N, a.ws != nullptr, a.bias != nullptr);
+  if (gemv_vector_ok(a, wt, pro)) {
+    EC_LAUNCH(fam, bytes, gemv(a, wt, epi, pro, s));
+    return 0;
+  }
+  const float *A = (const float *)a.A;
+  if (pro == PRO_QUANT) {
+    EC_LAUNCH("quant", 5.0 * a.M * a.K, quant_rows(A, a.lda, a.M, a.K, d->aq, d->aq_ld, d->as, s));
+  } else if ((pro == PRO_RMS || pro == PRO_LN) && wt == WT_I8) {
+    EC_LAUNCH("norm_quant", 5.0 * a.M * a.K,
+              norm_rows(A, a.M, a.K, a.gamma, a.beta, g->eps, nullptr, 0, d->aq, d->aq_ld, d->as, s));
+  } else if (pro == PRO_RMS || pro == PRO_LN) {
+    EC_LAUNCH("norm", 8.0 * a.M * a.K, norm_rows(A, a.M, a.K, a.gamma, a.beta, g->eps, d->h, a.K, nullptr, 0, nullptr, s));
+  }
+  if (wt == WT_I8 && pro != PRO_I8) {
+    a.A = d->aq;
+    a.lda = d->aq_ld;
+    a.as = d->as;
+  } else if (pro == PRO_RMS || pro == PRO_LN) {
+    a.A = d->h;
+    a.lda = a.K;
+  }
+  EC_LAUNCH(fam, bytes, gemv_generic(a, wt, epi, s));
+  return 0;
+}
+
 static int forward_impl(GPT2 *g, const int *tokens, const int *positions, const int *seqs, int M,
                         int lm_from, float *logits, int *argmax) {
   EC_INIT();
@@ -767,6 +823,8 @@ static int forward_impl(GPT2 *g, const int *tokens, const int *positions, const 
   if (!tokens || !positions) return set_err(-1, "null tokens/positions");
   const int E = g->n_embd, H = g->n_head, V = g->vocab, kv = g->n_kv_embd, hd = g->head_dim;
   const bool qwen = g->arch == ARCH_QWEN2, i8 = g->precision == 0, bf16 = g->precision == 2;
+  const int wt = i8 ? WT_I8 : (bf16 ? WT_BF16 : WT_F16);
+  const int pro_norm = qwen ? PRO_RMS : PRO_LN;
   int *st = d->h_stage;
   int max_npos = 0;
   for (int m = 0; m < M; m++) {
@@ -781,10 +839,18 @@ static int forward_impl(GPT2 *g, const int *tokens, const int *positions, const 
     st[2 * d->mmax + m] = slot;
     if (positions[m] + 1 > max_npos) max_npos = positions[m] + 1;
   }
-  const size_t lds = attention_lds_bytes(max_npos, hd);
-  if (lds > (size_t)g_max_lds)
-    return set_err(-1, "position %d needs %zu bytes of LDS for attention scores (limit %d)", max_npos - 1,
-                   lds, g_max_lds);
+  // attention LDS: scores for max_npos positions + a tile of V rows
+  if (hd > 256) return set_err(-1, "head_dim %d above 256 is not supported", hd);
+  const size_t lds_fixed = attention_lds_bytes(max_npos, hd, 0);
+  int vtile = 0;
+  if (lds_fixed < (size_t)g_max_lds) {
+    const size_t room = ((size_t)g_max_lds - lds_fixed) / ((size_t)hd * sizeof(uint16_t));
+    vtile = (int)(room < (size_t)kAttnVTile ? room : (size_t)kAttnVTile) & ~7;
+    if (vtile > ((max_npos + 7) & ~7)) vtile = (max_npos + 7) & ~7;
+  }
+  if (vtile < 8)
+    return set_err(-1, "position %d needs more LDS for attention scores than the device has (%d bytes)",
+                   max_npos - 1, g_max_lds);
   hipStream_t s = g_stream;
   EC_HIP(hipMemcpyAsync(d->d_tok, st, (size_t)M * 4, hipMemcpyHostToDevice, s));
   EC_HIP(hipMemcpyAsync(d->d_pos, st + d->mmax, (size_t)M * 4, hipMemcpyHostToDevice, s));
@@ -792,23 +858,20 @@ static int forward_impl(GPT2 *g, const int *tokens, const int *positions, const 
 
   EC_LAUNCH("embed", (double)M * E * (g->wpe ? 8 : 6), embed(g->wte, g->wpe, bf16, d->d_tok, d->d_pos, M, E, d->x, s));
 
-  const int F = d->F, ldq = d->qkv_ld, aql = d->aq_ld;
+  const int F = d->F, ldq = d->qkv_ld;
   const int nqkv = qwen ? E + 2 * kv : 3 * E;
+  double abytes = 0;
+  for (int m = 0; m < M; m++) abytes += (double)(positions[m] + 1) * kv * 4 + 8.0 * E;
+  int r;
   for (int l = 0; l < g->n_layer; l++) {
     const LayerDev &W = d->L[l];
     uint16_t *kcl = d->kc + d->kv_layer * l, *vcl = d->vc + d->kv_layer * l;
-    // norm -> qkv projection
-    if (i8) {
-      EC_LAUNCH("norm_quant", (double)M * E * 5 + 8.0 * E,
-                norm_rows(d->x, M, E, W.ln1_g, W.ln1_b, g->eps, nullptr, 0, d->aq, aql, d->as, s));
-      GemvI8Args a{d->aq, aql, d->as, (const int8_t *)W.wqkv, W.sqkv, W.bqkv, nullptr, nullptr, d->qkv, ldq, M, E, nqkv};
-      EC_LAUNCH("gemv_i8_qkv", gemv_i8_bytes(M, E, nqkv, true, W.bqkv, EPI_STORE), gemv_i8(a, EPI_STORE, s));
-    } else {
-      EC_LAUNCH("norm", (double)M * E * 8 + 8.0 * E,
-                norm_rows(d->x, M, E, W.ln1_g, W.ln1_b, g->eps, d->h, E, nullptr, 0, nullptr, s));
-      GemvW16Args a{d->h, E, (const uint16_t *)W.wqkv, W.bqkv, nullptr, d->qkv, ldq, M, E, nqkv};
-      const int epi = W.bqkv ? EPI_BIAS : EPI_STORE;
-      EC_LAUNCH("gemv_w16_qkv", gemv_w16_bytes(M, E, nqkv, W.bqkv, epi), gemv_w16(a, epi, bf16, s));
+    // norm -> q|k|v projection (GPT-2 bias: inside the int8 epilogue, a bias pass for 16-bit)
+    {
+      GemvArgs a{d->x, E, nullptr, W.ln1_g, W.ln1_b, g->eps, W.wqkv, nullptr, W.sqkv, nullptr, W.bqkv,
+                 d->qkv, ldq, M, E, nqkv, nullptr};
+      const int epi = (!i8 && W.bqkv) ? EPI_BIAS : EPI_STORE;
+      if ((r = linear(g, d, "gemv_qkv", a, wt, epi, pro_norm, s))) return r;
     }
     // RoPE (Qwen2) + fp16 KV append
     KvArgs ka{d->qkv, d->qkv + E, d->qkv + E + (qwen ? kv : E), ldq, ldq, H, g->n_kv_head, hd, kv,
@@ -816,68 +879,57 @@ static int forward_impl(GPT2 *g, const int *tokens, const int *positions, const 
     EC_LAUNCH("rope_kv", (double)M * (qwen ? (E + kv) * 8 + kv * 8 : kv * 12), rope_kv_append(ka, s));
     // attention
     AttnArgs aa{d->qkv, ldq, kcl, vcl, d->att, E, d->d_pos, d->d_slot, H, g->n_kv_head, hd, kv,
-                d->eff_ctx, qwen ? g->sliding_window : 0, 1.0 / sqrt((double)hd), M, max_npos};
-    double abytes = 0;
-    for (int m = 0; m < M; m++) abytes += (double)(positions[m] + 1) * kv * 4 + 8.0 * E;
+                d->eff_ctx, qwen ? g->sliding_window : 0, 1.0 / sqrt((double)hd), M, max_npos, vtile};
     EC_LAUNCH("attention", abytes, attention(aa, s));
     // output projection + residual
-    if (i8) {
-      EC_LAUNCH("quant", (double)M * E * 5, quant_rows(d->att, E, M, E, d->aq, aql, d->as, s));
-      GemvI8Args a{d->aq, aql, d->as, (const int8_t *)W.wo, W.so, W.bo, nullptr, nullptr, d->x, E, M, E, E};
-      EC_LAUNCH("gemv_i8_o", gemv_i8_bytes(M, E, E, true, W.bo, EPI_RESID), gemv_i8(a, EPI_RESID, s));
-    } else {
-      GemvW16Args a{d->att, E, (const uint16_t *)W.wo, W.bo, nullptr, d->x, E, M, E, E};
-      const int epi = W.bo ? EPI_BIAS_RESID : EPI_RESID;
-      EC_LAUNCH("gemv_w16_o", gemv_w16_bytes(M, E, E, W.bo, epi), gemv_w16(a, epi, bf16, s));
+    {
+      GemvArgs a{d->att, E, nullptr, nullptr, nullptr, 0.0, W.wo, nullptr, W.so, nullptr, W.bo, d->x, E, M, E, E,
+                 nullptr};
+      const int epi = i8 ? EPI_RESID : (W.bo ? EPI_BIAS_RESID : EPI_RESID);
+      if ((r = linear(g, d, "gemv_o", a, wt, epi, i8 ? PRO_QUANT : PRO_F32, s))) return r;
     }
-    // MLP
-    if (i8) {
-      EC_LAUNCH("norm_quant", (double)M * E * 5 + 8.0 * E,
-                norm_rows(d->x, M, E, W.ln2_g, W.ln2_b, g->eps, nullptr, 0, d->aq, aql, d->as, s));
-      if (qwen) {
-        GemvI8Args a{d->aq, aql, d->as, (const int8_t *)W.wg, W.sg, nullptr, (const int8_t *)W.wu, W.su, d->ff, F, M, E, F};
-        EC_LAUNCH("gemv_i8_gateup", 2 * gemv_i8_bytes(M, E, F, true, false, EPI_STORE) - (double)M * E - 4.0 * M - 4.0 * M * F,
-                  gemv_i8(a, EPI_SWIGLU, s));
-      } else {
-        GemvI8Args a{d->aq, aql, d->as, (const int8_t *)W.wfc, W.sfc, W.bfc, nullptr, nullptr, d->ff, F, M, E, F};
-        EC_LAUNCH("gemv_i8_fc", gemv_i8_bytes(M, E, F, true, true, EPI_GELU), gemv_i8(a, EPI_GELU, s));
-      }
-      EC_LAUNCH("quant", (double)M * F * 5, quant_rows(d->ff, F, M, F, d->aq, aql, d->as, s));
-      GemvI8Args a{d->aq, aql, d->as, (const int8_t *)W.wd, W.sd, W.bd, nullptr, nullptr, d->x, E, M, F, E};
-      EC_LAUNCH("gemv_i8_down", gemv_i8_bytes(M, F, E, true, W.bd, EPI_RESID), gemv_i8(a, EPI_RESID, s));
+    // MLP up: SwiGLU gate/up (Qwen2) or fc + GELU (GPT-2), norm fused
+    if (qwen) {
+      GemvArgs a{d->x, E, nullptr, W.ln2_g, nullptr, g->eps, W.wg, W.wu, W.sg, W.su, nullptr, d->ff, F, M, E, F,
+                 nullptr};
+      if ((r = linear(g, d, "gemv_gateup", a, wt, EPI_SWIGLU, PRO_RMS, s))) return r;
     } else {
-      EC_LAUNCH("norm", (double)M * E * 8 + 8.0 * E,
-                norm_rows(d->x, M, E, W.ln2_g, W.ln2_b, g->eps, d->h, E, nullptr, 0, nullptr, s));
-      if (qwen) {
-        GemvW16Args a{d->h, E, (const uint16_t *)W.wg, nullptr, (const uint16_t *)W.wu, d->ff, F, M, E, F};
-        EC_LAUNCH("gemv_w16_gateup", 2 * gemv_w16_bytes(M, E, F, false, EPI_STORE) - 4.0 * M * E - 4.0 * M * F,
-                  gemv_w16(a, EPI_SWIGLU, bf16, s));
-      } else {
-        GemvW16Args a{d->h, E, (const uint16_t *)W.wfc, W.bfc, nullptr, d->ff, F, M, E, F};
-        EC_LAUNCH("gemv_w16_fc", gemv_w16_bytes(M, E, F, true, EPI_BIAS_GELU), gemv_w16(a, EPI_BIAS_GELU, bf16, s));
-      }
-      GemvW16Args a{d->ff, F, (const uint16_t *)W.wd, W.bd, nullptr, d->x, E, M, F, E};
-      const int epi = W.bd ? EPI_BIAS_RESID : EPI_RESID;
-      EC_LAUNCH("gemv_w16_down", gemv_w16_bytes(M, F, E, W.bd, epi), gemv_w16(a, epi, bf16, s));
+      GemvArgs a{d->x, E, nullptr, W.ln2_g, W.ln2_b, g->eps, W.wfc, nullptr, W.sfc, nullptr, W.bfc, d->ff, F, M,
+                 E, F, nullptr};
+      if ((r = linear(g, d, "gemv_fc", a, wt, i8 ? EPI_GELU : EPI_BIAS_GELU, PRO_LN, s))) return r;
+    }
+    // MLP down + residual
+    {
+      GemvArgs a{d->ff, F, nullptr, nullptr, nullptr, 0.0, W.wd, nullptr, W.sd, nullptr, W.bd, d->x, E, M, F, E,
+                 nullptr};
+      const int epi = i8 ? EPI_RESID : (W.bd ? EPI_BIAS_RESID : EPI_RESID);
+      if ((r = linear(g, d, "gemv_down", a, wt, epi, i8 ? PRO_QUANT : PRO_F32, s))) return r;
     }
   }
-  // final norm + LM head (always fp16/bf16, src/gpt2.c:576-580 / 799-804)
-  if (lm_from < M) {
-    EC_LAUNCH("norm", (double)M * E * 8 + 8.0 * E,
-              norm_rows(d->x, M, E, g->lnf_g, g->lnf_b, g->eps, d->h, E, nullptr, 0, nullptr, s));
-    for (int r0 = lm_from; r0 < M; r0 += d->lm_rows) {
-      const int rows = M - r0 < d->lm_rows ? M - r0 : d->lm_rows;
-      GemvW16Args a{d->h + (size_t)r0 * E, E, d->lm, nullptr, nullptr, d->logits, V, rows, E, V};
-      EC_LAUNCH("gemv_w16_lmhead", gemv_w16_bytes(rows, E, V, false, EPI_STORE), gemv_w16(a, EPI_STORE, bf16, s));
-      if (argmax)
+  // final norm fused into the LM head (always fp16/bf16, src/gpt2.c:576-580 / 799-804);
+  // greedy ids from per-block argmax candidates
+  const int lwt = bf16 ? WT_BF16 : WT_F16;
+  for (int r0 = lm_from; r0 < M; r0 += d->lm_rows) {
+    const int rows = M - r0 < d->lm_rows ? M - r0 : d->lm_rows;
+    GemvArgs a{d->x + (size_t)r0 * E, E, nullptr, g->lnf_g, g->lnf_b, g->eps, d->lm, nullptr, nullptr, nullptr,
+               nullptr, d->logits, V, rows, E, V, nullptr};
+    const bool fused = gemv_vector_ok(a, lwt, pro_norm);
+    if (argmax && fused) a.cand = d->cand;
+    if ((r = linear(g, d, "gemv_lmhead", a, lwt, EPI_STORE, pro_norm, s))) return r;
+    if (argmax) {
+      if (fused)
+        EC_LAUNCH("argmax", 8.0 * rows * gemv_grid_x(a, lwt, EPI_STORE),
+                  argmax_finalize(d->cand, gemv_grid_x(a, lwt, EPI_STORE), d->logits, V, rows,
+                                  d->d_amax + (r0 - lm_from), s));
+      else
         EC_LAUNCH("argmax", 4.0 * rows * V, argmax_rows(d->logits, rows, V, d->d_amax + (r0 - lm_from), s));
-      if (logits)
-        EC_HIP(hipMemcpyAsync(logits + (size_t)(r0 - lm_from) * V, d->logits, (size_t)rows * V * 4,
-                              hipMemcpyDeviceToHost, s));
     }
-    if (argmax)
-      EC_HIP(hipMemcpyAsync(argmax, d->d_amax, (size_t)(M - lm_from) * 4, hipMemcpyDeviceToHost, s));
+    if (logits)
+      EC_HIP(hipMemcpyAsync(logits + (size_t)(r0 - lm_from) * V, d->logits, (size_t)rows * V * 4,
+                            hipMemcpyDeviceToHost, s));
   }
+  if (argmax && lm_from < M)
+    EC_HIP(hipMemcpyAsync(argmax, d->d_amax, (size_t)(M - lm_from) * 4, hipMemcpyDeviceToHost, s));
   EC_HIP(hipStreamSynchronize(s));
   return 0;
 }

@@ -331,6 +331,13 @@ int ec_memset_dev(void *dst, int value, size_t bytes);
 int ec_prof_start(const char *filter);
 int ec_prof_stop(char *buf, int len);
 
+/* Elementwise device arithmetic on n elements of device memory, for checking
+ * it against the host: op 0 expf (the reference's expf), 1 SiLU
+ * (src/gpt2.c:587-590), 2 GELU (src/gpt2.c:393-396), 3 fp32 -> fp16 bits
+ * (round to nearest even), 4 fp16 bits -> fp32, 5 int8 quantization with
+ * scale 1 (src/gpt2.c:456-459).  fp32 in/out except as noted.  0 or <0. */
+int ec_device_math(int op, const void *in, void *out, size_t n);
+
 /* int8 weight packing of edgecore/ecm.py:50-59 (float64 max|w|/127, zero row
  * -> scale 1, round half to even, clip), used by the synthetic generator. */
 void ec_quantize_int8_symmetric(const float *w, int rows, int cols, int8_t *q, float *scales);

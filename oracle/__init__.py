@@ -53,6 +53,7 @@ def olib() -> C.CDLL:
             "or_forward": (_I, [_P, _P, _P, _P, _I, _P]),
             "or_argmax": (_I, [_P, _I]),
             "or_generate": (_I, [_P, _P, _I, _I, _P, _P]),
+            "or_map": (None, [_I, _P, _P, C.c_size_t]),
         }
         for k, (r, a) in sig.items():
             f = getattr(L, k)
@@ -143,6 +144,14 @@ def quantize_int8_symmetric(w) -> tuple[np.ndarray, np.ndarray]:
     s = np.empty(r, np.float32)
     olib().or_quantize_int8_symmetric(_p(w), r, c, _p(q), _p(s))
     return q, s
+
+
+def map_op(op: int, x: np.ndarray) -> np.ndarray:
+    """Reference elementwise arithmetic (op codes of ec_device_math)."""
+    x = np.ascontiguousarray(x)
+    out = np.empty(x.shape, {3: np.uint16, 5: np.int8}.get(op, np.float32))
+    olib().or_map(op, _p(x), _p(out), x.size)
+    return out
 
 
 def f32_to_f16(x) -> np.ndarray:

@@ -379,6 +379,32 @@ void or_rope_inv_freq(double *inv_freq, int half, double theta, int yarn,
     }
 }
 
+/* Elementwise reference arithmetic over arrays, op codes as ec_device_math:
+ * 0 expf, 1 SiLU, 2 GELU, 3 fp32 -> fp16 bits, 4 fp16 bits -> fp32,
+ * 5 lrintf quantization with scale 1 clamped to [-128, 127]. */
+void or_map(int op, const void *in, void *out, size_t n)
+{
+    for (size_t i = 0; i < n; i++) {
+        if (op == 4) {
+            ((float *)out)[i] = or_f16_to_f32(((const uint16_t *)in)[i]);
+            continue;
+        }
+        const float x = ((const float *)in)[i];
+        switch (op) {
+        case 0: ((float *)out)[i] = expf(x); break;
+        case 1: ((float *)out)[i] = or_silu(x); break;
+        case 2: ((float *)out)[i] = or_gelu_new(x); break;
+        case 3: ((uint16_t *)out)[i] = or_f32_to_f16(x); break;
+        case 5: {
+            long v = lrintf(x);
+            ((int8_t *)out)[i] = (int8_t)(v > 127 ? 127 : v < -128 ? -128 : v);
+            break;
+        }
+        default: break;
+        }
+    }
+}
+
 /* ------------------------------------------------------------------ */
 /* model                                                                */
 /* ------------------------------------------------------------------ */

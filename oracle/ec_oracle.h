@@ -55,6 +55,10 @@ float or_silu(float x);
 void  or_rope_inv_freq(double *inv_freq, int half, double theta, int yarn,
                        double yarn_factor, double yarn_orig_max);
 
+/* ---- elementwise reference arithmetic over arrays (op codes of
+ * ec_device_math in the library header) ---- */
+void or_map(int op, const void *in, void *out, size_t n);
+
 /* ---- whole model (src/gpt2.c:161-366 load, 470-805 forward) ---- */
 typedef struct OrModel OrModel;
 

@@ -43,6 +43,8 @@ struct GemvArgs {
   int ldo;
   int M, K, N;
   unsigned long long *cand;  // EPI_STORE: [M][gridDim.x] argmax candidate keys, or null
+  const float *in_max;  // PRO_QUANT: precomputed max |A[m][:]| per row (skips the reduction), or null
+  float *out_max;       // EPI_SWIGLU: atomic max |out[m][:]| per row (zeroed beforehand), or null
 };
 
 // Weight types
@@ -77,9 +79,11 @@ hipError_t norm_rows(const float *x, int M, int E, const float *gamma, const flo
                      double eps, float *h, int ldh, int8_t *q, int ldq, float *qs,
                      hipStream_t st);
 
-// x[m][:] = wte[tok[m]] (+ wpe[pos[m]])
+// x[m][:] = wte[tok[m]] (+ wpe[pos[m]]); also zeroes the per-row maxima
+// slots[j*ld + m], j < nslots, that later kernels of the forward accumulate
 hipError_t embed(const uint16_t *wte, const uint16_t *wpe, bool bf16, const int *tok,
-                 const int *pos, int M, int E, float *x, hipStream_t st);
+                 const int *pos, int M, int E, float *x, float *slots, int nslots, int ld,
+                 hipStream_t st);
 
 // Qwen2: rotate q heads and k heads of each token in place (rotate-half, double
 // cos/sin table cs[pos][half] as (cos, sin) pairs), then append k and v to the
@@ -100,7 +104,10 @@ struct KvArgs {
 hipError_t rope_kv_append(const KvArgs &a, hipStream_t st);
 
 // causal attention over the fp16 cache for every (head, token), in the
-// reference's arithmetic order (see kernels.hip)
+// reference's arithmetic order (see kernels.hip).  With `cs`/`fuse_kv` set it
+// also applies RoPE to q and to the token's new k and appends k and v to the
+// cache (decode batches whose tokens use distinct slots); otherwise q is
+// already rotated and the cache already holds the new position.
 struct AttnArgs {
   const float *q;
   int ldq;
@@ -113,6 +120,14 @@ struct AttnArgs {
   int M;
   int max_npos;  // upper bound of pos+1 over the batch (sizes the LDS score array)
   int vtile;     // V positions staged in LDS per tile (multiple of 8)
+  // fused RoPE + KV append
+  int fuse_kv;
+  const float *k, *v;  // token rows of the new k / v (row stride ldk)
+  int ldk;
+  const double2 *cs;   // RoPE table [pos][half] or null (GPT-2)
+  int half;
+  uint16_t *kc_w, *vc_w;  // writable views of kc / vc for the append
+  float *out_max;  // atomic max |out[m][:]| per token row (zeroed beforehand), or null
 };
 hipError_t attention(const AttnArgs &a, hipStream_t st);
 size_t attention_lds_bytes(int max_npos, int hd, int vtile);

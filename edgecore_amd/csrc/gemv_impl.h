@@ -57,8 +57,9 @@ constexpr int kStrips = 8;  // activation strips of 256 kept in registers by the
 // scratch); longer rows re-read the remaining strips from global memory.
 template <int PRO, bool Q8>
 __device__ __forceinline__ void prologue_row(const float *row, int K, int Kp, const float *gamma,
-                                             const float *beta, double eps, int8_t *xq, float *xf,
-                                             float *xs, double *redd, float *redf) {
+                                             const float *beta, double eps, const float *rowmax,
+                                             int8_t *xq, float *xf, float *xs, double *redd,
+                                             float *redf) {
   const int t = threadIdx.x;
   const int nstrip = (K + 255) >> 8;
   float v[kStrips];
@@ -121,19 +122,23 @@ __device__ __forceinline__ void prologue_row(const float *row, int K, int Kp, co
   };
   if constexpr (Q8) {
     float mx = 0.0f;
+    if (PRO == PRO_QUANT && rowmax) {
+      mx = *rowmax;  // max |row| published by the producing kernel
+    } else {
 #pragma unroll
-    for (int j = 0; j < kStrips; j++) {
-      const int i = t + 256 * j;
-      if (i < K) {
-        v[j] = normed(v[j], i);
-        mx = fmaxf(mx, fabsf(v[j]));
+      for (int j = 0; j < kStrips; j++) {
+        const int i = t + 256 * j;
+        if (i < K) {
+          v[j] = normed(v[j], i);
+          mx = fmaxf(mx, fabsf(v[j]));
+        }
       }
+      for (int j = kStrips; j < nstrip; j++) {
+        const int i = t + 256 * j;
+        if (i < K) mx = fmaxf(mx, fabsf(normed(row[i], i)));
+      }
+      mx = block_max256(mx, redf);
     }
-    for (int j = kStrips; j < nstrip; j++) {
-      const int i = t + 256 * j;
-      if (i < K) mx = fmaxf(mx, fabsf(normed(row[i], i)));
-    }
-    mx = block_max256(mx, redf);
     const float sc = quant_scale(mx);
 #pragma unroll
     for (int j = 0; j < kStrips; j++) {
@@ -218,15 +223,19 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   } else if constexpr (PRO != PRO_F32) {
     for (int m = 0; m < mc; m++) {
       const float *row = reinterpret_cast<const float *>(a.A) + (size_t)(m0 + m) * a.lda;
-      prologue_row<PRO, Q8>(row, K, Kp, a.gamma, a.beta, a.eps, xq + (size_t)m * Kp,
-                            xf + (size_t)m * Kp, xs + m, redd, redf);
+      prologue_row<PRO, Q8>(row, K, Kp, a.gamma, a.beta, a.eps, a.in_max ? a.in_max + m0 + m : nullptr,
+                            xq + (size_t)m * Kp, xf + (size_t)m * Kp, xs + m, redd, redf);
     }
   }
   __syncthreads();
 
   unsigned long long best[MT];
+  float omax[MT];
 #pragma unroll
-  for (int m = 0; m < MT; m++) best[m] = 0ull;
+  for (int m = 0; m < MT; m++) {
+    best[m] = 0ull;
+    omax[m] = 0.0f;
+  }
 
   for (; rg < ngroups; rg += gridDim.x) {
     const int n = rg * RPB + rib;
@@ -315,8 +324,13 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
       __syncthreads();
       if (sub == 0 && valid && part == 0) {
 #pragma unroll
-        for (int m = 0; m < MT; m++)
-          if (m < mc) a.out[(size_t)(m0 + m) * a.ldo + n] = silu(vals[m]) * upx[m][rib];
+        for (int m = 0; m < MT; m++) {
+          if (m < mc) {
+            const float r = silu(vals[m]) * upx[m][rib];
+            a.out[(size_t)(m0 + m) * a.ldo + n] = r;
+            omax[m] = fmaxf(omax[m], fabsf(r));
+          }
+        }
       }
       __syncthreads();
     } else {
@@ -343,6 +357,16 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     }
   }
 
+  if constexpr (SWI) {
+    if (a.out_max) {  // row max |out| for the next linear's quantization
+#pragma unroll
+      for (int m = 0; m < MT; m++) {
+        const float r = block_max256(omax[m], redf);
+        if (threadIdx.x == 0 && m < mc)
+          atomicMax(reinterpret_cast<unsigned int *>(a.out_max + m0 + m), __float_as_uint(r));
+      }
+    }
+  }
   if constexpr (EPI == EPI_STORE) {
     if (a.cand) {  // one argmax candidate per (row, block)
 #pragma unroll

@@ -129,8 +129,10 @@ __global__ __launch_bounds__(256) void norm_kernel(const float *x, int E, const 
 template <bool BF16>
 __global__ __launch_bounds__(256) void embed_kernel(const uint16_t *wte, const uint16_t *wpe,
                                                     const int *tok, const int *pos, int E,
-                                                    float *x) {
+                                                    float *x, float *slots, int nslots, int ld) {
   const int m = blockIdx.x;
+  if (slots)
+    for (int j = threadIdx.x; j < nslots; j += 256) slots[(size_t)j * ld + m] = 0.0f;
   const uint16_t *et = wte + (size_t)tok[m] * E;
   const uint16_t *ep = wpe ? wpe + (size_t)pos[m] * E : nullptr;
   for (int d = threadIdx.x; d < E; d += 256) {
@@ -184,12 +186,47 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(KvArgs a) {
 // into different activation codes downstream, so the order is kept exactly.
 // The V rows of the attended positions are staged into LDS (tiles of vtile
 // positions) with loads issued before the scores, so the sequential sums read
-// LDS instead of waiting on memory latency.
+// LDS instead of waiting on memory.  HD > 0 fixes head_dim at compile time
+// (whole K rows are loaded before each dot); HD == 0 is the generic path.
+//
+// FUSED: the block also rotates its q head and the token's new k (RoPE,
+// src/gpt2.c:656-665, double cos/sin table) and uses the new k and v rounded
+// to fp16 for the token's own position; the first query head of each KV group
+// appends them to the cache (src/gpt2.c:726-741).  Only valid when no other
+// token of the launch reads this token's slot.
+template <int HD>
+__device__ __forceinline__ float dot_k_row(const float *qs, const uint16_t *kp, int hd) {
+  float s = 0.0f;
+  if constexpr (HD > 0) {
+    v4u kk[HD / 8];
+#pragma unroll
+    for (int c = 0; c < HD / 8; c++) kk[c] = *reinterpret_cast<const v4u *>(kp + 8 * c);
+#pragma unroll
+    for (int c = 0; c < HD / 8; c++) {
+      const uint32_t wv[4] = {kk[c].x, kk[c].y, kk[c].z, kk[c].w};
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const float p0 = qs[8 * c + 2 * j] * h2f((uint16_t)(wv[j] & 0xffffu));
+        s = s + p0;
+        const float p1 = qs[8 * c + 2 * j + 1] * h2f((uint16_t)(wv[j] >> 16));
+        s = s + p1;
+      }
+    }
+  } else {
+    for (int d = 0; d < hd; d++) {
+      const float p0 = qs[d] * h2f(kp[d]);
+      s = s + p0;
+    }
+  }
+  return s;
+}
+
+template <int HD, bool FUSED>
 __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   extern __shared__ __attribute__((aligned(16))) float lds[];
   __shared__ float redf[4];
   __shared__ double redd[4];
-  const int h = blockIdx.x, m = blockIdx.y;
+  const int h = blockIdx.x, m = blockIdx.y, t = threadIdx.x;
   const int pos = a.pos[m], slot = a.slot[m];
   const int kvh = h * a.KVH / a.H;
   int lo = 0;
@@ -198,58 +235,88 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     if (lo < 0) lo = 0;
   }
   const int n = pos + 1 - lo;
-  const int hd = a.hd, T = a.vtile;
+  const int hd = HD > 0 ? HD : a.hd, T = a.vtile;
+  const int hdp = (hd + 3) & ~3;
   float *qs = lds;
-  float *sc = lds + ((hd + 3) & ~3);
+  float *kn = qs + hdp;  // FUSED: the new k (fp16-rounded), fp32
+  float *sc = kn + (FUSED ? hdp : 0);
   uint16_t *vt = reinterpret_cast<uint16_t *>(sc + ((a.max_npos + 3) & ~3));
-  const float *q = a.q + (size_t)m * a.ldq + (size_t)h * hd;
   const size_t cbase = (size_t)slot * a.C * a.kv + (size_t)kvh * hd;
   const uint16_t *K = a.kc + cbase + (size_t)lo * a.kv;
   const uint16_t *V = a.vc + cbase + (size_t)lo * a.kv;
   const bool vec = (hd & 7) == 0 && (a.kv & 7) == 0;
+  const int ncache = FUSED ? n - 1 : n;  // positions read from the cache
 
-  auto stage_v = [&](int t0) {  // V rows [t0, t0 + T) of the attended range -> vt
-    const int cnt = min(T, n - t0);
+  auto stage_v = [&](int t0) {  // cached V rows [t0, t0 + T) of the attended range -> vt
+    const int cnt = min(T, ncache - t0);
+    if (cnt <= 0) return;
     if (vec) {
       const int cpr = hd >> 3;
-      for (int c = threadIdx.x; c < cnt * cpr; c += 256) {
+      for (int c = t; c < cnt * cpr; c += 256) {
         const int i = c / cpr, j = (c - i * cpr) << 3;
-        *reinterpret_cast<v4u *>(vt + i * hd + j) =
-            *reinterpret_cast<const v4u *>(V + (size_t)(t0 + i) * a.kv + j);
+        *reinterpret_cast<v4u *>(vt + i * hd + j) = *reinterpret_cast<const v4u *>(V + (size_t)(t0 + i) * a.kv + j);
       }
     } else {
-      for (int c = threadIdx.x; c < cnt * hd; c += 256) {
+      for (int c = t; c < cnt * hd; c += 256) {
         const int i = c / hd, j = c - i * hd;
         vt[i * hd + j] = V[(size_t)(t0 + i) * a.kv + j];
       }
     }
   };
 
-  for (int d = threadIdx.x; d < hd; d += 256) qs[d] = q[d];
+  const float *qrow = a.q + (size_t)m * a.ldq + (size_t)h * hd;
+  if constexpr (FUSED) {
+    const float *krow = a.k + (size_t)m * a.ldk + (size_t)kvh * hd;
+    const float *vrow = a.v + (size_t)m * a.ldk + (size_t)kvh * hd;
+    const bool writer = h == 0 || (h - 1) * a.KVH / a.H != kvh;  // first query head of the group
+    const size_t woff = ((size_t)slot * a.C + pos) * a.kv + (size_t)kvh * hd;
+    const int rot = a.cs ? a.half : 0;
+    const double2 *cs = a.cs ? a.cs + (size_t)pos * a.half : nullptr;
+    for (int i = t; i < hd; i += 256) {
+      float qv, kvv;
+      if (i < rot || (i >= rot && i < 2 * rot)) {
+        const int i0 = i < rot ? i : i - rot;
+        const double c = cs[i0].x, sn = cs[i0].y;
+        const float q0 = qrow[i0], q1 = qrow[i0 + rot], k0 = krow[i0], k1 = krow[i0 + rot];
+        if (i < rot) {
+          const double t1 = q0 * c, t2 = q1 * sn, u1 = k0 * c, u2 = k1 * sn;
+          qv = (float)(t1 - t2);
+          kvv = (float)(u1 - u2);
+        } else {
+          const double t3 = q0 * sn, t4 = q1 * c, u3 = k0 * sn, u4 = k1 * c;
+          qv = (float)(t3 + t4);
+          kvv = (float)(u3 + u4);
+        }
+      } else {
+        qv = qrow[i];
+        kvv = krow[i];
+      }
+      qs[i] = qv;
+      const uint16_t kh = f2h(kvv), vh = f2h(vrow[i]);
+      kn[i] = h2f(kh);
+      if (n - 1 < T) vt[(n - 1) * hd + i] = vh;  // own position lands in the first V tile
+      if (writer) {
+        a.kc_w[woff + i] = kh;
+        a.vc_w[woff + i] = vh;
+      }
+    }
+  } else {
+    for (int d = t; d < hd; d += 256) qs[d] = qrow[d];
+  }
   stage_v(0);
   __syncthreads();
 
   float mx = -FLT_MAX;
-  for (int i = threadIdx.x; i < n; i += 256) {
-    const uint16_t *kp = K + (size_t)i * a.kv;
-    float s = 0.0f;
-    if (vec) {
-      for (int d = 0; d < hd; d += 8) {
-        const v4u kk = *reinterpret_cast<const v4u *>(kp + d);
-        const uint32_t wv[4] = {kk.x, kk.y, kk.z, kk.w};
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-          const float p0 = qs[d + 2 * j] * h2f((uint16_t)(wv[j] & 0xffffu));
-          s = s + p0;
-          const float p1 = qs[d + 2 * j + 1] * h2f((uint16_t)(wv[j] >> 16));
-          s = s + p1;
-        }
-      }
-    } else {
+  for (int i = t; i < n; i += 256) {
+    float s;
+    if (FUSED && i == n - 1) {
+      s = 0.0f;
       for (int d = 0; d < hd; d++) {
-        const float p0 = qs[d] * h2f(kp[d]);
+        const float p0 = qs[d] * kn[d];
         s = s + p0;
       }
+    } else {
+      s = dot_k_row<HD>(qs, K + (size_t)i * a.kv, hd);
     }
     s = (float)((double)s * a.inv_hd);
     sc[i] = s;
@@ -257,14 +324,14 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   }
   mx = block_max256(mx, redf);
   double sum = 0.0;
-  for (int i = threadIdx.x; i < n; i += 256) {
+  for (int i = t; i < n; i += 256) {
     const float e = ec_expf_ref(sc[i] - mx);
     sc[i] = e;
     sum += (double)e;
   }
   sum = block_sum256(sum, redd);
   const double isum = 1.0 / sum;
-  for (int i = threadIdx.x; i < n; i += 256) sc[i] = (float)((double)sc[i] * isum);
+  for (int i = t; i < n; i += 256) sc[i] = (float)((double)sc[i] * isum);
   __syncthreads();
 
   float o = 0.0f;
@@ -272,11 +339,17 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     if (t0) {
       __syncthreads();
       stage_v(t0);
+      if constexpr (FUSED) {
+        if (n - 1 >= t0 && n - 1 < t0 + T) {  // own position lands in this tile
+          const float *vrow = a.v + (size_t)m * a.ldk + (size_t)kvh * hd;
+          for (int i = t; i < hd; i += 256) vt[(n - 1 - t0) * hd + i] = f2h(vrow[i]);
+        }
+      }
       __syncthreads();
     }
-    if ((int)threadIdx.x < hd) {
+    if (t < hd) {
       const int cnt = min(T, n - t0);
-      const uint16_t *vc = vt + threadIdx.x;
+      const uint16_t *vc = vt + t;
       const float *pp = sc + t0;
       int i = 0;
       for (; i + 8 <= cnt; i += 8) {
@@ -298,7 +371,11 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
       }
     }
   }
-  if ((int)threadIdx.x < hd) a.out[(size_t)m * a.ldo + (size_t)h * hd + threadIdx.x] = o;
+  if (t < hd) a.out[(size_t)m * a.ldo + (size_t)h * hd + t] = o;
+  if (a.out_max) {  // row max |out| for the next linear's int8 quantization (NaN ignored)
+    const float r = block_max256(t < hd ? fabsf(o) : 0.0f, redf);
+    if (t == 0) atomicMax(reinterpret_cast<unsigned int *>(a.out_max + m), __float_as_uint(r));
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -496,9 +573,12 @@ hipError_t norm_rows(const float *x, int M, int E, const float *gamma, const flo
 }
 
 hipError_t embed(const uint16_t *wte, const uint16_t *wpe, bool bf16, const int *tok,
-                 const int *pos, int M, int E, float *x, hipStream_t st) {
-  if (bf16) hipLaunchKernelGGL(embed_kernel<true>, dim3(M), dim3(256), 0, st, wte, wpe, tok, pos, E, x);
-  else hipLaunchKernelGGL(embed_kernel<false>, dim3(M), dim3(256), 0, st, wte, wpe, tok, pos, E, x);
+                 const int *pos, int M, int E, float *x, float *slots, int nslots, int ld,
+                 hipStream_t st) {
+  if (bf16)
+    hipLaunchKernelGGL(embed_kernel<true>, dim3(M), dim3(256), 0, st, wte, wpe, tok, pos, E, x, slots, nslots, ld);
+  else
+    hipLaunchKernelGGL(embed_kernel<false>, dim3(M), dim3(256), 0, st, wte, wpe, tok, pos, E, x, slots, nslots, ld);
   return hipGetLastError();
 }
 
@@ -512,9 +592,20 @@ size_t attention_lds_bytes(int max_npos, int hd, int vtile) {
          (size_t)vtile * hd * sizeof(uint16_t);
 }
 
+template <int HD>
+static void launch_attn(const AttnArgs &a, size_t lds, hipStream_t st) {
+  if (a.fuse_kv) hipLaunchKernelGGL((attn_kernel<HD, true>), dim3(a.H, a.M), dim3(256), lds, st, a);
+  else hipLaunchKernelGGL((attn_kernel<HD, false>), dim3(a.H, a.M), dim3(256), lds, st, a);
+}
+
 hipError_t attention(const AttnArgs &a, hipStream_t st) {
-  const size_t lds = attention_lds_bytes(a.max_npos, a.hd, a.vtile);
-  hipLaunchKernelGGL(attn_kernel, dim3(a.H, a.M), dim3(256), lds, st, a);
+  const size_t lds = attention_lds_bytes(a.max_npos, a.hd, a.vtile) +
+                     (a.fuse_kv ? (size_t)((a.hd + 3) & ~3) * sizeof(float) : 0);
+  const bool vec = (a.kv & 7) == 0;
+  if (vec && a.hd == 64) launch_attn<64>(a, lds, st);
+  else if (vec && a.hd == 128) launch_attn<128>(a, lds, st);
+  else if (vec && a.hd == 32) launch_attn<32>(a, lds, st);
+  else launch_attn<0>(a, lds, st);
   return hipGetLastError();
 }
 

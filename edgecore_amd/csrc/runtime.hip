@@ -429,6 +429,7 @@ struct DevModel {
   const uint16_t *lm = nullptr;
   unsigned long long *cand = nullptr;  // LM-head argmax candidates [lm_rows][gemv blocks]
   int ncand = 0;
+  float *rowmax = nullptr;  // [2 * n_layer][mmax]: max |attention out| and |SwiGLU out| per token
 };
 
 // V positions staged per attention tile (LDS: 64 KB at head_dim 64)
@@ -477,7 +478,7 @@ struct Loader {
 static void free_dev(DevModel *d) {
   if (!d) return;
   void *ps[] = {d->arena, d->rope, d->d_tok, d->d_pos, d->d_slot, d->d_amax, d->x, d->h, d->qkv,
-                d->att, d->ff, d->aq, d->as, d->logits, d->kc, d->vc, d->cand};
+                d->att, d->ff, d->aq, d->as, d->logits, d->kc, d->vc, d->cand, d->rowmax};
   for (void *p : ps)
     if (p) (void)hipFree(p);
   if (d->h_stage) (void)hipHostFree(d->h_stage);
@@ -735,6 +736,7 @@ static int load_impl(GPT2 *g, const char *path, int batch_cap, int max_ctx) {
   EC_HIP(hipMalloc(&d->d_slot, (size_t)mmax * 4));
   EC_HIP(hipMalloc(&d->d_amax, (size_t)mmax * 4));
   EC_HIP(hipHostMalloc((void **)&d->h_stage, (size_t)mmax * 3 * 4, hipHostMallocDefault));
+  EC_HIP(hipMalloc(&d->rowmax, (size_t)2 * Lc * mmax * sizeof(float)));
   d->ncand = gemv_max_blocks();
   EC_HIP(hipMalloc(&d->cand, (size_t)d->lm_rows * d->ncand * sizeof(unsigned long long)));
   g->ws_x = d->x;
@@ -841,7 +843,7 @@ static int forward_impl(GPT2 *g, const int *tokens, const int *positions, const 
   }
   // attention LDS: scores for max_npos positions + a tile of V rows
   if (hd > 256) return set_err(-1, "head_dim %d above 256 is not supported", hd);
-  const size_t lds_fixed = attention_lds_bytes(max_npos, hd, 0);
+  const size_t lds_fixed = attention_lds_bytes(max_npos, hd, 0) + (size_t)((hd + 3) & ~3) * sizeof(float);
   int vtile = 0;
   if (lds_fixed < (size_t)g_max_lds) {
     const size_t room = ((size_t)g_max_lds - lds_fixed) / ((size_t)hd * sizeof(uint16_t));
@@ -856,7 +858,17 @@ static int forward_impl(GPT2 *g, const int *tokens, const int *positions, const 
   EC_HIP(hipMemcpyAsync(d->d_pos, st + d->mmax, (size_t)M * 4, hipMemcpyHostToDevice, s));
   EC_HIP(hipMemcpyAsync(d->d_slot, st + 2 * d->mmax, (size_t)M * 4, hipMemcpyHostToDevice, s));
 
-  EC_LAUNCH("embed", (double)M * E * (g->wpe ? 8 : 6), embed(g->wte, g->wpe, bf16, d->d_tok, d->d_pos, M, E, d->x, s));
+  EC_LAUNCH("embed", (double)M * E * (g->wpe ? 8 : 6),
+            embed(g->wte, g->wpe, bf16, d->d_tok, d->d_pos, M, E, d->x, d->rowmax, 2 * g->n_layer, d->mmax, s));
+  // RoPE and the KV append run inside attention when no token of the batch
+  // reads another token's slot (decode); otherwise as their own kernel first
+  bool distinct = true;
+  for (int m = 0; m < M && distinct; m++)
+    for (int j = 0; j < m; j++)
+      if (st[2 * d->mmax + j] == st[2 * d->mmax + m]) {
+        distinct = false;
+        break;
+      }
 
   const int F = d->F, ldq = d->qkv_ld;
   const int nqkv = qwen ? E + 2 * kv : 3 * E;
@@ -873,25 +885,30 @@ static int forward_impl(GPT2 *g, const int *tokens, const int *positions, const 
       const int epi = (!i8 && W.bqkv) ? EPI_BIAS : EPI_STORE;
       if ((r = linear(g, d, "gemv_qkv", a, wt, epi, pro_norm, s))) return r;
     }
-    // RoPE (Qwen2) + fp16 KV append
-    KvArgs ka{d->qkv, d->qkv + E, d->qkv + E + (qwen ? kv : E), ldq, ldq, H, g->n_kv_head, hd, kv,
-              qwen ? d->rope : nullptr, d->half, d->d_pos, d->d_slot, kcl, vcl, d->eff_ctx, M};
-    EC_LAUNCH("rope_kv", (double)M * (qwen ? (E + kv) * 8 + kv * 8 : kv * 12), rope_kv_append(ka, s));
-    // attention
+    float *att_max = i8 ? d->rowmax + (size_t)(2 * l) * d->mmax : nullptr;
+    float *ff_max = (i8 && qwen) ? d->rowmax + (size_t)(2 * l + 1) * d->mmax : nullptr;
+    float *kq = d->qkv + E, *vq = d->qkv + E + (qwen ? kv : E);
+    if (!distinct) {  // RoPE (Qwen2) + fp16 KV append
+      KvArgs ka{d->qkv, kq, vq, ldq, ldq, H, g->n_kv_head, hd, kv, qwen ? d->rope : nullptr, d->half,
+                d->d_pos, d->d_slot, kcl, vcl, d->eff_ctx, M};
+      EC_LAUNCH("rope_kv", (double)M * (qwen ? (E + kv) * 8 + kv * 8 : kv * 12), rope_kv_append(ka, s));
+    }
     AttnArgs aa{d->qkv, ldq, kcl, vcl, d->att, E, d->d_pos, d->d_slot, H, g->n_kv_head, hd, kv,
-                d->eff_ctx, qwen ? g->sliding_window : 0, 1.0 / sqrt((double)hd), M, max_npos, vtile};
+                d->eff_ctx, qwen ? g->sliding_window : 0, 1.0 / sqrt((double)hd), M, max_npos, vtile,
+                distinct ? 1 : 0, kq, vq, ldq, (distinct && qwen) ? d->rope : nullptr, d->half, kcl, vcl,
+                att_max};
     EC_LAUNCH("attention", abytes, attention(aa, s));
     // output projection + residual
     {
       GemvArgs a{d->att, E, nullptr, nullptr, nullptr, 0.0, W.wo, nullptr, W.so, nullptr, W.bo, d->x, E, M, E, E,
-                 nullptr};
+                 nullptr, att_max, nullptr};
       const int epi = i8 ? EPI_RESID : (W.bo ? EPI_BIAS_RESID : EPI_RESID);
       if ((r = linear(g, d, "gemv_o", a, wt, epi, i8 ? PRO_QUANT : PRO_F32, s))) return r;
     }
     // MLP up: SwiGLU gate/up (Qwen2) or fc + GELU (GPT-2), norm fused
     if (qwen) {
       GemvArgs a{d->x, E, nullptr, W.ln2_g, nullptr, g->eps, W.wg, W.wu, W.sg, W.su, nullptr, d->ff, F, M, E, F,
-                 nullptr};
+                 nullptr, nullptr, ff_max};
       if ((r = linear(g, d, "gemv_gateup", a, wt, EPI_SWIGLU, PRO_RMS, s))) return r;
     } else {
       GemvArgs a{d->x, E, nullptr, W.ln2_g, W.ln2_b, g->eps, W.wfc, nullptr, W.sfc, nullptr, W.bfc, d->ff, F, M,
@@ -901,7 +918,7 @@ static int forward_impl(GPT2 *g, const int *tokens, const int *positions, const 
     // MLP down + residual
     {
       GemvArgs a{d->ff, F, nullptr, nullptr, nullptr, 0.0, W.wd, nullptr, W.sd, nullptr, W.bd, d->x, E, M, F, E,
-                 nullptr};
+                 nullptr, ff_max, nullptr};
       const int epi = i8 ? EPI_RESID : (W.bd ? EPI_BIAS_RESID : EPI_RESID);
       if ((r = linear(g, d, "gemv_down", a, wt, epi, i8 ? PRO_QUANT : PRO_F32, s))) return r;
     }

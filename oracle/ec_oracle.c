@@ -12,12 +12,15 @@
  *   or_f32_to_f16 / or_f16_to_f32 : exhaustive vs the host F16C instruction
  *                                   (or_check_f16c below) + the reference build
  *   or_quantize_int8_symmetric     : closed-form special cases (zero row,
- *                                   +-maxabs, exact .5 ties) + the sha256 of the
- *                                   reference's shipped tiny-gpt2-int8.ecm
+ *                                   +-maxabs, exact .5 ties); the reference's
+ *                                   generator sits behind numpy, so this packer
+ *                                   is also cross-checked against the
+ *                                   library's independent C packer
  *   or_quantize_rows               : closed-form ties / clamp cases + the
  *                                   reference build (through gpt2_forward)
  *   or_gemm_int8                   : brute-force int64 dot + adversarial
  *                                   (-128/127) rows + reference build vectors
+ *                                   (tests/golden/kernels.npz)
  *   or_gemm_fp16_fp32 / bf16       : float64 brute force within gamma_K bound +
  *                                   bit-exact vs the reference build vectors
  *   norms, RoPE, attention, GELU,  : closed forms (constant row, pos 0 identity,

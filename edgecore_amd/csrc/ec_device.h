@@ -37,9 +37,10 @@ __device__ __forceinline__ float w2f(uint16_t w) {
   if constexpr (BF16) return b2f(w); else return h2f(w);
 }
 
-// src/gpt2.c:587-590, with the reference's expf (ec_expf.h)
-__device__ __forceinline__ float silu(float x) {
-  float e = ec_expf_ref(-x);
+// src/gpt2.c:587-590, with the reference's expf (ec_expf.h); tab is the
+// 2^(i/32) table (ec_exp2_32 or a copy of it in LDS)
+__device__ __forceinline__ float silu(float x, const uint64_t *tab = ec_exp2_32) {
+  float e = ec_expf_tab(-x, tab);
   float den = 1.0f + e;
   return x / den;
 }
@@ -52,6 +53,14 @@ __device__ __forceinline__ float gelu_new(float x) {
   float t = (float)tanh((double)u);
   float hx = 0.5f * x;
   return hx * (1.0f + t);
+}
+
+// Load of a value that is uniform across the block and not written while the
+// kernel runs (positions, slots): through the constant address space, so the
+// compiler emits a scalar load that needs no vector-memory wait.
+template <typename T>
+__device__ __forceinline__ T ld_uniform(const T *p) {
+  return *(const __attribute__((address_space(4))) T *)(uintptr_t)p;
 }
 
 // ---- wave / block reductions (wave64) ----
@@ -83,6 +92,63 @@ __device__ __forceinline__ float block_max256(float v, float *red) {
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
   __syncthreads();
   if (l == 0) red[w] = v;
+  __syncthreads();
+  return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+// ---- DPP / readlane based reductions (every lane of the wave active) ----
+// dpp_mov<CTRL>(v): v of the lane that the DPP control CTRL names
+template <int CTRL, typename T>
+__device__ __forceinline__ T dpp_mov(T v) {
+  if constexpr (sizeof(T) == 8) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, 0xF, 0xF, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, 0xF, 0xF, false);
+    return __builtin_bit_cast(T, ((uint64_t)hi << 32) | lo);
+  } else {
+    return __builtin_bit_cast(T, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+  }
+}
+template <typename T>
+__device__ __forceinline__ T readlane(T v, int l) {
+  if constexpr (sizeof(T) == 8) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, l);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), l);
+    return __builtin_bit_cast(T, ((uint64_t)hi << 32) | lo);
+  } else {
+    return __builtin_bit_cast(T, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+  }
+}
+// sum over the wave: pairs, quads, rows of 8 and 16 by DPP, then the four
+// rows of 16 in the order (r0 + r1) + (r2 + r3).  Every lane gets the result.
+__device__ __forceinline__ double wave_sum_dpp(double v) {
+  v = v + dpp_mov<0xB1>(v);   // quad_perm [1,0,3,2]
+  v = v + dpp_mov<0x4E>(v);   // quad_perm [2,3,0,1]
+  v = v + dpp_mov<0x141>(v);  // row_half_mirror
+  v = v + dpp_mov<0x140>(v);  // row_mirror
+  return (readlane(v, 0) + readlane(v, 16)) + (readlane(v, 32) + readlane(v, 48));
+}
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  v = fmaxf(v, dpp_mov<0xB1>(v));
+  v = fmaxf(v, dpp_mov<0x4E>(v));
+  v = fmaxf(v, dpp_mov<0x141>(v));
+  v = fmaxf(v, dpp_mov<0x140>(v));
+  return fmaxf(fmaxf(readlane(v, 0), readlane(v, 16)), fmaxf(readlane(v, 32), readlane(v, 48)));
+}
+// Block reductions for blockDim.x == 256 with a single barrier.  `red` (4
+// slots) must not be written by another reduction until every thread has
+// passed one more barrier: callers alternate between slot sets or separate
+// reuses with a barrier.
+__device__ __forceinline__ double block_sum256_1b(double v, double *red) {
+  v = wave_sum_dpp(v);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return (red[0] + red[1]) + (red[2] + red[3]);
+}
+__device__ __forceinline__ float block_max256_1b(float v, float *red) {
+  v = wave_max_dpp(v);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
   __syncthreads();
   return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
 }

@@ -42,7 +42,9 @@ EC_EXPF_TABLE uint64_t ec_exp2_32[32] = {
     0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
 };
 
-EC_EXPF_FN float ec_expf_ref(float x)
+/* tab: the 32 entries of ec_exp2_32, wherever the caller keeps a copy
+ * (kernels stage them in LDS so the lookup does not wait on memory) */
+EC_EXPF_FN float ec_expf_tab(float x, const uint64_t *tab)
 {
     const double inv_ln2_n = 0x1.71547652b82fep+0 * 32.0;
     const double shift = 0x1.8p+52;
@@ -65,7 +67,7 @@ EC_EXPF_FN float ec_expf_ref(float x)
     memcpy(&ki, &kd, 8);
     kd -= shift;
     const double r = __builtin_fma(inv_ln2_n, xd, -kd);
-    uint64_t t = ec_exp2_32[ki % 32];
+    uint64_t t = tab[ki % 32];
     t += ki << 47;
     double s;
     memcpy(&s, &t, 8);
@@ -76,5 +78,7 @@ EC_EXPF_FN float ec_expf_ref(float x)
     y = y * s;
     return (float)y;
 }
+
+EC_EXPF_FN float ec_expf_ref(float x) { return ec_expf_tab(x, ec_exp2_32); }
 
 #endif

@@ -2,12 +2,29 @@
 // nothing: callers (runtime.hip) validate shapes and pointers first.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 #include <type_traits>
 
 namespace ec {
+
+// Per-launch timing: when a profiler sets g_launch_ev, the next kernel launch
+// records its own start and stop timestamps on these two events
+// (hipExtLaunchKernel, the dispatch packet's times) and clears them.  Every
+// kernel of the library is launched through klaunch.
+extern hipEvent_t g_launch_ev[2];
+template <typename F, typename... Args>
+inline void klaunch(F kernel, dim3 grid, dim3 block, uint32_t lds, hipStream_t s, Args... args) {
+  if (g_launch_ev[0]) {
+    hipEvent_t e0 = g_launch_ev[0], e1 = g_launch_ev[1];
+    g_launch_ev[0] = g_launch_ev[1] = nullptr;
+    hipExtLaunchKernelGGL(kernel, grid, block, lds, s, e0, e1, 0, args...);
+  } else {
+    hipLaunchKernelGGL(kernel, grid, block, lds, s, args...);
+  }
+}
 
 // GEMV/GEMM epilogues.  `out` has row stride ldo.
 enum Epi {
@@ -43,8 +60,6 @@ struct GemvArgs {
   int ldo;
   int M, K, N;
   unsigned long long *cand;  // EPI_STORE: [M][gridDim.x] argmax candidate keys, or null
-  const float *in_max;  // PRO_QUANT: precomputed max |A[m][:]| per row (skips the reduction), or null
-  float *out_max;       // EPI_SWIGLU: atomic max |out[m][:]| per row (zeroed beforehand), or null
 };
 
 // Weight types
@@ -63,6 +78,9 @@ hipError_t gemv_generic(const GemvArgs &a, int wt, int epi, hipStream_t s);
 // grid-size cap of the grid-stride GEMV (set from the CU count at init)
 void gemv_set_max_blocks(int n);
 int gemv_max_blocks();
+// row shape (GS_* of gemv_impl.h) and M tile of the fused kernel for a launch
+int gemv_pick_shape(int wt, int K);
+int gemv_pick_mt(int M);
 // LDS budget per block (device limit), checked by gemv_vector_ok
 void gemv_set_max_lds(int bytes);
 size_t gemv_lds_bytes(int wt, int pro, int MT, int K);
@@ -79,11 +97,9 @@ hipError_t norm_rows(const float *x, int M, int E, const float *gamma, const flo
                      double eps, float *h, int ldh, int8_t *q, int ldq, float *qs,
                      hipStream_t st);
 
-// x[m][:] = wte[tok[m]] (+ wpe[pos[m]]); also zeroes the per-row maxima
-// slots[j*ld + m], j < nslots, that later kernels of the forward accumulate
+// x[m][:] = wte[tok[m]] (+ wpe[pos[m]])
 hipError_t embed(const uint16_t *wte, const uint16_t *wpe, bool bf16, const int *tok,
-                 const int *pos, int M, int E, float *x, float *slots, int nslots, int ld,
-                 hipStream_t st);
+                 const int *pos, int M, int E, float *x, hipStream_t st);
 
 // Qwen2: rotate q heads and k heads of each token in place (rotate-half, double
 // cos/sin table cs[pos][half] as (cos, sin) pairs), then append k and v to the
@@ -119,7 +135,7 @@ struct AttnArgs {
   double inv_hd;
   int M;
   int max_npos;  // upper bound of pos+1 over the batch (sizes the LDS score array)
-  int vtile;     // V positions staged in LDS per tile (multiple of 8)
+  int vtile;     // positions per product tile in LDS (multiple of 4, <= attention_max_vtile)
   // fused RoPE + KV append
   int fuse_kv;
   const float *k, *v;  // token rows of the new k / v (row stride ldk)
@@ -127,10 +143,31 @@ struct AttnArgs {
   const double2 *cs;   // RoPE table [pos][half] or null (GPT-2)
   int half;
   uint16_t *kc_w, *vc_w;  // writable views of kc / vc for the append
-  float *out_max;  // atomic max |out[m][:]| per token row (zeroed beforehand), or null
 };
 hipError_t attention(const AttnArgs &a, hipStream_t st);
+// V units (4 positions x 8 elements) per thread held in registers
+constexpr int kAttnUnits = 4;
+// head_dim with the 16-byte-load kernel (else the generic one)
+__host__ __device__ inline bool attn_vec(int hd, int kv) {
+  return (kv & 7) == 0 && (hd == 32 || hd == 64 || hd == 128);
+}
+// Product tile layout: 16-byte slots (4 positions of one element) per quad
+// of positions, padded so that two (hd 64) or four (hd 32) quads written by
+// one 16-lane group start on different banks; the element index is swizzled
+// by d ^ ((d >> 4) & attn_swz) within its group of 16.  (kv is unused: the
+// layout depends on head_dim only.)
+__host__ __device__ inline int attn_pitch(int hd, int kv) {
+  (void)kv;
+  return (hd == 32 || hd == 64 || hd == 128) ? hd + (hd < 128 ? hd / 16 : 0) : hd;
+}
+__host__ __device__ inline int attn_swz(int hd, int kv) {
+  (void)kv;
+  return hd == 32 ? 1 : hd == 64 ? 3 : hd == 128 ? 7 : 0;
+}
+// dynamic LDS of a launch: q, new k, new v, max_npos scores, the product tile
 size_t attention_lds_bytes(int max_npos, int hd, int vtile);
+// largest vtile the kernel accepts for this head_dim / KV row length
+int attention_max_vtile(int hd, int kv);
 
 // greedy argmax per row (src/runtime_main.c:215-218 semantics)
 hipError_t argmax_rows(const float *logits, int rows, int V, int *out, hipStream_t st);

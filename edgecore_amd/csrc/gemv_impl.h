@@ -3,12 +3,18 @@
 //   out[m][n] = epilogue( dot( act[m][:], W[n][:] ) )       m < M (tiles of MT rows)
 //
 // Weights keep the reference layout [N][K] row-major (int8, fp16 or bf16).
-// A row is read by LPR lanes of a wave with 16-byte non-temporal loads: one
-// wave instruction covers 64/LPR rows x LPR*16 contiguous bytes.  A block of
-// 256 threads (4 waves) owns a "row group" of 4*64/LPR output rows (2*64/LPR
-// gate/up row pairs for SwiGLU) and walks the row groups grid-stride, so the
-// activation prologue runs once per block, and the first row group's weights
-// are already in flight (prefetched into registers) while it runs.
+// A row is read by LPR lanes of a wave, CPL 16-byte non-temporal loads per
+// lane per pass: one wave instruction covers 64/LPR rows x LPR*16 contiguous
+// bytes.  A block of 256 threads (4 waves) owns a "row group" of 4*64/LPR
+// output rows and walks the row groups grid-stride.  For SwiGLU a lane loads
+// the matching gate and up rows, so both halves meet in the same lane.
+//
+// Load order is what makes the kernel fast at decode sizes: the activation
+// row (and the norm weights) are loaded first, then the first row group's
+// weights, scales, bias and residual, all unconditionally (indices clamped
+// into range, results masked), so the hardware's in-order load counter lets
+// the prologue wait for the activation alone while the weight stream is in
+// flight.
 //
 // Prologues (activation side; every block computes it, which at decode sizes
 // is cheaper than another dependent launch):
@@ -48,142 +54,68 @@ __device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v)
   return v;
 }
 
-constexpr int lpr_cpl(int lpr) { return lpr == 64 ? 10 : 4; }
-constexpr int kStrips = 8;  // activation strips of 256 kept in registers by the prologue
+// Row shapes of the fused kernel: (lanes per row, 16-byte chunks per lane).
+// GS_NARROW: 4 rows per wave, rows up to 64 (int8) / 128 (16-bit) chunks;
+// GS_MID: one row per wave, up to 320 chunks in one pass; GS_WIDE: one row
+// per wave, 640 chunks per pass, any K.
+enum { GS_NARROW = 0, GS_MID = 1, GS_WIDE = 2 };
+template <int WT, int SHAPE>
+struct GemvShape {
+  static constexpr int LPR = SHAPE == GS_NARROW ? 16 : 64;
+  static constexpr int CPL = SHAPE == GS_NARROW ? (WT == WT_I8 ? 4 : 8) : SHAPE == GS_MID ? 5 : 10;
+};
 
-// One fp32 activation row -> normalized (RMS/LN) and/or quantized into LDS.
-// Thread t owns elements t + 256*j.  The first kStrips strips are kept in
-// registers (every loop over them is unrolled, so they never spill to
-// scratch); longer rows re-read the remaining strips from global memory.
-template <int PRO, bool Q8>
-__device__ __forceinline__ void prologue_row(const float *row, int K, int Kp, const float *gamma,
-                                             const float *beta, double eps, const float *rowmax,
-                                             int8_t *xq, float *xf, float *xs, double *redd,
-                                             float *redf) {
-  const int t = threadIdx.x;
-  const int nstrip = (K + 255) >> 8;
-  float v[kStrips];
-#pragma unroll
-  for (int j = 0; j < kStrips; j++) {
-    const int i = t + 256 * j;
-    v[j] = (i < K) ? row[i] : 0.0f;
+// fp32 activation strips of 1024 (float4 per thread) kept in registers by the
+// prologue: the quantizing prologue holds rows up to 10240, the norms up to
+// 4096 (gemv_vector_ok enforces both).
+template <int PRO>
+struct ProStrips {
+  static constexpr int NS = PRO == PRO_QUANT ? 10 : (PRO == PRO_RMS || PRO == PRO_LN) ? 4 : 0;
+};
+
+// Sum of the LPR lanes of each row group (LPR in {16, 64}); the result is
+// valid in every lane of the group.  Integer sums are exact; fp32 sums use a
+// fixed tree.
+template <int LPR, typename T>
+__device__ __forceinline__ T group_sum(T v) {
+  v = v + dpp_mov<0xB1>(v);   // quad_perm [1,0,3,2]
+  v = v + dpp_mov<0x4E>(v);   // quad_perm [2,3,0,1]
+  v = v + dpp_mov<0x141>(v);  // row_half_mirror
+  v = v + dpp_mov<0x140>(v);  // row_mirror
+  if constexpr (LPR == 64) {
+    const T r0 = readlane(v, 0), r1 = readlane(v, 16), r2 = readlane(v, 32), r3 = readlane(v, 48);
+    v = (r0 + r1) + (r2 + r3);
   }
-  double mean = 0.0, rstd = 1.0;
-  if constexpr (PRO == PRO_RMS || PRO == PRO_LN) {
-    double s1 = 0.0;
-#pragma unroll
-    for (int j = 0; j < kStrips; j++) {
-      if (t + 256 * j < K) {
-        const double d = (double)v[j];
-        s1 += (PRO == PRO_LN) ? d : d * d;
-      }
-    }
-    for (int j = kStrips; j < nstrip; j++) {
-      const int i = t + 256 * j;
-      if (i < K) {
-        const double d = (double)row[i];
-        s1 += (PRO == PRO_LN) ? d : d * d;
-      }
-    }
-    s1 = block_sum256(s1, redd);
-    if constexpr (PRO == PRO_LN) {
-      mean = s1 / K;
-      double s2 = 0.0;
-#pragma unroll
-      for (int j = 0; j < kStrips; j++) {
-        if (t + 256 * j < K) {
-          const double d = (double)v[j] - mean;
-          s2 += d * d;
-        }
-      }
-      for (int j = kStrips; j < nstrip; j++) {
-        const int i = t + 256 * j;
-        if (i < K) {
-          const double d = (double)row[i] - mean;
-          s2 += d * d;
-        }
-      }
-      const double var = block_sum256(s2, redd) / K;
-      rstd = 1.0 / sqrt(var + eps);
-    } else {
-      rstd = 1.0 / sqrt(s1 / K + eps);
-    }
-  }
-  auto normed = [&](float x, int i) -> float {
-    if constexpr (PRO == PRO_RMS) {
-      x = (float)((double)x * rstd);
-      x = x * gamma[i];
-    } else if constexpr (PRO == PRO_LN) {
-      x = (float)(((double)x - mean) * rstd);
-      x = x * gamma[i];
-      x = x + beta[i];
-    }
-    return x;
-  };
-  if constexpr (Q8) {
-    float mx = 0.0f;
-    if (PRO == PRO_QUANT && rowmax) {
-      mx = *rowmax;  // max |row| published by the producing kernel
-    } else {
-#pragma unroll
-      for (int j = 0; j < kStrips; j++) {
-        const int i = t + 256 * j;
-        if (i < K) {
-          v[j] = normed(v[j], i);
-          mx = fmaxf(mx, fabsf(v[j]));
-        }
-      }
-      for (int j = kStrips; j < nstrip; j++) {
-        const int i = t + 256 * j;
-        if (i < K) mx = fmaxf(mx, fabsf(normed(row[i], i)));
-      }
-      mx = block_max256(mx, redf);
-    }
-    const float sc = quant_scale(mx);
-#pragma unroll
-    for (int j = 0; j < kStrips; j++) {
-      const int i = t + 256 * j;
-      if (i < Kp) xq[i] = (i < K) ? quant1(v[j], sc) : (int8_t)0;
-    }
-    for (int j = kStrips; j < (Kp + 255) / 256; j++) {
-      const int i = t + 256 * j;
-      if (i < Kp) xq[i] = (i < K) ? quant1(normed(row[i], i), sc) : (int8_t)0;
-    }
-    if (t == 0) *xs = sc;
-  } else {
-#pragma unroll
-    for (int j = 0; j < kStrips; j++) {
-      const int i = t + 256 * j;
-      if (i < Kp) xf[i] = (i < K) ? normed(v[j], i) : 0.0f;
-    }
-    for (int j = kStrips; j < (Kp + 255) / 256; j++) {
-      const int i = t + 256 * j;
-      if (i < Kp) xf[i] = (i < K) ? normed(row[i], i) : 0.0f;
-    }
-  }
+  return v;
 }
 
-// WT: 0 int8, 1 fp16, 2 bf16
-template <int WT, int LPR, int MT, int EPI, int PRO>
+template <int WT, int SHAPE, int MT, int EPI, int PRO>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
-  constexpr bool Q8 = WT == 0;
-  constexpr int CPL = lpr_cpl(LPR);
+  constexpr bool Q8 = WT == WT_I8;
+  constexpr int LPR = GemvShape<WT, SHAPE>::LPR, CPL = GemvShape<WT, SHAPE>::CPL;
   constexpr int RPW = kWave / LPR;
   constexpr bool SWI = EPI == EPI_SWIGLU;
-  constexpr int RPB = (SWI ? 2 : 4) * RPW;
+  constexpr bool RES = EPI == EPI_RESID || EPI == EPI_BIAS_RESID;
+  constexpr int RPB = 4 * RPW;
   constexpr int CHB = Q8 ? 16 : 8;  // elements per 16-byte chunk
   constexpr bool LDS_ACT = PRO != PRO_F32;
+  constexpr bool NORM = PRO == PRO_RMS || PRO == PRO_LN;
+  constexpr int NS = ProStrips<PRO>::NS;
 
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
-  __shared__ double redd[4];
+  __shared__ double redd[2][4];
   __shared__ float redf[4];
-  __shared__ float upx[SWI ? MT : 1][SWI ? 2 * RPW : 1];
   __shared__ unsigned long long keyred[4][MT];
+  __shared__ uint64_t etab[SWI ? 32 : 1];  // expf table of the SiLU
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int t = threadIdx.x;
+  uint64_t et = 0;
+  if constexpr (SWI) {
+    if (t < 32) et = ec_exp2_32[t];
+  }
+  const int lane = t & 63, wave = t >> 6;
   const int grp = lane / LPR, sub = lane % LPR;
-  const int part = SWI ? (wave >> 1) : 0;
-  const int rib = SWI ? ((wave & 1) * RPW + grp) : (wave * RPW + grp);
+  const int rib = wave * RPW + grp;
   const int K = a.K;
   const int Kp = (K + CHB - 1) / CHB * CHB;
   const int nch = K / CHB;
@@ -192,64 +124,192 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   const int ngroups = (a.N + RPB - 1) / RPB;
 
   typedef typename std::conditional<Q8, v4i, v4u>::type vec_t;
-  const void *Wsel = (SWI && part) ? a.W2 : a.W;
-  vec_t w[CPL];
-  auto load_w = [&](int rg, int kb) {
-    const int n = rg * RPB + rib;
-    const bool ok = n < a.N;
-    const vec_t *wrow = reinterpret_cast<const vec_t *>(
-        reinterpret_cast<const unsigned char *>(Wsel) + (size_t)n * K * (Q8 ? 1 : 2));
+  constexpr size_t WB = Q8 ? 1 : 2;
+
+  // ---- 1. activation row 0 of the tile (+ norm weights) ----
+  float4 xv[NS > 0 ? NS : 1], gv[NORM ? NS : 1], bv[PRO == PRO_LN ? NS : 1];
+  const int nstrip = (K + 1023) >> 10;
+  auto load_act = [&](int m) {
+    const float *row = reinterpret_cast<const float *>(a.A) + (size_t)(m0 + m) * a.lda;
 #pragma unroll
-    for (int c = 0; c < CPL; c++) {
-      const int ch = kb + sub + c * LPR;
-      if (ok && ch < nch) w[c] = __builtin_nontemporal_load(wrow + ch);
+    for (int j = 0; j < NS; j++) {
+      if (j < nstrip) {
+        const int i = min(4 * t + 1024 * j, K - 4);
+        xv[j] = *reinterpret_cast<const float4 *>(row + i);
+        if constexpr (NORM) {
+          if (m == 0) {
+            gv[j] = *reinterpret_cast<const float4 *>(a.gamma + i);
+            if constexpr (PRO == PRO_LN) bv[j] = *reinterpret_cast<const float4 *>(a.beta + i);
+          }
+        }
+      }
     }
   };
+  if constexpr (NS > 0) load_act(0);
 
+  // ---- 2. first row group: weights, scales, bias, residual ----
+  const vec_t *Wv = reinterpret_cast<const vec_t *>(a.W);
+  const vec_t *W2v = reinterpret_cast<const vec_t *>(a.W2);
+  vec_t w[CPL], w2[SWI ? CPL : 1];
+  auto load_w = [&](int rg, int kb) {
+    const int n = min(rg * RPB + rib, a.N - 1);
+    const size_t base = (size_t)n * K * WB / 16;
+#pragma unroll
+    for (int c = 0; c < CPL; c++) {
+      const int ch = min(kb + sub + c * LPR, nch - 1);
+      w[c] = __builtin_nontemporal_load(Wv + base + ch);
+      if constexpr (SWI) w2[c] = __builtin_nontemporal_load(W2v + base + ch);
+    }
+  };
+  float bs = 1.0f, bs2 = 1.0f, bia = 0.0f, res[RES ? MT : 1];
+  auto load_meta = [&](int rg) {
+    const int n = min(rg * RPB + rib, a.N - 1);
+    if constexpr (Q8) {
+      if (a.ws) bs = a.ws[n];
+      if constexpr (SWI) {
+        if (a.ws2) bs2 = a.ws2[n];
+      }
+    }
+    if (a.bias) bia = a.bias[n];
+    if constexpr (RES) {
+#pragma unroll
+      for (int m = 0; m < MT; m++)
+        if (m < mc) res[m] = a.out[(size_t)(m0 + m) * a.ldo + n];
+    }
+  };
   int rg = blockIdx.x;
-  if (rg < ngroups) load_w(rg, 0);
+  load_w(rg, 0);
+  load_meta(rg);
 
-  // ---- prologue: activation rows of this M tile into LDS ----
+  // ---- 3. prologue: activation rows of this M tile into LDS ----
+  if constexpr (SWI) {
+    if (t < 32) etab[t] = et;
+  }
   int8_t *xq = reinterpret_cast<int8_t *>(lds);
   float *xf = reinterpret_cast<float *>(lds);
   float *xs = reinterpret_cast<float *>(lds + (size_t)MT * Kp);  // int8 path only
   if constexpr (PRO == PRO_I8) {
     for (int m = 0; m < mc; m++) {
       const int8_t *src = reinterpret_cast<const int8_t *>(a.A) + (size_t)(m0 + m) * a.lda;
-      for (int i = threadIdx.x * 16; i < K; i += 256 * 16)
+      for (int i = t * 16; i < K; i += 256 * 16)
         *reinterpret_cast<v4i *>(xq + (size_t)m * Kp + i) = *reinterpret_cast<const v4i *>(src + i);
-      if (threadIdx.x == 0) xs[m] = a.as[m0 + m];
+      if (t == 0) xs[m] = a.as[m0 + m];
     }
-  } else if constexpr (PRO != PRO_F32) {
+  } else if constexpr (NS > 0) {
     for (int m = 0; m < mc; m++) {
-      const float *row = reinterpret_cast<const float *>(a.A) + (size_t)(m0 + m) * a.lda;
-      prologue_row<PRO, Q8>(row, K, Kp, a.gamma, a.beta, a.eps, a.in_max ? a.in_max + m0 + m : nullptr,
-                            xq + (size_t)m * Kp, xf + (size_t)m * Kp, xs + m, redd, redf);
+      if (m) load_act(m);
+      // lanes past the end of the row hold a clamped copy: zero them
+#pragma unroll
+      for (int j = 0; j < NS; j++) {
+        if (j < nstrip && 4 * t + 1024 * j >= K) xv[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+      double mean = 0.0, rstd = 1.0;
+      if constexpr (NORM) {
+        double s1 = 0.0;
+#pragma unroll
+        for (int j = 0; j < NS; j++) {
+          if (j < nstrip) {
+            const double d0 = xv[j].x, d1 = xv[j].y, d2 = xv[j].z, d3 = xv[j].w;
+            if constexpr (PRO == PRO_LN) s1 += ((d0 + d1) + d2) + d3;
+            else s1 += ((d0 * d0 + d1 * d1) + d2 * d2) + d3 * d3;
+          }
+        }
+        s1 = block_sum256_1b(s1, redd[0]);
+        if constexpr (PRO == PRO_LN) {
+          mean = s1 / K;
+          double s2 = 0.0;
+#pragma unroll
+          for (int j = 0; j < NS; j++) {
+            if (j < nstrip && 4 * t + 1024 * j < K) {
+              const double d0 = xv[j].x - mean, d1 = xv[j].y - mean, d2 = xv[j].z - mean, d3 = xv[j].w - mean;
+              s2 += ((d0 * d0 + d1 * d1) + d2 * d2) + d3 * d3;
+            }
+          }
+          const double var = block_sum256_1b(s2, redd[1]) / K;
+          rstd = 1.0 / sqrt(var + a.eps);
+        } else {
+          rstd = 1.0 / sqrt(s1 / K + a.eps);
+        }
+        auto nrm = [&](float x, float g, float b) -> float {
+          if constexpr (PRO == PRO_RMS) {
+            x = (float)((double)x * rstd);
+            return x * g;
+          } else {
+            x = (float)(((double)x - mean) * rstd);
+            x = x * g;
+            return x + b;
+          }
+        };
+#pragma unroll
+        for (int j = 0; j < NS; j++) {
+          if (j < nstrip) {
+            const float4 b = PRO == PRO_LN ? bv[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+            xv[j].x = nrm(xv[j].x, gv[j].x, b.x);
+            xv[j].y = nrm(xv[j].y, gv[j].y, b.y);
+            xv[j].z = nrm(xv[j].z, gv[j].z, b.z);
+            xv[j].w = nrm(xv[j].w, gv[j].w, b.w);
+            if (4 * t + 1024 * j >= K) xv[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+          }
+        }
+      }
+      if constexpr (Q8) {
+        float mx = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NS; j++) {
+          if (j < nstrip) {
+            mx = fmaxf(mx, fabsf(xv[j].x));
+            mx = fmaxf(mx, fabsf(xv[j].y));
+            mx = fmaxf(mx, fabsf(xv[j].z));
+            mx = fmaxf(mx, fabsf(xv[j].w));
+          }
+        }
+        mx = block_max256_1b(mx, redf);
+        const float sc = quant_scale(mx);
+        int8_t *q = xq + (size_t)m * Kp;
+#pragma unroll
+        for (int j = 0; j < NS; j++) {
+          const int i = 4 * t + 1024 * j;
+          if (j < nstrip && i < Kp) {
+            const uint32_t b0 = (uint8_t)quant1(xv[j].x, sc), b1 = (uint8_t)quant1(xv[j].y, sc);
+            const uint32_t b2 = (uint8_t)quant1(xv[j].z, sc), b3 = (uint8_t)quant1(xv[j].w, sc);
+            *reinterpret_cast<uint32_t *>(q + i) = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+          }
+        }
+        if (t == 0) xs[m] = sc;
+      } else {
+        float *f = xf + (size_t)m * Kp;
+#pragma unroll
+        for (int j = 0; j < NS; j++) {
+          const int i = 4 * t + 1024 * j;
+          if (j < nstrip && i < Kp) *reinterpret_cast<float4 *>(f + i) = xv[j];
+        }
+      }
+      // the two reductions of the next row reuse redd/redf: separate them
+      if (m + 1 < mc) __syncthreads();
     }
   }
   __syncthreads();
 
   unsigned long long best[MT];
-  float omax[MT];
 #pragma unroll
-  for (int m = 0; m < MT; m++) {
-    best[m] = 0ull;
-    omax[m] = 0.0f;
-  }
+  for (int m = 0; m < MT; m++) best[m] = 0ull;
 
   for (; rg < ngroups; rg += gridDim.x) {
     const int n = rg * RPB + rib;
     const bool valid = n < a.N;
     typedef typename std::conditional<Q8, int, float>::type acc_t;
-    acc_t acc[MT];
+    acc_t acc[MT], acc2[SWI ? MT : 1];
 #pragma unroll
-    for (int m = 0; m < MT; m++) acc[m] = 0;
+    for (int m = 0; m < MT; m++) {
+      acc[m] = 0;
+      if constexpr (SWI) acc2[m] = 0;
+    }
     for (int kb = 0; kb < nch; kb += LPR * CPL) {
       if (kb) load_w(rg, kb);
 #pragma unroll
       for (int c = 0; c < CPL; c++) {
         const int ch = kb + sub + c * LPR;
-        if (!valid || ch >= nch) continue;
+        if (ch >= nch) continue;
         if constexpr (Q8) {
 #pragma unroll
           for (int m = 0; m < MT; m++) {
@@ -261,15 +321,33 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
               s = __builtin_amdgcn_sdot4(x.z, w[c].z, s, false);
               s = __builtin_amdgcn_sdot4(x.w, w[c].w, s, false);
               acc[m] = s;
+              if constexpr (SWI) {
+                int u = acc2[m];
+                u = __builtin_amdgcn_sdot4(x.x, w2[c].x, u, false);
+                u = __builtin_amdgcn_sdot4(x.y, w2[c].y, u, false);
+                u = __builtin_amdgcn_sdot4(x.z, w2[c].z, u, false);
+                u = __builtin_amdgcn_sdot4(x.w, w2[c].w, u, false);
+                acc2[m] = u;
+              }
             }
           }
         } else {
-          float wf[8];
-          const uint32_t wv[4] = {w[c].x, w[c].y, w[c].z, w[c].w};
+          float wf[8], wf2[SWI ? 8 : 1];
+          {
+            const uint32_t wv[4] = {w[c].x, w[c].y, w[c].z, w[c].w};
 #pragma unroll
-          for (int j = 0; j < 4; j++) {
-            wf[2 * j] = w2f<WT == 2>((uint16_t)(wv[j] & 0xffffu));
-            wf[2 * j + 1] = w2f<WT == 2>((uint16_t)(wv[j] >> 16));
+            for (int j = 0; j < 4; j++) {
+              wf[2 * j] = w2f<WT == WT_BF16>((uint16_t)(wv[j] & 0xffffu));
+              wf[2 * j + 1] = w2f<WT == WT_BF16>((uint16_t)(wv[j] >> 16));
+            }
+          }
+          if constexpr (SWI) {
+            const uint32_t wv[4] = {w2[c].x, w2[c].y, w2[c].z, w2[c].w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+              wf2[2 * j] = w2f<WT == WT_BF16>((uint16_t)(wv[j] & 0xffffu));
+              wf2[2 * j + 1] = w2f<WT == WT_BF16>((uint16_t)(wv[j] >> 16));
+            }
           }
 #pragma unroll
           for (int m = 0; m < MT; m++) {
@@ -289,84 +367,72 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
               s = __builtin_fmaf(x1.z, wf[6], s);
               s = __builtin_fmaf(x1.w, wf[7], s);
               acc[m] = s;
-            }
-          }
-        }
-      }
-    }
-    if (rg + (int)gridDim.x < ngroups) load_w(rg + gridDim.x, 0);  // prefetch the next group
-#pragma unroll
-    for (int m = 0; m < MT; m++) {
-#pragma unroll
-      for (int o = LPR / 2; o > 0; o >>= 1) acc[m] += __shfl_xor(acc[m], o, kWave);
-    }
-
-    // ---- epilogue ----
-    float vals[MT];
-#pragma unroll
-    for (int m = 0; m < MT; m++) {
-      if constexpr (Q8) {
-        const float as = xs[m];
-        const float *wsc = (SWI && part) ? a.ws2 : a.ws;
-        const float bs = (valid && wsc) ? wsc[n] : 1.0f;
-        const float bv = (valid && a.bias && !SWI) ? a.bias[n] : 0.0f;
-        vals[m] = i8_epilogue((int)acc[m], as, bs, bv);
-      } else {
-        vals[m] = (float)acc[m];
-      }
-    }
-    if constexpr (SWI) {
-      if (sub == 0 && valid && part == 1) {
-#pragma unroll
-        for (int m = 0; m < MT; m++)
-          if (m < mc) upx[m][rib] = vals[m];
-      }
-      __syncthreads();
-      if (sub == 0 && valid && part == 0) {
-#pragma unroll
-        for (int m = 0; m < MT; m++) {
-          if (m < mc) {
-            const float r = silu(vals[m]) * upx[m][rib];
-            a.out[(size_t)(m0 + m) * a.ldo + n] = r;
-            omax[m] = fmaxf(omax[m], fabsf(r));
-          }
-        }
-      }
-      __syncthreads();
-    } else {
-      if (sub == 0 && valid) {
-        const float bv = (!Q8 && a.bias) ? a.bias[n] : 0.0f;
-#pragma unroll
-        for (int m = 0; m < MT; m++) {
-          if (m < mc) {
-            float v = vals[m];
-            float *o = a.out + (size_t)(m0 + m) * a.ldo + n;
-            if constexpr (EPI == EPI_BIAS || EPI == EPI_BIAS_RESID || EPI == EPI_BIAS_GELU) v = v + bv;
-            if constexpr (EPI == EPI_RESID || EPI == EPI_BIAS_RESID) v = *o + v;
-            if constexpr (EPI == EPI_GELU || EPI == EPI_BIAS_GELU) v = gelu_new(v);
-            *o = v;
-            if constexpr (EPI == EPI_STORE) {
-              if (a.cand && v == v) {
-                const unsigned long long k = amax_key(v, n);
-                best[m] = k > best[m] ? k : best[m];
+              if constexpr (SWI) {
+                float u = acc2[m];
+                u = __builtin_fmaf(x0.x, wf2[0], u);
+                u = __builtin_fmaf(x0.y, wf2[1], u);
+                u = __builtin_fmaf(x0.z, wf2[2], u);
+                u = __builtin_fmaf(x0.w, wf2[3], u);
+                u = __builtin_fmaf(x1.x, wf2[4], u);
+                u = __builtin_fmaf(x1.y, wf2[5], u);
+                u = __builtin_fmaf(x1.z, wf2[6], u);
+                u = __builtin_fmaf(x1.w, wf2[7], u);
+                acc2[m] = u;
               }
             }
           }
         }
       }
     }
-  }
+    // this group's scales/bias/residual; then prefetch the next group
+    const float cbs = bs, cbs2 = bs2, cbia = bia;
+    float cres[RES ? MT : 1];
+    if constexpr (RES) {
+#pragma unroll
+      for (int m = 0; m < MT; m++) cres[m] = res[m];
+    }
+    if (rg + (int)gridDim.x < ngroups) {
+      load_w(rg + gridDim.x, 0);
+      load_meta(rg + gridDim.x);
+    }
+#pragma unroll
+    for (int m = 0; m < MT; m++) {
+      acc[m] = group_sum<LPR>(acc[m]);
+      if constexpr (SWI) acc2[m] = group_sum<LPR>(acc2[m]);
+    }
 
-  if constexpr (SWI) {
-    if (a.out_max) {  // row max |out| for the next linear's quantization
+    // ---- epilogue ----
+    if (sub == 0 && valid) {
 #pragma unroll
       for (int m = 0; m < MT; m++) {
-        const float r = block_max256(omax[m], redf);
-        if (threadIdx.x == 0 && m < mc)
-          atomicMax(reinterpret_cast<unsigned int *>(a.out_max + m0 + m), __float_as_uint(r));
+        if (m < mc) {
+          float v;
+          if constexpr (Q8) {
+            v = i8_epilogue((int)acc[m], xs[m], cbs, SWI ? 0.0f : cbia);
+          } else {
+            v = (float)acc[m];
+          }
+          float *o = a.out + (size_t)(m0 + m) * a.ldo + n;
+          if constexpr (SWI) {
+            const float u = Q8 ? i8_epilogue((int)acc2[m], xs[m], cbs2, 0.0f) : (float)acc2[m];
+            v = silu(v, etab) * u;
+          } else {
+            if constexpr (!Q8 && (EPI == EPI_BIAS || EPI == EPI_BIAS_RESID || EPI == EPI_BIAS_GELU)) v = v + cbia;
+            if constexpr (RES) v = cres[m] + v;
+            if constexpr (EPI == EPI_GELU || EPI == EPI_BIAS_GELU) v = gelu_new(v);
+          }
+          *o = v;
+          if constexpr (EPI == EPI_STORE) {
+            if (a.cand && v == v) {
+              const unsigned long long k = amax_key(v, n);
+              best[m] = k > best[m] ? k : best[m];
+            }
+          }
+        }
       }
     }
   }
+
   if constexpr (EPI == EPI_STORE) {
     if (a.cand) {  // one argmax candidate per (row, block)
 #pragma unroll
@@ -375,11 +441,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
         if (lane == 0) keyred[wave][m] = b;
       }
       __syncthreads();
-      if (threadIdx.x < MT && (int)threadIdx.x < mc) {
-        const int m = threadIdx.x;
-        unsigned long long b = keyred[0][m];
-        for (int i = 1; i < 4; i++) b = keyred[i][m] > b ? keyred[i][m] : b;
-        a.cand[(size_t)(m0 + m) * gridDim.x + blockIdx.x] = b;
+      if (t < MT && t < mc) {
+        unsigned long long b = keyred[0][t];
+        for (int i = 1; i < 4; i++) b = keyred[i][t] > b ? keyred[i][t] : b;
+        a.cand[(size_t)(m0 + t) * gridDim.x + blockIdx.x] = b;
       }
     }
   }
@@ -389,26 +454,37 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
 // host-side launch helpers (instantiated per weight type in gemv_*.hip)
 // ---------------------------------------------------------------------------
 
-template <int WT, int LPR, int MT, int EPI, int PRO>
+template <int WT, int SHAPE, int MT, int EPI, int PRO>
 hipError_t gemv_launch(const GemvArgs &a, hipStream_t s) {
-  constexpr int RPW = kWave / LPR;
-  constexpr int RPB = (EPI == EPI_SWIGLU ? 2 : 4) * RPW;
+  constexpr int RPB = 4 * (kWave / GemvShape<WT, SHAPE>::LPR);
   const int ngroups = (a.N + RPB - 1) / RPB;
-  const int gx = ngroups < gemv_max_blocks() ? ngroups : gemv_max_blocks();
+  const int cap = gemv_max_blocks();
+  const int gx = ngroups < cap ? ngroups : cap;
   dim3 grid(gx, (a.M + MT - 1) / MT);
   const size_t lds = gemv_lds_bytes(WT, PRO, MT, a.K);
-  hipLaunchKernelGGL((gemv_kernel<WT, LPR, MT, EPI, PRO>), grid, dim3(256), lds, s, a);
+  klaunch((gemv_kernel<WT, SHAPE, MT, EPI, PRO>), grid, dim3(256), lds, s, a);
   return hipGetLastError();
 }
 
-template <int WT, int LPR, int EPI, int PRO>
-hipError_t gemv_launch_mt(const GemvArgs &a, int mt, hipStream_t s) {
-  switch (mt) {
-  case 1: return gemv_launch<WT, LPR, 1, EPI, PRO>(a, s);
-  case 2: return gemv_launch<WT, LPR, 2, EPI, PRO>(a, s);
-  case 4: return gemv_launch<WT, LPR, 4, EPI, PRO>(a, s);
-  default: return gemv_launch<WT, LPR, 8, EPI, PRO>(a, s);
+template <int WT, int EPI, int PRO>
+hipError_t gemv_launch_shape(const GemvArgs &a, hipStream_t s) {
+  const int shape = gemv_pick_shape(WT, a.K);
+  const int mt = gemv_pick_mt(a.M);
+#define EC_MT(SH)                                                   \
+  switch (mt) {                                                     \
+  case 1: return gemv_launch<WT, SH, 1, EPI, PRO>(a, s);            \
+  case 2: return gemv_launch<WT, SH, 2, EPI, PRO>(a, s);            \
+  case 4: return gemv_launch<WT, SH, 4, EPI, PRO>(a, s);            \
+  default: return gemv_launch<WT, SH, 8, EPI, PRO>(a, s);           \
   }
+  if (shape == GS_NARROW) {
+    EC_MT(GS_NARROW)
+  } else if (shape == GS_MID) {
+    EC_MT(GS_MID)
+  } else {
+    EC_MT(GS_WIDE)
+  }
+#undef EC_MT
 }
 
 }  // namespace ec

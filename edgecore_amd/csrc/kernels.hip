@@ -1,18 +1,15 @@
 // gfx950 kernels of the EdgeCore transformer forward hot path.
 //
-// Decode GEMV (M <= 8 rows per tile): weights stay in the reference layout
-// [N][K] row-major.  A row is read by LPR lanes of one wave with 16-byte
-// non-temporal loads (each instruction of a wave covers 64/LPR rows x LPR*16
-// contiguous bytes), int8 rows are multiplied with v_dot4_i32_i8 into an exact
-// int32 (any summation order gives the reference's int32), fp16/bf16 rows are
-// widened to fp32 and accumulated with FMA.  The LPR partial sums are combined
-// with a wave64 xor-shuffle tree and the epilogue (scales, bias, residual,
-// GELU or SwiGLU) is applied in registers before the single store.
+// The fused decode GEMV lives in gemv_impl.h (instantiated per weight type in
+// gemv_*.hip); this file holds the generic GEMV, norms, quantizer, embedding,
+// RoPE/KV append, attention, argmax, elementwise math and the launchers.
 #include "gemv_impl.h"
 
 #include <float.h>
 
 namespace ec {
+
+hipEvent_t g_launch_ev[2] = {nullptr, nullptr};
 
 // ---------------------------------------------------------------------------
 // generic GEMV (any K, any alignment, every epilogue): one thread per output
@@ -129,10 +126,8 @@ __global__ __launch_bounds__(256) void norm_kernel(const float *x, int E, const 
 template <bool BF16>
 __global__ __launch_bounds__(256) void embed_kernel(const uint16_t *wte, const uint16_t *wpe,
                                                     const int *tok, const int *pos, int E,
-                                                    float *x, float *slots, int nslots, int ld) {
+                                                    float *x) {
   const int m = blockIdx.x;
-  if (slots)
-    for (int j = threadIdx.x; j < nslots; j += 256) slots[(size_t)j * ld + m] = 0.0f;
   const uint16_t *et = wte + (size_t)tok[m] * E;
   const uint16_t *ep = wpe ? wpe + (size_t)pos[m] * E : nullptr;
   for (int d = threadIdx.x; d < E; d += 256) {
@@ -177,17 +172,26 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(KvArgs a) {
 // ---------------------------------------------------------------------------
 // attention (src/gpt2.c:527-557 and 744-777)
 // ---------------------------------------------------------------------------
-
 // One block per (head, token), reproducing the reference's arithmetic in its
-// order: each score is one thread's sequential fp32 dot over head_dim, scaled
-// in double; max; e = expf(s - max) with the reference's expf; double sum;
-// p = (float)(e * (1/sum)); each output element is one thread's sequential
-// fp32 sum over positions.  The int8 path turns any last-bit difference here
-// into different activation codes downstream, so the order is kept exactly.
-// The V rows of the attended positions are staged into LDS (tiles of vtile
-// positions) with loads issued before the scores, so the sequential sums read
-// LDS instead of waiting on memory.  HD > 0 fixes head_dim at compile time
-// (whole K rows are loaded before each dot); HD == 0 is the generic path.
+// order: each score is one thread's sequential fp32 dot over head_dim (a
+// rounded product, then a rounded add), scaled in double; max; e = expf(s -
+// max) with the reference's expf; double sum; p = (float)(e * (1/sum)); each
+// output element is a sequential fp32 sum over positions of the rounded
+// products p*v.  The int8 path turns any last-bit difference here into
+// different activation codes downstream, so the order is kept exactly.
+//
+// Work split: the products p*v of a tile of `vtile` positions are formed by
+// all 256 threads into LDS, laid out [position/4][d][position%4] with the d
+// index XOR-swizzled by the quad index (no bank conflicts on either side), so
+// the thread owning output element d runs its sequential sum reading four
+// positions per 16-byte LDS load.  With HD > 0 (head_dim fixed at compile
+// time, 16-byte loads) the K rows of the first positions and the first V
+// tile are read with coalesced loads (8 lanes per 128-byte row) issued at the
+// start, unconditionally (indices clamped into the attended range), after the
+// q/k/v elements: the hardware's in-order load counter then lets each phase
+// wait for its own data only.  The K rows go through LDS (swizzled 16-byte
+// chunks) so that each score is still one thread's sequential dot.  HD == 0
+// is the generic path.
 //
 // FUSED: the block also rotates its q head and the token's new k (RoPE,
 // src/gpt2.c:656-665, double cos/sin table) and uses the new k and v rounded
@@ -221,13 +225,26 @@ __device__ __forceinline__ float dot_k_row(const float *qs, const uint16_t *kp, 
   return s;
 }
 
+// the own position's score from the fp16-rounded new k in LDS
+__device__ __forceinline__ float dot_new_k(const float *qs, const float *kn, int hd) {
+  float s = 0.0f;
+  for (int d = 0; d < hd; d++) {
+    const float p0 = qs[d] * kn[d];
+    s = s + p0;
+  }
+  return s;
+}
+
 template <int HD, bool FUSED>
 __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   extern __shared__ __attribute__((aligned(16))) float lds[];
   __shared__ float redf[4];
   __shared__ double redd[4];
+  __shared__ uint64_t etab[32];  // expf table
+  constexpr int CPR = HD > 0 ? HD / 8 : 1;         // 16-byte chunks per K/V row
   const int h = blockIdx.x, m = blockIdx.y, t = threadIdx.x;
-  const int pos = a.pos[m], slot = a.slot[m];
+  const int pos = ld_uniform(a.pos + m), slot = ld_uniform(a.slot + m);
+  const uint64_t et = ec_exp2_32[t & 31];
   const int kvh = h * a.KVH / a.H;
   int lo = 0;
   if (a.window > 0) {
@@ -238,144 +255,278 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   const int hd = HD > 0 ? HD : a.hd, T = a.vtile;
   const int hdp = (hd + 3) & ~3;
   float *qs = lds;
-  float *kn = qs + hdp;  // FUSED: the new k (fp16-rounded), fp32
-  float *sc = kn + (FUSED ? hdp : 0);
-  uint16_t *vt = reinterpret_cast<uint16_t *>(sc + ((a.max_npos + 3) & ~3));
+  float *kn = qs + hdp;  // FUSED: the new k, fp16-rounded
+  float *vn = kn + hdp;  // FUSED: the new v, fp16-rounded
+  float *sc = vn + hdp;
+  float *prod = sc + ((a.max_npos + 3) & ~3);  // [T/4][P][4]
+  const int P = attn_pitch(hd, a.kv);         // 16-byte slots per quad of positions
   const size_t cbase = (size_t)slot * a.C * a.kv + (size_t)kvh * hd;
   const uint16_t *K = a.kc + cbase + (size_t)lo * a.kv;
   const uint16_t *V = a.vc + cbase + (size_t)lo * a.kv;
-  const bool vec = (hd & 7) == 0 && (a.kv & 7) == 0;
   const int ncache = FUSED ? n - 1 : n;  // positions read from the cache
+  const int last = ncache > 0 ? ncache - 1 : 0;  // clamp target of the unconditional loads
 
-  auto stage_v = [&](int t0) {  // cached V rows [t0, t0 + T) of the attended range -> vt
-    const int cnt = min(T, ncache - t0);
-    if (cnt <= 0) return;
-    if (vec) {
-      const int cpr = hd >> 3;
-      for (int c = t; c < cnt * cpr; c += 256) {
-        const int i = c / cpr, j = (c - i * cpr) << 3;
-        *reinterpret_cast<v4u *>(vt + i * hd + j) = *reinterpret_cast<const v4u *>(V + (size_t)(t0 + i) * a.kv + j);
+  // ---- 1. this thread's element of q (and of the new k and v) ----
+  // Branch-free loads (index clamped into the head) so that every load of
+  // steps 1-2 is issued before the first wait.
+  const float *qrow = a.q + (size_t)m * a.ldq + (size_t)h * hd;
+  const float *krow = a.k + (size_t)m * a.ldk + (size_t)kvh * hd;
+  const float *vrow = a.v + (size_t)m * a.ldk + (size_t)kvh * hd;
+  const int rot = (FUSED && a.cs) ? a.half : 0;
+  const int tt = min(t, hd - 1);
+  const bool rr = tt < 2 * rot;  // element of the rotated part
+  const int i0 = rr ? (tt < rot ? tt : tt - rot) : tt, i1 = rr ? i0 + rot : tt;
+  const float qa = qrow[i0], qb = qrow[i1];
+  float ka = 0.0f, kb = 0.0f, vv = 0.0f;
+  double2 c2 = make_double2(1.0, 0.0);
+  if constexpr (FUSED) {
+    ka = krow[i0];
+    kb = krow[i1];
+    vv = vrow[tt];
+    if (rot) c2 = a.cs[(size_t)pos * a.half + (rr ? i0 : 0)];
+  }
+
+  // ---- 2. K rows of the first KQ positions, first V tile ----
+  // unit = 4 positions x 8 elements (16 bytes each); kAttnUnits per thread
+  constexpr int KQMAX = HD > 0 ? 256 * kAttnUnits * 4 / CPR : 0;  // K positions staged
+  constexpr int KP = CPR + 1;  // K tile row pitch in 16-byte chunks (odd: rows spread over the banks)
+  // the K tile lives in the product area (T/4 * P slots of 16 bytes)
+  const int KQ = min(KQMAX, (T / 4) * P / KP);
+  v4u kr[HD > 0 ? kAttnUnits : 1][4], vr[HD > 0 ? kAttnUnits : 1][4];
+  if constexpr (HD > 0) {
+#pragma unroll
+    for (int u = 0; u < kAttnUnits; u++) {
+      const int unit = t + 256 * u, qd = unit / CPR, cd = unit - qd * CPR;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const int i = min(4 * qd + e, last);
+        kr[u][e] = *reinterpret_cast<const v4u *>(K + (size_t)i * a.kv + 8 * cd);
       }
-    } else {
-      for (int c = t; c < cnt * hd; c += 256) {
-        const int i = c / hd, j = c - i * hd;
-        vt[i * hd + j] = V[(size_t)(t0 + i) * a.kv + j];
+    }
+  }
+  auto load_v = [&](int t0) {  // V units (4 positions x 8 elements) of the tile at t0
+#pragma unroll
+    for (int u = 0; u < kAttnUnits; u++) {
+      const int unit = t + 256 * u, qd = unit / CPR, cd = unit - qd * CPR;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const int i = min(t0 + 4 * qd + e, last);
+        vr[u][e] = *reinterpret_cast<const v4u *>(V + (size_t)i * a.kv + 8 * cd);
       }
     }
   };
+  if constexpr (HD > 0) load_v(0);
+  __builtin_amdgcn_sched_barrier(0);
 
-  const float *qrow = a.q + (size_t)m * a.ldq + (size_t)h * hd;
-  if constexpr (FUSED) {
-    const float *krow = a.k + (size_t)m * a.ldk + (size_t)kvh * hd;
-    const float *vrow = a.v + (size_t)m * a.ldk + (size_t)kvh * hd;
-    const bool writer = h == 0 || (h - 1) * a.KVH / a.H != kvh;  // first query head of the group
-    const size_t woff = ((size_t)slot * a.C + pos) * a.kv + (size_t)kvh * hd;
-    const int rot = a.cs ? a.half : 0;
-    const double2 *cs = a.cs ? a.cs + (size_t)pos * a.half : nullptr;
-    for (int i = t; i < hd; i += 256) {
-      float qv, kvv;
-      if (i < rot || (i >= rot && i < 2 * rot)) {
-        const int i0 = i < rot ? i : i - rot;
-        const double c = cs[i0].x, sn = cs[i0].y;
-        const float q0 = qrow[i0], q1 = qrow[i0 + rot], k0 = krow[i0], k1 = krow[i0 + rot];
-        if (i < rot) {
-          const double t1 = q0 * c, t2 = q1 * sn, u1 = k0 * c, u2 = k1 * sn;
-          qv = (float)(t1 - t2);
-          kvv = (float)(u1 - u2);
-        } else {
-          const double t3 = q0 * sn, t4 = q1 * c, u3 = k0 * sn, u4 = k1 * c;
-          qv = (float)(t3 + t4);
-          kvv = (float)(u3 + u4);
-        }
+  // ---- 3. RoPE, fp16 rounding of the new k/v, cache append ----
+  if (t < 32) etab[t] = et;
+  if (t < hd) {
+    float qv = qa, kv_ = ka;
+    if (rr) {
+      // rotate-half: qa/ka hold element i0, qb/kb element i0 + half
+      const double cr = c2.x, sr = c2.y;
+      if (t < rot) {
+        const double t1 = (double)qa * cr, t2 = (double)qb * sr, u1 = (double)ka * cr, u2 = (double)kb * sr;
+        qv = (float)(t1 - t2);
+        kv_ = (float)(u1 - u2);
       } else {
-        qv = qrow[i];
-        kvv = krow[i];
-      }
-      qs[i] = qv;
-      const uint16_t kh = f2h(kvv), vh = f2h(vrow[i]);
-      kn[i] = h2f(kh);
-      if (n - 1 < T) vt[(n - 1) * hd + i] = vh;  // own position lands in the first V tile
-      if (writer) {
-        a.kc_w[woff + i] = kh;
-        a.vc_w[woff + i] = vh;
+        const double t3 = (double)qa * sr, t4 = (double)qb * cr, u3 = (double)ka * sr, u4 = (double)kb * cr;
+        qv = (float)(t3 + t4);
+        kv_ = (float)(u3 + u4);
       }
     }
-  } else {
-    for (int d = t; d < hd; d += 256) qs[d] = qrow[d];
+    qs[t] = qv;
+    if constexpr (FUSED) {
+      const uint16_t kh = f2h(kv_), vh = f2h(vv);
+      kn[t] = h2f(kh);
+      vn[t] = h2f(vh);
+      const bool writer = h == 0 || (h - 1) * a.KVH / a.H != kvh;  // first query head of the group
+      if (writer) {
+        const size_t woff = ((size_t)slot * a.C + pos) * a.kv + (size_t)kvh * hd + t;
+        a.kc_w[woff] = kh;
+        a.vc_w[woff] = vh;
+      }
+    }
   }
-  stage_v(0);
+  // K tile: row i, chunk c at 16-byte slot i*KP + c
+  v4u *ktile = reinterpret_cast<v4u *>(prod);
+  if constexpr (HD > 0) {
+#pragma unroll
+    for (int u = 0; u < kAttnUnits; u++) {
+      const int unit = t + 256 * u, qd = unit / CPR, cd = unit - qd * CPR;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const int i = 4 * qd + e;
+        if (i < KQ) ktile[i * KP + cd] = kr[u][e];
+      }
+    }
+  }
   __syncthreads();
 
+  // ---- 4. scores ----
   float mx = -FLT_MAX;
-  for (int i = t; i < n; i += 256) {
-    float s;
-    if (FUSED && i == n - 1) {
-      s = 0.0f;
-      for (int d = 0; d < hd; d++) {
-        const float p0 = qs[d] * kn[d];
-        s = s + p0;
-      }
-    } else {
-      s = dot_k_row<HD>(qs, K + (size_t)i * a.kv, hd);
-    }
+  auto put = [&](int i, float s) {
+    if (FUSED && i == n - 1) s = dot_new_k(qs, kn, hd);
     s = (float)((double)s * a.inv_hd);
     sc[i] = s;
     mx = fmaxf(mx, s);
+  };
+  if constexpr (HD > 0) {
+    // R positions per thread, their sequential dots interleaved
+    constexpr int R = KQMAX / 256;
+    float s[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) s[r] = 0.0f;
+#pragma unroll
+    for (int c = 0; c < CPR; c++) {
+      uint32_t wv[R][4];
+#pragma unroll
+      for (int r = 0; r < R; r++) {
+        const int ir = min(t + 256 * r, KQ - 1);
+        const v4u kk = ktile[ir * KP + c];
+        wv[r][0] = kk.x;
+        wv[r][1] = kk.y;
+        wv[r][2] = kk.z;
+        wv[r][3] = kk.w;
+      }
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const float q0 = qs[8 * c + 2 * j], q1 = qs[8 * c + 2 * j + 1];
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+          const float p0 = q0 * h2f((uint16_t)(wv[r][j] & 0xffffu));
+          s[r] = s[r] + p0;
+          const float p1 = q1 * h2f((uint16_t)(wv[r][j] >> 16));
+          s[r] = s[r] + p1;
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      const int i = t + 256 * r;
+      if (i < n && i < KQ) put(i, s[r]);
+    }
   }
-  mx = block_max256(mx, redf);
+  // positions past the K tile (long contexts) and the generic path
+  for (int i = t; i < n; i += 256) {
+    if (HD > 0 && i < KQ) continue;  // scored from the K tile above
+    put(i, (FUSED && i == n - 1) ? 0.0f : dot_k_row<HD>(qs, K + (size_t)i * a.kv, hd));
+  }
+  mx = block_max256_1b(mx, redf);
   double sum = 0.0;
   for (int i = t; i < n; i += 256) {
-    const float e = ec_expf_ref(sc[i] - mx);
+    const float e = ec_expf_tab(sc[i] - mx, etab);
     sc[i] = e;
     sum += (double)e;
   }
-  sum = block_sum256(sum, redd);
+  sum = block_sum256_1b(sum, redd);
   const double isum = 1.0 / sum;
   for (int i = t; i < n; i += 256) sc[i] = (float)((double)sc[i] * isum);
-  __syncthreads();
 
+  // ---- 5. products p*v per tile, then the sequential sums ----
+  // element d of quad q sits in 16-byte slot q*P + (d ^ ((d >> 4) & sw)); with
+  // P and sw from attn_pitch/attn_swz every 16 consecutive lanes of the
+  // product writes (units of 4 positions x 8 elements) and of the sums' reads
+  // (consecutive d) touch 16 distinct bank slots
+  const int sw = attn_swz(hd, a.kv);
   float o = 0.0f;
   for (int t0 = 0; t0 < n; t0 += T) {
-    if (t0) {
-      __syncthreads();
-      stage_v(t0);
-      if constexpr (FUSED) {
-        if (n - 1 >= t0 && n - 1 < t0 + T) {  // own position lands in this tile
-          const float *vrow = a.v + (size_t)m * a.ldk + (size_t)kvh * hd;
-          for (int i = t; i < hd; i += 256) vt[(n - 1 - t0) * hd + i] = f2h(vrow[i]);
+    const int cnt = min(T, n - t0);
+    __syncthreads();  // probabilities written / previous tile's sums done
+    if constexpr (HD > 0) {
+      if (t0) load_v(t0);
+#pragma unroll
+      for (int u = 0; u < kAttnUnits; u++) {
+        const int unit = t + 256 * u, qd = unit / CPR, cd = unit - qd * CPR;
+        if (4 * qd < cnt) {
+          const float4 pq = *reinterpret_cast<const float4 *>(sc + t0 + 4 * qd);
+          const float pe[4] = {pq.x, pq.y, pq.z, pq.w};
+          float pr[8][4];
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            const uint32_t hv[4] = {vr[u][e].x, vr[u][e].y, vr[u][e].z, vr[u][e].w};
+            float vf[8];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+              vf[2 * j] = h2f((uint16_t)(hv[j] & 0xffffu));
+              vf[2 * j + 1] = h2f((uint16_t)(hv[j] >> 16));
+            }
+            if (FUSED && t0 + 4 * qd + e == n - 1) {
+#pragma unroll
+              for (int k = 0; k < 8; k++) vf[k] = vn[8 * cd + k];
+            }
+#pragma unroll
+            for (int k = 0; k < 8; k++) pr[k][e] = pe[e] * vf[k];
+          }
+#pragma unroll
+          for (int k = 0; k < 8; k++)
+            *reinterpret_cast<float4 *>(prod + ((size_t)qd * P + ((8 * cd + k) ^ (((8 * cd + k) >> 4) & sw))) * 4) =
+                make_float4(pr[k][0], pr[k][1], pr[k][2], pr[k][3]);
         }
       }
-      __syncthreads();
+    } else {
+      for (int e = t; e < cnt * hd; e += 256) {
+        const int i = e / hd, d = e - i * hd;
+        const float v = (FUSED && t0 + i == n - 1) ? vn[d] : h2f(V[(size_t)(t0 + i) * a.kv + d]);
+        prod[((size_t)(i >> 2) * P + (d ^ ((d >> 4) & sw))) * 4 + (i & 3)] = sc[t0 + i] * v;
+      }
     }
+    __syncthreads();
     if (t < hd) {
-      const int cnt = min(T, n - t0);
-      const uint16_t *vc = vt + t;
-      const float *pp = sc + t0;
-      int i = 0;
-      for (; i + 8 <= cnt; i += 8) {
-        float vv[8], pw[8];
+      // sequential sum over the tile, 8 quads at a time: the loads of the
+      // next 8 quads (two register sets) are in flight while the current 8
+      // are added.  Look-ahead loads reach at most 8 quads past the tile,
+      // into the slack that attention_lds_bytes reserves.
+      const float4 *pp = reinterpret_cast<const float4 *>(prod) + (t ^ ((t >> 4) & sw));
+      const int nq = cnt >> 2, nq8 = nq & ~7;
+      float4 A[8], B[8];
+      auto add8 = [&](const float4 *X) {
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-          vv[j] = h2f(vc[(i + j) * hd]);
-          pw[j] = pp[i + j];
+          o = o + X[j].x;
+          o = o + X[j].y;
+          o = o + X[j].z;
+          o = o + X[j].w;
         }
+      };
+      int q = 0;
+      if (nq8 > 0) {
+        const float4 *pq = pp;
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-          const float pr = pw[j] * vv[j];
-          o = o + pr;
+        for (int j = 0; j < 8; j++) A[j] = pq[j * P];
+        for (;; q += 16, pq += 16 * P) {
+#pragma unroll
+          for (int j = 0; j < 8; j++) B[j] = pq[(8 + j) * P];
+          __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the adds
+          add8(A);
+          __builtin_amdgcn_sched_barrier(0);
+          if (q + 8 >= nq8) {
+            q += 8;
+            break;
+          }
+#pragma unroll
+          for (int j = 0; j < 8; j++) A[j] = pq[(16 + j) * P];
+          __builtin_amdgcn_sched_barrier(0);
+          add8(B);
+          __builtin_amdgcn_sched_barrier(0);
+          if (q + 16 >= nq8) {
+            q += 16;
+            break;
+          }
         }
       }
-      for (; i < cnt; i++) {
-        const float pr = pp[i] * h2f(vc[i * hd]);
-        o = o + pr;
+      for (; q < nq; q++) {
+        const float4 v = pp[(size_t)q * P];
+        o = o + v.x;
+        o = o + v.y;
+        o = o + v.z;
+        o = o + v.w;
       }
+      const float *tail = reinterpret_cast<const float *>(pp + (size_t)nq * P);
+      for (int e = 0; e < (cnt & 3); e++) o = o + tail[e];
     }
   }
   if (t < hd) a.out[(size_t)m * a.ldo + (size_t)h * hd + t] = o;
-  if (a.out_max) {  // row max |out| for the next linear's int8 quantization (NaN ignored)
-    const float r = block_max256(t < hd ? fabsf(o) : 0.0f, redf);
-    if (t == 0) atomicMax(reinterpret_cast<unsigned int *>(a.out_max + m), __float_as_uint(r));
-  }
 }
 
 // ---------------------------------------------------------------------------
@@ -460,7 +611,7 @@ __global__ __launch_bounds__(256) void math_kernel(int op, const void *in, void 
 
 hipError_t device_math(int op, const void *in, void *out, size_t n, hipStream_t st) {
   if (op < 0 || op > MATH_QUANT1) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(math_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, op, in, out, n);
+  klaunch(math_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, op, in, out, n);
   return hipGetLastError();
 }
 
@@ -470,27 +621,24 @@ hipError_t device_math(int op, const void *in, void *out, size_t n, hipStream_t 
 
 static inline bool al16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
-static int g_gemv_max_blocks = 1024;
-void gemv_set_max_blocks(int n) { g_gemv_max_blocks = n > 0 ? n : 1024; }
+static int g_gemv_max_blocks = 2048;
+void gemv_set_max_blocks(int n) { g_gemv_max_blocks = n > 0 ? n : 2048; }
 int gemv_max_blocks() { return g_gemv_max_blocks; }
 
 int gemv_pick_mt(int M) { return M >= 5 ? 8 : M >= 3 ? 4 : M == 2 ? 2 : 1; }
 
-// lanes per row: the narrow variant (4 or 2 rows per wave) when the whole
-// row fits its register block and there are enough row groups to fill the
-// chip, else one row per wave
-int gemv_pick_lpr(int wt, int epi, int K, int N) {
-  const int chb = wt == WT_I8 ? 16 : 8;
-  const int narrow = wt == WT_I8 ? 16 : 32;
-  const int nch = K / chb;
-  const int rpb = (epi == EPI_SWIGLU ? 2 : 4) * (64 / narrow);
-  if (nch <= narrow * lpr_cpl(narrow) && (N + rpb - 1) / rpb >= 256) return narrow;
-  return 64;
+// row shape: 4 rows per wave when a row fits one pass of 16 lanes, one row
+// per wave otherwise (one pass up to 320 chunks, else the wide loop)
+int gemv_pick_shape(int wt, int K) {
+  const int nch = K / (wt == WT_I8 ? 16 : 8);
+  if (nch <= 16 * (wt == WT_I8 ? 4 : 8)) return GS_NARROW;
+  if (nch <= 64 * 5) return GS_MID;
+  return GS_WIDE;
 }
 
 int gemv_grid_x(const GemvArgs &a, int wt, int epi) {
-  const int lpr = gemv_pick_lpr(wt, epi, a.K, a.N);
-  const int rpb = (epi == EPI_SWIGLU ? 2 : 4) * (64 / lpr);
+  (void)epi;
+  const int rpb = gemv_pick_shape(wt, a.K) == GS_NARROW ? 16 : 4;
   const int ng = (a.N + rpb - 1) / rpb;
   return ng < g_gemv_max_blocks ? ng : g_gemv_max_blocks;
 }
@@ -509,11 +657,16 @@ static int g_max_lds_bytes = 65536;
 
 bool gemv_vector_ok(const GemvArgs &a, int wt, int pro) {
   const int chb = wt == WT_I8 ? 16 : 8;
-  if (a.K <= 0 || a.K % chb || !al16(a.W) || (a.W2 && !al16(a.W2))) return false;
+  if (a.K <= 0 || a.K % chb || a.N <= 0 || !al16(a.W) || (a.W2 && !al16(a.W2))) return false;
   if (pro == PRO_I8 && (a.lda % 16 || !al16(a.A))) return false;
-  if (pro == PRO_F32 && (a.lda % 4 || !al16(a.A))) return false;
+  if (pro != PRO_I8 && (a.lda % 4 || !al16(a.A))) return false;
   if (wt == WT_I8 && pro == PRO_F32) return false;
   if (wt != WT_I8 && (pro == PRO_I8 || pro == PRO_QUANT)) return false;
+  // activation rows the prologue keeps in registers (float4 strips of 1024)
+  if (pro == PRO_QUANT && a.K > 10 * 1024) return false;
+  if (pro == PRO_RMS || pro == PRO_LN) {
+    if (a.K > 4 * 1024 || !al16(a.gamma) || (pro == PRO_LN && !al16(a.beta))) return false;
+  }
   return gemv_lds_bytes(wt, pro, gemv_pick_mt(a.M), a.K) <= (size_t)g_max_lds_bytes;
 }
 
@@ -528,7 +681,7 @@ hipError_t gemv(const GemvArgs &a, int wt, int epi, int pro, hipStream_t s) {
 template <int WT, int EPI>
 static hipError_t launch_generic(const GemvArgs &a, hipStream_t s) {
   const size_t tot = (size_t)a.M * a.N;
-  hipLaunchKernelGGL((gemv_generic_kernel<WT, EPI>), dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s, a);
+  klaunch((gemv_generic_kernel<WT, EPI>), dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
@@ -554,7 +707,7 @@ hipError_t gemv_generic(const GemvArgs &a, int wt, int epi, hipStream_t s) {
 
 hipError_t quant_rows(const float *in, int ldi, int M, int K, int8_t *q, int ldq, float *s,
                       hipStream_t st) {
-  hipLaunchKernelGGL(quant_kernel, dim3(M), dim3(256), 0, st, in, ldi, K, q, ldq, s);
+  klaunch(quant_kernel, dim3(M), dim3(256), 0, st, in, ldi, K, q, ldq, s);
   return hipGetLastError();
 }
 
@@ -563,60 +716,66 @@ hipError_t norm_rows(const float *x, int M, int E, const float *gamma, const flo
                      hipStream_t st) {
   const size_t lds = (size_t)E * sizeof(float);
   if (beta) {
-    if (q) hipLaunchKernelGGL((norm_kernel<true, true>), dim3(M), dim3(256), lds, st, x, E, gamma, beta, eps, h, ldh, q, ldq, qs);
-    else hipLaunchKernelGGL((norm_kernel<true, false>), dim3(M), dim3(256), lds, st, x, E, gamma, beta, eps, h, ldh, q, ldq, qs);
+    if (q) klaunch((norm_kernel<true, true>), dim3(M), dim3(256), lds, st, x, E, gamma, beta, eps, h, ldh, q, ldq, qs);
+    else klaunch((norm_kernel<true, false>), dim3(M), dim3(256), lds, st, x, E, gamma, beta, eps, h, ldh, q, ldq, qs);
   } else {
-    if (q) hipLaunchKernelGGL((norm_kernel<false, true>), dim3(M), dim3(256), lds, st, x, E, gamma, beta, eps, h, ldh, q, ldq, qs);
-    else hipLaunchKernelGGL((norm_kernel<false, false>), dim3(M), dim3(256), lds, st, x, E, gamma, beta, eps, h, ldh, q, ldq, qs);
+    if (q) klaunch((norm_kernel<false, true>), dim3(M), dim3(256), lds, st, x, E, gamma, beta, eps, h, ldh, q, ldq, qs);
+    else klaunch((norm_kernel<false, false>), dim3(M), dim3(256), lds, st, x, E, gamma, beta, eps, h, ldh, q, ldq, qs);
   }
   return hipGetLastError();
 }
 
 hipError_t embed(const uint16_t *wte, const uint16_t *wpe, bool bf16, const int *tok,
-                 const int *pos, int M, int E, float *x, float *slots, int nslots, int ld,
-                 hipStream_t st) {
+                 const int *pos, int M, int E, float *x, hipStream_t st) {
   if (bf16)
-    hipLaunchKernelGGL(embed_kernel<true>, dim3(M), dim3(256), 0, st, wte, wpe, tok, pos, E, x, slots, nslots, ld);
+    klaunch(embed_kernel<true>, dim3(M), dim3(256), 0, st, wte, wpe, tok, pos, E, x);
   else
-    hipLaunchKernelGGL(embed_kernel<false>, dim3(M), dim3(256), 0, st, wte, wpe, tok, pos, E, x, slots, nslots, ld);
+    klaunch(embed_kernel<false>, dim3(M), dim3(256), 0, st, wte, wpe, tok, pos, E, x);
   return hipGetLastError();
 }
 
 hipError_t rope_kv_append(const KvArgs &a, hipStream_t st) {
-  hipLaunchKernelGGL(rope_kv_kernel, dim3(a.M), dim3(256), 0, st, a);
+  klaunch(rope_kv_kernel, dim3(a.M), dim3(256), 0, st, a);
   return hipGetLastError();
 }
 
 size_t attention_lds_bytes(int max_npos, int hd, int vtile) {
-  return ((size_t)((hd + 3) & ~3) + (size_t)((max_npos + 3) & ~3)) * sizeof(float) +
-         (size_t)vtile * hd * sizeof(uint16_t);
+  // q, new k, new v; scores; product tile of vtile/4 quads + 8 quads of slack
+  return ((size_t)3 * ((hd + 3) & ~3) + (size_t)((max_npos + 3) & ~3) +
+          (size_t)(vtile + 32) * attn_pitch(hd, 0)) * sizeof(float);
+}
+
+int attention_max_vtile(int hd, int kv) {
+  if (!attn_vec(hd, kv)) return 512;
+  const int t = 256 * kAttnUnits * 4 / (hd / 8);
+  return t < 512 ? t : 512;
 }
 
 template <int HD>
 static void launch_attn(const AttnArgs &a, size_t lds, hipStream_t st) {
-  if (a.fuse_kv) hipLaunchKernelGGL((attn_kernel<HD, true>), dim3(a.H, a.M), dim3(256), lds, st, a);
-  else hipLaunchKernelGGL((attn_kernel<HD, false>), dim3(a.H, a.M), dim3(256), lds, st, a);
+  if (a.fuse_kv) klaunch((attn_kernel<HD, true>), dim3(a.H, a.M), dim3(256), lds, st, a);
+  else klaunch((attn_kernel<HD, false>), dim3(a.H, a.M), dim3(256), lds, st, a);
 }
 
 hipError_t attention(const AttnArgs &a, hipStream_t st) {
-  const size_t lds = attention_lds_bytes(a.max_npos, a.hd, a.vtile) +
-                     (a.fuse_kv ? (size_t)((a.hd + 3) & ~3) * sizeof(float) : 0);
-  const bool vec = (a.kv & 7) == 0;
-  if (vec && a.hd == 64) launch_attn<64>(a, lds, st);
-  else if (vec && a.hd == 128) launch_attn<128>(a, lds, st);
-  else if (vec && a.hd == 32) launch_attn<32>(a, lds, st);
+  if (a.vtile < 4 || (a.vtile & 3) || a.vtile > attention_max_vtile(a.hd, a.kv) || a.hd > 256)
+    return hipErrorInvalidValue;
+  const size_t lds = attention_lds_bytes(a.max_npos, a.hd, a.vtile);
+  if (attn_vec(a.hd, a.kv) && a.hd == 64) launch_attn<64>(a, lds, st);
+  else if (attn_vec(a.hd, a.kv) && a.hd == 128) launch_attn<128>(a, lds, st);
+  else if (attn_vec(a.hd, a.kv) && a.hd == 32) launch_attn<32>(a, lds, st);
   else launch_attn<0>(a, lds, st);
   return hipGetLastError();
 }
 
 hipError_t argmax_finalize(const unsigned long long *cand, int ncand, const float *logits, int ldl, int rows,
                            int *out, hipStream_t st) {
-  hipLaunchKernelGGL(argmax_finalize_kernel, dim3(rows), dim3(256), 0, st, cand, ncand, logits, ldl, out);
+  klaunch(argmax_finalize_kernel, dim3(rows), dim3(256), 0, st, cand, ncand, logits, ldl, out);
   return hipGetLastError();
 }
 
 hipError_t argmax_rows(const float *logits, int rows, int V, int *out, hipStream_t st) {
-  hipLaunchKernelGGL(argmax_kernel, dim3(rows), dim3(256), 0, st, logits, V, out);
+  klaunch(argmax_kernel, dim3(rows), dim3(256), 0, st, logits, V, out);
   return hipGetLastError();
 }
 

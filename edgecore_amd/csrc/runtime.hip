@@ -75,7 +75,7 @@ extern "C" int ec_init(void) {
       lds > 0)
     g_max_lds = lds;
   EC_HIP(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
-  gemv_set_max_blocks(4 * g_prop.multiProcessorCount);
+  gemv_set_max_blocks(8 * g_prop.multiProcessorCount);
   gemv_set_max_lds(g_max_lds);
   g_inited = 1;
   return 0;
@@ -162,7 +162,7 @@ static std::vector<ProfRec> g_prof;
 
 static int prof_begin(const char *fam, double bytes) {
   if (!g_prof_on) return -1;
-  if (!g_prof_filter.empty() && !strstr(fam, g_prof_filter.c_str())) return -1;
+  if (!g_prof_filter.empty() && strcmp(fam, g_prof_filter.c_str()) != 0) return -1;
   while (g_ev_pool.size() < g_ev_used + 2) {
     hipEvent_t e;
     if (hipEventCreate(&e) != hipSuccess) return -1;
@@ -170,14 +170,20 @@ static int prof_begin(const char *fam, double bytes) {
   }
   const int ev = (int)g_ev_used;
   g_ev_used += 2;
-  (void)hipEventRecord(g_ev_pool[ev], g_stream);
+  g_launch_ev[0] = g_ev_pool[ev];
+  g_launch_ev[1] = g_ev_pool[ev + 1];
   g_prof.push_back({fam, ev, bytes});
   return (int)g_prof.size() - 1;
 }
 
+// the launch inside the EC_LAUNCH call consumed the events; if it did not
+// launch (an error path), the record is dropped
 static void prof_end(int rec) {
   if (rec < 0) return;
-  (void)hipEventRecord(g_ev_pool[g_prof[rec].ev + 1], g_stream);
+  if (g_launch_ev[0]) {
+    g_launch_ev[0] = g_launch_ev[1] = nullptr;
+    g_prof.pop_back();
+  }
 }
 
 extern "C" int ec_prof_start(const char *filter) {
@@ -429,11 +435,7 @@ struct DevModel {
   const uint16_t *lm = nullptr;
   unsigned long long *cand = nullptr;  // LM-head argmax candidates [lm_rows][gemv blocks]
   int ncand = 0;
-  float *rowmax = nullptr;  // [2 * n_layer][mmax]: max |attention out| and |SwiGLU out| per token
 };
-
-// V positions staged per attention tile (LDS: 64 KB at head_dim 64)
-static constexpr int kAttnVTile = 512;
 
 namespace {
 
@@ -478,7 +480,7 @@ struct Loader {
 static void free_dev(DevModel *d) {
   if (!d) return;
   void *ps[] = {d->arena, d->rope, d->d_tok, d->d_pos, d->d_slot, d->d_amax, d->x, d->h, d->qkv,
-                d->att, d->ff, d->aq, d->as, d->logits, d->kc, d->vc, d->cand, d->rowmax};
+                d->att, d->ff, d->aq, d->as, d->logits, d->kc, d->vc, d->cand};
   for (void *p : ps)
     if (p) (void)hipFree(p);
   if (d->h_stage) (void)hipHostFree(d->h_stage);
@@ -736,7 +738,6 @@ static int load_impl(GPT2 *g, const char *path, int batch_cap, int max_ctx) {
   EC_HIP(hipMalloc(&d->d_slot, (size_t)mmax * 4));
   EC_HIP(hipMalloc(&d->d_amax, (size_t)mmax * 4));
   EC_HIP(hipHostMalloc((void **)&d->h_stage, (size_t)mmax * 3 * 4, hipHostMallocDefault));
-  EC_HIP(hipMalloc(&d->rowmax, (size_t)2 * Lc * mmax * sizeof(float)));
   d->ncand = gemv_max_blocks();
   EC_HIP(hipMalloc(&d->cand, (size_t)d->lm_rows * d->ncand * sizeof(unsigned long long)));
   g->ws_x = d->x;
@@ -841,16 +842,17 @@ static int forward_impl(GPT2 *g, const int *tokens, const int *positions, const 
     st[2 * d->mmax + m] = slot;
     if (positions[m] + 1 > max_npos) max_npos = positions[m] + 1;
   }
-  // attention LDS: scores for max_npos positions + a tile of V rows
+  // attention LDS: scores for max_npos positions + a tile of p*v products
   if (hd > 256) return set_err(-1, "head_dim %d above 256 is not supported", hd);
-  const size_t lds_fixed = attention_lds_bytes(max_npos, hd, 0) + (size_t)((hd + 3) & ~3) * sizeof(float);
+  const size_t lds_fixed = attention_lds_bytes(max_npos, hd, 0);
   int vtile = 0;
   if (lds_fixed < (size_t)g_max_lds) {
-    const size_t room = ((size_t)g_max_lds - lds_fixed) / ((size_t)hd * sizeof(uint16_t));
-    vtile = (int)(room < (size_t)kAttnVTile ? room : (size_t)kAttnVTile) & ~7;
-    if (vtile > ((max_npos + 7) & ~7)) vtile = (max_npos + 7) & ~7;
+    const size_t room = ((size_t)g_max_lds - lds_fixed) / ((size_t)attn_pitch(hd, kv) * sizeof(float));
+    const size_t cap = (size_t)attention_max_vtile(hd, kv);
+    vtile = (int)(room < cap ? room : cap) & ~3;
+    if (vtile > ((max_npos + 3) & ~3)) vtile = (max_npos + 3) & ~3;
   }
-  if (vtile < 8)
+  if (vtile < 4)
     return set_err(-1, "position %d needs more LDS for attention scores than the device has (%d bytes)",
                    max_npos - 1, g_max_lds);
   hipStream_t s = g_stream;
@@ -859,7 +861,7 @@ static int forward_impl(GPT2 *g, const int *tokens, const int *positions, const 
   EC_HIP(hipMemcpyAsync(d->d_slot, st + 2 * d->mmax, (size_t)M * 4, hipMemcpyHostToDevice, s));
 
   EC_LAUNCH("embed", (double)M * E * (g->wpe ? 8 : 6),
-            embed(g->wte, g->wpe, bf16, d->d_tok, d->d_pos, M, E, d->x, d->rowmax, 2 * g->n_layer, d->mmax, s));
+            embed(g->wte, g->wpe, bf16, d->d_tok, d->d_pos, M, E, d->x, s));
   // RoPE and the KV append run inside attention when no token of the batch
   // reads another token's slot (decode); otherwise as their own kernel first
   bool distinct = true;
@@ -885,8 +887,6 @@ static int forward_impl(GPT2 *g, const int *tokens, const int *positions, const 
       const int epi = (!i8 && W.bqkv) ? EPI_BIAS : EPI_STORE;
       if ((r = linear(g, d, "gemv_qkv", a, wt, epi, pro_norm, s))) return r;
     }
-    float *att_max = i8 ? d->rowmax + (size_t)(2 * l) * d->mmax : nullptr;
-    float *ff_max = (i8 && qwen) ? d->rowmax + (size_t)(2 * l + 1) * d->mmax : nullptr;
     float *kq = d->qkv + E, *vq = d->qkv + E + (qwen ? kv : E);
     if (!distinct) {  // RoPE (Qwen2) + fp16 KV append
       KvArgs ka{d->qkv, kq, vq, ldq, ldq, H, g->n_kv_head, hd, kv, qwen ? d->rope : nullptr, d->half,
@@ -895,20 +895,19 @@ static int forward_impl(GPT2 *g, const int *tokens, const int *positions, const 
     }
     AttnArgs aa{d->qkv, ldq, kcl, vcl, d->att, E, d->d_pos, d->d_slot, H, g->n_kv_head, hd, kv,
                 d->eff_ctx, qwen ? g->sliding_window : 0, 1.0 / sqrt((double)hd), M, max_npos, vtile,
-                distinct ? 1 : 0, kq, vq, ldq, (distinct && qwen) ? d->rope : nullptr, d->half, kcl, vcl,
-                att_max};
+                distinct ? 1 : 0, kq, vq, ldq, (distinct && qwen) ? d->rope : nullptr, d->half, kcl, vcl};
     EC_LAUNCH("attention", abytes, attention(aa, s));
     // output projection + residual
     {
       GemvArgs a{d->att, E, nullptr, nullptr, nullptr, 0.0, W.wo, nullptr, W.so, nullptr, W.bo, d->x, E, M, E, E,
-                 nullptr, att_max, nullptr};
+                 nullptr};
       const int epi = i8 ? EPI_RESID : (W.bo ? EPI_BIAS_RESID : EPI_RESID);
       if ((r = linear(g, d, "gemv_o", a, wt, epi, i8 ? PRO_QUANT : PRO_F32, s))) return r;
     }
     // MLP up: SwiGLU gate/up (Qwen2) or fc + GELU (GPT-2), norm fused
     if (qwen) {
       GemvArgs a{d->x, E, nullptr, W.ln2_g, nullptr, g->eps, W.wg, W.wu, W.sg, W.su, nullptr, d->ff, F, M, E, F,
-                 nullptr, nullptr, ff_max};
+                 nullptr};
       if ((r = linear(g, d, "gemv_gateup", a, wt, EPI_SWIGLU, PRO_RMS, s))) return r;
     } else {
       GemvArgs a{d->x, E, nullptr, W.ln2_g, W.ln2_b, g->eps, W.wfc, nullptr, W.sfc, nullptr, W.bfc, d->ff, F, M,
@@ -918,7 +917,7 @@ static int forward_impl(GPT2 *g, const int *tokens, const int *positions, const 
     // MLP down + residual
     {
       GemvArgs a{d->ff, F, nullptr, nullptr, nullptr, 0.0, W.wd, nullptr, W.sd, nullptr, W.bd, d->x, E, M, F, E,
-                 nullptr, ff_max, nullptr};
+                 nullptr};
       const int epi = i8 ? EPI_RESID : (W.bd ? EPI_BIAS_RESID : EPI_RESID);
       if ((r = linear(g, d, "gemv_down", a, wt, epi, i8 ? PRO_QUANT : PRO_F32, s))) return r;
     }

@@ -323,8 +323,9 @@ int ec_memcpy_d2h(void *dst, const void *src, size_t bytes);
 int ec_memset_dev(void *dst, int value, size_t bytes);
 
 /* Per-kernel timing.  While enabled, every launch of a kernel whose family
- * name contains `filter` ("" = all) is bracketed by HIP events recorded on
- * the stream the kernel runs on.  ec_prof_stop synchronises and writes a JSON
+ * name equals `filter` ("" = all) records its start and stop time on HIP
+ * events (hipExtLaunchKernel: the dispatch's own timestamps, on the stream the
+ * kernel runs on).  ec_prof_stop synchronises and writes a JSON
  * array of {"kernel", "launches", "total_us", "avg_us", "bytes_per_launch",
  * "gbps"} (bytes are the algorithmic bytes of each launch) into buf and
  * returns its length, or a negative error code. */

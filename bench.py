@@ -9,14 +9,16 @@ token: the forward at M=1 plus the GPU argmax and the copy of the id back to
 the host.  The prompt is prefilled first (reported as prefill tok/s, untimed),
 then W warmup steps, then K timed steps bracketed by stream synchronisation.
 
-Kernel durations come from HIP events that a kernel launch records itself
-(hipExtLaunchKernel start/stop events on the library's stream, ec_prof_*).
-Three passes of the same K steps run: every launch timed (the per-kernel
-table, which names the family with the largest total time), then the timed
-region proper with events on that family's launches only (value, ms_per_step
-and the roofline object), then no events at all (ms_per_step_without_events).
-roofline_int8_gemv is computed from the first pass for the int8-weight GEMV
-family with the largest total time.  The
+Two passes of the same K steps run, each after the same prefill and warmup.
+In the first, every kernel launch records its own dispatch start and stop on
+HIP events (hipExtLaunchKernel on the library's stream, ec_prof_*): that
+gives the per-kernel table and the launch durations of the roofline object
+(the family with the largest total time; roofline_int8_gemv: the int8-weight
+GEMV family with the largest total time).  The second is the timed region
+proper (value, ms_per_step), with nothing but the work.  The launch durations
+agree with rocprofv3's kernel trace of the same command (profiles/), and
+both passes must produce the same tokens.  roofline.traffic is the HBM bytes
+per launch measured with rocprofv3 counters (profiles/traffic.json).  The
 CPU baseline is the reference runtime built from its own sources
 (oracle/_ref/edgecore-runtime) on the same model file and prompt, timed on
 the host cores.
@@ -112,6 +114,9 @@ def main() -> int:
     ap.add_argument("--cache", default=os.environ.get("EDGECORE_BENCH_DIR", "/tmp/edgecore_bench"))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-tokens", type=int, default=16)
+    ap.add_argument("--copy-bytes", type=int, default=0,
+                    help="also run the plain copy kernel (ec_device_math op 6) 8 times on this many "
+                         "bytes: the reference for HBM traffic counters and achievable bandwidth")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -122,6 +127,22 @@ def main() -> int:
     import numpy as np
 
     import edgecore_amd as ec
+
+    copy = None
+    if args.copy_bytes:
+        n = args.copy_bytes // 16 * 4  # floats, a multiple of 4
+        src, dst = ec.DeviceBuffer(n * 4), ec.DeviceBuffer(n * 4)
+        L0 = ec.lib()
+        L0.ec_prof_start(b"copy")
+        for _ in range(8):
+            if L0.ec_device_math(6, src.ptr, dst.ptr, n):
+                raise SystemExit(f"bench.py: copy kernel failed: {ec.last_error()}")
+        buf = __import__("ctypes").create_string_buffer(1 << 12)
+        L0.ec_prof_stop(buf, len(buf))
+        row = json.loads(buf.value.decode())[0]
+        copy = {"bytes_per_launch": 8 * n, "avg_us": row["avg_us"], "gbps": round(8 * n / (row["avg_us"] * 1e3), 1)}
+        src.close()
+        dst.close()
 
     model, prompt_file = ensure_inputs(Path(args.cache))
     prompt = ec.read_ids(prompt_file)
@@ -168,32 +189,39 @@ def main() -> int:
             kern = json.loads(buf.value.decode()) if n > 0 else []
         return elapsed, kern, ids
 
-    # 1. every launch timed (per-kernel table, names the dominant family)
-    _, kernels, ids_all = decode_pass("")
-    dom_name = max(kernels, key=lambda k: k["total_us"])["kernel"] if kernels else ""
-    # 2. the timed region: events on the dominant family's launches only
-    elapsed, dom_rows, ids = decode_pass(dom_name)
-    # 3. the same steps with no events at all
-    elapsed_clean, _, ids_clean = decode_pass(None)
-    if not (ids == ids_all == ids_clean):
-        raise SystemExit("bench.py: decode passes produced different tokens")
+    # 1. K steps with every launch recording its own dispatch timestamps
+    #    (per-kernel table and the roofline's launch durations)
+    elapsed_ev, kernels, ids_ev = decode_pass("")
+    # 2. the timed region: the same K steps, nothing but the work
+    elapsed, _, ids = decode_pass(None)
+    if ids != ids_ev:
+        raise SystemExit("bench.py: the two decode passes produced different tokens")
     m.close()
 
     tot = sum(k["total_us"] for k in kernels) or 1.0
     for k in kernels:
         k["share"] = round(k["total_us"] / tot, 4)
         k["hbm_frac"] = round(k["gbps"] / HBM_PEAK_GBPS, 4)
-    dom = dom_rows[0] if dom_rows else None
+    dom = max(kernels, key=lambda k: k["total_us"]) if kernels else None
     # the int8-weight GEMVs of the layers (the LM head is tied fp16)
     int8 = [k for k in kernels if k["kernel"] in ("gemv_qkv", "gemv_o", "gemv_gateup", "gemv_down")]
     dom_i8 = max(int8, key=lambda k: k["total_us"]) if int8 else None
+
+    # HBM bytes per launch measured with rocprofv3 counters on this workload
+    # (profiles/traffic.json: FETCH_SIZE + WRITE_SIZE of the decode launches,
+    # scaled by the copy kernel's counter-to-true-bytes factor)
+    traffic = {}
+    tpath = REPO / "profiles" / "traffic.json"
+    if tpath.exists():
+        traffic = json.loads(tpath.read_text()).get("families", {})
 
     def roof(k):
         if not k:
             return None
         ach = k["bytes_per_launch"] / (k["avg_us"] * 1e3)
+        t = traffic.get(k["kernel"], {}).get("hbm_bytes_per_launch")
         return {"kernel": k["kernel"], "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBPS,
-                "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBPS, 4), "traffic": None,
+                "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBPS, 4), "traffic": t,
                 "bytes_per_launch": k["bytes_per_launch"], "avg_us": k["avg_us"]}
 
     # algorithmic bytes of one decode step (weights once + fp16 KV read), mean position
@@ -214,10 +242,11 @@ def main() -> int:
         "roofline_int8_gemv": roof(dom_i8),
         "decode_bytes_per_step": int(step_bytes),
         "decode_effective_gbps": round(step_bytes * value / 1e9, 1),
-        "ms_per_step_without_events": round(elapsed_clean / K * 1e3, 4),
+        "ms_per_step_with_kernel_timestamps": round(elapsed_ev / K * 1e3, 4),
         "prefill_tok_s": round(PROMPT / ttft, 1), "ttft_ms": round(ttft * 1e3, 3),
+        "copy_kernel": copy,
         "kernels": kernels,
-        "kernels_note": "per-launch start/stop timestamps of every kernel in a separate pass of the same K steps",
+        "kernels_note": "per-launch dispatch start/stop timestamps of every kernel, second pass of the same K steps",
         "device": ec.device_info(),
     }
     if not args.no_cpu_baseline:

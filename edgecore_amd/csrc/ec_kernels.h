@@ -143,6 +143,7 @@ struct AttnArgs {
   const double2 *cs;   // RoPE table [pos][half] or null (GPT-2)
   int half;
   uint16_t *kc_w, *vc_w;  // writable views of kc / vc for the append
+  int xcd_r;  // set by attention(): query heads per KV group when the launch is XCD-grouped, else 0
 };
 hipError_t attention(const AttnArgs &a, hipStream_t st);
 // V units (4 positions x 8 elements) per thread held in registers
@@ -176,7 +177,7 @@ hipError_t argmax_finalize(const unsigned long long *cand, int ncand, const floa
                            int ldl, int rows, int *out, hipStream_t st);
 
 // elementwise device math (ec_device_math)
-enum { MATH_EXPF = 0, MATH_SILU = 1, MATH_GELU = 2, MATH_F32_TO_F16 = 3, MATH_F16_TO_F32 = 4, MATH_QUANT1 = 5 };
+enum { MATH_EXPF = 0, MATH_SILU = 1, MATH_GELU = 2, MATH_F32_TO_F16 = 3, MATH_F16_TO_F32 = 4, MATH_QUANT1 = 5, MATH_COPY = 6 };
 hipError_t device_math(int op, const void *in, void *out, size_t n, hipStream_t st);
 
 }  // namespace ec

@@ -11,6 +11,8 @@ namespace ec {
 
 hipEvent_t g_launch_ev[2] = {nullptr, nullptr};
 
+static inline bool al16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
 // ---------------------------------------------------------------------------
 // generic GEMV (any K, any alignment, every epilogue): one thread per output
 // element, activations given as int8 rows + scales (PRO_I8) or fp32 rows
@@ -242,7 +244,16 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   __shared__ double redd[4];
   __shared__ uint64_t etab[32];  // expf table
   constexpr int CPR = HD > 0 ? HD / 8 : 1;         // 16-byte chunks per K/V row
-  const int h = blockIdx.x, m = blockIdx.y, t = threadIdx.x;
+  const int m = blockIdx.y, t = threadIdx.x;
+  int h = blockIdx.x;
+  if (a.xcd_r) {
+    // XCD-aware launch: blocks are dispatched to the 8 XCDs round-robin, so
+    // block x runs on XCD x % 8; group g's heads use blocks g, g + 8, ...
+    // and share that XCD's L2 for the group's K/V rows
+    const int g = blockIdx.x & 7, j = blockIdx.x >> 3;
+    if (g >= a.KVH || j >= a.xcd_r) return;
+    h = g * a.xcd_r + j;
+  }
   const int pos = ld_uniform(a.pos + m), slot = ld_uniform(a.slot + m);
   const uint64_t et = ec_exp2_32[t & 31];
   const int kvh = h * a.KVH / a.H;
@@ -591,6 +602,13 @@ __global__ __launch_bounds__(256) void argmax_finalize_kernel(const unsigned lon
 // elementwise device math, for checking the device arithmetic from tests
 // ---------------------------------------------------------------------------
 
+// plain copy of n4 16-byte elements (grid-stride): the reference kernel for
+// HBM traffic counters and achievable bandwidth
+__global__ __launch_bounds__(256) void copy_kernel(const v4u *in, v4u *out, size_t n4) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (size_t)gridDim.x * 256)
+    __builtin_nontemporal_store(__builtin_nontemporal_load(in + i), out + i);
+}
+
 __global__ __launch_bounds__(256) void math_kernel(int op, const void *in, void *out, size_t n) {
   const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= n) return;
@@ -605,12 +623,19 @@ __global__ __launch_bounds__(256) void math_kernel(int op, const void *in, void 
   case MATH_GELU: reinterpret_cast<float *>(out)[i] = gelu_new(x); break;
   case MATH_F32_TO_F16: reinterpret_cast<uint16_t *>(out)[i] = f2h(x); break;
   case MATH_QUANT1: reinterpret_cast<int8_t *>(out)[i] = quant1(x, 1.0f); break;
+  case MATH_COPY: reinterpret_cast<float *>(out)[i] = x; break;
   default: break;
   }
 }
 
 hipError_t device_math(int op, const void *in, void *out, size_t n, hipStream_t st) {
-  if (op < 0 || op > MATH_QUANT1) return hipErrorInvalidValue;
+  if (op < 0 || op > MATH_COPY) return hipErrorInvalidValue;
+  if (op == MATH_COPY && n % 4 == 0 && al16(in) && al16(out)) {
+    const size_t n4 = n / 4, blocks = (n4 + 255) / 256;
+    klaunch(copy_kernel, dim3((unsigned)(blocks < 2048 ? blocks : 2048)), dim3(256), 0, st,
+            reinterpret_cast<const v4u *>(in), reinterpret_cast<v4u *>(out), n4);
+    return hipGetLastError();
+  }
   klaunch(math_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, op, in, out, n);
   return hipGetLastError();
 }
@@ -619,7 +644,6 @@ hipError_t device_math(int op, const void *in, void *out, size_t n, hipStream_t 
 // launchers
 // ---------------------------------------------------------------------------
 
-static inline bool al16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
 static int g_gemv_max_blocks = 2048;
 void gemv_set_max_blocks(int n) { g_gemv_max_blocks = n > 0 ? n : 2048; }
@@ -752,9 +776,13 @@ int attention_max_vtile(int hd, int kv) {
 }
 
 template <int HD>
-static void launch_attn(const AttnArgs &a, size_t lds, hipStream_t st) {
-  if (a.fuse_kv) klaunch((attn_kernel<HD, true>), dim3(a.H, a.M), dim3(256), lds, st, a);
-  else klaunch((attn_kernel<HD, false>), dim3(a.H, a.M), dim3(256), lds, st, a);
+static void launch_attn(AttnArgs a, size_t lds, hipStream_t st) {
+  // grouped-query heads: one XCD per KV group (8 XCDs, block x -> XCD x % 8)
+  const int r = a.H / a.KVH;
+  a.xcd_r = (a.KVH <= 8 && a.H % a.KVH == 0 && r > 1) ? r : 0;
+  const dim3 grid(a.xcd_r ? 8 * r : a.H, a.M);
+  if (a.fuse_kv) klaunch((attn_kernel<HD, true>), grid, dim3(256), lds, st, a);
+  else klaunch((attn_kernel<HD, false>), grid, dim3(256), lds, st, a);
 }
 
 hipError_t attention(const AttnArgs &a, hipStream_t st) {

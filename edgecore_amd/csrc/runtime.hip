@@ -309,7 +309,7 @@ extern "C" int ec_device_math(int op, const void *in, void *out, size_t n) {
   EC_INIT();
   if (!in || !out) return set_err(-1, "ec_device_math: null pointer");
   if (n == 0) return 0;
-  EC_LAUNCH("math", 8.0 * n, device_math(op, in, out, n, g_stream));
+  EC_LAUNCH(op == MATH_COPY ? "copy" : "math", 8.0 * n, device_math(op, in, out, n, g_stream));
   EC_HIP(hipStreamSynchronize(g_stream));
   return 0;
 }

@@ -336,7 +336,9 @@ int ec_prof_stop(char *buf, int len);
  * it against the host: op 0 expf (the reference's expf), 1 SiLU
  * (src/gpt2.c:587-590), 2 GELU (src/gpt2.c:393-396), 3 fp32 -> fp16 bits
  * (round to nearest even), 4 fp16 bits -> fp32, 5 int8 quantization with
- * scale 1 (src/gpt2.c:456-459).  fp32 in/out except as noted.  0 or <0. */
+ * scale 1 (src/gpt2.c:456-459), 6 copy (16-byte loads and stores when n is a
+ * multiple of 4 and both pointers are 16-byte aligned: the reference kernel
+ * for HBM traffic counters).  fp32 in/out except as noted.  0 or <0. */
 int ec_device_math(int op, const void *in, void *out, size_t n);
 
 /* int8 weight packing of edgecore/ecm.py:50-59 (float64 max|w|/127, zero row

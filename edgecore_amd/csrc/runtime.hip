@@ -38,6 +38,8 @@ static int g_device = 0;
 static hipStream_t g_stream = nullptr;
 static hipDeviceProp_t g_prop;
 static int g_max_lds = 65536;
+// replay the single-token greedy step as a HIP graph (EDGECORE_GRAPHS=0 turns it off)
+static bool g_use_graphs = true;
 
 static int set_err(int code, const char *fmt, ...) {
   va_list ap;
@@ -75,6 +77,8 @@ extern "C" int ec_init(void) {
       lds > 0)
     g_max_lds = lds;
   EC_HIP(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
+  const char *gr = getenv("EDGECORE_GRAPHS");
+  g_use_graphs = !(gr && !strcmp(gr, "0"));
   gemv_set_max_blocks(8 * g_prop.multiProcessorCount);
   gemv_set_max_lds(g_max_lds);
   g_inited = 1;
@@ -435,6 +439,10 @@ struct DevModel {
   const uint16_t *lm = nullptr;
   unsigned long long *cand = nullptr;  // LM-head argmax candidates [lm_rows][gemv blocks]
   int ncand = 0;
+  // single-token greedy decode step captured as one HIP graph (see forward_impl)
+  hipGraphExec_t step_graph = nullptr;
+  int step_bucket = 0;  // the graph's attention LDS covers positions < step_bucket
+  int *h_amax = nullptr;  // pinned: the graph's argmax output
 };
 
 namespace {
@@ -484,6 +492,8 @@ static void free_dev(DevModel *d) {
   for (void *p : ps)
     if (p) (void)hipFree(p);
   if (d->h_stage) (void)hipHostFree(d->h_stage);
+  if (d->h_amax) (void)hipHostFree(d->h_amax);
+  if (d->step_graph) (void)hipGraphExecDestroy(d->step_graph);
   delete d;
 }
 
@@ -738,6 +748,7 @@ static int load_impl(GPT2 *g, const char *path, int batch_cap, int max_ctx) {
   EC_HIP(hipMalloc(&d->d_slot, (size_t)mmax * 4));
   EC_HIP(hipMalloc(&d->d_amax, (size_t)mmax * 4));
   EC_HIP(hipHostMalloc((void **)&d->h_stage, (size_t)mmax * 3 * 4, hipHostMallocDefault));
+  EC_HIP(hipHostMalloc((void **)&d->h_amax, 4 * sizeof(int), hipHostMallocDefault));
   d->ncand = gemv_max_blocks();
   EC_HIP(hipMalloc(&d->cand, (size_t)d->lm_rows * d->ncand * sizeof(unsigned long long)));
   g->ws_x = d->x;
@@ -816,66 +827,44 @@ static int linear(GPT2 *g, DevModel *d, const char *fam, GemvArgs a, int wt, int
   return 0;
 }
 
-static int forward_impl(GPT2 *g, const int *tokens, const int *positions, const int *seqs, int M,
-                        int lm_from, float *logits, int *argmax) {
-  EC_INIT();
-  DevModel *d = (DevModel *)g->dev;
-  if (!d) return set_err(-1, "model not loaded");
-  if (M < 1 || M > d->mmax) return set_err(-1, "M=%d outside [1, %d]", M, d->mmax);
-  if (lm_from < 0 || lm_from > M) return set_err(-1, "lm_from=%d outside [0, %d]", lm_from, M);
-  if (!tokens || !positions) return set_err(-1, "null tokens/positions");
+// positions per attention product tile for launches with positions < max_npos
+// (multiple of 4); below 4 the device LDS cannot hold the scores
+static int attn_vtile(int max_npos, int hd, int kv) {
+  const size_t lds_fixed = attention_lds_bytes(max_npos, hd, 0);
+  if (lds_fixed >= (size_t)g_max_lds) return 0;
+  const size_t room = ((size_t)g_max_lds - lds_fixed) / ((size_t)attn_pitch(hd, kv) * sizeof(float));
+  const size_t cap = (size_t)attention_max_vtile(hd, kv);
+  int vtile = (int)(room < cap ? room : cap) & ~3;
+  if (vtile > ((max_npos + 3) & ~3)) vtile = (max_npos + 3) & ~3;
+  return vtile;
+}
+
+// Enqueue one forward on stream s: the copy of the staged tokens / positions
+// / slots, every kernel, and the copies of logits and argmax ids into the
+// given host buffers (either may be null).  max_npos bounds pos + 1 over the
+// batch and sizes the attention LDS; distinct: no two tokens share a slot
+// (RoPE and the KV append then run inside attention); abytes: algorithmic
+// attention bytes, for the profiler only.
+static int enqueue_forward(GPT2 *g, DevModel *d, int M, int lm_from, bool distinct, int max_npos,
+                           double abytes, float *logits, int *argmax, hipStream_t s) {
   const int E = g->n_embd, H = g->n_head, V = g->vocab, kv = g->n_kv_embd, hd = g->head_dim;
   const bool qwen = g->arch == ARCH_QWEN2, i8 = g->precision == 0, bf16 = g->precision == 2;
   const int wt = i8 ? WT_I8 : (bf16 ? WT_BF16 : WT_F16);
   const int pro_norm = qwen ? PRO_RMS : PRO_LN;
-  int *st = d->h_stage;
-  int max_npos = 0;
-  for (int m = 0; m < M; m++) {
-    if (tokens[m] < 0 || tokens[m] >= V) return set_err(-1, "token %d at row %d outside [0, %d)", tokens[m], m, V);
-    if (positions[m] < 0 || positions[m] >= d->eff_ctx)
-      return set_err(-1, "position %d at row %d outside [0, %d)", positions[m], m, d->eff_ctx);
-    int slot = seqs ? seqs[m] : m;
-    if (slot < 0) return set_err(-1, "negative slot %d at row %d", slot, m);
-    if (slot >= g->batch_cap) slot = g->batch_cap - 1;  // src/gpt2.c:512-513
-    st[m] = tokens[m];
-    st[d->mmax + m] = positions[m];
-    st[2 * d->mmax + m] = slot;
-    if (positions[m] + 1 > max_npos) max_npos = positions[m] + 1;
-  }
-  // attention LDS: scores for max_npos positions + a tile of p*v products
-  if (hd > 256) return set_err(-1, "head_dim %d above 256 is not supported", hd);
-  const size_t lds_fixed = attention_lds_bytes(max_npos, hd, 0);
-  int vtile = 0;
-  if (lds_fixed < (size_t)g_max_lds) {
-    const size_t room = ((size_t)g_max_lds - lds_fixed) / ((size_t)attn_pitch(hd, kv) * sizeof(float));
-    const size_t cap = (size_t)attention_max_vtile(hd, kv);
-    vtile = (int)(room < cap ? room : cap) & ~3;
-    if (vtile > ((max_npos + 3) & ~3)) vtile = (max_npos + 3) & ~3;
-  }
+  const int vtile = attn_vtile(max_npos, hd, kv);
   if (vtile < 4)
     return set_err(-1, "position %d needs more LDS for attention scores than the device has (%d bytes)",
                    max_npos - 1, g_max_lds);
-  hipStream_t s = g_stream;
+  const int *st = d->h_stage;
   EC_HIP(hipMemcpyAsync(d->d_tok, st, (size_t)M * 4, hipMemcpyHostToDevice, s));
   EC_HIP(hipMemcpyAsync(d->d_pos, st + d->mmax, (size_t)M * 4, hipMemcpyHostToDevice, s));
   EC_HIP(hipMemcpyAsync(d->d_slot, st + 2 * d->mmax, (size_t)M * 4, hipMemcpyHostToDevice, s));
 
   EC_LAUNCH("embed", (double)M * E * (g->wpe ? 8 : 6),
             embed(g->wte, g->wpe, bf16, d->d_tok, d->d_pos, M, E, d->x, s));
-  // RoPE and the KV append run inside attention when no token of the batch
-  // reads another token's slot (decode); otherwise as their own kernel first
-  bool distinct = true;
-  for (int m = 0; m < M && distinct; m++)
-    for (int j = 0; j < m; j++)
-      if (st[2 * d->mmax + j] == st[2 * d->mmax + m]) {
-        distinct = false;
-        break;
-      }
 
   const int F = d->F, ldq = d->qkv_ld;
   const int nqkv = qwen ? E + 2 * kv : 3 * E;
-  double abytes = 0;
-  for (int m = 0; m < M; m++) abytes += (double)(positions[m] + 1) * kv * 4 + 8.0 * E;
   int r;
   for (int l = 0; l < g->n_layer; l++) {
     const LayerDev &W = d->L[l];
@@ -946,6 +935,84 @@ static int forward_impl(GPT2 *g, const int *tokens, const int *positions, const 
   }
   if (argmax && lm_from < M)
     EC_HIP(hipMemcpyAsync(argmax, d->d_amax, (size_t)(M - lm_from) * 4, hipMemcpyDeviceToHost, s));
+  return 0;
+}
+
+static int forward_impl(GPT2 *g, const int *tokens, const int *positions, const int *seqs, int M,
+                        int lm_from, float *logits, int *argmax) {
+  EC_INIT();
+  DevModel *d = (DevModel *)g->dev;
+  if (!d) return set_err(-1, "model not loaded");
+  if (M < 1 || M > d->mmax) return set_err(-1, "M=%d outside [1, %d]", M, d->mmax);
+  if (lm_from < 0 || lm_from > M) return set_err(-1, "lm_from=%d outside [0, %d]", lm_from, M);
+  if (!tokens || !positions) return set_err(-1, "null tokens/positions");
+  const int E = g->n_embd, V = g->vocab, kv = g->n_kv_embd, hd = g->head_dim;
+  int *st = d->h_stage;
+  int max_npos = 0;
+  for (int m = 0; m < M; m++) {
+    if (tokens[m] < 0 || tokens[m] >= V) return set_err(-1, "token %d at row %d outside [0, %d)", tokens[m], m, V);
+    if (positions[m] < 0 || positions[m] >= d->eff_ctx)
+      return set_err(-1, "position %d at row %d outside [0, %d)", positions[m], m, d->eff_ctx);
+    int slot = seqs ? seqs[m] : m;
+    if (slot < 0) return set_err(-1, "negative slot %d at row %d", slot, m);
+    if (slot >= g->batch_cap) slot = g->batch_cap - 1;  // src/gpt2.c:512-513
+    st[m] = tokens[m];
+    st[d->mmax + m] = positions[m];
+    st[2 * d->mmax + m] = slot;
+    if (positions[m] + 1 > max_npos) max_npos = positions[m] + 1;
+  }
+  if (hd > 256) return set_err(-1, "head_dim %d above 256 is not supported", hd);
+  if (attn_vtile(max_npos, hd, kv) < 4)
+    return set_err(-1, "position %d needs more LDS for attention scores than the device has (%d bytes)",
+                   max_npos - 1, g_max_lds);
+  // RoPE and the KV append run inside attention when no token of the batch
+  // reads another token's slot (decode); otherwise as their own kernel first
+  bool distinct = true;
+  for (int m = 0; m < M && distinct; m++)
+    for (int j = 0; j < m; j++)
+      if (st[2 * d->mmax + j] == st[2 * d->mmax + m]) {
+        distinct = false;
+        break;
+      }
+  double abytes = 0;
+  for (int m = 0; m < M; m++) abytes += (double)(positions[m] + 1) * kv * 4 + 8.0 * E;
+  hipStream_t s = g_stream;
+
+  // The single-token greedy step (the decode loop) runs as one HIP graph: the
+  // staging copies, every kernel and the copy of the argmax id, captured once
+  // per 512-position bucket (the attention LDS is sized for the bucket; the
+  // kernels read position and slot from device memory).  The host writes the
+  // token / position / slot into the pinned stage before each replay.
+  int bucket = (max_npos + 511) / 512 * 512;
+  if (bucket > d->eff_ctx) bucket = d->eff_ctx;
+  if (M == 1 && lm_from == 0 && argmax && !logits && !g_prof_on && g_use_graphs &&
+      attn_vtile(bucket, hd, kv) >= 4) {
+    if (!d->step_graph || d->step_bucket != bucket) {
+      if (d->step_graph) {
+        EC_HIP(hipGraphExecDestroy(d->step_graph));
+        d->step_graph = nullptr;
+      }
+      EC_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+      const int r = enqueue_forward(g, d, 1, 0, true, bucket, abytes, nullptr, d->h_amax, s);
+      hipGraph_t graph = nullptr;
+      const hipError_t e = hipStreamEndCapture(s, &graph);
+      if (r) {
+        if (graph) (void)hipGraphDestroy(graph);
+        return r;
+      }
+      EC_HIP(e);
+      const hipError_t ei = hipGraphInstantiate(&d->step_graph, graph, nullptr, nullptr, 0);
+      (void)hipGraphDestroy(graph);
+      EC_HIP(ei);
+      d->step_bucket = bucket;
+    }
+    EC_HIP(hipGraphLaunch(d->step_graph, s));
+    EC_HIP(hipStreamSynchronize(s));
+    argmax[0] = d->h_amax[0];
+    return 0;
+  }
+  const int r = enqueue_forward(g, d, M, lm_from, distinct, max_npos, abytes, logits, argmax, s);
+  if (r) return r;
   EC_HIP(hipStreamSynchronize(s));
   return 0;
 }

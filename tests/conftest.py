@@ -26,6 +26,9 @@ MODEL_SPECS = {
     # hd 128, GQA 6:1, an odd vocabulary and intermediate size
     "qwen2-hd128-int8": dict(arch="qwen2", layers=3, embd=768, heads=6, kv_heads=1, ffn=1000,
                              ctx=512, vocab=4099, precision="int8", tie=1),
+    # long context: decode crosses 512-position boundaries
+    "qwen2-long-int8": dict(arch="qwen2", layers=2, embd=128, heads=4, kv_heads=2, ffn=256,
+                            ctx=1536, vocab=1000, precision="int8"),
     # reference smoke-test shape (scripts/make_synthetic.py defaults), byte vocab
     "smoke-gpt2-int8": dict(arch="gpt2", layers=2, embd=32, heads=2, ctx=64, vocab=256,
                             precision="int8"),

@@ -109,3 +109,36 @@ def test_invalid_inputs_rejected_before_launch(make_model):
         m.kv_reset()
         lg, _ = m.forward([1, 2], [0, 1], [0, 0])
         assert np.isfinite(lg).all()
+
+
+@pytest.mark.parametrize("name", ["tiny-qwen2-int8", "tiny-gpt2-fp16", "tiny-qwen2-bf16", "qwen2-hd128-int8"])
+def test_graph_decode_equals_direct_and_oracle(make_model, name):
+    """The single-token greedy step replays a captured HIP graph (argmax only);
+    asking for logits takes the direct launches.  Both must give the oracle's ids."""
+    path = make_model(name)
+    with ec.Model(path, 1, 0) as m:
+        prompt = prompt_ids(8, m.vocab, seed=3)
+        ids_graph, _ = m.generate(prompt, 32, want_logits=False)
+        ids_direct, _ = m.generate(prompt, 32, want_logits=True)
+        ids_again, _ = m.generate(prompt, 32, want_logits=False)  # the cached graph, after kv_reset
+    oids, _ = oracle.OracleModel(path, 1, 0).generate(prompt, 32)
+    assert np.array_equal(ids_graph, ids_direct)
+    assert np.array_equal(ids_graph, ids_again)
+    assert np.array_equal(ids_graph, oids)
+
+
+def test_graph_recaptured_across_position_buckets(make_model):
+    """Decode positions 1000..1039 cross the 1024 bucket (the graph is captured
+    again with a larger attention LDS); two models keep separate graphs."""
+    path = make_model("qwen2-long-int8")
+    other = make_model("tiny-qwen2-int8")
+    with ec.Model(path, 1, 0) as m, ec.Model(other, 1, 0) as m2:
+        prompt = prompt_ids(1000, m.vocab, seed=4)
+        p2 = prompt_ids(8, m2.vocab, seed=5)
+        a2, _ = m2.generate(p2, 16)
+        ids, _ = m.generate(prompt, 40)
+        b2, _ = m2.generate(p2, 16)
+    oids, _ = oracle.OracleModel(path, 1, 0).generate(prompt, 40)
+    o2, _ = oracle.OracleModel(other, 1, 0).generate(p2, 16)
+    assert np.array_equal(ids, oids)
+    assert np.array_equal(a2, o2) and np.array_equal(b2, o2)

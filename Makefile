@@ -33,7 +33,7 @@ all: $(LIB) $(RUNTIME) $(SYNTH) oracle
 $(OBJ) $(PKG)/lib $(PKG)/bin:
 	mkdir -p $@
 
-$(OBJ)/%.o: $(SRC)/%.hip $(SRC)/ec_device.h $(SRC)/ec_kernels.h $(SRC)/gemv_impl.h include/edgecore.h | $(OBJ)
+$(OBJ)/%.o: $(SRC)/%.hip $(SRC)/ec_device.h $(SRC)/ec_kernels.h $(SRC)/gemv_impl.h $(SRC)/ec_expf.h $(SRC)/ec_quant.h include/edgecore.h | $(OBJ)
 	$(HIPCC) $(HIPFLAGS) -c $< -o $@
 
 $(OBJ)/ecm.o: $(SRC)/ecm.c include/edgecore.h | $(OBJ)

@@ -11,6 +11,7 @@
 #include <stdint.h>
 
 #include "ec_expf.h"
+#include "ec_quant.h"
 
 namespace ec {
 
@@ -153,15 +154,8 @@ __device__ __forceinline__ float block_max256_1b(float v, float *red) {
   return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
 }
 
-// int8 quantization of one activation with the row scale s
-// (src/gpt2.c:456-459: lrintf(a / s) clamped to [-128, 127]).  On x86-64,
-// lrintf of NaN or of a magnitude >= 2^63 returns LONG_MIN, which clamps to
-// -128; every other value rounds half to even and clamps.
-__device__ __forceinline__ int8_t quant1(float a, float s) {
-  const float r = __builtin_rintf(a / s);
-  if (!(fabsf(r) < 9.2233720368547758e18f)) return (int8_t)-128;
-  return (int8_t)(int)fminf(fmaxf(r, -128.0f), 127.0f);
-}
+// int8 quantization of one activation with the row scale s (ec_quant.h)
+__device__ __forceinline__ int8_t quant1(float a, float s) { return ec_quant1(a, s); }
 
 // row scale of src/gpt2.c:453
 __device__ __forceinline__ float quant_scale(float maxa) {

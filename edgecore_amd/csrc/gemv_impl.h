@@ -31,6 +31,7 @@
 
 #include "ec_device.h"
 #include "ec_kernels.h"
+#include "ec_quant.h"
 
 #include <float.h>
 
@@ -108,11 +109,15 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   __shared__ unsigned long long keyred[4][MT];
   __shared__ uint64_t etab[SWI ? 32 : 1];  // expf table of the SiLU
 
+  // every kernel argument into registers here: one wait on the argument
+  // loads instead of one per first use
+  asm volatile("" ::"s"(a.A), "s"(a.W), "s"(a.W2), "s"(a.ws), "s"(a.ws2), "s"(a.bias), "s"(a.out));
+  asm volatile("" ::"s"(a.gamma), "s"(a.beta), "s"(a.as), "s"(a.cand), "s"(a.lda), "s"(a.ldo), "s"(a.M),
+               "s"(a.K), "s"(a.N));
+
   const int t = threadIdx.x;
   uint64_t et = 0;
-  if constexpr (SWI) {
-    if (t < 32) et = ec_exp2_32[t];
-  }
+  if constexpr (SWI) et = ec_exp2_32[t & 31];
   const int lane = t & 63, wave = t >> 6;
   const int grp = lane / LPR, sub = lane % LPR;
   const int rib = wave * RPW + grp;
@@ -126,9 +131,12 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   typedef typename std::conditional<Q8, v4i, v4u>::type vec_t;
   constexpr size_t WB = Q8 ? 1 : 2;
 
+  // Prologue layout: thread t owns activation elements 4t + 1024j; the block
+  // reduces through LDS into one shared copy of the quantized / normalized row.
+  const int nstrip = (K + 1023) >> 10;
+
   // ---- 1. activation row 0 of the tile (+ norm weights) ----
   float4 xv[NS > 0 ? NS : 1], gv[NORM ? NS : 1], bv[PRO == PRO_LN ? NS : 1];
-  const int nstrip = (K + 1023) >> 10;
   auto load_act = [&](int m) {
     const float *row = reinterpret_cast<const float *>(a.A) + (size_t)(m0 + m) * a.lda;
 #pragma unroll
@@ -148,6 +156,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   if constexpr (NS > 0) load_act(0);
 
   // ---- 2. first row group: weights, scales, bias, residual ----
+  // All unconditional: absent scales / bias read a valid dummy address and
+  // are replaced afterwards, so the number of loads after the activation is
+  // the same on every path and the prologue waits for the activation only.
   const vec_t *Wv = reinterpret_cast<const vec_t *>(a.W);
   const vec_t *W2v = reinterpret_cast<const vec_t *>(a.W2);
   vec_t w[CPL], w2[SWI ? CPL : 1];
@@ -161,21 +172,25 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
       if constexpr (SWI) w2[c] = __builtin_nontemporal_load(W2v + base + ch);
     }
   };
+  const float *dummy = reinterpret_cast<const float *>(a.W);
+  const float *wsp = a.ws ? a.ws : dummy, *ws2p = a.ws2 ? a.ws2 : dummy, *bp = a.bias ? a.bias : dummy;
   float bs = 1.0f, bs2 = 1.0f, bia = 0.0f, res[RES ? MT : 1];
   auto load_meta = [&](int rg) {
     const int n = min(rg * RPB + rib, a.N - 1);
     if constexpr (Q8) {
-      if (a.ws) bs = a.ws[n];
-      if constexpr (SWI) {
-        if (a.ws2) bs2 = a.ws2[n];
-      }
+      bs = wsp[a.ws ? n : 0];
+      if constexpr (SWI) bs2 = ws2p[a.ws2 ? n : 0];
     }
-    if (a.bias) bia = a.bias[n];
+    bia = bp[a.bias ? n : 0];
     if constexpr (RES) {
 #pragma unroll
-      for (int m = 0; m < MT; m++)
-        if (m < mc) res[m] = a.out[(size_t)(m0 + m) * a.ldo + n];
+      for (int m = 0; m < MT; m++) res[m] = a.out[(size_t)(m0 + min(m, mc - 1)) * a.ldo + n];
     }
+  };
+  auto fix_meta = [&](float &cbs, float &cbs2, float &cbia) {
+    if (!a.ws) cbs = 1.0f;
+    if (!a.ws2) cbs2 = 1.0f;
+    if (!a.bias) cbia = 0.0f;
   };
   int rg = blockIdx.x;
   load_w(rg, 0);
@@ -266,12 +281,26 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
         mx = block_max256_1b(mx, redf);
         const float sc = quant_scale(mx);
         int8_t *q = xq + (size_t)m * Kp;
+        // the reference's rint(a / s) codes, from one reciprocal per row
+        // (ec_quant.h) where the scale allows it
+        const bool fast = ec_quant_rcp_ok(sc);
+        const float rcp = 1.0f / sc;
 #pragma unroll
         for (int j = 0; j < NS; j++) {
           const int i = 4 * t + 1024 * j;
           if (j < nstrip && i < Kp) {
-            const uint32_t b0 = (uint8_t)quant1(xv[j].x, sc), b1 = (uint8_t)quant1(xv[j].y, sc);
-            const uint32_t b2 = (uint8_t)quant1(xv[j].z, sc), b3 = (uint8_t)quant1(xv[j].w, sc);
+            uint32_t b0, b1, b2, b3;
+            if (fast) {
+              b0 = (uint8_t)ec_quant1_rcp(xv[j].x, sc, rcp);
+              b1 = (uint8_t)ec_quant1_rcp(xv[j].y, sc, rcp);
+              b2 = (uint8_t)ec_quant1_rcp(xv[j].z, sc, rcp);
+              b3 = (uint8_t)ec_quant1_rcp(xv[j].w, sc, rcp);
+            } else {
+              b0 = (uint8_t)quant1(xv[j].x, sc);
+              b1 = (uint8_t)quant1(xv[j].y, sc);
+              b2 = (uint8_t)quant1(xv[j].z, sc);
+              b3 = (uint8_t)quant1(xv[j].w, sc);
+            }
             *reinterpret_cast<uint32_t *>(q + i) = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
           }
         }
@@ -385,7 +414,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
       }
     }
     // this group's scales/bias/residual; then prefetch the next group
-    const float cbs = bs, cbs2 = bs2, cbia = bia;
+    float cbs = bs, cbs2 = bs2, cbia = bia;
+    fix_meta(cbs, cbs2, cbia);
     float cres[RES ? MT : 1];
     if constexpr (RES) {
 #pragma unroll

@@ -55,6 +55,14 @@ def test_device_expf_source_exhaustive(tmp_path):
     assert p.returncode == 0 and "mismatches 0" in p.stdout, p.stdout
 
 
+def test_reciprocal_quantizer_equals_division(tmp_path):
+    """edgecore_amd/csrc/ec_quant.h: the kernels' division-free activation
+    quantizer (reciprocal + Markstein correction) gives the reference's
+    rint(a / s) code, and the same quotient, around every half-integer."""
+    p = _compile_and_run("quant_rcp_check.c", tmp_path)
+    assert p.returncode == 0 and "ec_quant1_rcp == ec_quant1" in p.stdout, p.stdout
+
+
 # ---------------------------------------------------------------- quantizers
 
 @pytest.mark.parametrize("packer", ["oracle", "library"])

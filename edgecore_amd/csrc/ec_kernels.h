@@ -75,6 +75,13 @@ hipError_t gemv_i8_fused(const GemvArgs &a, int epi, int pro, hipStream_t s);
 hipError_t gemv_f16_fused(const GemvArgs &a, int epi, int pro, hipStream_t s);
 hipError_t gemv_bf16_fused(const GemvArgs &a, int epi, int pro, hipStream_t s);
 hipError_t gemv_generic(const GemvArgs &a, int wt, int epi, hipStream_t s);
+// int8 matrix-core GEMM (gemm_mfma.hip) for M >= kGemmMinM: int8 A rows with
+// scales as (PRO_I8 input), every epilogue but argmax candidates; the floats
+// equal the vector GEMV's for the same rows.  gemm_i8_ok: shape and alignment
+// (K % 16, lda % 16, 16-byte aligned A / W / W2).
+constexpr int kGemmMinM = 16;
+bool gemm_i8_ok(const GemvArgs &a, int epi);
+hipError_t gemm_i8(const GemvArgs &a, int epi, hipStream_t s);
 // grid-size cap of the grid-stride GEMV (set from the CU count at init)
 void gemv_set_max_blocks(int n);
 int gemv_max_blocks();

@@ -1,0 +1,233 @@
+// int8 x int8 -> int32 GEMM on the gfx950 matrix cores, for the linears of a
+// prefill and of batched decode (M >= kGemmMinM rows):
+//
+//   C[m][n] = epi( bias[n] + ((float)sum_k A[m][k]*B[n][k] * as[m]) * bs[n] )
+//
+// which is src/kernels.c:153-168 (gemm_int8) with the epilogues src/gpt2.c
+// applies after it (residual add :782-784, SwiGLU :788-791, GELU :568).  The
+// int32 dot is exact whatever the summation order, so v_mfma_i32_16x16x64_i8
+// reproduces the reference's dot bit for bit; the fp32 epilogue is the same
+// device code as the decode GEMV's (i8_epilogue, silu, gelu_new), so a row gives
+// the same floats through either kernel.
+//
+// Tiling: a block of 256 threads (4 waves, 2 x 2) computes a BM x 128 tile of
+// C (for SwiGLU: BM x 64 outputs, each from a gate row and an up row).  K runs
+// in stages of 128 bytes through two LDS buffers; each thread holds the next
+// stage's 16-byte chunks in registers while the waves multiply the current
+// one.  Rows of the LDS tiles are 144 bytes apart, so the 16-byte fragment
+// reads of 8 consecutive lanes (16 rows, same k) fall on distinct banks.
+//
+// MFMA lane layout (16x16x64, checked on the device): lane l supplies row
+// l % 16 of A (column l % 16 of B) with the 16 k-bytes 16*(l/16) .. +15, and
+// receives D[4*(l/16) + r][l % 16] in accumulator register r.
+#include "ec_device.h"
+#include "ec_kernels.h"
+
+namespace ec {
+
+namespace {
+
+constexpr int kBK = 128;            // K bytes per LDS stage
+constexpr int kPitch = kBK + 16;    // LDS row pitch in bytes
+constexpr int kBN = 128;            // B rows per block tile
+
+template <int BM>
+constexpr size_t gemm_lds_bytes() {
+  return (size_t)2 * (BM + kBN) * kPitch;
+}
+
+template <int BM, int EPI>
+__global__ __launch_bounds__(256) void gemm_i8_kernel(GemvArgs a) {
+  constexpr bool SWI = EPI == EPI_SWIGLU;
+  constexpr bool RES = EPI == EPI_RESID || EPI == EPI_BIAS_RESID;
+  constexpr bool GELU = EPI == EPI_GELU || EPI == EPI_BIAS_GELU;
+  constexpr int WM = BM / 2, WN = kBN / 2;   // wave tile
+  constexpr int TI = WM / 16, TJ = WN / 16;  // 16 x 16 MFMA tiles per wave
+  constexpr int CPR = kBK / 16;              // 16-byte chunks per tile row and stage
+  constexpr int ACH = BM * CPR / 256;        // A chunks per thread and stage
+  constexpr int BCH = kBN * CPR / 256;       // B chunks per thread and stage
+  constexpr int NOUT = SWI ? kBN / 2 : kBN;  // output columns per block
+  static_assert(ACH >= 1 && BCH >= 1 && TJ % 2 == 0, "tile shape");
+
+  extern __shared__ __attribute__((aligned(16))) int8_t lds[];
+  int8_t *la = lds;                       // [2][BM][kPitch]
+  int8_t *lb = lds + 2 * BM * kPitch;     // [2][kBN][kPitch]
+  __shared__ uint64_t etab[SWI ? 32 : 1];
+
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int lr = lane & 15, lq = lane >> 4;
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * NOUT;
+  const int M = a.M, K = a.K, N = a.N;
+  if constexpr (SWI) {
+    if (t < 32) etab[t] = ec_exp2_32[t];
+  }
+
+  // global chunk sources of this thread: tile row, 16-byte column, row base
+  const int8_t *arow[ACH];
+  const int8_t *brow[BCH];
+  int acol[ACH], bcol[BCH], aoff[ACH], boff[BCH];
+  const int8_t *A = (const int8_t *)a.A;
+#pragma unroll
+  for (int j = 0; j < ACH; j++) {
+    const int c = t + 256 * j, r = c / CPR;
+    acol[j] = c % CPR;
+    arow[j] = A + (size_t)min(m0 + r, M - 1) * a.lda;
+    aoff[j] = r * kPitch + 16 * acol[j];
+  }
+#pragma unroll
+  for (int j = 0; j < BCH; j++) {
+    const int c = t + 256 * j, r = c / CPR;
+    bcol[j] = c % CPR;
+    const int8_t *W = (const int8_t *)a.W;
+    int n = n0 + r;
+    if (SWI && r >= kBN / 2) {
+      W = (const int8_t *)a.W2;
+      n = n0 + r - kBN / 2;
+    }
+    brow[j] = W + (size_t)min(n, N - 1) * K;
+    boff[j] = r * kPitch + 16 * bcol[j];
+  }
+
+  v4i ra[ACH], rb[BCH];
+  auto load = [&](int k0) {
+#pragma unroll
+    for (int j = 0; j < ACH; j++) {
+      const int k = k0 + 16 * acol[j];
+      ra[j] = *reinterpret_cast<const v4i *>(arow[j] + min(k, K - 16));
+      if (k >= K) ra[j] = v4i{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int j = 0; j < BCH; j++) {
+      const int k = k0 + 16 * bcol[j];
+      rb[j] = *reinterpret_cast<const v4i *>(brow[j] + min(k, K - 16));
+      if (k >= K) rb[j] = v4i{0, 0, 0, 0};
+    }
+  };
+  auto store = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < ACH; j++) *reinterpret_cast<v4i *>(la + buf * BM * kPitch + aoff[j]) = ra[j];
+#pragma unroll
+    for (int j = 0; j < BCH; j++) *reinterpret_cast<v4i *>(lb + buf * kBN * kPitch + boff[j]) = rb[j];
+  };
+
+  // B tile rows of this wave's column tiles: plain, or gate (j < TJ/2) and up
+  int bt[TJ];
+#pragma unroll
+  for (int j = 0; j < TJ; j++) {
+    if constexpr (SWI) {
+      const int jj = j % (TJ / 2);
+      bt[j] = (j < TJ / 2 ? 0 : kBN / 2) + wn * (kBN / 4) + 16 * jj;
+    } else {
+      bt[j] = wn * WN + 16 * j;
+    }
+  }
+
+  v4i acc[TI][TJ];
+#pragma unroll
+  for (int i = 0; i < TI; i++)
+#pragma unroll
+    for (int j = 0; j < TJ; j++) acc[i][j] = v4i{0, 0, 0, 0};
+
+  const int ns = (K + kBK - 1) / kBK;
+  load(0);
+  store(0);
+  __syncthreads();
+  for (int s = 0; s < ns; s++) {
+    const int buf = s & 1;
+    if (s + 1 < ns) load((s + 1) * kBK);
+    const int8_t *ta = la + buf * BM * kPitch + (wm * WM + lr) * kPitch + 16 * lq;
+    const int8_t *tb = lb + buf * kBN * kPitch + lr * kPitch + 16 * lq;
+#pragma unroll
+    for (int kk = 0; kk < kBK / 64; kk++) {
+      v4i fa[TI], fb[TJ];
+#pragma unroll
+      for (int i = 0; i < TI; i++) fa[i] = *reinterpret_cast<const v4i *>(ta + 16 * i * kPitch + 64 * kk);
+#pragma unroll
+      for (int j = 0; j < TJ; j++) fb[j] = *reinterpret_cast<const v4i *>(tb + bt[j] * kPitch + 64 * kk);
+#pragma unroll
+      for (int i = 0; i < TI; i++)
+#pragma unroll
+        for (int j = 0; j < TJ; j++)
+          acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
+    }
+    if (s + 1 < ns) store(buf ^ 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue: lane holds D[4*lq + r][lr] of each tile ----
+  constexpr int JO = SWI ? TJ / 2 : TJ;  // output column tiles
+#pragma unroll
+  for (int j = 0; j < JO; j++) {
+    const int n = n0 + (SWI ? wn * (kBN / 4) : wn * WN) + 16 * j + lr;
+    if (n >= N) continue;
+    const float bs = a.ws ? a.ws[n] : 1.0f;
+    const float bv = (!SWI && a.bias) ? a.bias[n] : 0.0f;
+    float bs2 = 1.0f;
+    if constexpr (SWI) bs2 = a.ws2 ? a.ws2[n] : 1.0f;
+#pragma unroll
+    for (int i = 0; i < TI; i++) {
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int m = m0 + wm * WM + 16 * i + 4 * lq + r;
+        if (m >= M) continue;
+        const float as = a.as[m];
+        float v = i8_epilogue(acc[i][j][r], as, bs, bv);
+        float *o = a.out + (size_t)m * a.ldo + n;
+        if constexpr (SWI) {
+          const float u = i8_epilogue(acc[i][j + TJ / 2][r], as, bs2, 0.0f);
+          v = silu(v, etab) * u;
+        } else {
+          if constexpr (RES) v = *o + v;
+          if constexpr (GELU) v = gelu_new(v);
+        }
+        *o = v;
+      }
+    }
+  }
+}
+
+template <int BM, int EPI>
+hipError_t launch_bm(const GemvArgs &a, hipStream_t s) {
+  constexpr int NOUT = EPI == EPI_SWIGLU ? kBN / 2 : kBN;
+  const dim3 grid((a.N + NOUT - 1) / NOUT, (a.M + BM - 1) / BM);
+  klaunch((gemm_i8_kernel<BM, EPI>), grid, dim3(256), gemm_lds_bytes<BM>(), s, a);
+  return hipGetLastError();
+}
+
+template <int EPI>
+hipError_t launch_epi(const GemvArgs &a, hipStream_t s) {
+  // the largest row tile that still gives every CU a block or more
+  constexpr int NOUT = EPI == EPI_SWIGLU ? kBN / 2 : kBN;
+  const long gx = (a.N + NOUT - 1) / NOUT;
+  if (gx * ((a.M + 127) / 128) >= 256) return launch_bm<128, EPI>(a, s);
+  if (gx * ((a.M + 63) / 64) >= 256 || a.M > 32) return launch_bm<64, EPI>(a, s);
+  return launch_bm<32, EPI>(a, s);
+}
+
+}  // namespace
+
+bool gemm_i8_ok(const GemvArgs &a, int epi) {
+  const auto al = [](const void *p) { return ((uintptr_t)p & 15u) == 0; };
+  if (a.M < 1 || a.N < 1 || a.K < 16 || a.K % 16 || a.lda % 16 || !a.as || a.cand) return false;
+  if (!al(a.A) || !al(a.W)) return false;
+  if (epi == EPI_SWIGLU && (!a.W2 || !al(a.W2))) return false;
+  return epi == EPI_STORE || epi == EPI_RESID || epi == EPI_GELU || epi == EPI_SWIGLU || epi == EPI_BIAS ||
+         epi == EPI_BIAS_RESID || epi == EPI_BIAS_GELU;
+}
+
+hipError_t gemm_i8(const GemvArgs &a, int epi, hipStream_t s) {
+  if (!gemm_i8_ok(a, epi)) return hipErrorInvalidValue;
+  switch (epi) {
+    case EPI_STORE:
+    case EPI_BIAS: return launch_epi<EPI_STORE>(a, s);
+    case EPI_RESID:
+    case EPI_BIAS_RESID: return launch_epi<EPI_RESID>(a, s);
+    case EPI_GELU:
+    case EPI_BIAS_GELU: return launch_epi<EPI_GELU>(a, s);
+    case EPI_SWIGLU: return launch_epi<EPI_SWIGLU>(a, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace ec

@@ -40,6 +40,9 @@ static hipDeviceProp_t g_prop;
 static int g_max_lds = 65536;
 // replay the single-token greedy step as a HIP graph (EDGECORE_GRAPHS=0 turns it off)
 static bool g_use_graphs = true;
+// int8 linears with kGemmMinM rows or more on the matrix cores
+// (EDGECORE_MFMA=0: the vector GEMV for every M)
+static bool g_use_mfma = true;
 
 static int set_err(int code, const char *fmt, ...) {
   va_list ap;
@@ -79,6 +82,8 @@ extern "C" int ec_init(void) {
   EC_HIP(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
   const char *gr = getenv("EDGECORE_GRAPHS");
   g_use_graphs = !(gr && !strcmp(gr, "0"));
+  const char *mf = getenv("EDGECORE_MFMA");
+  g_use_mfma = !(mf && !strcmp(mf, "0"));
   gemv_set_max_blocks(8 * g_prop.multiProcessorCount);
   gemv_set_max_lds(g_max_lds);
   g_inited = 1;
@@ -275,8 +280,12 @@ extern "C" int ec_gemm_int8_dev(float *C, const int8_t *A, const float *a_scale,
   if (M == 0 || N == 0) return 0;
   if (!C || !a_scale || (K > 0 && (!A || !B))) return set_err(-1, "gemm_int8: null pointer");
   GemvArgs a{A, K, a_scale, nullptr, nullptr, 0.0, B, nullptr, b_scale, nullptr, bias, C, N, M, K, N, nullptr};
-  EC_LAUNCH("gemv_i8", gemv_bytes(WT_I8, PRO_I8, EPI_STORE, M, K, N, b_scale, bias),
-            gemv_any(a, WT_I8, EPI_STORE, PRO_I8, g_stream));
+  const double bytes = gemv_bytes(WT_I8, PRO_I8, EPI_STORE, M, K, N, b_scale, bias);
+  if (g_use_mfma && M >= kGemmMinM && gemm_i8_ok(a, EPI_STORE)) {
+    EC_LAUNCH("gemm_i8", bytes, gemm_i8(a, EPI_STORE, g_stream));
+    return 0;
+  }
+  EC_LAUNCH("gemv_i8", bytes, gemv_any(a, WT_I8, EPI_STORE, PRO_I8, g_stream));
   return 0;
 }
 
@@ -802,6 +811,27 @@ extern "C" int gpt2_kv_reset(GPT2 *g) {
 // workspace) and the generic kernel does the product.
 static int linear(GPT2 *g, DevModel *d, const char *fam, GemvArgs a, int wt, int epi, int pro, hipStream_t s) {
   const double bytes = gemv_bytes(wt, pro, epi, a.M, a.K, a.N, a.ws != nullptr, a.bias != nullptr);
+  if (wt == WT_I8 && g_use_mfma && a.M >= kGemmMinM) {
+    // many rows: the norm / quantization as its own pass into int8 rows, then
+    // the matrix-core GEMM
+    GemvArgs q = a;
+    if (pro != PRO_I8) {
+      q.A = d->aq;
+      q.lda = d->aq_ld;
+      q.as = d->as;
+    }
+    if (gemm_i8_ok(q, epi)) {
+      const float *A = (const float *)a.A;
+      if (pro == PRO_QUANT) {
+        EC_LAUNCH("quant", 5.0 * a.M * a.K, quant_rows(A, a.lda, a.M, a.K, d->aq, d->aq_ld, d->as, s));
+      } else if (pro == PRO_RMS || pro == PRO_LN) {
+        EC_LAUNCH("norm_quant", 5.0 * a.M * a.K,
+                  norm_rows(A, a.M, a.K, a.gamma, a.beta, g->eps, nullptr, 0, d->aq, d->aq_ld, d->as, s));
+      }
+      EC_LAUNCH(fam, bytes, gemm_i8(q, epi, s));
+      return 0;
+    }
+  }
   if (gemv_vector_ok(a, wt, pro)) {
     EC_LAUNCH(fam, bytes, gemv(a, wt, epi, pro, s));
     return 0;

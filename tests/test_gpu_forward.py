@@ -36,6 +36,25 @@ def test_prefill_logits(make_model, name):
         assert (got.argmax(1) == want.argmax(1)).mean() >= 0.95
 
 
+@pytest.mark.parametrize("name", ["tiny-gpt2-int8", "tiny-qwen2-int8", "qwen2-hd128-int8"])
+@pytest.mark.parametrize("n", [16, 64, 120])
+def test_prefill_int8_rows_match_oracle(make_model, name, n):
+    """Prompts of 16+ tokens run the int8 linears on the matrix-core GEMM
+    (row tiles 32/64/128 by size): its int32 dots are exact and its epilogues
+    (bias, residual, GELU, SwiGLU) are the GEMV's, so every row's logits stay
+    at the fp16 LM head's rounding distance from the oracle."""
+    path = make_model(name)
+    with ec.Model(path, 1, 0) as m:
+        om = oracle.OracleModel(path, 1, 0)
+        toks = prompt_ids(n, m.vocab, seed=7 + n)
+        m.kv_reset()
+        om.kv_reset()
+        got, _ = m.forward(toks, np.arange(n), np.zeros(n, np.int32))
+        want = om.forward(toks, np.arange(n), np.zeros(n, np.int32))
+        assert np.abs(got - want).max() <= 1e-4
+        assert np.array_equal(got.argmax(1), want.argmax(1))
+
+
 @pytest.mark.parametrize("name", SMALL)
 def test_generate_32_tokens_identical(make_model, name):
     path = make_model(name)

@@ -18,6 +18,8 @@ I8_SHAPES = [
     (1, 896, 1152), (1, 896, 896), (1, 4864, 896), (1, 896, 4864),  # Qwen2-0.5B decode
     (1, 1536, 256), (1, 8960, 1536),                                  # Qwen2.5-1.5B
     (3, 896, 896), (8, 4864, 896), (16, 1536, 1536), (37, 896, 1152),  # batched / prefill
+    (256, 896, 1152), (300, 4864, 896), (64, 896, 4864),              # matrix-core tiles
+    (130, 64, 192), (17, 1040, 200), (33, 16, 129),                   # K, M and N tails
     (1, 64, 192), (2, 256, 64),                                       # tiny GPT-2
     (5, 40, 7), (2, 1, 3), (3, 17, 33),                               # odd K: generic path
 ]

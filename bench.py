@@ -23,6 +23,11 @@ CPU baseline is the reference runtime built from its own sources
 (oracle/_ref/edgecore-runtime) on the same model file and prompt, timed on
 the host cores.
 
+prefill_4x2048 is the prefill-heavy workload on the same model: 4 prompts of
+2048 ids, prefilled one slot at a time, then 32 decode steps at M=4, with the
+matrix-core GEMMs' TOP/s against the int8 dense peak.  It is reported beside
+the decode line, not as its value.
+
 Prints one JSON line.
 """
 import argparse
@@ -38,7 +43,11 @@ sys.path.insert(0, str(REPO))
 
 METRIC = "decode tok/s + int8 GEMV HBM GB/s (% of peak), Qwen2-0.5B-shape int8 bs=1"
 HBM_PEAK_GBPS = 8000.0
+INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 matrix-core peak, TOP/s
 PROMPT = 256
+# prefill-heavy workload: 4 prompts of 2048 ids (seeds 1..4), one slot each,
+# prefilled one at a time as the reference driver does, then 32 decode steps at M=4
+C4_PROMPT, C4_SEQS, C4_DECODE = 2048, 4, 32
 
 
 def ensure_inputs(cache: Path):
@@ -54,6 +63,81 @@ def ensure_inputs(cache: Path):
     if not prompt.exists():
         ec.synth(None, prompt_out=prompt, prompt_len=PROMPT, prompt_seed=1, vocab=151936)
     return model, prompt
+
+
+def prefill_c4(ec, np, model: Path, cache: Path):
+    """4 x 2048-token prefills into slots 0..3 (each with the LM head on its
+    last row and the device argmax, i.e. time to first token), then 32 greedy
+    decode steps at M=4.  A second pass of one prefill records every launch's
+    dispatch timestamps: the per-family table and the matrix-core GEMMs'
+    TOP/s (2*M*N*K per launch)."""
+    E, F, kv = 896, 4864, 128
+    prompts = []
+    for b in range(C4_SEQS):
+        f = cache / f"prompt{C4_PROMPT}_s{b + 1}.txt"
+        if not f.exists():
+            ec.synth(None, prompt_out=f, prompt_len=C4_PROMPT, prompt_seed=b + 1, vocab=151936)
+        prompts.append(ec.read_ids(f))
+    m = ec.Model(model, C4_SEQS, C4_PROMPT + C4_DECODE + 8)
+    L = ec.lib()
+    n = C4_PROMPT
+    pos = np.arange(n)
+
+    def prefill(b):
+        _, am = m.forward(prompts[b], pos, np.full(n, b, np.int32), lm_from=n - 1, want_logits=False,
+                          want_argmax=True)
+        return int(am[0])
+
+    m.kv_reset()
+    prefill(0)  # warm
+    m.kv_reset()
+    L.ec_sync()
+    t0 = time.perf_counter()
+    first = [prefill(b) for b in range(C4_SEQS)]
+    L.ec_sync()
+    t_prefill = time.perf_counter() - t0
+
+    cur, p = list(first), [n] * C4_SEQS
+    L.ec_sync()
+    t0 = time.perf_counter()
+    for _ in range(C4_DECODE):
+        _, am = m.forward(cur, p, None, want_logits=False, want_argmax=True)
+        cur, p = [int(x) for x in am], [x + 1 for x in p]
+    L.ec_sync()
+    t_decode = time.perf_counter() - t0
+
+    # one more prefill of slot 0 with per-launch timestamps
+    L.ec_prof_start(b"")
+    prefill(0)
+    L.ec_sync()
+    buf = __import__("ctypes").create_string_buffer(1 << 16)
+    kernels = json.loads(buf.value.decode()) if L.ec_prof_stop(buf, len(buf)) > 0 else []
+    m.close()
+    shapes = {"gemm_qkv": (E + 2 * kv, E), "gemm_o": (E, E), "gemm_gateup": (2 * F, E), "gemm_down": (E, F)}
+    tot = sum(k["total_us"] for k in kernels) or 1.0
+    for k in kernels:
+        k["share"] = round(k["total_us"] / tot, 4)
+        if k["kernel"] in shapes:
+            N_, K_ = shapes[k["kernel"]]
+            k["tops"] = round(2.0 * n * N_ * K_ / (k["avg_us"] * 1e6), 1)
+            k["int8_mfma_frac"] = round(k["tops"] / INT8_PEAK_TOPS, 4)
+    gemms = [k for k in kernels if k["kernel"] in shapes]
+    gflop = sum(2.0 * n * shapes[k["kernel"]][0] * shapes[k["kernel"]][1] * k["launches"] for k in gemms)
+    gus = sum(k["total_us"] for k in gemms)
+    dom = max(gemms, key=lambda k: k["total_us"]) if gemms else None
+    return {
+        "workload": f"Qwen2-0.5B-shape int8, {C4_SEQS} x {C4_PROMPT}-token prompts (seeds 1-{C4_SEQS}), "
+                    f"one slot each, prefilled one at a time; then {C4_DECODE} greedy steps at M={C4_SEQS}",
+        "prefill_tok_s": round(C4_SEQS * n / t_prefill, 1),
+        "ms_per_prompt": round(t_prefill / C4_SEQS * 1e3, 3),
+        "batched_decode_tok_s": round(C4_SEQS * C4_DECODE / t_decode, 1),
+        "batched_decode_ms_per_step": round(t_decode / C4_DECODE * 1e3, 4),
+        "gemm_roofline": None if not dom else {
+            "kernel": dom["kernel"], "bound": "mfma", "achieved": dom["tops"], "peak": INT8_PEAK_TOPS,
+            "unit": "TOP/s (int8)", "frac": dom["int8_mfma_frac"], "avg_us": dom["avg_us"]},
+        "gemm_all_tops": round(gflop / (gus * 1e6), 1) if gus else None,
+        "kernels": kernels,
+    }
 
 
 def physical_cores() -> int:
@@ -114,6 +198,7 @@ def main() -> int:
     ap.add_argument("--cache", default=os.environ.get("EDGECORE_BENCH_DIR", "/tmp/edgecore_bench"))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-tokens", type=int, default=16)
+    ap.add_argument("--no-prefill", action="store_true", help="skip the 4 x 2048-token prefill leg")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="also run the plain copy kernel (ec_device_math op 6) 8 times on this many "
                          "bytes: the reference for HBM traffic counters and achievable bandwidth")
@@ -249,6 +334,8 @@ def main() -> int:
         "kernels_note": "per-launch dispatch start/stop timestamps of every kernel, second pass of the same K steps",
         "device": ec.device_info(),
     }
+    if not args.no_prefill:
+        out["prefill_4x2048"] = prefill_c4(ec, np, model, Path(args.cache))
     if not args.no_cpu_baseline:
         try:
             out["cpu_baseline"] = cpu_baseline(model, prompt_file, args.cpu_tokens)

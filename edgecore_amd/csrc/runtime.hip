@@ -809,6 +809,16 @@ extern "C" int gpt2_kv_reset(GPT2 *g) {
 // One linear layer: the fused GEMV when the shape allows it; otherwise the
 // prologue runs as its own kernel (norm / quantize into the aq or h
 // workspace) and the generic kernel does the product.
+// profiler family of a linear that runs on the matrix-core GEMM: "gemv_X" -> "gemm_X"
+static const char *gemm_family(const char *fam) {
+  static const char *const names[][2] = {{"gemv_qkv", "gemm_qkv"},       {"gemv_o", "gemm_o"},
+                                         {"gemv_gateup", "gemm_gateup"}, {"gemv_fc", "gemm_fc"},
+                                         {"gemv_down", "gemm_down"}};
+  for (const auto &n : names)
+    if (!strcmp(fam, n[0])) return n[1];
+  return "gemm_i8";
+}
+
 static int linear(GPT2 *g, DevModel *d, const char *fam, GemvArgs a, int wt, int epi, int pro, hipStream_t s) {
   const double bytes = gemv_bytes(wt, pro, epi, a.M, a.K, a.N, a.ws != nullptr, a.bias != nullptr);
   if (wt == WT_I8 && g_use_mfma && a.M >= kGemmMinM) {
@@ -828,7 +838,7 @@ static int linear(GPT2 *g, DevModel *d, const char *fam, GemvArgs a, int wt, int
         EC_LAUNCH("norm_quant", 5.0 * a.M * a.K,
                   norm_rows(A, a.M, a.K, a.gamma, a.beta, g->eps, nullptr, 0, d->aq, d->aq_ld, d->as, s));
       }
-      EC_LAUNCH(fam, bytes, gemm_i8(q, epi, s));
+      EC_LAUNCH(gemm_family(fam), bytes, gemm_i8(q, epi, s));
       return 0;
     }
   }
@@ -875,7 +885,7 @@ static int attn_vtile(int max_npos, int hd, int kv) {
 // batch and sizes the attention LDS; distinct: no two tokens share a slot
 // (RoPE and the KV append then run inside attention); abytes: algorithmic
 // attention bytes, for the profiler only.
-static int enqueue_forward(GPT2 *g, DevModel *d, int M, int lm_from, bool distinct, int max_npos,
+static int enqueue_forward(GPT2 *g, DevModel *d, int M, int lm_from, bool distinct, bool run, int max_npos,
                            double abytes, float *logits, int *argmax, hipStream_t s) {
   const int E = g->n_embd, H = g->n_head, V = g->vocab, kv = g->n_kv_embd, hd = g->head_dim;
   const bool qwen = g->arch == ARCH_QWEN2, i8 = g->precision == 0, bf16 = g->precision == 2;
@@ -915,7 +925,11 @@ static int enqueue_forward(GPT2 *g, DevModel *d, int M, int lm_from, bool distin
     AttnArgs aa{d->qkv, ldq, kcl, vcl, d->att, E, d->d_pos, d->d_slot, H, g->n_kv_head, hd, kv,
                 d->eff_ctx, qwen ? g->sliding_window : 0, 1.0 / sqrt((double)hd), M, max_npos, vtile,
                 distinct ? 1 : 0, kq, vq, ldq, (distinct && qwen) ? d->rope : nullptr, d->half, kcl, vcl};
-    EC_LAUNCH("attention", abytes, attention(aa, s));
+    if (run && attention_prefill_ok(aa, g_max_lds)) {
+      EC_LAUNCH("attention_prefill", abytes, attention_prefill(aa, g_max_lds, s));
+    } else {
+      EC_LAUNCH("attention", abytes, attention(aa, s));
+    }
     // output projection + residual
     {
       GemvArgs a{d->att, E, nullptr, nullptr, nullptr, 0.0, W.wo, nullptr, W.so, nullptr, W.bo, d->x, E, M, E, E,
@@ -1004,6 +1018,10 @@ static int forward_impl(GPT2 *g, const int *tokens, const int *positions, const 
         distinct = false;
         break;
       }
+  // one slot's run of consecutive positions (a prefill): the prefill attention
+  bool run = M > 1;
+  for (int m = 1; m < M && run; m++)
+    run = st[2 * d->mmax + m] == st[2 * d->mmax] && st[d->mmax + m] == st[d->mmax] + m;
   double abytes = 0;
   for (int m = 0; m < M; m++) abytes += (double)(positions[m] + 1) * kv * 4 + 8.0 * E;
   hipStream_t s = g_stream;
@@ -1023,7 +1041,7 @@ static int forward_impl(GPT2 *g, const int *tokens, const int *positions, const 
         d->step_graph = nullptr;
       }
       EC_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
-      const int r = enqueue_forward(g, d, 1, 0, true, bucket, abytes, nullptr, d->h_amax, s);
+      const int r = enqueue_forward(g, d, 1, 0, true, false, bucket, abytes, nullptr, d->h_amax, s);
       hipGraph_t graph = nullptr;
       const hipError_t e = hipStreamEndCapture(s, &graph);
       if (r) {
@@ -1041,7 +1059,7 @@ static int forward_impl(GPT2 *g, const int *tokens, const int *positions, const 
     argmax[0] = d->h_amax[0];
     return 0;
   }
-  const int r = enqueue_forward(g, d, M, lm_from, distinct, max_npos, abytes, logits, argmax, s);
+  const int r = enqueue_forward(g, d, M, lm_from, distinct, run, max_npos, abytes, logits, argmax, s);
   if (r) return r;
   EC_HIP(hipStreamSynchronize(s));
   return 0;

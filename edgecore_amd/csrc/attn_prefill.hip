@@ -50,7 +50,7 @@ __global__ __launch_bounds__(NW * 64) void attn_prefill_kernel(AttnArgs a, int n
   constexpr int NCH = (TCH + NT - 1) / NT;     // chunks per thread
   constexpr int DPL = HD > 64 ? HD / 64 : 1;   // output elements per lane
   extern __shared__ __attribute__((aligned(16))) float lds[];
-  float *tile = lds;                           // [kPfTile][KP]: K rows, then V rows
+  float *tile = lds;  // [kPfTile + 4][KP]: K rows, then V rows (4 spare rows for look-ahead reads)
   __shared__ uint64_t etab[32];
 
   const int t = threadIdx.x, lane = t & 63;
@@ -72,20 +72,31 @@ __global__ __launch_bounds__(NW * 64) void attn_prefill_kernel(AttnArgs a, int n
     mq[i] = min(m, a.M - 1);
     pos[i] = ld_uniform(a.pos + mq[i]);
     lo[i] = a.window > 0 ? max(0, pos[i] - a.window + 1) : 0;
-    scq[i] = lds + kPfTile * KP + (QW * w + i) * nsc;
+    scq[i] = lds + (kPfTile + 4) * KP + (QW * w + i) * nsc;
   }
   if (t < 32) etab[t] = ec_exp2_32[t];
   const size_t cbase = (size_t)slot * a.C * a.kv + (size_t)kvh * HD;
   const uint16_t *Kc = a.kc + cbase, *Vc = a.vc + cbase;
 
-  // q rows (uniform)
+  // q rows of the block's tokens through the (still free) tile area into
+  // each wave's registers
+  for (int e = t; e < QB * HD / 4; e += NT) {
+    const int r = e / (HD / 4), c4 = e - r * (HD / 4);
+    const float *qrow = a.q + (size_t)min(m0 + r, a.M - 1) * a.ldq + (size_t)h * HD;
+    *reinterpret_cast<float4 *>(tile + r * HD + 4 * c4) = *reinterpret_cast<const float4 *>(qrow + 4 * c4);
+  }
+  __syncthreads();
   float q[QW][HD];
 #pragma unroll
-  for (int i = 0; i < QW; i++) {
-    const float *qrow = a.q + (size_t)mq[i] * a.ldq + (size_t)h * HD;
+  for (int i = 0; i < QW; i++)
 #pragma unroll
-    for (int d = 0; d < HD; d++) q[i][d] = ld_uniform(qrow + d);
-  }
+    for (int c4 = 0; c4 < HD / 4; c4++) {
+      const float4 v = *reinterpret_cast<const float4 *>(tile + (QW * w + i) * HD + 4 * c4);
+      q[i][4 * c4] = v.x;
+      q[i][4 * c4 + 1] = v.y;
+      q[i][4 * c4 + 2] = v.z;
+      q[i][4 * c4 + 3] = v.w;
+    }
 
   // tile staging: the next tile's 16-byte chunks are loaded into registers
   // (gload) while the waves work on the current one, then converted to fp32
@@ -149,6 +160,10 @@ __global__ __launch_bounds__(NW * 64) void attn_prefill_kernel(AttnArgs a, int n
           }
         }
       }
+      // every token's dot is formed in full, interleaved with the others;
+      // only the stores below depend on the token's range
+#pragma unroll
+      for (int i = 0; i < QW; i++) asm volatile("" : "+v"(s[i]));
 #pragma unroll
       for (int i = 0; i < QW; i++) {
         if (p >= lo[i] && p <= pos[i]) {
@@ -212,12 +227,16 @@ __global__ __launch_bounds__(NW * 64) void attn_prefill_kernel(AttnArgs a, int n
     int p = r0;
     for (; p < c0; p++) add_some(p);
     for (; p <= c1 && ((p - lo0) & 3); p++) add_some(p);
-    if (p + 3 <= c1) {
-      // groups of 4 positions: the probabilities (one 16-byte read per
-      // token) and V elements of the next group are read before the adds
-      // of the current one
-      float4 pa[QW];
-      float va[4][DPL];
+    const int ng = p <= c1 ? (c1 - p + 1) >> 2 : 0;
+    if (ng > 0) {
+      // groups of 4 positions in two register sets (ping-pong): the
+      // probabilities (one 16-byte read per token) and V elements of the next
+      // group are read before the adds of the current one.  The look-ahead
+      // reads are unconditional; past c1 they reach at most 4 positions
+      // further: the tile's 4 spare rows, the next token's score slots or the
+      // 4 spare floats after the last token's (values not used).
+      float4 pa[QW], pb[QW];
+      float va[4][DPL], vb[4][DPL];
       auto load4 = [&](int pp, float4 *pr, float (*vv)[DPL]) {
 #pragma unroll
         for (int i = 0; i < QW; i++) pr[i] = *reinterpret_cast<const float4 *>(scq[i] + (pp - lo0));
@@ -242,20 +261,20 @@ __global__ __launch_bounds__(NW * 64) void attn_prefill_kernel(AttnArgs a, int n
         }
       };
       load4(p, pa, va);
-      for (; p + 7 <= c1; p += 4) {
-        float4 pb[QW];
-        float vb[4][DPL];
+      for (int g = 0;;) {
         load4(p + 4, pb, vb);
+        __builtin_amdgcn_sched_barrier(0);
         add4(pa, va);
-#pragma unroll
-        for (int i = 0; i < QW; i++) pa[i] = pb[i];
-#pragma unroll
-        for (int e = 0; e < 4; e++)
-#pragma unroll
-          for (int j = 0; j < DPL; j++) va[e][j] = vb[e][j];
+        __builtin_amdgcn_sched_barrier(0);
+        p += 4;
+        if (++g == ng) break;
+        load4(p + 4, pa, va);
+        __builtin_amdgcn_sched_barrier(0);
+        add4(pb, vb);
+        __builtin_amdgcn_sched_barrier(0);
+        p += 4;
+        if (++g == ng) break;
       }
-      add4(pa, va);
-      p += 4;
     }
     for (; p <= r1; p++) add_some(p);
   }
@@ -276,8 +295,10 @@ int pf_nsc(const AttnArgs &a, int qb) {
   return (r + 3) & ~3;
 }
 
+// tile with 4 spare rows, the score slots of qb tokens and 4 spare floats,
+// plus the static expf table (256 bytes)
 size_t pf_lds_bytes(const AttnArgs &a, int qb) {
-  return ((size_t)kPfTile * (a.hd + 4) + (size_t)qb * pf_nsc(a, qb)) * sizeof(float) + 256;
+  return ((size_t)(kPfTile + 4) * (a.hd + 4) + (size_t)qb * pf_nsc(a, qb) + 4) * sizeof(float) + 256;
 }
 
 // block shapes, largest first: (waves, tokens per wave)
@@ -317,6 +338,7 @@ void launch_hd(const AttnArgs &a, int shape, hipStream_t st) {
 
 bool attention_prefill_ok(const AttnArgs &a, int max_lds) {
   if (!(a.hd == 32 || a.hd == 64 || a.hd == 128) || !attn_vec(a.hd, a.kv) || a.fuse_kv || a.M < 1) return false;
+  if (a.ldq % 4 || ((uintptr_t)a.q & 15u)) return false;  // q rows read as float4
   return pf_pick(a, max_lds) >= 0;
 }
 

@@ -155,8 +155,9 @@ struct AttnArgs {
 hipError_t attention(const AttnArgs &a, hipStream_t st);
 // Prefill attention (attn_prefill.hip): the M tokens are one slot's run of
 // consecutive positions whose k / v are already in the cache (fuse_kv 0);
-// blocks of 4 tokens per head.  _ok: head_dim 32/64/128 and the LDS of the
-// scores (4 x max_npos floats, window-bounded) within max_lds bytes.
+// blocks of 16, 8 or 4 tokens per head.  _ok: head_dim 32/64/128, q rows
+// 16-byte aligned, and the LDS of the scores (tokens per block x max_npos
+// floats, window-bounded) within max_lds bytes.
 bool attention_prefill_ok(const AttnArgs &a, int max_lds);
 hipError_t attention_prefill(const AttnArgs &a, int max_lds, hipStream_t st);
 // V units (4 positions x 8 elements) per thread held in registers

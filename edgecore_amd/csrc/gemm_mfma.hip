@@ -57,8 +57,14 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemvArgs a) {
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int lr = lane & 15, lq = lane >> 4;
-  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * NOUT;
   const int M = a.M, K = a.K, N = a.N;
+  // XCD-aware tile order: block b runs on XCD b % 8; XCD x takes tiles
+  // [x * per, (x + 1) * per) of the weight-row-major order, i.e. a contiguous
+  // share of the weight rows with every row tile of A, so its L2 holds both
+  const int nM = (M + BM - 1) / BM, nN = (N + NOUT - 1) / NOUT, T = nM * nN, per = (T + 7) / 8;
+  const int tl = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
+  if (tl >= T) return;
+  const int m0 = (tl % nM) * BM, n0 = (tl / nM) * NOUT;
   if constexpr (SWI) {
     if (t < 32) etab[t] = ec_exp2_32[t];
   }
@@ -89,26 +95,28 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemvArgs a) {
     boff[j] = r * kPitch + 16 * bcol[j];
   }
 
+  // chunks past K (a last stage shorter than kBK) are loaded clamped and
+  // zeroed when stored to LDS, so that nothing waits on the loads before the
+  // multiplies of the current stage
   v4i ra[ACH], rb[BCH];
+  int kl = 0;  // k0 of the stage held in ra / rb
   auto load = [&](int k0) {
+    kl = k0;
 #pragma unroll
-    for (int j = 0; j < ACH; j++) {
-      const int k = k0 + 16 * acol[j];
-      ra[j] = *reinterpret_cast<const v4i *>(arow[j] + min(k, K - 16));
-      if (k >= K) ra[j] = v4i{0, 0, 0, 0};
-    }
+    for (int j = 0; j < ACH; j++)
+      ra[j] = *reinterpret_cast<const v4i *>(arow[j] + min(k0 + 16 * acol[j], K - 16));
 #pragma unroll
-    for (int j = 0; j < BCH; j++) {
-      const int k = k0 + 16 * bcol[j];
-      rb[j] = *reinterpret_cast<const v4i *>(brow[j] + min(k, K - 16));
-      if (k >= K) rb[j] = v4i{0, 0, 0, 0};
-    }
+    for (int j = 0; j < BCH; j++)
+      rb[j] = *reinterpret_cast<const v4i *>(brow[j] + min(k0 + 16 * bcol[j], K - 16));
   };
   auto store = [&](int buf) {
+    const v4i z = {0, 0, 0, 0};
 #pragma unroll
-    for (int j = 0; j < ACH; j++) *reinterpret_cast<v4i *>(la + buf * BM * kPitch + aoff[j]) = ra[j];
+    for (int j = 0; j < ACH; j++)
+      *reinterpret_cast<v4i *>(la + buf * BM * kPitch + aoff[j]) = kl + 16 * acol[j] < K ? ra[j] : z;
 #pragma unroll
-    for (int j = 0; j < BCH; j++) *reinterpret_cast<v4i *>(lb + buf * kBN * kPitch + boff[j]) = rb[j];
+    for (int j = 0; j < BCH; j++)
+      *reinterpret_cast<v4i *>(lb + buf * kBN * kPitch + boff[j]) = kl + 16 * bcol[j] < K ? rb[j] : z;
   };
 
   // B tile rows of this wave's column tiles: plain, or gate (j < TJ/2) and up
@@ -190,7 +198,8 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemvArgs a) {
 template <int BM, int EPI>
 hipError_t launch_bm(const GemvArgs &a, hipStream_t s) {
   constexpr int NOUT = EPI == EPI_SWIGLU ? kBN / 2 : kBN;
-  const dim3 grid((a.N + NOUT - 1) / NOUT, (a.M + BM - 1) / BM);
+  const int T = ((a.N + NOUT - 1) / NOUT) * ((a.M + BM - 1) / BM);
+  const dim3 grid(8 * ((T + 7) / 8));
   klaunch((gemm_i8_kernel<BM, EPI>), grid, dim3(256), gemm_lds_bytes<BM>(), s, a);
   return hipGetLastError();
 }

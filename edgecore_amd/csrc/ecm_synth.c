@@ -32,9 +32,9 @@
 #endif
 
 typedef struct {
-    const char *out, *name, *arch, *precision, *prompt_out;
-    int L, E, H, KVH, F, C, V, tie, prompt_len;
-    double std, eps, theta;
+    const char *out, *name, *arch, *precision, *prompt_out, *rope_type;
+    int L, E, H, KVH, F, C, V, tie, prompt_len, window, yarn_orig_max;
+    double std, eps, theta, yarn_factor, yarn_attn;
     unsigned long long seed, prompt_seed;
 } Opts;
 
@@ -187,8 +187,18 @@ static void build_table(const Opts *o)
 
 static size_t dt_bytes(int d) { return d == 0 ? 4 : d == 2 ? 1 : d == 3 ? 1 : 2; }
 
+/* %.17g, with ".0" appended to an integral value ("1.0", "4.0"), the form of
+   the YaRN meta values in files written before these options existed */
+static const char *fmt_real(char *buf, size_t n, double v)
+{
+    snprintf(buf, n, "%.17g", v);
+    if (!strpbrk(buf, ".eEn")) strncat(buf, ".0", n - strlen(buf) - 1);
+    return buf;
+}
+
 static int write_model(const Opts *o)
 {
+    char yf[40], ya[40];
     FILE *f = fopen(o->out, "wb");
     if (!f) { perror(o->out); return 1; }
     size_t n_params = 0;
@@ -199,10 +209,12 @@ static int write_model(const Opts *o)
             o->name, o->L, o->H, o->E, o->C, o->V);
     fprintf(f, "eps=%.17g\narch=%s\n", o->eps, o->arch);
     if (!strcmp(o->arch, "qwen2"))
-        fprintf(f, "n_kv_head=%d\nintermediate=%d\nrope_theta=%.17g\nrope_type=default\n"
-                   "yarn_factor=1.0\nyarn_orig_max=%d\nyarn_attention_factor=1.0\n"
-                   "sliding_window=0\ntie_word_embeddings=%d\neos_token_id=%d\n",
-                o->KVH, o->F, o->theta, o->C, o->tie, o->V - 1);
+        fprintf(f, "n_kv_head=%d\nintermediate=%d\nrope_theta=%.17g\nrope_type=%s\n"
+                   "yarn_factor=%s\nyarn_orig_max=%d\nyarn_attention_factor=%s\n"
+                   "sliding_window=%d\ntie_word_embeddings=%d\neos_token_id=%d\n",
+                o->KVH, o->F, o->theta, o->rope_type, fmt_real(yf, sizeof yf, o->yarn_factor),
+                o->yarn_orig_max > 0 ? o->yarn_orig_max : o->C, fmt_real(ya, sizeof ya, o->yarn_attn),
+                o->window, o->tie, o->V - 1);
     fprintf(f, "n_params=%zu\nEND_META\n", n_params);
     static const char *dn[] = {"fp32", "fp16", "int8", "text", "bf16"};
     for (int i = 0; i < g_n; i++) {
@@ -314,6 +326,8 @@ static void usage(void)
             "  [--arch gpt2|qwen2] [--layers N] [--embd E] [--heads H] [--kv-heads N] [--ffn F]\n"
             "  [--ctx C] [--vocab V] [--precision int8|fp16|bf16] [--tie 0|1] [--seed S]\n"
             "  [--std X] [--eps X] [--rope-theta X] [--name NAME]\n"
+            "  [--sliding-window W] [--rope-type default|yarn] [--yarn-factor X]\n"
+            "  [--yarn-orig-max N] [--yarn-attention-factor X]   (qwen2 only)\n"
             "  [--prompt-out FILE --prompt-len N [--prompt-seed S]]\n");
 }
 
@@ -324,6 +338,7 @@ int main(int argc, char **argv)
     o.arch = "gpt2"; o.precision = "int8"; o.name = NULL;
     o.L = 2; o.E = 64; o.H = 2; o.C = 128; o.V = 256;
     o.std = 0.02; o.eps = 1e-5; o.theta = 1e6; o.seed = 0; o.prompt_seed = 1;
+    o.rope_type = "default"; o.yarn_factor = 1.0; o.yarn_attn = 1.0;
     for (int i = 1; i < argc; i++) {
         const char *a = argv[i];
         const char *v = i + 1 < argc ? argv[i + 1] : NULL;
@@ -345,6 +360,11 @@ int main(int argc, char **argv)
         else if (ARG("--eps")) o.eps = atof(v);
         else if (ARG("--rope-theta")) o.theta = atof(v);
         else if (ARG("--name")) o.name = v;
+        else if (ARG("--sliding-window")) o.window = atoi(v);
+        else if (ARG("--rope-type")) o.rope_type = v;
+        else if (ARG("--yarn-factor")) o.yarn_factor = atof(v);
+        else if (ARG("--yarn-orig-max")) o.yarn_orig_max = atoi(v);
+        else if (ARG("--yarn-attention-factor")) o.yarn_attn = atof(v);
         else if (ARG("--prompt-out")) o.prompt_out = v;
         else if (ARG("--prompt-len")) o.prompt_len = atoi(v);
         else if (ARG("--prompt-seed")) o.prompt_seed = strtoull(v, NULL, 10);
@@ -354,6 +374,7 @@ int main(int argc, char **argv)
     if (!o.out && !o.prompt_out) { usage(); return 2; }
     if (strcmp(o.arch, "gpt2") && strcmp(o.arch, "qwen2")) { usage(); return 2; }
     if (strcmp(o.precision, "int8") && strcmp(o.precision, "fp16") && strcmp(o.precision, "bf16")) { usage(); return 2; }
+    if ((strcmp(o.rope_type, "default") && strcmp(o.rope_type, "yarn")) || o.window < 0) { usage(); return 2; }
     if (!strcmp(o.arch, "qwen2")) {
         if (o.KVH <= 0) o.KVH = o.H;
         if (o.F <= 0) o.F = 4 * o.E;

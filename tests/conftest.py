@@ -26,6 +26,11 @@ MODEL_SPECS = {
     # hd 128, GQA 6:1, an odd vocabulary and intermediate size
     "qwen2-hd128-int8": dict(arch="qwen2", layers=3, embd=768, heads=6, kv_heads=1, ffn=1000,
                              ctx=512, vocab=4099, precision="int8", tie=1),
+    # sliding window 48 and YaRN RoPE (factor 4 over an original 64 positions)
+    "qwen2-window-yarn-int8": dict(arch="qwen2", layers=2, embd=256, heads=4, kv_heads=2, ffn=384,
+                                   ctx=256, vocab=1000, precision="int8", sliding_window=48,
+                                   rope_type="yarn", yarn_factor=4.0, yarn_orig_max=64,
+                                   yarn_attention_factor=1.1),
     # long context: decode crosses 512-position boundaries
     "qwen2-long-int8": dict(arch="qwen2", layers=2, embd=128, heads=4, kv_heads=2, ffn=256,
                             ctx=1536, vocab=1000, precision="int8"),

@@ -68,6 +68,28 @@ def test_generate_32_tokens_identical(make_model, name):
         assert err <= TOL[m.precision], err
 
 
+def test_sliding_window_and_yarn(make_model):
+    """Qwen2 with a 48-position sliding window and YaRN RoPE (src/gpt2.c:616-643,
+    753-754): a 60-token prompt (prefill attention with lo > 0 from position 48)
+    and 40 greedy steps (decode attention, graph-replayed, every step windowed)."""
+    path = make_model("qwen2-window-yarn-int8")
+    with ec.Model(path, 1, 0) as m:
+        om = oracle.OracleModel(path, 1, 0)
+        prompt = prompt_ids(60, m.vocab, seed=9)
+        ids_graph, _ = m.generate(prompt, 40, want_logits=False)
+        ids, lg = m.generate(prompt, 40, want_logits=True)
+        oids, olg = om.generate(prompt, 40, want_logits=True)
+        assert np.array_equal(ids, oids), (ids[60:], oids[60:])
+        assert np.array_equal(ids_graph, oids)
+        assert np.abs(lg - olg).max() <= 1e-4
+        m.kv_reset()
+        om.kv_reset()
+        n = len(prompt)
+        got, _ = m.forward(prompt, np.arange(n), np.zeros(n, np.int32))
+        want = om.forward(prompt, np.arange(n), np.zeros(n, np.int32))
+        assert np.abs(got - want).max() <= 1e-4
+
+
 def test_batched_decode_slots(make_model):
     """Per-slot prefill (seqs=b), then M=4 decode with seqs=NULL (src/runtime_main.c:325-352)."""
     path = make_model("tiny-qwen2-int8")

@@ -250,7 +250,11 @@ def test_oracle_reproduces_reference_golden_qwen2_05b(tmp_path):
                                   dict(arch="qwen2", layers=2, embd=96, heads=6, kv_heads=2, ffn=160, ctx=96,
                                        vocab=700, precision="fp16"),
                                   dict(arch="gpt2", layers=3, embd=48, heads=3, ctx=80, vocab=300,
-                                       precision="int8")])
+                                       precision="int8"),
+                                  # sliding window 16 (positions reach 31) and YaRN RoPE
+                                  dict(arch="qwen2", layers=2, embd=128, heads=4, kv_heads=2, ffn=192, ctx=96,
+                                       vocab=600, precision="int8", sliding_window=16, rope_type="yarn",
+                                       yarn_factor=4.0, yarn_orig_max=24, yarn_attention_factor=1.1)])
 def test_oracle_equals_reference_live(spec, tmp_path):
     path = tmp_path / "m.ecm"
     ec.synth(path, name="m", **spec)

@@ -25,7 +25,7 @@ HIPFLAGS := --offload-arch=$(ARCH) -O3 -std=c++17 -fPIC -ffp-contract=off \
             -Xclang -target-feature -Xclang -packed-fp32-ops -Iinclude -I$(SRC) -Wall
 CFLAGS   := -O2 -std=c11 -Wall -Wextra -fPIC -Iinclude -ffp-contract=off
 
-HIPSRC := $(SRC)/kernels.hip $(SRC)/gemm_mfma.hip $(SRC)/attn_prefill.hip $(SRC)/gemv_i8.hip $(SRC)/gemv_f16.hip $(SRC)/gemv_bf16.hip $(SRC)/runtime.hip
+HIPSRC := $(SRC)/kernels.hip $(SRC)/gemm_mfma.hip $(SRC)/attn_prefill.hip $(SRC)/topk.hip $(SRC)/gemv_i8.hip $(SRC)/gemv_f16.hip $(SRC)/gemv_bf16.hip $(SRC)/runtime.hip
 HIPOBJ := $(HIPSRC:$(SRC)/%.hip=$(OBJ)/%.o)
 
 all: $(LIB) $(RUNTIME) $(SYNTH) oracle
@@ -39,7 +39,10 @@ $(OBJ)/%.o: $(SRC)/%.hip $(SRC)/ec_device.h $(SRC)/ec_kernels.h $(SRC)/gemv_impl
 $(OBJ)/ecm.o: $(SRC)/ecm.c include/edgecore.h | $(OBJ)
 	$(CC) $(CFLAGS) -c $< -o $@
 
-$(LIB): $(HIPOBJ) $(OBJ)/ecm.o | $(PKG)/lib
+$(OBJ)/sample.o: $(SRC)/sample.c include/edgecore.h | $(OBJ)
+	$(CC) $(CFLAGS) -c $< -o $@
+
+$(LIB): $(HIPOBJ) $(OBJ)/ecm.o $(OBJ)/sample.o | $(PKG)/lib
 	$(HIPCC) --offload-arch=$(ARCH) -shared -fPIC $^ -o $@
 
 $(RUNTIME): $(SRC)/runtime_main.c include/edgecore.h $(LIB) | $(PKG)/bin

@@ -27,7 +27,7 @@ HEADER = REPO_DIR / "include" / "edgecore.h"
 
 __all__ = [
     "EdgeCoreError", "lib", "GPT2", "Model", "gemm_int8", "gemm_fp16_fp32",
-    "gemm_bf16_fp32", "quantize_int8_symmetric", "synth", "PKG_DIR", "LIB_PATH",
+    "gemm_bf16_fp32", "quantize_int8_symmetric", "synth", "sample_full", "sample_candidates", "topk_dev", "PKG_DIR", "LIB_PATH",
     "RUNTIME", "SYNTH", "HEADER",
 ]
 
@@ -89,6 +89,13 @@ _SIG = {
     "gpt2_forward": (None, [_P, _P, _P, _P, _I, _P]),
     "qwen2_forward": (None, [_P, _P, _P, _P, _I, _P]),
     "gpt2_forward_ex": (_I, [_P, _P, _P, _P, _I, _I, _P, _P]),
+    "gpt2_forward_topk": (_I, [_P, _P, _P, _P, _I, _I, _I, _P, _P, _P]),
+    "ec_topk_max": (_I, []),
+    "ec_last_logits": (_I, [_P, _I, _P]),
+    "ec_topk_dev": (_I, [_P, _I, _I, _I, _I, _P, _P, _P]),
+    "ec_rng_next": (C.c_uint, [C.POINTER(C.c_ulonglong)]),
+    "ec_sample_full": (_I, [_P, _I, C.c_float, _I, C.POINTER(C.c_ulonglong)]),
+    "ec_sample_candidates": (_I, [_P, _P, _I, _I, C.c_float, _I, C.POINTER(C.c_ulonglong)]),
     "gpt2_kv_reset": (_I, [_P]),
     "ecm_parse": (_I, [_P, C.c_size_t, _P, _I, _P]),
     "ec_last_error": (C.c_char_p, []),
@@ -274,6 +281,27 @@ class Model:
         _check(rc, "gpt2_forward_ex")
         return lg, am
 
+    def forward_topk(self, tokens: Sequence[int], positions: Sequence[int],
+                     seqs: Optional[Sequence[int]] = None, lm_from: int = 0, top_k: int = 40):
+        """gpt2_forward_topk; returns (vals, idx [M - lm_from, top_k + 1], status [M - lm_from])."""
+        t = np.ascontiguousarray(tokens, np.int32)
+        p = np.ascontiguousarray(positions, np.int32)
+        s = None if seqs is None else np.ascontiguousarray(seqs, np.int32)
+        M = len(t)
+        rows = M - lm_from
+        vals = np.empty((rows, top_k + 1), np.float32)
+        idx = np.empty((rows, top_k + 1), np.int32)
+        status = np.empty(rows, np.int32)
+        rc = lib().gpt2_forward_topk(C.byref(self.g), _ptr(t), _ptr(p), _ptr(s), M, lm_from, top_k,
+                                     _ptr(vals), _ptr(idx), _ptr(status))
+        _check(rc, "gpt2_forward_topk")
+        return vals, idx, status
+
+    def last_logits(self, row: int) -> np.ndarray:
+        out = np.empty(self.vocab, np.float32)
+        _check(lib().ec_last_logits(C.byref(self.g), row, _ptr(out)), "ec_last_logits")
+        return out
+
     def generate(self, prompt: Sequence[int], n_gen: int, want_logits: bool = False):
         """gen_and_measure at batch 1, greedy (src/runtime_main.c:293-362):
         returns (ids, [n_gen, V] step logits or None)."""
@@ -310,6 +338,43 @@ class Model:
             self.close()
         except Exception:
             pass
+
+
+# ---------------------------------------------------------------------------
+# sampling (src/runtime_main.c:205-248)
+# ---------------------------------------------------------------------------
+
+def sample_full(logits: np.ndarray, temp: float, top_k: int, state: int) -> tuple[int, int]:
+    """ec_sample_full on one row; returns (token, new LCG state)."""
+    row = np.ascontiguousarray(logits, np.float32)
+    st = C.c_ulonglong(state)
+    tok = lib().ec_sample_full(_ptr(row), len(row), temp, top_k, C.byref(st))
+    return tok, st.value
+
+
+def sample_candidates(vals: np.ndarray, idx: np.ndarray, vocab: int, temp: float, top_k: int,
+                      state: int) -> tuple[int, int]:
+    """ec_sample_candidates on a row's top_k + 1 candidates; returns (token, new state)."""
+    v = np.ascontiguousarray(vals, np.float32)
+    i = np.ascontiguousarray(idx, np.int32)
+    st = C.c_ulonglong(state)
+    tok = lib().ec_sample_candidates(_ptr(v), _ptr(i), len(v), vocab, temp, top_k, C.byref(st))
+    return tok, st.value
+
+
+def topk_dev(logits: np.ndarray, top_k: int):
+    """ec_topk_dev on host rows (copied to the device): (vals, idx, status)."""
+    L = np.ascontiguousarray(np.atleast_2d(logits), np.float32)
+    rows, V = L.shape
+    buf = DeviceBuffer.from_array(L)
+    try:
+        vals = np.empty((rows, top_k + 1), np.float32)
+        idx = np.empty((rows, top_k + 1), np.int32)
+        status = np.empty(rows, np.int32)
+        _check(lib().ec_topk_dev(buf.ptr, rows, V, V, top_k, _ptr(vals), _ptr(idx), _ptr(status)), "ec_topk_dev")
+        return vals, idx, status
+    finally:
+        buf.close()
 
 
 # ---------------------------------------------------------------------------

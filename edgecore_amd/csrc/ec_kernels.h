@@ -190,6 +190,18 @@ hipError_t argmax_rows(const float *logits, int rows, int V, int *out, hipStream
 hipError_t argmax_finalize(const unsigned long long *cand, int ncand, const float *logits,
                            int ldl, int rows, int *out, hipStream_t st);
 
+// top_k + 1 largest logits per row for sampling (topk.hip).  topk_select sorts
+// chunks of 4096 logits into cand [rows][topk_chunks(V)][top_k + 1] keys and
+// nan_flag [rows][topk_chunks(V)]; topk_merge writes vals/idx [rows][top_k + 1]
+// (value descending, index ascending) and status [rows] (device pointers).
+constexpr int kTopkMax = 128;
+int topk_chunks(int V);
+bool topk_ok(int V, int top_k);
+hipError_t topk_select(const float *L, int rows, int V, int ld, int top_k, unsigned long long *cand,
+                       unsigned char *nan_flag, hipStream_t st);
+hipError_t topk_merge(const unsigned long long *cand, const unsigned char *nan_flag, int rows, int V, int top_k,
+                      float *vals, int *idx, int *status, hipStream_t st);
+
 // elementwise device math (ec_device_math)
 enum { MATH_EXPF = 0, MATH_SILU = 1, MATH_GELU = 2, MATH_F32_TO_F16 = 3, MATH_F16_TO_F32 = 4, MATH_QUANT1 = 5, MATH_COPY = 6 };
 hipError_t device_math(int op, const void *in, void *out, size_t n, hipStream_t st);

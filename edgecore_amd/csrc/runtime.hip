@@ -452,6 +452,20 @@ struct DevModel {
   hipGraphExec_t step_graph = nullptr;
   int step_bucket = 0;  // the graph's attention LDS covers positions < step_bucket
   int *h_amax = nullptr;  // pinned: the graph's argmax output
+  // device top-k for sampled decoding: chunk candidates, NaN flags, results
+  unsigned long long *tk_cand = nullptr;  // [lm_rows][topk_chunks(V)][kTopkMax + 1]
+  unsigned char *tk_nan = nullptr;        // [lm_rows][topk_chunks(V)]
+  float *tk_vals = nullptr;               // [lm_rows][kTopkMax + 1]
+  int *tk_idx = nullptr, *tk_status = nullptr;
+  int last_lm_rows = 0;  // rows of the LM-head chunk the last forward left in `logits`
+};
+
+// host outputs of a forward that selects the top-k logits of its LM-head rows
+struct TopkReq {
+  int top_k;
+  float *vals;
+  int *idx;
+  int *status;
 };
 
 namespace {
@@ -497,7 +511,8 @@ struct Loader {
 static void free_dev(DevModel *d) {
   if (!d) return;
   void *ps[] = {d->arena, d->rope, d->d_tok, d->d_pos, d->d_slot, d->d_amax, d->x, d->h, d->qkv,
-                d->att, d->ff, d->aq, d->as, d->logits, d->kc, d->vc, d->cand};
+                d->att, d->ff, d->aq, d->as, d->logits, d->kc, d->vc, d->cand, d->tk_cand,
+                d->tk_nan, d->tk_vals, d->tk_idx, d->tk_status};
   for (void *p : ps)
     if (p) (void)hipFree(p);
   if (d->h_stage) (void)hipHostFree(d->h_stage);
@@ -760,6 +775,14 @@ static int load_impl(GPT2 *g, const char *path, int batch_cap, int max_ctx) {
   EC_HIP(hipHostMalloc((void **)&d->h_amax, 4 * sizeof(int), hipHostMallocDefault));
   d->ncand = gemv_max_blocks();
   EC_HIP(hipMalloc(&d->cand, (size_t)d->lm_rows * d->ncand * sizeof(unsigned long long)));
+  {
+    const size_t nb = (size_t)topk_chunks(V), n = kTopkMax + 1;
+    EC_HIP(hipMalloc(&d->tk_cand, (size_t)d->lm_rows * nb * n * sizeof(unsigned long long)));
+    EC_HIP(hipMalloc(&d->tk_nan, (size_t)d->lm_rows * nb));
+    EC_HIP(hipMalloc(&d->tk_vals, (size_t)d->lm_rows * n * sizeof(float)));
+    EC_HIP(hipMalloc(&d->tk_idx, (size_t)d->lm_rows * n * sizeof(int)));
+    EC_HIP(hipMalloc(&d->tk_status, (size_t)d->lm_rows * sizeof(int)));
+  }
   g->ws_x = d->x;
   g->ws_tmp = d->h;
   g->ws_qkv = d->qkv;
@@ -886,7 +909,7 @@ static int attn_vtile(int max_npos, int hd, int kv) {
 // (RoPE and the KV append then run inside attention); abytes: algorithmic
 // attention bytes, for the profiler only.
 static int enqueue_forward(GPT2 *g, DevModel *d, int M, int lm_from, bool distinct, bool run, int max_npos,
-                           double abytes, float *logits, int *argmax, hipStream_t s) {
+                           double abytes, float *logits, int *argmax, const TopkReq *tk, hipStream_t s) {
   const int E = g->n_embd, H = g->n_head, V = g->vocab, kv = g->n_kv_embd, hd = g->head_dim;
   const bool qwen = g->arch == ARCH_QWEN2, i8 = g->precision == 0, bf16 = g->precision == 2;
   const int wt = i8 ? WT_I8 : (bf16 ? WT_BF16 : WT_F16);
@@ -976,6 +999,17 @@ static int enqueue_forward(GPT2 *g, DevModel *d, int M, int lm_from, bool distin
     if (logits)
       EC_HIP(hipMemcpyAsync(logits + (size_t)(r0 - lm_from) * V, d->logits, (size_t)rows * V * 4,
                             hipMemcpyDeviceToHost, s));
+    if (tk) {
+      const int n = tk->top_k + 1, ro = r0 - lm_from;
+      EC_LAUNCH("topk_select", 4.0 * rows * V,
+                topk_select(d->logits, rows, V, V, tk->top_k, d->tk_cand, d->tk_nan, s));
+      EC_LAUNCH("topk_merge", 8.0 * rows * topk_chunks(V) * n,
+                topk_merge(d->tk_cand, d->tk_nan, rows, V, tk->top_k, d->tk_vals, d->tk_idx, d->tk_status, s));
+      EC_HIP(hipMemcpyAsync(tk->vals + (size_t)ro * n, d->tk_vals, (size_t)rows * n * 4, hipMemcpyDeviceToHost, s));
+      EC_HIP(hipMemcpyAsync(tk->idx + (size_t)ro * n, d->tk_idx, (size_t)rows * n * 4, hipMemcpyDeviceToHost, s));
+      EC_HIP(hipMemcpyAsync(tk->status + ro, d->tk_status, (size_t)rows * 4, hipMemcpyDeviceToHost, s));
+    }
+    d->last_lm_rows = rows;
   }
   if (argmax && lm_from < M)
     EC_HIP(hipMemcpyAsync(argmax, d->d_amax, (size_t)(M - lm_from) * 4, hipMemcpyDeviceToHost, s));
@@ -983,7 +1017,7 @@ static int enqueue_forward(GPT2 *g, DevModel *d, int M, int lm_from, bool distin
 }
 
 static int forward_impl(GPT2 *g, const int *tokens, const int *positions, const int *seqs, int M,
-                        int lm_from, float *logits, int *argmax) {
+                        int lm_from, float *logits, int *argmax, const TopkReq *tk = nullptr) {
   EC_INIT();
   DevModel *d = (DevModel *)g->dev;
   if (!d) return set_err(-1, "model not loaded");
@@ -1033,7 +1067,9 @@ static int forward_impl(GPT2 *g, const int *tokens, const int *positions, const 
   // token / position / slot into the pinned stage before each replay.
   int bucket = (max_npos + 511) / 512 * 512;
   if (bucket > d->eff_ctx) bucket = d->eff_ctx;
-  if (M == 1 && lm_from == 0 && argmax && !logits && !g_prof_on && g_use_graphs &&
+  if (tk && !topk_ok(V, tk->top_k))
+    return set_err(-1, "top_k=%d outside (0, %d) or above %d", tk->top_k, V, kTopkMax);
+  if (M == 1 && lm_from == 0 && argmax && !logits && !tk && !g_prof_on && g_use_graphs &&
       attn_vtile(bucket, hd, kv) >= 4) {
     if (!d->step_graph || d->step_bucket != bucket) {
       if (d->step_graph) {
@@ -1041,7 +1077,7 @@ static int forward_impl(GPT2 *g, const int *tokens, const int *positions, const 
         d->step_graph = nullptr;
       }
       EC_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
-      const int r = enqueue_forward(g, d, 1, 0, true, false, bucket, abytes, nullptr, d->h_amax, s);
+      const int r = enqueue_forward(g, d, 1, 0, true, false, bucket, abytes, nullptr, d->h_amax, nullptr, s);
       hipGraph_t graph = nullptr;
       const hipError_t e = hipStreamEndCapture(s, &graph);
       if (r) {
@@ -1059,7 +1095,7 @@ static int forward_impl(GPT2 *g, const int *tokens, const int *positions, const 
     argmax[0] = d->h_amax[0];
     return 0;
   }
-  const int r = enqueue_forward(g, d, M, lm_from, distinct, run, max_npos, abytes, logits, argmax, s);
+  const int r = enqueue_forward(g, d, M, lm_from, distinct, run, max_npos, abytes, logits, argmax, tk, s);
   if (r) return r;
   EC_HIP(hipStreamSynchronize(s));
   return 0;
@@ -1068,6 +1104,57 @@ static int forward_impl(GPT2 *g, const int *tokens, const int *positions, const 
 extern "C" int gpt2_forward_ex(GPT2 *g, const int *tokens, const int *positions, const int *seqs, int M,
                                int lm_from, float *logits, int *argmax) {
   return forward_impl(g, tokens, positions, seqs, M, lm_from, logits, argmax);
+}
+
+extern "C" int gpt2_forward_topk(GPT2 *g, const int *tokens, const int *positions, const int *seqs, int M,
+                                 int lm_from, int top_k, float *vals, int *idx, int *status) {
+  if (lm_from < M && (!vals || !idx || !status)) return set_err(-1, "gpt2_forward_topk: null output");
+  const TopkReq tk{top_k, vals, idx, status};
+  return forward_impl(g, tokens, positions, seqs, M, lm_from, nullptr, nullptr, &tk);
+}
+
+extern "C" int ec_topk_max(void) { return kTopkMax; }
+
+extern "C" int ec_last_logits(GPT2 *g, int row, float *out) {
+  EC_INIT();
+  DevModel *d = g ? (DevModel *)g->dev : nullptr;
+  if (!d) return set_err(-1, "model not loaded");
+  if (!out || row < 0 || row >= d->last_lm_rows)
+    return set_err(-1, "ec_last_logits: row %d outside the last LM-head chunk (%d rows)", row, d->last_lm_rows);
+  EC_HIP(hipMemcpyAsync(out, d->logits + (size_t)row * g->vocab, (size_t)g->vocab * 4, hipMemcpyDeviceToHost,
+                        g_stream));
+  EC_HIP(hipStreamSynchronize(g_stream));
+  return 0;
+}
+
+extern "C" int ec_topk_dev(const float *logits, int rows, int vocab, int ld, int top_k, float *vals, int *idx,
+                           int *status) {
+  EC_INIT();
+  if (rows < 0 || ld < vocab) return set_err(-1, "ec_topk_dev: rows=%d ld=%d vocab=%d", rows, ld, vocab);
+  if (rows == 0) return 0;
+  if (!topk_ok(vocab, top_k))
+    return set_err(-1, "ec_topk_dev: top_k=%d outside (0, %d) or above %d", top_k, vocab, kTopkMax);
+  if (!logits || !vals || !idx || !status) return set_err(-1, "ec_topk_dev: null pointer");
+  const int nb = topk_chunks(vocab), n = top_k + 1;
+  unsigned long long *cand = nullptr;
+  unsigned char *nanf = nullptr;
+  float *dv = nullptr;
+  int *di = nullptr, *ds = nullptr;
+  hipError_t e = hipMalloc(&cand, (size_t)rows * nb * n * sizeof(unsigned long long));
+  if (e == hipSuccess) e = hipMalloc(&nanf, (size_t)rows * nb);
+  if (e == hipSuccess) e = hipMalloc(&dv, (size_t)rows * n * 4);
+  if (e == hipSuccess) e = hipMalloc(&di, (size_t)rows * n * 4);
+  if (e == hipSuccess) e = hipMalloc(&ds, (size_t)rows * 4);
+  if (e == hipSuccess) e = topk_select(logits, rows, vocab, ld, top_k, cand, nanf, g_stream);
+  if (e == hipSuccess) e = topk_merge(cand, nanf, rows, vocab, top_k, dv, di, ds, g_stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(vals, dv, (size_t)rows * n * 4, hipMemcpyDeviceToHost, g_stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(idx, di, (size_t)rows * n * 4, hipMemcpyDeviceToHost, g_stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(status, ds, (size_t)rows * 4, hipMemcpyDeviceToHost, g_stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
+  for (void *p : {(void *)cand, (void *)nanf, (void *)dv, (void *)di, (void *)ds})
+    if (p) (void)hipFree(p);
+  if (e != hipSuccess) return set_err(-3, "ec_topk_dev: %s", hipGetErrorString(e));
+  return 0;
 }
 
 extern "C" void gpt2_forward(GPT2 *g, const int *tokens, const int *positions, const int *seqs, int M,

@@ -169,50 +169,9 @@ static void usage(const char *prog)
             prog);
 }
 
-/* 64-bit LCG of src/runtime_main.c:206-211 */
-static unsigned long rng_state;
-static unsigned rng_next(void)
-{
-    rng_state = rng_state * 6364136223846793005UL + 1442695040888963407UL;
-    return (unsigned)(rng_state >> 33);
-}
-
-/* sample_token of src/runtime_main.c:213-248 (host side, temp > 0) */
-static int sample_token(const float *logits, int vocab, float temp, int top_k)
-{
-    if (temp <= 0.0f) {
-        int best = 0;
-        for (int i = 1; i < vocab; i++)
-            if (logits[i] > logits[best]) best = i;
-        return best;
-    }
-    int *idx = malloc((size_t)vocab * sizeof(int));
-    for (int i = 0; i < vocab; i++) idx[i] = i;
-    for (int i = 0; i < top_k && i < vocab; i++) {
-        int best = i;
-        for (int j = i + 1; j < vocab; j++)
-            if (logits[idx[j]] > logits[idx[best]]) best = j;
-        int t = idx[i]; idx[i] = idx[best]; idx[best] = t;
-    }
-    int n = top_k > 0 && top_k < vocab ? top_k : vocab;
-    float maxl = logits[idx[0]];
-    double sum = 0.0;
-    float *p = malloc((size_t)n * sizeof(float));
-    for (int i = 0; i < n; i++) {
-        p[i] = expf((logits[idx[i]] - maxl) / temp);
-        sum += p[i];
-    }
-    double r = (double)rng_next() / (double)0xffffffffu;
-    double acc = 0.0;
-    int pick = idx[n - 1];
-    for (int i = 0; i < n; i++) {
-        acc += p[i] / sum;
-        if (r < acc) { pick = idx[i]; break; }
-    }
-    free(p);
-    free(idx);
-    return pick;
-}
+/* the LCG state of src/runtime_main.c:205-211; sample_token (:213-248) is
+   ec_sample_full / ec_sample_candidates of the library */
+static unsigned long long rng_state;
 
 static int read_tokens(const char *path, int *out, int cap, int *n)
 {
@@ -257,6 +216,12 @@ static void gen_and_measure(GPT2 *g, const int *prompt, int nprompt, int n_gen, 
     int *positions = malloc((size_t)batch * sizeof(int)), *cur = malloc((size_t)batch * sizeof(int));
     int *next = malloc((size_t)batch * sizeof(int));
     float *logits = temp > 0.0f ? malloc((size_t)batch * V * sizeof(float)) : NULL;
+    /* sampled steps select the top_k + 1 logits on the GPU when top_k allows */
+    const int use_topk = temp > 0.0f && top_k > 0 && top_k < V && top_k <= ec_topk_max();
+    const int nc = top_k + 1;
+    float *tk_vals = use_topk ? malloc((size_t)batch * nc * sizeof(float)) : NULL;
+    int *tk_idx = use_topk ? malloc((size_t)batch * nc * sizeof(int)) : NULL;
+    int *tk_status = use_topk ? malloc((size_t)batch * sizeof(int)) : NULL;
     int first;
 
     if (gpt2_kv_reset(g)) die_forward();
@@ -274,12 +239,22 @@ static void gen_and_measure(GPT2 *g, const int *prompt, int nprompt, int n_gen, 
     for (int step = 0; step < n_gen; step++) {
         for (int b = 0; b < batch; b++) positions[b] = npos;
         double s0 = now_sec();
-        int rc = temp > 0.0f ? gpt2_forward_ex(g, cur, positions, NULL, batch, 0, logits, NULL)
-                             : gpt2_forward_ex(g, cur, positions, NULL, batch, 0, NULL, next);
+        int rc = use_topk ? gpt2_forward_topk(g, cur, positions, NULL, batch, 0, top_k, tk_vals, tk_idx, tk_status)
+                 : temp > 0.0f ? gpt2_forward_ex(g, cur, positions, NULL, batch, 0, logits, NULL)
+                               : gpt2_forward_ex(g, cur, positions, NULL, batch, 0, NULL, next);
         if (rc) die_forward();
         tok_ms[step] = (now_sec() - s0) * 1000.0;
         for (int b = 0; b < batch; b++) {
-            int tok = temp > 0.0f ? sample_token(logits + (size_t)b * V, V, temp, top_k) : next[b];
+            int tok;
+            if (use_topk && !tk_status[b]) {
+                tok = ec_sample_candidates(tk_vals + (size_t)b * nc, tk_idx + (size_t)b * nc, nc, V, temp, top_k,
+                                           &rng_state);
+            } else if (use_topk) {  /* NaN or a tie at the top_k boundary: the whole row */
+                if (ec_last_logits(g, b, logits + (size_t)b * V)) die_forward();
+                tok = ec_sample_full(logits + (size_t)b * V, V, temp, top_k, &rng_state);
+            } else {
+                tok = temp > 0.0f ? ec_sample_full(logits + (size_t)b * V, V, temp, top_k, &rng_state) : next[b];
+            }
             cur[b] = tok;
             if (b == 0) ids[n_ids++] = tok;
         }
@@ -288,6 +263,7 @@ static void gen_and_measure(GPT2 *g, const int *prompt, int nprompt, int n_gen, 
     *out_n = n_ids;
     memcpy(out_ids, ids, (size_t)n_ids * sizeof(int));
     free(ids); free(ppos); free(pseq); free(positions); free(cur); free(next); free(logits);
+    free(tk_vals); free(tk_idx); free(tk_status);
 }
 
 static int cmp_double(const void *a, const void *b)
@@ -535,7 +511,7 @@ int main(int argc, char **argv)
     if (!a.model) { usage(argv[0]); return 2; }
     if (a.batch < 1) a.batch = 1;
     if (a.n_tokens < 0) a.n_tokens = 0;
-    rng_state = (unsigned long)a.seed;
+    rng_state = (unsigned long long)(unsigned long)a.seed;
     Affinity aff;
     affinity_apply(a.affinity, &aff);
     int want = -1;

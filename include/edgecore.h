@@ -298,6 +298,40 @@ int gpt2_kv_reset(GPT2 *g);
 int gpt2_forward_ex(GPT2 *g, const int *tokens, const int *positions, const int *seqs,
                     int M, int lm_from, float *logits, int *argmax);
 
+/* Forward whose LM-head rows [lm_from, M) return their top_k + 1 largest
+ * logits instead of all vocab: vals/idx [M - lm_from][top_k + 1] (value
+ * descending, index ascending) and status [M - lm_from]: 0 when the row has
+ * no NaN and its top_k-th and (top_k+1)-th values differ, so that
+ * ec_sample_candidates gives sample_token's token (src/runtime_main.c:213-248);
+ * 1 otherwise (take the row from ec_last_logits and use ec_sample_full).
+ * 0 < top_k < vocab, top_k <= ec_topk_max().  Replaces copying every logit
+ * row back for sampled decoding.  0 or <0. */
+int gpt2_forward_topk(GPT2 *g, const int *tokens, const int *positions, const int *seqs,
+                      int M, int lm_from, int top_k, float *vals, int *idx, int *status);
+
+/* Largest top_k of gpt2_forward_topk / ec_topk_dev. */
+int ec_topk_max(void);
+
+/* Row `row` (counted from lm_from, < the LM-head chunk of the last forward,
+ * which holds at least batch_cap rows) of the last forward's logits, into out
+ * [vocab] (host).  0 or <0. */
+int ec_last_logits(GPT2 *g, int row, float *out);
+
+/* The device top-k selection alone: rows x vocab fp32 logits in device memory
+ * (row stride ld) -> vals/idx/status as in gpt2_forward_topk (host). */
+int ec_topk_dev(const float *logits, int rows, int vocab, int ld, int top_k, float *vals, int *idx,
+                int *status);
+
+/* Sampling of src/runtime_main.c:205-248.  ec_rng_next: the driver's LCG
+ * (state advances, returns the top 31 bits).  ec_sample_full: sample_token on
+ * a whole row (temp <= 0: greedy).  ec_sample_candidates: the same token from
+ * the row's top_k + 1 candidates of a status-0 row; -1 when the arguments do
+ * not allow it (temp <= 0, top_k outside (0, vocab), too few candidates). */
+unsigned ec_rng_next(unsigned long long *state);
+int ec_sample_full(const float *logits, int vocab, float temp, int top_k, unsigned long long *state);
+int ec_sample_candidates(const float *vals, const int *idx, int ncand, int vocab, float temp, int top_k,
+                         unsigned long long *state);
+
 /* sizeof(GPT2) as compiled into the library (lets foreign-function hosts
  * check their mirror of the struct). */
 size_t ec_gpt2_sizeof(void);

@@ -18,6 +18,7 @@ ORACLE_DIR = Path(__file__).resolve().parent
 ORACLE_LIB = ORACLE_DIR / "liboracle.so"
 REF_LIB = ORACLE_DIR / "_ref" / "libref.so"
 REF_RUNTIME = ORACLE_DIR / "_ref" / "edgecore-runtime"
+REF_SAMPLE = ORACLE_DIR / "_ref" / "libref_sample.so"
 
 _P, _I = C.c_void_p, C.c_int
 _O: Optional[C.CDLL] = None
@@ -67,6 +68,33 @@ def olib() -> C.CDLL:
 
 def ref_available() -> bool:
     return REF_LIB.exists()
+
+
+_RS: Optional[C.CDLL] = None
+
+
+def ref_sample_available() -> bool:
+    return REF_SAMPLE.exists()
+
+
+def ref_sample(logits: np.ndarray, temp: float, top_k: int, state: int) -> tuple[int, int]:
+    """The reference driver's own sample_token (src/runtime_main.c:213-248, built
+    from that file by ref_sample.c) on one row, with its LCG state set to
+    `state` first; returns (token, state after)."""
+    global _RS
+    if _RS is None:
+        L = C.CDLL(str(REF_SAMPLE))
+        L.ref_sample_token.restype = _I
+        L.ref_sample_token.argtypes = [_P, _I, C.c_float, _I]
+        L.ref_rng_set.restype = None
+        L.ref_rng_set.argtypes = [C.c_ulonglong]
+        L.ref_rng_get.restype = C.c_ulonglong
+        L.ref_rng_get.argtypes = []
+        _RS = L
+    row = np.ascontiguousarray(logits, np.float32)
+    _RS.ref_rng_set(state)
+    tok = _RS.ref_sample_token(row.ctypes.data, len(row), temp, top_k)
+    return tok, _RS.ref_rng_get()
 
 
 def rlib() -> C.CDLL:

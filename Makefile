@@ -42,7 +42,10 @@ $(OBJ)/ecm.o: $(SRC)/ecm.c include/edgecore.h | $(OBJ)
 $(OBJ)/sample.o: $(SRC)/sample.c include/edgecore.h | $(OBJ)
 	$(CC) $(CFLAGS) -c $< -o $@
 
-$(LIB): $(HIPOBJ) $(OBJ)/ecm.o $(OBJ)/sample.o | $(PKG)/lib
+$(OBJ)/tokenizer.o: $(SRC)/tokenizer.c include/edgecore.h | $(OBJ)
+	$(CC) $(CFLAGS) -c $< -o $@
+
+$(LIB): $(HIPOBJ) $(OBJ)/ecm.o $(OBJ)/sample.o $(OBJ)/tokenizer.o | $(PKG)/lib
 	$(HIPCC) --offload-arch=$(ARCH) -shared -fPIC $^ -o $@
 
 $(RUNTIME): $(SRC)/runtime_main.c include/edgecore.h $(LIB) | $(PKG)/bin

@@ -114,6 +114,9 @@ _SIG = {
     "ec_gpt2_sizeof": (C.c_size_t, []),
     "ec_device_math": (_I, [_I, _P, _P, C.c_size_t]),
     "tokenizer_encode": (_I, [_P, C.c_char_p, _P, _I]),
+    "tokenizer_load": (_I, [_P, C.c_char_p, C.c_size_t, C.c_char_p, C.c_size_t, _I, _I]),
+    "tokenizer_free": (None, [_P]),
+    "tokenizer_decode": (_P, [_P, _P, _I]),
     "now_sec": (C.c_double, []),
     "peak_rss_gb": (C.c_float, []),
 }

@@ -1,7 +1,6 @@
 /*
  * Host side of the .ecm format and small host utilities of the library:
- * ecm_parse (src/gpt2.c:11-136 of the reference), the byte-level tokenizer
- * (subset of src/tokenizer.c:925-1186), the int8 weight packer
+ * ecm_parse (src/gpt2.c:11-136 of the reference), the int8 weight packer
  * (edgecore/ecm.py:50-59), now_sec / peak_rss_gb (src/runtime_main.c:10-28).
  */
 #define _GNU_SOURCE
@@ -181,97 +180,3 @@ void ec_quantize_int8_symmetric(const float *w, int rows, int cols, int8_t *q, f
     }
 }
 
-/* ------------------------------------------------------------------ */
-/* byte-level tokenizer                                                 */
-/* ------------------------------------------------------------------ */
-
-static uint32_t rd32(const uint8_t *p)
-{
-    uint32_t v;
-    memcpy(&v, p, 4);
-    return v;
-}
-
-/* Vocab blob: u32 count, then (u32 id, u32 len, bytes) entries; merges blob:
- * u32 count, then (u32 len, bytes, u32 len, bytes) pairs
- * (edgecore/ecm.py:127-171, src/tokenizer.c:925-1015). */
-int tokenizer_load(Tokenizer *t, const void *vocab_blob, size_t vocab_bytes,
-                   const void *merges_blob, size_t merges_bytes, int vocab_size, int variant)
-{
-    memset(t, 0, sizeof *t);
-    t->vocab_size = vocab_size;
-    t->variant = variant;
-    t->eos_id = -1;
-    t->id_to_token = (char **)calloc((size_t)(vocab_size > 0 ? vocab_size : 1), sizeof(char *));
-    t->byte_to_id = (int32_t *)malloc(256 * sizeof(int32_t));
-    if (!t->id_to_token || !t->byte_to_id) return -1;
-    for (int b = 0; b < 256; b++) t->byte_to_id[b] = -1;
-    const uint8_t *p = (const uint8_t *)vocab_blob, *end = p + vocab_bytes;
-    uint32_t count = vocab_bytes >= 4 ? rd32(p) : 0;
-    p += 4;
-    for (uint32_t i = 0; i < count && p + 8 <= end; i++) {
-        uint32_t id = rd32(p), len = rd32(p + 4);
-        p += 8;
-        if (p + len > end) break;
-        if (id < (uint32_t)vocab_size && !t->id_to_token[id]) {
-            char *s = (char *)malloc((size_t)len + 1);
-            memcpy(s, p, len);
-            s[len] = 0;
-            t->id_to_token[id] = s;
-            if (len == 1 && t->byte_to_id[(uint8_t)s[0]] < 0) t->byte_to_id[(uint8_t)s[0]] = (int32_t)id;
-            if (len == 13 && !memcmp(s, "<|endoftext|>", 13)) t->eos_id = (int)id;
-        }
-        p += len;
-    }
-    t->n_merges = merges_bytes >= 4 ? (int)rd32((const uint8_t *)merges_blob) : 0;
-    return 0;
-}
-
-void tokenizer_free(Tokenizer *t)
-{
-    if (t->id_to_token) {
-        for (int i = 0; i < t->vocab_size; i++) free(t->id_to_token[i]);
-        free(t->id_to_token);
-    }
-    free(t->byte_to_id);
-    memset(t, 0, sizeof *t);
-}
-
-int tokenizer_encode(const Tokenizer *t, const char *text, int *out, int max_out)
-{
-    if (t->n_merges > 0) {
-        fprintf(stderr, "tokenizer: BPE merges are not supported here; pass token ids "
-                        "with --tokens-file\n");
-        return -1;
-    }
-    int n = 0;
-    for (const uint8_t *s = (const uint8_t *)text; *s; s++) {
-        if (n >= max_out) return -1;
-        int id = t->byte_to_id ? t->byte_to_id[*s] : -1;
-        out[n++] = id >= 0 ? id : *s;
-    }
-    return n;
-}
-
-char *tokenizer_decode(const Tokenizer *t, const int *ids, int n)
-{
-    size_t total = 0;
-    for (int i = 0; i < n; i++) {
-        int id = ids[i];
-        if (id < 0 || id >= t->vocab_size || !t->id_to_token[id]) id = 0;
-        if (t->id_to_token[id]) total += strlen(t->id_to_token[id]);
-    }
-    char *out = (char *)malloc(total + 1);
-    size_t o = 0;
-    for (int i = 0; i < n; i++) {
-        int id = ids[i];
-        if (id < 0 || id >= t->vocab_size || !t->id_to_token[id]) id = 0;
-        const char *s = t->id_to_token[id];
-        if (!s) continue;
-        size_t l = strlen(s);
-        memcpy(out + o, s, l);
-        o += l;
-    }
-    out[o] = 0;
-    return out;
-}

@@ -133,10 +133,11 @@ int ec_quantize_rows_dev(const float *in, int M, int K, int8_t *q, float *s);
 /* tokenizer (src/edgecore.h:142-164)                                   */
 /* ------------------------------------------------------------------ */
 
-/* Byte-level only: the library reads the .ecm vocab blob and maps each input
- * byte to its single-byte token (the raw byte value when the vocab has none),
- * which is what the reference BPE produces for byte vocabularies without
- * merges.  A vocabulary with merges is rejected by tokenizer_encode (-1). */
+/* Byte-level BPE over the .ecm tokenizer blobs (src/tokenizer.c:500-1186):
+ * GPT-2 (variant 0) or Qwen2 (variant 1) pre-tokenization, merges applied in
+ * file order, <|...|> special tokens; tokenizer_encode returns the id count
+ * or -1 when max_out is too small; tokenizer_decode returns a malloc'ed
+ * string. */
 typedef struct {
     char **id_to_token;
     int32_t *byte_to_id;

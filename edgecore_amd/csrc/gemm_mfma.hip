@@ -69,6 +69,41 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemvArgs a) {
     if (t < 32) etab[t] = ec_exp2_32[t];
   }
 
+  // epilogue operands, loaded before the K loop so that their latency hides
+  // behind it: the row scales of this lane's rows, the weight scales / bias
+  // of its columns and, for a residual, the old output values.  Indices are
+  // clamped into the matrix and absent vectors read a stand-in (the weight
+  // rows); the values are selected at use.
+  constexpr int JO = SWI ? TJ / 2 : TJ;  // output column tiles
+  const int lrow0 = m0 + wm * WM + 4 * lq, lcol0 = n0 + (SWI ? wn * (kBN / 4) : wn * WN) + lr;
+  float e_as[TI][4], e_bs[JO], e_bv[JO], e_bs2[JO];
+  float e_old[RES ? TI : 1][RES ? JO : 1][4];
+  {
+    const float *stand = (const float *)a.W;  // N*K >= 4N bytes: valid for every column index
+    const float *wsp = a.ws ? a.ws : stand, *bvp = a.bias ? a.bias : stand;
+    const float *ws2p = (SWI && a.ws2) ? a.ws2 : stand;
+#pragma unroll
+    for (int i = 0; i < TI; i++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) e_as[i][r] = a.as[min(lrow0 + 16 * i + r, M - 1)];
+#pragma unroll
+    for (int j = 0; j < JO; j++) {
+      const int n = min(lcol0 + 16 * j, N - 1);
+      e_bs[j] = wsp[n];
+      e_bv[j] = bvp[n];
+      e_bs2[j] = ws2p[n];
+    }
+    if constexpr (RES) {
+#pragma unroll
+      for (int i = 0; i < TI; i++)
+#pragma unroll
+        for (int j = 0; j < JO; j++)
+#pragma unroll
+          for (int r = 0; r < 4; r++)
+            e_old[i][j][r] = a.out[(size_t)min(lrow0 + 16 * i + r, M - 1) * a.ldo + min(lcol0 + 16 * j, N - 1)];
+    }
+  }
+
   // global chunk sources of this thread: tile row, 16-byte column, row base
   const int8_t *arow[ACH];
   const int8_t *brow[BCH];
@@ -164,32 +199,29 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemvArgs a) {
   }
 
   // ---- epilogue: lane holds D[4*lq + r][lr] of each tile ----
-  constexpr int JO = SWI ? TJ / 2 : TJ;  // output column tiles
 #pragma unroll
   for (int j = 0; j < JO; j++) {
-    const int n = n0 + (SWI ? wn * (kBN / 4) : wn * WN) + 16 * j + lr;
+    const int n = lcol0 + 16 * j;
     if (n >= N) continue;
-    const float bs = a.ws ? a.ws[n] : 1.0f;
-    const float bv = (!SWI && a.bias) ? a.bias[n] : 0.0f;
-    float bs2 = 1.0f;
-    if constexpr (SWI) bs2 = a.ws2 ? a.ws2[n] : 1.0f;
+    const float bs = a.ws ? e_bs[j] : 1.0f;
+    const float bv = (!SWI && a.bias) ? e_bv[j] : 0.0f;
+    const float bs2 = (SWI && a.ws2) ? e_bs2[j] : 1.0f;
 #pragma unroll
     for (int i = 0; i < TI; i++) {
 #pragma unroll
       for (int r = 0; r < 4; r++) {
-        const int m = m0 + wm * WM + 16 * i + 4 * lq + r;
+        const int m = lrow0 + 16 * i + r;
         if (m >= M) continue;
-        const float as = a.as[m];
+        const float as = e_as[i][r];
         float v = i8_epilogue(acc[i][j][r], as, bs, bv);
-        float *o = a.out + (size_t)m * a.ldo + n;
         if constexpr (SWI) {
           const float u = i8_epilogue(acc[i][j + TJ / 2][r], as, bs2, 0.0f);
           v = silu(v, etab) * u;
         } else {
-          if constexpr (RES) v = *o + v;
+          if constexpr (RES) v = e_old[i][j][r] + v;
           if constexpr (GELU) v = gelu_new(v);
         }
-        *o = v;
+        a.out[(size_t)m * a.ldo + n] = v;
       }
     }
   }

@@ -33,6 +33,38 @@ __device__ __forceinline__ uint16_t f2h(float f) {
   return __builtin_bit_cast(uint16_t, (_Float16)f);
 }
 
+// a * fp32(h) rounded once, for the binary16 h in the low (HI = 0) or high
+// (HI = 1) half of w: one v_fma_mix_f32 with addend -0 instead of a convert
+// and a multiply.  The fp16 operand converts exactly and x + (-0) == x for
+// every x (signed zeros included), so the result equals a * h2f(h) bit for
+// bit; written in asm because the compiler folds that fma back into the two
+// instructions.
+template <int HI>
+__device__ __forceinline__ float mul_h(float a, uint32_t w) {
+  const float mz = __builtin_bit_cast(float, 0x80000000u);
+  float r;
+  if constexpr (HI) asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "=v"(r) : "v"(a), "v"(w), "v"(mz));
+  else asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[0,1,0]" : "=v"(r) : "v"(a), "v"(w), "v"(mz));
+  return r;
+}
+
+// s + a * fp32(h), the product rounded and then the add rounded (the
+// reference's order, no fusion): mul_h and the add in one asm statement so
+// that the product is consumed at once instead of being hoisted with all the
+// others of a dot into registers
+template <int HI>
+__device__ __forceinline__ float mac_h(float s, float a, uint32_t w) {
+  const float mz = __builtin_bit_cast(float, 0x80000000u);
+  float p;
+  if constexpr (HI)
+    asm("v_fma_mix_f32 %1, %2, %3, %4 op_sel:[0,1,0] op_sel_hi:[0,1,0]\n\tv_add_f32 %0, %0, %1"
+        : "+v"(s), "=&v"(p) : "v"(a), "v"(w), "v"(mz));
+  else
+    asm("v_fma_mix_f32 %1, %2, %3, %4 op_sel_hi:[0,1,0]\n\tv_add_f32 %0, %0, %1"
+        : "+v"(s), "=&v"(p) : "v"(a), "v"(w), "v"(mz));
+  return s;
+}
+
 template <bool BF16>
 __device__ __forceinline__ float w2f(uint16_t w) {
   if constexpr (BF16) return b2f(w); else return h2f(w);

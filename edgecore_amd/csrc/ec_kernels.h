@@ -171,11 +171,11 @@ __host__ __device__ inline bool attn_vec(int hd, int kv) {
 // one 16-lane group start on different banks; the element index is swizzled
 // by d ^ ((d >> 4) & attn_swz) within its group of 16.  (kv is unused: the
 // layout depends on head_dim only.)
-__host__ __device__ inline int attn_pitch(int hd, int kv) {
+__host__ __device__ constexpr inline int attn_pitch(int hd, int kv) {
   (void)kv;
   return (hd == 32 || hd == 64 || hd == 128) ? hd + (hd < 128 ? hd / 16 : 0) : hd;
 }
-__host__ __device__ inline int attn_swz(int hd, int kv) {
+__host__ __device__ constexpr inline int attn_swz(int hd, int kv) {
   (void)kv;
   return hd == 32 ? 1 : hd == 64 ? 3 : hd == 128 ? 7 : 0;
 }

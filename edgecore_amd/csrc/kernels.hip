@@ -200,6 +200,75 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(KvArgs a) {
 // to fp16 for the token's own position; the first query head of each KV group
 // appends them to the cache (src/gpt2.c:726-741).  Only valid when no other
 // token of the launch reads this token's slot.
+// Sequential sum of the decode attention's output element: o += the four
+// floats of each of 8*n8 quads (n8 >= 1), quad j at LDS byte address
+// a + j*STRIDE, in order.  The loads of the next four quads are in flight
+// while the current four are added, with one wait per two quads; the
+// compiler's own schedule of this loop waits for every outstanding load at
+// the top of each iteration.  Reads 4 quads past the end (values unused).
+template <int STRIDE>
+__device__ __forceinline__ float attn_chain8(float o, uint32_t a, int n8) {
+  asm volatile(
+      "ds_read_b128 v[224:227], %[a] offset:%[q0]\n"
+      "ds_read_b128 v[228:231], %[a] offset:%[q1]\n"
+      "ds_read_b128 v[232:235], %[a] offset:%[q2]\n"
+      "ds_read_b128 v[236:239], %[a] offset:%[q3]\n"
+      "L_attn_chain%=:\n"
+      "ds_read_b128 v[240:243], %[a] offset:%[q4]\n"
+      "ds_read_b128 v[244:247], %[a] offset:%[q5]\n"
+      "ds_read_b128 v[248:251], %[a] offset:%[q6]\n"
+      "ds_read_b128 v[252:255], %[a] offset:%[q7]\n"
+      "s_waitcnt lgkmcnt(6)\n"
+      "v_add_f32 %[o], %[o], v224\n"
+      "v_add_f32 %[o], %[o], v225\n"
+      "v_add_f32 %[o], %[o], v226\n"
+      "v_add_f32 %[o], %[o], v227\n"
+      "v_add_f32 %[o], %[o], v228\n"
+      "v_add_f32 %[o], %[o], v229\n"
+      "v_add_f32 %[o], %[o], v230\n"
+      "v_add_f32 %[o], %[o], v231\n"
+      "s_waitcnt lgkmcnt(4)\n"
+      "v_add_f32 %[o], %[o], v232\n"
+      "v_add_f32 %[o], %[o], v233\n"
+      "v_add_f32 %[o], %[o], v234\n"
+      "v_add_f32 %[o], %[o], v235\n"
+      "v_add_f32 %[o], %[o], v236\n"
+      "v_add_f32 %[o], %[o], v237\n"
+      "v_add_f32 %[o], %[o], v238\n"
+      "v_add_f32 %[o], %[o], v239\n"
+      "ds_read_b128 v[224:227], %[a] offset:%[q8]\n"
+      "ds_read_b128 v[228:231], %[a] offset:%[q9]\n"
+      "ds_read_b128 v[232:235], %[a] offset:%[q10]\n"
+      "ds_read_b128 v[236:239], %[a] offset:%[q11]\n"
+      "s_waitcnt lgkmcnt(6)\n"
+      "v_add_f32 %[o], %[o], v240\n"
+      "v_add_f32 %[o], %[o], v241\n"
+      "v_add_f32 %[o], %[o], v242\n"
+      "v_add_f32 %[o], %[o], v243\n"
+      "v_add_f32 %[o], %[o], v244\n"
+      "v_add_f32 %[o], %[o], v245\n"
+      "v_add_f32 %[o], %[o], v246\n"
+      "v_add_f32 %[o], %[o], v247\n"
+      "s_waitcnt lgkmcnt(4)\n"
+      "v_add_f32 %[o], %[o], v248\n"
+      "v_add_f32 %[o], %[o], v249\n"
+      "v_add_f32 %[o], %[o], v250\n"
+      "v_add_f32 %[o], %[o], v251\n"
+      "v_add_f32 %[o], %[o], v252\n"
+      "v_add_f32 %[o], %[o], v253\n"
+      "v_add_f32 %[o], %[o], v254\n"
+      "v_add_f32 %[o], %[o], v255\n"
+      "v_add_u32 %[a], %[inc], %[a]\n"
+      "s_sub_u32 %[n], %[n], 1\n"
+      "s_cmp_lg_u32 %[n], 0\n"
+      "s_cbranch_scc1 L_attn_chain%=\n"
+      "s_waitcnt lgkmcnt(0)\n"
+      : [o] "+v"(o), [a] "+v"(a), [n] "+s"(n8)
+      : [inc] "v"(8 * STRIDE), [q0] "i"(0 * STRIDE), [q1] "i"(1 * STRIDE), [q2] "i"(2 * STRIDE), [q3] "i"(3 * STRIDE), [q4] "i"(4 * STRIDE), [q5] "i"(5 * STRIDE), [q6] "i"(6 * STRIDE), [q7] "i"(7 * STRIDE), [q8] "i"(8 * STRIDE), [q9] "i"(9 * STRIDE), [q10] "i"(10 * STRIDE), [q11] "i"(11 * STRIDE)
+      : "v224", "v225", "v226", "v227", "v228", "v229", "v230", "v231", "v232", "v233", "v234", "v235", "v236", "v237", "v238", "v239", "v240", "v241", "v242", "v243", "v244", "v245", "v246", "v247", "v248", "v249", "v250", "v251", "v252", "v253", "v254", "v255", "scc", "memory");
+  return o;
+}
+
 template <int HD>
 __device__ __forceinline__ float dot_k_row(const float *qs, const uint16_t *kp, int hd) {
   float s = 0.0f;
@@ -212,10 +281,8 @@ __device__ __forceinline__ float dot_k_row(const float *qs, const uint16_t *kp, 
       const uint32_t wv[4] = {kk[c].x, kk[c].y, kk[c].z, kk[c].w};
 #pragma unroll
       for (int j = 0; j < 4; j++) {
-        const float p0 = qs[8 * c + 2 * j] * h2f((uint16_t)(wv[j] & 0xffffu));
-        s = s + p0;
-        const float p1 = qs[8 * c + 2 * j + 1] * h2f((uint16_t)(wv[j] >> 16));
-        s = s + p1;
+        s = mac_h<0>(s, qs[8 * c + 2 * j], wv[j]);
+        s = mac_h<1>(s, qs[8 * c + 2 * j + 1], wv[j]);
       }
     }
   } else {
@@ -297,13 +364,23 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     if (rot) c2 = a.cs[(size_t)pos * a.half + (rr ? i0 : 0)];
   }
 
-  // ---- 2. K rows of the first KQ positions, first V tile ----
+  // ---- 2. K rows of the first KQ positions ----
   // unit = 4 positions x 8 elements (16 bytes each); kAttnUnits per thread
   constexpr int KQMAX = HD > 0 ? 256 * kAttnUnits * 4 / CPR : 0;  // K positions staged
   constexpr int KP = CPR + 1;  // K tile row pitch in 16-byte chunks (odd: rows spread over the banks)
   // the K tile lives in the product area (T/4 * P slots of 16 bytes)
   const int KQ = min(KQMAX, (T / 4) * P / KP);
-  v4u kr[HD > 0 ? kAttnUnits : 1][4], vr[HD > 0 ? kAttnUnits : 1][4];
+  // V: the product threads (all but the first SWV waves, which hold the
+  // output elements) keep the tile's V in registers, one unit of 4 positions
+  // x 8 elements per stage of SQ quads; NSTG stages cover the largest tile
+  constexpr int SWV = HD > 64 ? HD / 64 : 1;
+  constexpr int NPT = 256 - 64 * SWV;
+  constexpr int SQ = HD > 0 ? NPT / CPR : 1;
+  constexpr int MAXQ = HD > 0 ? (256 * kAttnUnits * 4 / CPR < 512 ? 256 * kAttnUnits * 4 / CPR : 512) / 4 : 1;
+  constexpr int NSTG = HD > 0 ? (MAXQ + SQ - 1) / SQ : 1;
+  static_assert(HD == 0 || NPT % CPR == 0, "product threads cover whole quads");
+  const int pt = t - 64 * SWV;  // product thread index (negative in the summing waves)
+  v4u kr[HD > 0 ? kAttnUnits : 1][4], vr[NSTG][4];
   if constexpr (HD > 0) {
 #pragma unroll
     for (int u = 0; u < kAttnUnits; u++) {
@@ -315,18 +392,19 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
       }
     }
   }
-  auto load_v = [&](int t0) {  // V units (4 positions x 8 elements) of the tile at t0
+  auto load_v = [&](int t0) {  // this product thread's V units of the tile at t0
+    if (HD > 0 && pt >= 0) {
+      const int qd0 = pt / CPR, cd = pt - qd0 * CPR;
 #pragma unroll
-    for (int u = 0; u < kAttnUnits; u++) {
-      const int unit = t + 256 * u, qd = unit / CPR, cd = unit - qd * CPR;
+      for (int s = 0; s < NSTG; s++) {
 #pragma unroll
-      for (int e = 0; e < 4; e++) {
-        const int i = min(t0 + 4 * qd + e, last);
-        vr[u][e] = *reinterpret_cast<const v4u *>(V + (size_t)i * a.kv + 8 * cd);
+        for (int e = 0; e < 4; e++) {
+          const int i = min(t0 + 4 * (SQ * s + qd0) + e, last);
+          vr[s][e] = *reinterpret_cast<const v4u *>(V + (size_t)i * a.kv + 8 * cd);
+        }
       }
     }
   };
-  if constexpr (HD > 0) load_v(0);
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- 3. RoPE, fp16 rounding of the new k/v, cache append ----
@@ -372,6 +450,9 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
       }
     }
   }
+  // the product threads' V loads go out after the K rows are written, so no
+  // wait before this point counts them; scores and softmax cover their latency
+  load_v(0);
   __syncthreads();
 
   // ---- 4. scores ----
@@ -405,10 +486,8 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         const float q0 = qs[8 * c + 2 * j], q1 = qs[8 * c + 2 * j + 1];
 #pragma unroll
         for (int r = 0; r < R; r++) {
-          const float p0 = q0 * h2f((uint16_t)(wv[r][j] & 0xffffu));
-          s[r] = s[r] + p0;
-          const float p1 = q1 * h2f((uint16_t)(wv[r][j] >> 16));
-          s[r] = s[r] + p1;
+          s[r] = mac_h<0>(s[r], q0, wv[r][j]);
+          s[r] = mac_h<1>(s[r], q1, wv[r][j]);
         }
       }
     }
@@ -434,46 +513,90 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   const double isum = 1.0 / sum;
   for (int i = t; i < n; i += 256) sc[i] = (float)((double)sc[i] * isum);
 
-  // ---- 5. products p*v per tile, then the sequential sums ----
+  // ---- 5. products p*v, and the sequential sums ----
   // element d of quad q sits in 16-byte slot q*P + (d ^ ((d >> 4) & sw)); with
   // P and sw from attn_pitch/attn_swz every 16 consecutive lanes of the
   // product writes (units of 4 positions x 8 elements) and of the sums' reads
   // (consecutive d) touch 16 distinct bank slots
   const int sw = attn_swz(hd, a.kv);
+  const float4 *pp = reinterpret_cast<const float4 *>(prod) + (t ^ ((t >> 4) & sw));
   float o = 0.0f;
+  // sequential sum of the complete quads [qa, qe) of the tile into o
+  auto sum_quads = [&](int qa, int qe) {
+    const float4 *pq = pp + (size_t)qa * P;
+    int nr = qe - qa;
+    if constexpr (HD > 0) {
+      if (nr >= 8) {
+        o = attn_chain8<attn_pitch(HD, 0) * 16>(o, (uint32_t)(uintptr_t)pq, nr >> 3);
+        pq += (size_t)(nr & ~7) * P;
+        nr &= 7;
+      }
+    }
+    for (; nr > 0; nr--, pq += P) {
+      const float4 v = *pq;
+      o = o + v.x;
+      o = o + v.y;
+      o = o + v.z;
+      o = o + v.w;
+    }
+  };
+  // the partial quad nq of a tile (cnt & 3 positions)
+  auto sum_tail = [&](int nq, int cnt) {
+    const float *tail = reinterpret_cast<const float *>(pp + (size_t)nq * P);
+    for (int e = 0; e < (cnt & 3); e++) o = o + tail[e];
+  };
   for (int t0 = 0; t0 < n; t0 += T) {
     const int cnt = min(T, n - t0);
+    const int nq = cnt >> 2;  // complete quads
     __syncthreads();  // probabilities written / previous tile's sums done
     if constexpr (HD > 0) {
+      // Stage s: the product threads form the products of their unit s
+      // (quads [SQ*s, SQ*(s+1))) while the summing lanes add the quads of
+      // stage s - 1; a barrier separates the stages.
       if (t0) load_v(t0);
+      const int nst = ((cnt + 3) / 4 + SQ - 1) / SQ;  // stages holding positions
 #pragma unroll
-      for (int u = 0; u < kAttnUnits; u++) {
-        const int unit = t + 256 * u, qd = unit / CPR, cd = unit - qd * CPR;
-        if (4 * qd < cnt) {
-          const float4 pq = *reinterpret_cast<const float4 *>(sc + t0 + 4 * qd);
-          const float pe[4] = {pq.x, pq.y, pq.z, pq.w};
-          float pr[8][4];
+      for (int s = 0; s <= NSTG; s++) {
+        if (s > nst) continue;  // uniform
+        if (pt >= 0) {
+          const int qd = SQ * s + pt / CPR, cd = pt % CPR;
+          if (s < nst && 4 * qd < cnt) {
+            if (FUSED) {
+              // the token's own position takes the fp16-rounded new v (one lane)
+              const int en = n - 1 - t0 - 4 * qd;
+              if (en >= 0 && en < 4) {
+                uint32_t w[4];
 #pragma unroll
-          for (int e = 0; e < 4; e++) {
-            const uint32_t hv[4] = {vr[u][e].x, vr[u][e].y, vr[u][e].z, vr[u][e].w};
-            float vf[8];
+                for (int j = 0; j < 4; j++)
+                  w[j] = (uint32_t)f2h(vn[8 * cd + 2 * j]) | ((uint32_t)f2h(vn[8 * cd + 2 * j + 1]) << 16);
+                const v4u nv = {w[0], w[1], w[2], w[3]};
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-              vf[2 * j] = h2f((uint16_t)(hv[j] & 0xffffu));
-              vf[2 * j + 1] = h2f((uint16_t)(hv[j] >> 16));
+                for (int e = 0; e < 4; e++)
+                  if (e == en) vr[s][e] = nv;
+              }
             }
-            if (FUSED && t0 + 4 * qd + e == n - 1) {
+            const float4 pq = *reinterpret_cast<const float4 *>(sc + t0 + 4 * qd);
+            const float pe[4] = {pq.x, pq.y, pq.z, pq.w};
+            float pr[8][4];
 #pragma unroll
-              for (int k = 0; k < 8; k++) vf[k] = vn[8 * cd + k];
+            for (int e = 0; e < 4; e++) {
+              const uint32_t hv[4] = {vr[s][e].x, vr[s][e].y, vr[s][e].z, vr[s][e].w};
+#pragma unroll
+              for (int j = 0; j < 4; j++) {
+                pr[2 * j][e] = mul_h<0>(pe[e], hv[j]);
+                pr[2 * j + 1][e] = mul_h<1>(pe[e], hv[j]);
+              }
             }
 #pragma unroll
-            for (int k = 0; k < 8; k++) pr[k][e] = pe[e] * vf[k];
+            for (int k = 0; k < 8; k++)
+              *reinterpret_cast<float4 *>(prod + ((size_t)qd * P + ((8 * cd + k) ^ (((8 * cd + k) >> 4) & sw))) * 4) =
+                  make_float4(pr[k][0], pr[k][1], pr[k][2], pr[k][3]);
           }
-#pragma unroll
-          for (int k = 0; k < 8; k++)
-            *reinterpret_cast<float4 *>(prod + ((size_t)qd * P + ((8 * cd + k) ^ (((8 * cd + k) >> 4) & sw))) * 4) =
-                make_float4(pr[k][0], pr[k][1], pr[k][2], pr[k][3]);
+        } else if (t < hd && s > 0) {
+          sum_quads(SQ * (s - 1), min(SQ * s, nq));
+          if (s == nst) sum_tail(nq, cnt);
         }
+        if (s < nst) __syncthreads();
       }
     } else {
       for (int e = t; e < cnt * hd; e += 256) {
@@ -481,60 +604,11 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         const float v = (FUSED && t0 + i == n - 1) ? vn[d] : h2f(V[(size_t)(t0 + i) * a.kv + d]);
         prod[((size_t)(i >> 2) * P + (d ^ ((d >> 4) & sw))) * 4 + (i & 3)] = sc[t0 + i] * v;
       }
-    }
-    __syncthreads();
-    if (t < hd) {
-      // sequential sum over the tile, 8 quads at a time: the loads of the
-      // next 8 quads (two register sets) are in flight while the current 8
-      // are added.  Look-ahead loads reach at most 8 quads past the tile,
-      // into the slack that attention_lds_bytes reserves.
-      const float4 *pp = reinterpret_cast<const float4 *>(prod) + (t ^ ((t >> 4) & sw));
-      const int nq = cnt >> 2, nq8 = nq & ~7;
-      float4 A[8], B[8];
-      auto add8 = [&](const float4 *X) {
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-          o = o + X[j].x;
-          o = o + X[j].y;
-          o = o + X[j].z;
-          o = o + X[j].w;
-        }
-      };
-      int q = 0;
-      if (nq8 > 0) {
-        const float4 *pq = pp;
-#pragma unroll
-        for (int j = 0; j < 8; j++) A[j] = pq[j * P];
-        for (;; q += 16, pq += 16 * P) {
-#pragma unroll
-          for (int j = 0; j < 8; j++) B[j] = pq[(8 + j) * P];
-          __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the adds
-          add8(A);
-          __builtin_amdgcn_sched_barrier(0);
-          if (q + 8 >= nq8) {
-            q += 8;
-            break;
-          }
-#pragma unroll
-          for (int j = 0; j < 8; j++) A[j] = pq[(16 + j) * P];
-          __builtin_amdgcn_sched_barrier(0);
-          add8(B);
-          __builtin_amdgcn_sched_barrier(0);
-          if (q + 16 >= nq8) {
-            q += 16;
-            break;
-          }
-        }
+      __syncthreads();
+      if (t < hd) {
+        sum_quads(0, nq);
+        sum_tail(nq, cnt);
       }
-      for (; q < nq; q++) {
-        const float4 v = pp[(size_t)q * P];
-        o = o + v.x;
-        o = o + v.y;
-        o = o + v.z;
-        o = o + v.w;
-      }
-      const float *tail = reinterpret_cast<const float *>(pp + (size_t)nq * P);
-      for (int e = 0; e < (cnt & 3); e++) o = o + tail[e];
     }
   }
   if (t < hd) a.out[(size_t)m * a.ldo + (size_t)h * hd + t] = o;

@@ -88,6 +88,12 @@ int gemv_max_blocks();
 // row shape (GS_* of gemv_impl.h) and M tile of the fused kernel for a launch
 int gemv_pick_shape(int wt, int K);
 int gemv_pick_mt(int M);
+// prologue computed by every wave alone (one activation row of at most 1024
+// fp32 elements, quantized or normalized): no block barrier, one LDS copy of
+// the row per wave
+inline bool gemv_wave_pro(int pro, int MT, int K) {
+  return MT == 1 && K <= 1024 && (pro == PRO_QUANT || pro == PRO_RMS || pro == PRO_LN);
+}
 // LDS budget per block (device limit), checked by gemv_vector_ok
 void gemv_set_max_lds(int bytes);
 size_t gemv_lds_bytes(int wt, int pro, int MT, int K);

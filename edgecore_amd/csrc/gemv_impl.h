@@ -90,7 +90,7 @@ __device__ __forceinline__ T group_sum(T v) {
   return v;
 }
 
-template <int WT, int SHAPE, int MT, int EPI, int PRO>
+template <int WT, int SHAPE, int MT, int EPI, int PRO, bool WL>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   constexpr bool Q8 = WT == WT_I8;
   constexpr int LPR = GemvShape<WT, SHAPE>::LPR, CPL = GemvShape<WT, SHAPE>::CPL;
@@ -102,12 +102,13 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   constexpr bool LDS_ACT = PRO != PRO_F32;
   constexpr bool NORM = PRO == PRO_RMS || PRO == PRO_LN;
   constexpr int NS = ProStrips<PRO>::NS;
+  static_assert(!WL || (MT == 1 && (PRO == PRO_QUANT || NORM)), "wave-local prologue: one row, fp32 input");
 
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
   __shared__ double redd[2][4];
   __shared__ float redf[4];
   __shared__ unsigned long long keyred[4][MT];
-  __shared__ uint64_t etab[SWI ? 32 : 1];  // expf table of the SiLU
+  __shared__ uint64_t etab[SWI ? 4 * 32 : 1];  // expf table of the SiLU, one copy per wave
 
   // every kernel argument into registers here: one wait on the argument
   // loads instead of one per first use
@@ -153,7 +154,25 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
       }
     }
   };
-  if constexpr (NS > 0) load_act(0);
+  // WL: every wave holds the whole row (K <= 1024), lane l elements
+  // 4l + 256j, and computes the prologue alone: no block barrier, and each
+  // wave writes its own copy of the quantized / normalized row to LDS
+  float4 xw[WL ? 4 : 1], gw[WL && NORM ? 4 : 1], bw[WL && PRO == PRO_LN ? 4 : 1];
+  if constexpr (WL) {
+    const float *row = reinterpret_cast<const float *>(a.A) + (size_t)m0 * a.lda;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int i = min(4 * lane + 256 * j, K - 4);
+      xw[j] = *reinterpret_cast<const float4 *>(row + i);
+      if constexpr (NORM) gw[j] = *reinterpret_cast<const float4 *>(a.gamma + i);
+      if constexpr (PRO == PRO_LN) bw[j] = *reinterpret_cast<const float4 *>(a.beta + i);
+    }
+    // the SiLU table and the row ahead of the weights: the stores of the
+    // table would otherwise wait for the whole weight stream
+    __builtin_amdgcn_sched_barrier(0);
+  } else if constexpr (NS > 0) {
+    load_act(0);
+  }
 
   // ---- 2. first row group: weights, scales, bias, residual ----
   // All unconditional: absent scales / bias read a valid dummy address and
@@ -195,15 +214,108 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   int rg = blockIdx.x;
   load_w(rg, 0);
   load_meta(rg);
+  if constexpr (WL) __builtin_amdgcn_sched_barrier(0);  // every weight load out before the first wait
 
   // ---- 3. prologue: activation rows of this M tile into LDS ----
-  if constexpr (SWI) {
-    if (t < 32) etab[t] = et;
-  }
+  // unconditional (lanes 32..63 repeat lanes 0..31): a conditional store
+  // lets the compiler sink the table load behind the weight loads
+  if constexpr (SWI) etab[32 * wave + (lane & 31)] = et;
   int8_t *xq = reinterpret_cast<int8_t *>(lds);
   float *xf = reinterpret_cast<float *>(lds);
-  float *xs = reinterpret_cast<float *>(lds + (size_t)MT * Kp);  // int8 path only
-  if constexpr (PRO == PRO_I8) {
+  float *xs = reinterpret_cast<float *>(lds + (size_t)(WL ? 4 : MT) * Kp);  // int8 path only
+  float xsw = 1.0f;  // WL: the row's scale (int8 path)
+  if constexpr (WL) {
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      if (4 * lane + 256 * j >= K) xw[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    if constexpr (NORM) {
+      double s1 = 0.0;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const double d0 = xw[j].x, d1 = xw[j].y, d2 = xw[j].z, d3 = xw[j].w;
+        if constexpr (PRO == PRO_LN) s1 += ((d0 + d1) + d2) + d3;
+        else s1 += ((d0 * d0 + d1 * d1) + d2 * d2) + d3 * d3;
+      }
+      s1 = wave_sum_dpp(s1);
+      double mean = 0.0, rstd;
+      if constexpr (PRO == PRO_LN) {
+        mean = s1 / K;
+        double s2 = 0.0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          if (4 * lane + 256 * j < K) {
+            const double d0 = xw[j].x - mean, d1 = xw[j].y - mean, d2 = xw[j].z - mean, d3 = xw[j].w - mean;
+            s2 += ((d0 * d0 + d1 * d1) + d2 * d2) + d3 * d3;
+          }
+        }
+        rstd = 1.0 / sqrt(wave_sum_dpp(s2) / K + a.eps);
+      } else {
+        rstd = 1.0 / sqrt(s1 / K + a.eps);
+      }
+      auto nrm = [&](float x, float g, float b) -> float {
+        if constexpr (PRO == PRO_RMS) {
+          x = (float)((double)x * rstd);
+          return x * g;
+        } else {
+          x = (float)(((double)x - mean) * rstd);
+          x = x * g;
+          return x + b;
+        }
+      };
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const float4 b = PRO == PRO_LN ? bw[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+        xw[j].x = nrm(xw[j].x, gw[j].x, b.x);
+        xw[j].y = nrm(xw[j].y, gw[j].y, b.y);
+        xw[j].z = nrm(xw[j].z, gw[j].z, b.z);
+        xw[j].w = nrm(xw[j].w, gw[j].w, b.w);
+        if (4 * lane + 256 * j >= K) xw[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
+    if constexpr (Q8) {
+      float mx = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        mx = fmaxf(mx, fabsf(xw[j].x));
+        mx = fmaxf(mx, fabsf(xw[j].y));
+        mx = fmaxf(mx, fabsf(xw[j].z));
+        mx = fmaxf(mx, fabsf(xw[j].w));
+      }
+      mx = wave_max_dpp(mx);
+      const float sc = quant_scale(mx);
+      int8_t *q = xq + (size_t)wave * Kp;
+      const bool fast = ec_quant_rcp_ok(sc);
+      const float rcp = 1.0f / sc;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int i = 4 * lane + 256 * j;
+        if (i < K) {
+          uint32_t b0, b1, b2, b3;
+          if (fast) {
+            b0 = (uint8_t)ec_quant1_rcp(xw[j].x, sc, rcp);
+            b1 = (uint8_t)ec_quant1_rcp(xw[j].y, sc, rcp);
+            b2 = (uint8_t)ec_quant1_rcp(xw[j].z, sc, rcp);
+            b3 = (uint8_t)ec_quant1_rcp(xw[j].w, sc, rcp);
+          } else {
+            b0 = (uint8_t)quant1(xw[j].x, sc);
+            b1 = (uint8_t)quant1(xw[j].y, sc);
+            b2 = (uint8_t)quant1(xw[j].z, sc);
+            b3 = (uint8_t)quant1(xw[j].w, sc);
+          }
+          *reinterpret_cast<uint32_t *>(q + i) = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+        }
+      }
+      xsw = sc;
+    } else {
+      float *f = xf + (size_t)wave * Kp;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int i = 4 * lane + 256 * j;
+        if (i < K) *reinterpret_cast<float4 *>(f + i) = xw[j];
+      }
+    }
+  } else if constexpr (PRO == PRO_I8) {
     for (int m = 0; m < mc; m++) {
       const int8_t *src = reinterpret_cast<const int8_t *>(a.A) + (size_t)(m0 + m) * a.lda;
       for (int i = t * 16; i < K; i += 256 * 16)
@@ -317,7 +429,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
       if (m + 1 < mc) __syncthreads();
     }
   }
-  __syncthreads();
+  if constexpr (!WL) __syncthreads();
 
   unsigned long long best[MT];
 #pragma unroll
@@ -343,7 +455,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
 #pragma unroll
           for (int m = 0; m < MT; m++) {
             if (m < mc) {
-              const v4i x = *reinterpret_cast<const v4i *>(xq + (size_t)m * Kp + (size_t)ch * 16);
+              const v4i x = *reinterpret_cast<const v4i *>(xq + (size_t)(WL ? wave : m) * Kp + (size_t)ch * 16);
               int s = acc[m];
               s = __builtin_amdgcn_sdot4(x.x, w[c].x, s, false);
               s = __builtin_amdgcn_sdot4(x.y, w[c].y, s, false);
@@ -382,7 +494,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
           for (int m = 0; m < MT; m++) {
             if (m < mc) {
               const float4 *xp =
-                  LDS_ACT ? reinterpret_cast<const float4 *>(xf + (size_t)m * Kp + (size_t)ch * 8)
+                  LDS_ACT ? reinterpret_cast<const float4 *>(xf + (size_t)(WL ? wave : m) * Kp + (size_t)ch * 8)
                           : reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(a.A) +
                                                              (size_t)(m0 + m) * a.lda + (size_t)ch * 8);
               const float4 x0 = xp[0], x1 = xp[1];
@@ -438,14 +550,14 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
         if (m < mc) {
           float v;
           if constexpr (Q8) {
-            v = i8_epilogue((int)acc[m], xs[m], cbs, SWI ? 0.0f : cbia);
+            v = i8_epilogue((int)acc[m], WL ? xsw : xs[m], cbs, SWI ? 0.0f : cbia);
           } else {
             v = (float)acc[m];
           }
           float *o = a.out + (size_t)(m0 + m) * a.ldo + n;
           if constexpr (SWI) {
-            const float u = Q8 ? i8_epilogue((int)acc2[m], xs[m], cbs2, 0.0f) : (float)acc2[m];
-            v = silu(v, etab) * u;
+            const float u = Q8 ? i8_epilogue((int)acc2[m], WL ? xsw : xs[m], cbs2, 0.0f) : (float)acc2[m];
+            v = silu(v, etab + 32 * wave) * u;
           } else {
             if constexpr (!Q8 && (EPI == EPI_BIAS || EPI == EPI_BIAS_RESID || EPI == EPI_BIAS_GELU)) v = v + cbia;
             if constexpr (RES) v = cres[m] + v;
@@ -484,7 +596,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
 // host-side launch helpers (instantiated per weight type in gemv_*.hip)
 // ---------------------------------------------------------------------------
 
-template <int WT, int SHAPE, int MT, int EPI, int PRO>
+template <int WT, int SHAPE, int MT, int EPI, int PRO, bool WL = false>
 hipError_t gemv_launch(const GemvArgs &a, hipStream_t s) {
   constexpr int RPB = 4 * (kWave / GemvShape<WT, SHAPE>::LPR);
   const int ngroups = (a.N + RPB - 1) / RPB;
@@ -492,7 +604,7 @@ hipError_t gemv_launch(const GemvArgs &a, hipStream_t s) {
   const int gx = ngroups < cap ? ngroups : cap;
   dim3 grid(gx, (a.M + MT - 1) / MT);
   const size_t lds = gemv_lds_bytes(WT, PRO, MT, a.K);
-  klaunch((gemv_kernel<WT, SHAPE, MT, EPI, PRO>), grid, dim3(256), lds, s, a);
+  klaunch((gemv_kernel<WT, SHAPE, MT, EPI, PRO, WL>), grid, dim3(256), lds, s, a);
   return hipGetLastError();
 }
 
@@ -502,7 +614,10 @@ hipError_t gemv_launch_shape(const GemvArgs &a, hipStream_t s) {
   const int mt = gemv_pick_mt(a.M);
 #define EC_MT(SH)                                                   \
   switch (mt) {                                                     \
-  case 1: return gemv_launch<WT, SH, 1, EPI, PRO>(a, s);            \
+  case 1:                                                           \
+    if constexpr (PRO == PRO_QUANT || PRO == PRO_RMS || PRO == PRO_LN) \
+      if (gemv_wave_pro(PRO, 1, a.K)) return gemv_launch<WT, SH, 1, EPI, PRO, true>(a, s); \
+    return gemv_launch<WT, SH, 1, EPI, PRO>(a, s);                  \
   case 2: return gemv_launch<WT, SH, 2, EPI, PRO>(a, s);            \
   case 4: return gemv_launch<WT, SH, 4, EPI, PRO>(a, s);            \
   default: return gemv_launch<WT, SH, 8, EPI, PRO>(a, s);           \

@@ -743,12 +743,13 @@ int gemv_grid_x(const GemvArgs &a, int wt, int epi) {
 
 size_t gemv_lds_bytes(int wt, int pro, int MT, int K) {
   if (pro == PRO_F32) return 0;
+  const int rows = gemv_wave_pro(pro, MT, K) ? 4 : MT;  // one row per wave, or the M tile
   if (wt == WT_I8) {
     const size_t kp = (size_t)(K + 15) / 16 * 16;
-    return (MT * kp + 4 * MT + 15) / 16 * 16;
+    return (rows * kp + 4 * MT + 15) / 16 * 16;
   }
   const size_t kp = (size_t)(K + 7) / 8 * 8;
-  return MT * kp * 4;
+  return rows * kp * 4;
 }
 
 static int g_max_lds_bytes = 65536;

@@ -304,6 +304,11 @@ __device__ __forceinline__ float dot_new_k(const float *qs, const float *kn, int
   return s;
 }
 
+// stages of the decode attention's products for the largest tile (timed at
+// 2, 3 and 6 stages for head_dim 64 at 504 positions: 8.0k, 7.6k and 8.4k
+// cycles)
+constexpr int kAttnStages = 3;
+
 template <int HD, bool FUSED>
 __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   extern __shared__ __attribute__((aligned(16))) float lds[];
@@ -371,16 +376,19 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   // the K tile lives in the product area (T/4 * P slots of 16 bytes)
   const int KQ = min(KQMAX, (T / 4) * P / KP);
   // V: the product threads (all but the first SWV waves, which hold the
-  // output elements) keep the tile's V in registers, one unit of 4 positions
-  // x 8 elements per stage of SQ quads; NSTG stages cover the largest tile
+  // output elements) keep the tile's V in registers in units of 4 positions x
+  // 8 elements: QPU quads per unit index across the product threads, UPS units
+  // per thread and stage of SQ quads, NSTG stages for the largest tile
   constexpr int SWV = HD > 64 ? HD / 64 : 1;
   constexpr int NPT = 256 - 64 * SWV;
-  constexpr int SQ = HD > 0 ? NPT / CPR : 1;
+  constexpr int QPU = HD > 0 ? NPT / CPR : 1;
   constexpr int MAXQ = HD > 0 ? (256 * kAttnUnits * 4 / CPR < 512 ? 256 * kAttnUnits * 4 / CPR : 512) / 4 : 1;
-  constexpr int NSTG = HD > 0 ? (MAXQ + SQ - 1) / SQ : 1;
+  constexpr int UPS = (MAXQ + kAttnStages * QPU - 1) / (kAttnStages * QPU);
+  constexpr int SQ = UPS * QPU;
+  constexpr int NSTG = (MAXQ + SQ - 1) / SQ;
   static_assert(HD == 0 || NPT % CPR == 0, "product threads cover whole quads");
   const int pt = t - 64 * SWV;  // product thread index (negative in the summing waves)
-  v4u kr[HD > 0 ? kAttnUnits : 1][4], vr[NSTG][4];
+  v4u kr[HD > 0 ? kAttnUnits : 1][4], vr[NSTG * UPS][4];
   if constexpr (HD > 0) {
 #pragma unroll
     for (int u = 0; u < kAttnUnits; u++) {
@@ -398,9 +406,12 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
 #pragma unroll
       for (int s = 0; s < NSTG; s++) {
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-          const int i = min(t0 + 4 * (SQ * s + qd0) + e, last);
-          vr[s][e] = *reinterpret_cast<const v4u *>(V + (size_t)i * a.kv + 8 * cd);
+        for (int u = 0; u < UPS; u++) {
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            const int i = min(t0 + 4 * (SQ * s + QPU * u + qd0) + e, last);
+            vr[s * UPS + u][e] = *reinterpret_cast<const v4u *>(V + (size_t)i * a.kv + 8 * cd);
+          }
         }
       }
     }
@@ -550,47 +561,51 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     const int nq = cnt >> 2;  // complete quads
     __syncthreads();  // probabilities written / previous tile's sums done
     if constexpr (HD > 0) {
-      // Stage s: the product threads form the products of their unit s
-      // (quads [SQ*s, SQ*(s+1))) while the summing lanes add the quads of
-      // stage s - 1; a barrier separates the stages.
+      // Stage s: the product threads form the products of their UPS units of
+      // stage s (quads [SQ*s, SQ*(s+1))) while the summing lanes add the
+      // quads of stage s - 1; a barrier separates the stages.
       if (t0) load_v(t0);
       const int nst = ((cnt + 3) / 4 + SQ - 1) / SQ;  // stages holding positions
 #pragma unroll
       for (int s = 0; s <= NSTG; s++) {
         if (s > nst) continue;  // uniform
         if (pt >= 0) {
-          const int qd = SQ * s + pt / CPR, cd = pt % CPR;
-          if (s < nst && 4 * qd < cnt) {
-            if (FUSED) {
-              // the token's own position takes the fp16-rounded new v (one lane)
-              const int en = n - 1 - t0 - 4 * qd;
-              if (en >= 0 && en < 4) {
-                uint32_t w[4];
 #pragma unroll
-                for (int j = 0; j < 4; j++)
-                  w[j] = (uint32_t)f2h(vn[8 * cd + 2 * j]) | ((uint32_t)f2h(vn[8 * cd + 2 * j + 1]) << 16);
-                const v4u nv = {w[0], w[1], w[2], w[3]};
+          for (int u = 0; u < UPS; u++) {
+            const int qd = SQ * s + QPU * u + pt / CPR, cd = pt % CPR;
+            v4u *vu = vr[min(s, NSTG - 1) * UPS + u];
+            if (s < nst && 4 * qd < cnt) {
+              if (FUSED) {
+                // the token's own position takes the fp16-rounded new v (one lane)
+                const int en = n - 1 - t0 - 4 * qd;
+                if (en >= 0 && en < 4) {
+                  uint32_t w[4];
 #pragma unroll
-                for (int e = 0; e < 4; e++)
-                  if (e == en) vr[s][e] = nv;
+                  for (int j = 0; j < 4; j++)
+                    w[j] = (uint32_t)f2h(vn[8 * cd + 2 * j]) | ((uint32_t)f2h(vn[8 * cd + 2 * j + 1]) << 16);
+                  const v4u nv = {w[0], w[1], w[2], w[3]};
+#pragma unroll
+                  for (int e = 0; e < 4; e++)
+                    if (e == en) vu[e] = nv;
+                }
               }
-            }
-            const float4 pq = *reinterpret_cast<const float4 *>(sc + t0 + 4 * qd);
-            const float pe[4] = {pq.x, pq.y, pq.z, pq.w};
-            float pr[8][4];
+              const float4 pq = *reinterpret_cast<const float4 *>(sc + t0 + 4 * qd);
+              const float pe[4] = {pq.x, pq.y, pq.z, pq.w};
+              float pr[8][4];
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-              const uint32_t hv[4] = {vr[s][e].x, vr[s][e].y, vr[s][e].z, vr[s][e].w};
+              for (int e = 0; e < 4; e++) {
+                const uint32_t hv[4] = {vu[e].x, vu[e].y, vu[e].z, vu[e].w};
 #pragma unroll
-              for (int j = 0; j < 4; j++) {
-                pr[2 * j][e] = mul_h<0>(pe[e], hv[j]);
-                pr[2 * j + 1][e] = mul_h<1>(pe[e], hv[j]);
+                for (int j = 0; j < 4; j++) {
+                  pr[2 * j][e] = mul_h<0>(pe[e], hv[j]);
+                  pr[2 * j + 1][e] = mul_h<1>(pe[e], hv[j]);
+                }
               }
-            }
 #pragma unroll
-            for (int k = 0; k < 8; k++)
-              *reinterpret_cast<float4 *>(prod + ((size_t)qd * P + ((8 * cd + k) ^ (((8 * cd + k) >> 4) & sw))) * 4) =
-                  make_float4(pr[k][0], pr[k][1], pr[k][2], pr[k][3]);
+              for (int k = 0; k < 8; k++)
+                *reinterpret_cast<float4 *>(prod + ((size_t)qd * P + ((8 * cd + k) ^ (((8 * cd + k) >> 4) & sw))) * 4) =
+                    make_float4(pr[k][0], pr[k][1], pr[k][2], pr[k][3]);
+            }
           }
         } else if (t < hd && s > 0) {
           sum_quads(SQ * (s - 1), min(SQ * s, nq));

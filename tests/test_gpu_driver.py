@@ -80,7 +80,9 @@ def test_bench_keys_batch2(make_model):
                        "--warmup", 1, "--iters", 3, "--batch", 2, "--threads", 2,
                        "--affinity", "physical").stdout)
     assert d["n_generated_tokens"] == 32
-    assert 0 < d["avg_token_ms"] <= d["p95_ms"]
+    # the mean may exceed the 95th percentile when one step is slow; the
+    # percentiles themselves are ordered
+    assert d["avg_token_ms"] > 0 and 0 < d["p50_ms"] <= d["p95_ms"] <= d["p99_ms"]
     assert d["tokens_per_sec"] > 0 and d["tokens_per_sec_aggregate"] > 0
     assert d["affinity_applied"] is True and len(d["affinity_cpus"]) >= 1
     assert "ttft_p95_ms" in d and "ttft_p99_ms" in d

@@ -65,6 +65,97 @@ __device__ __forceinline__ float mac_h(float s, float a, uint32_t w) {
   return s;
 }
 
+// Two sequential dots at once: s0 += a[j] * fp32(k0[j]) and s1 += a[j] *
+// fp32(k1[j]) for the eight binary16 elements j of the 16-byte chunks k0, k1
+// (element j in the low (even j) or high half of dword j/2), in element
+// order, each product rounded before its add (mul_h's product, then the add).
+// One asm statement: the compiler pads every boundary between asm statements
+// with a wait state, which per element would cost another instruction slot.
+__device__ __forceinline__ void mac8x2(float &s0, float &s1, const float *a, v4u k0, v4u k1) {
+  const float mz = __builtin_bit_cast(float, 0x80000000u);
+  float t0, t1;
+  asm(
+      "v_fma_mix_f32 %[t0], %[a0], %[k00], %[mz] op_sel_hi:[0,1,0]\n"
+      "v_fma_mix_f32 %[t1], %[a0], %[k10], %[mz] op_sel_hi:[0,1,0]\n"
+      "v_add_f32 %[s0], %[s0], %[t0]\n"
+      "v_add_f32 %[s1], %[s1], %[t1]\n"
+      "v_fma_mix_f32 %[t0], %[a1], %[k00], %[mz] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+      "v_fma_mix_f32 %[t1], %[a1], %[k10], %[mz] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+      "v_add_f32 %[s0], %[s0], %[t0]\n"
+      "v_add_f32 %[s1], %[s1], %[t1]\n"
+      "v_fma_mix_f32 %[t0], %[a2], %[k01], %[mz] op_sel_hi:[0,1,0]\n"
+      "v_fma_mix_f32 %[t1], %[a2], %[k11], %[mz] op_sel_hi:[0,1,0]\n"
+      "v_add_f32 %[s0], %[s0], %[t0]\n"
+      "v_add_f32 %[s1], %[s1], %[t1]\n"
+      "v_fma_mix_f32 %[t0], %[a3], %[k01], %[mz] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+      "v_fma_mix_f32 %[t1], %[a3], %[k11], %[mz] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+      "v_add_f32 %[s0], %[s0], %[t0]\n"
+      "v_add_f32 %[s1], %[s1], %[t1]\n"
+      "v_fma_mix_f32 %[t0], %[a4], %[k02], %[mz] op_sel_hi:[0,1,0]\n"
+      "v_fma_mix_f32 %[t1], %[a4], %[k12], %[mz] op_sel_hi:[0,1,0]\n"
+      "v_add_f32 %[s0], %[s0], %[t0]\n"
+      "v_add_f32 %[s1], %[s1], %[t1]\n"
+      "v_fma_mix_f32 %[t0], %[a5], %[k02], %[mz] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+      "v_fma_mix_f32 %[t1], %[a5], %[k12], %[mz] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+      "v_add_f32 %[s0], %[s0], %[t0]\n"
+      "v_add_f32 %[s1], %[s1], %[t1]\n"
+      "v_fma_mix_f32 %[t0], %[a6], %[k03], %[mz] op_sel_hi:[0,1,0]\n"
+      "v_fma_mix_f32 %[t1], %[a6], %[k13], %[mz] op_sel_hi:[0,1,0]\n"
+      "v_add_f32 %[s0], %[s0], %[t0]\n"
+      "v_add_f32 %[s1], %[s1], %[t1]\n"
+      "v_fma_mix_f32 %[t0], %[a7], %[k03], %[mz] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+      "v_fma_mix_f32 %[t1], %[a7], %[k13], %[mz] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+      "v_add_f32 %[s0], %[s0], %[t0]\n"
+      "v_add_f32 %[s1], %[s1], %[t1]\n"
+      : [s0] "+v"(s0), [s1] "+v"(s1), [t0] "=&v"(t0), [t1] "=&v"(t1)
+      : [a0] "v"(a[0]), [a1] "v"(a[1]), [a2] "v"(a[2]), [a3] "v"(a[3]), [a4] "v"(a[4]), [a5] "v"(a[5]),
+        [a6] "v"(a[6]), [a7] "v"(a[7]), [k00] "v"(k0.x), [k01] "v"(k0.y), [k02] "v"(k0.z), [k03] "v"(k0.w),
+        [k10] "v"(k1.x), [k11] "v"(k1.y), [k12] "v"(k1.z), [k13] "v"(k1.w), [mz] "v"(mz));
+}
+// one dot of mac8x2
+__device__ __forceinline__ void mac8(float &s0, const float *a, v4u k0) {
+  const float mz = __builtin_bit_cast(float, 0x80000000u);
+  float t0;
+  asm(
+      "v_fma_mix_f32 %[t0], %[a0], %[k00], %[mz] op_sel_hi:[0,1,0]\n"
+      "v_add_f32 %[s0], %[s0], %[t0]\n"
+      "v_fma_mix_f32 %[t0], %[a1], %[k00], %[mz] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+      "v_add_f32 %[s0], %[s0], %[t0]\n"
+      "v_fma_mix_f32 %[t0], %[a2], %[k01], %[mz] op_sel_hi:[0,1,0]\n"
+      "v_add_f32 %[s0], %[s0], %[t0]\n"
+      "v_fma_mix_f32 %[t0], %[a3], %[k01], %[mz] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+      "v_add_f32 %[s0], %[s0], %[t0]\n"
+      "v_fma_mix_f32 %[t0], %[a4], %[k02], %[mz] op_sel_hi:[0,1,0]\n"
+      "v_add_f32 %[s0], %[s0], %[t0]\n"
+      "v_fma_mix_f32 %[t0], %[a5], %[k02], %[mz] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+      "v_add_f32 %[s0], %[s0], %[t0]\n"
+      "v_fma_mix_f32 %[t0], %[a6], %[k03], %[mz] op_sel_hi:[0,1,0]\n"
+      "v_add_f32 %[s0], %[s0], %[t0]\n"
+      "v_fma_mix_f32 %[t0], %[a7], %[k03], %[mz] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+      "v_add_f32 %[s0], %[s0], %[t0]\n"
+      : [s0] "+v"(s0), [t0] "=&v"(t0)
+      : [a0] "v"(a[0]), [a1] "v"(a[1]), [a2] "v"(a[2]), [a3] "v"(a[3]), [a4] "v"(a[4]), [a5] "v"(a[5]),
+        [a6] "v"(a[6]), [a7] "v"(a[7]), [k00] "v"(k0.x), [k01] "v"(k0.y), [k02] "v"(k0.z), [k03] "v"(k0.w),
+        [mz] "v"(mz));
+}
+// r[j] = a * fp32(h[j]) for the eight binary16 elements of the 16-byte chunk
+// h (mul_h eight times, one asm statement)
+__device__ __forceinline__ void mul8h(float *r, float a, v4u h) {
+  const float mz = __builtin_bit_cast(float, 0x80000000u);
+  asm(
+      "v_fma_mix_f32 %[r0], %[a], %[h0], %[mz] op_sel_hi:[0,1,0]\n"
+      "v_fma_mix_f32 %[r1], %[a], %[h0], %[mz] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+      "v_fma_mix_f32 %[r2], %[a], %[h1], %[mz] op_sel_hi:[0,1,0]\n"
+      "v_fma_mix_f32 %[r3], %[a], %[h1], %[mz] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+      "v_fma_mix_f32 %[r4], %[a], %[h2], %[mz] op_sel_hi:[0,1,0]\n"
+      "v_fma_mix_f32 %[r5], %[a], %[h2], %[mz] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+      "v_fma_mix_f32 %[r6], %[a], %[h3], %[mz] op_sel_hi:[0,1,0]\n"
+      "v_fma_mix_f32 %[r7], %[a], %[h3], %[mz] op_sel:[0,1,0] op_sel_hi:[0,1,0]\n"
+      : [r0] "=&v"(r[0]), [r1] "=&v"(r[1]), [r2] "=&v"(r[2]), [r3] "=&v"(r[3]), [r4] "=&v"(r[4]),
+        [r5] "=&v"(r[5]), [r6] "=&v"(r[6]), [r7] "=&v"(r[7])
+      : [a] "v"(a), [h0] "v"(h.x), [h1] "v"(h.y), [h2] "v"(h.z), [h3] "v"(h.w), [mz] "v"(mz));
+}
+
 template <bool BF16>
 __device__ __forceinline__ float w2f(uint16_t w) {
   if constexpr (BF16) return b2f(w); else return h2f(w);

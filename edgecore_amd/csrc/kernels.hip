@@ -294,12 +294,28 @@ __device__ __forceinline__ float dot_k_row(const float *qs, const uint16_t *kp, 
   return s;
 }
 
-// the own position's score from the fp16-rounded new k in LDS
+// the own position's score from the fp16-rounded new k in LDS (one thread;
+// unrolled with 16-byte reads, since every wave waits for it at the next
+// barrier)
+template <int HD>
 __device__ __forceinline__ float dot_new_k(const float *qs, const float *kn, int hd) {
   float s = 0.0f;
-  for (int d = 0; d < hd; d++) {
-    const float p0 = qs[d] * kn[d];
-    s = s + p0;
+  if constexpr (HD > 0) {
+#pragma unroll
+    for (int c = 0; c < HD / 4; c++) {
+      const float4 q4 = *reinterpret_cast<const float4 *>(qs + 4 * c);
+      const float4 k4 = *reinterpret_cast<const float4 *>(kn + 4 * c);
+      const float p0 = q4.x * k4.x, p1 = q4.y * k4.y, p2 = q4.z * k4.z, p3 = q4.w * k4.w;
+      s = s + p0;
+      s = s + p1;
+      s = s + p2;
+      s = s + p3;
+    }
+  } else {
+    for (int d = 0; d < hd; d++) {
+      const float p0 = qs[d] * kn[d];
+      s = s + p0;
+    }
   }
   return s;
 }
@@ -446,6 +462,10 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         a.kc_w[woff] = kh;
         a.vc_w[woff] = vh;
       }
+      // the own position's row of the K tile takes the new k (its cache row
+      // is read before the append), so the position is scored with the others
+      if (HD > 0 && n - 1 < KQ)
+        reinterpret_cast<uint16_t *>(prod)[((size_t)(n - 1) * KP + (t >> 3)) * 8 + (t & 7)] = kh;
     }
   }
   // K tile: row i, chunk c at 16-byte slot i*KP + c
@@ -457,7 +477,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
 #pragma unroll
       for (int e = 0; e < 4; e++) {
         const int i = 4 * qd + e;
-        if (i < KQ) ktile[i * KP + cd] = kr[u][e];
+        if (i < KQ && !(FUSED && i == n - 1)) ktile[i * KP + cd] = kr[u][e];
       }
     }
   }
@@ -469,7 +489,6 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   // ---- 4. scores ----
   float mx = -FLT_MAX;
   auto put = [&](int i, float s) {
-    if (FUSED && i == n - 1) s = dot_new_k(qs, kn, hd);
     s = (float)((double)s * a.inv_hd);
     sc[i] = s;
     mx = fmaxf(mx, s);
@@ -482,25 +501,15 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     for (int r = 0; r < R; r++) s[r] = 0.0f;
 #pragma unroll
     for (int c = 0; c < CPR; c++) {
-      uint32_t wv[R][4];
+      v4u kk[R];
 #pragma unroll
-      for (int r = 0; r < R; r++) {
-        const int ir = min(t + 256 * r, KQ - 1);
-        const v4u kk = ktile[ir * KP + c];
-        wv[r][0] = kk.x;
-        wv[r][1] = kk.y;
-        wv[r][2] = kk.z;
-        wv[r][3] = kk.w;
-      }
+      for (int r = 0; r < R; r++) kk[r] = ktile[min(t + 256 * r, KQ - 1) * KP + c];
+      float qv[8];
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const float q0 = qs[8 * c + 2 * j], q1 = qs[8 * c + 2 * j + 1];
+      for (int j = 0; j < 8; j++) qv[j] = qs[8 * c + j];
 #pragma unroll
-        for (int r = 0; r < R; r++) {
-          s[r] = mac_h<0>(s[r], q0, wv[r][j]);
-          s[r] = mac_h<1>(s[r], q1, wv[r][j]);
-        }
-      }
+      for (int r = 0; r + 1 < R; r += 2) mac8x2(s[r], s[r + 1], qv, kk[r], kk[r + 1]);
+      if constexpr (R & 1) mac8(s[R - 1], qv, kk[R - 1]);
     }
 #pragma unroll
     for (int r = 0; r < R; r++) {
@@ -511,18 +520,35 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   // positions past the K tile (long contexts) and the generic path
   for (int i = t; i < n; i += 256) {
     if (HD > 0 && i < KQ) continue;  // scored from the K tile above
-    put(i, (FUSED && i == n - 1) ? 0.0f : dot_k_row<HD>(qs, K + (size_t)i * a.kv, hd));
+    put(i, (FUSED && i == n - 1) ? dot_new_k<HD>(qs, kn, hd) : dot_k_row<HD>(qs, K + (size_t)i * a.kv, hd));
   }
   mx = block_max256_1b(mx, redf);
+  // this thread's first two values stay in registers until the sum is known
+  // (positions below 512); further ones go through LDS
   double sum = 0.0;
-  for (int i = t; i < n; i += 256) {
+  float ev[2];
+#pragma unroll
+  for (int k = 0; k < 2; k++) {
+    const int i = t + 256 * k;
+    ev[k] = 0.0f;
+    if (i < n) {
+      ev[k] = ec_expf_tab(sc[i] - mx, etab);
+      sum += (double)ev[k];
+    }
+  }
+  for (int i = t + 512; i < n; i += 256) {
     const float e = ec_expf_tab(sc[i] - mx, etab);
     sc[i] = e;
     sum += (double)e;
   }
   sum = block_sum256_1b(sum, redd);
   const double isum = 1.0 / sum;
-  for (int i = t; i < n; i += 256) sc[i] = (float)((double)sc[i] * isum);
+#pragma unroll
+  for (int k = 0; k < 2; k++) {
+    const int i = t + 256 * k;
+    if (i < n) sc[i] = (float)((double)ev[k] * isum);
+  }
+  for (int i = t + 512; i < n; i += 256) sc[i] = (float)((double)sc[i] * isum);
 
   // ---- 5. products p*v, and the sequential sums ----
   // element d of quad q sits in 16-byte slot q*P + (d ^ ((d >> 4) & sw)); with
@@ -594,12 +620,10 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
               float pr[8][4];
 #pragma unroll
               for (int e = 0; e < 4; e++) {
-                const uint32_t hv[4] = {vu[e].x, vu[e].y, vu[e].z, vu[e].w};
+                float r8[8];
+                mul8h(r8, pe[e], vu[e]);
 #pragma unroll
-                for (int j = 0; j < 4; j++) {
-                  pr[2 * j][e] = mul_h<0>(pe[e], hv[j]);
-                  pr[2 * j + 1][e] = mul_h<1>(pe[e], hv[j]);
-                }
+                for (int k = 0; k < 8; k++) pr[k][e] = r8[k];
               }
 #pragma unroll
               for (int k = 0; k < 8; k++)

@@ -93,6 +93,7 @@ _SIG = {
     "ec_topk_max": (_I, []),
     "ec_last_logits": (_I, [_P, _I, _P]),
     "ec_topk_dev": (_I, [_P, _I, _I, _I, _I, _P, _P, _P]),
+    "ec_attention_dev": (_I, [_P, _I, _P, _P, _I, _I, _I, _I, _I, _P, _P, _I, _I, _P, _I, _I]),
     "ec_rng_next": (C.c_uint, [C.POINTER(C.c_ulonglong)]),
     "ec_sample_full": (_I, [_P, _I, C.c_float, _I, C.POINTER(C.c_ulonglong)]),
     "ec_sample_candidates": (_I, [_P, _P, _I, _I, C.c_float, _I, C.POINTER(C.c_ulonglong)]),
@@ -378,6 +379,30 @@ def topk_dev(logits: np.ndarray, top_k: int):
         return vals, idx, status
     finally:
         buf.close()
+
+
+def attention_dev(q: np.ndarray, kc: np.ndarray, vc: np.ndarray, pos, slot, H: int, KVH: int,
+                  window: int = 0, path: int = 0) -> np.ndarray:
+    """ec_attention_dev on host arrays (copied to the device): q [M][H*hd]
+    fp32, kc / vc [nslots][C][KVH*hd] fp16 bits (uint16), pos / slot [M];
+    returns out [M][H*hd] fp32."""
+    q = np.ascontiguousarray(q, np.float32)
+    kc = np.ascontiguousarray(kc, np.uint16)
+    vc = np.ascontiguousarray(vc, np.uint16)
+    pos = np.ascontiguousarray(pos, np.int32)
+    slot = np.ascontiguousarray(slot, np.int32)
+    M, E = q.shape
+    nslots, C, kv = kc.shape
+    hd = E // H
+    bufs = [DeviceBuffer.from_array(a) for a in (q, kc, vc)] + [DeviceBuffer(q.nbytes)]
+    try:
+        _check(lib().ec_attention_dev(bufs[0].ptr, E, bufs[1].ptr, bufs[2].ptr, nslots, C, H, KVH, hd,
+                                      _ptr(pos), _ptr(slot), M, window, bufs[3].ptr, E, path),
+               "ec_attention_dev")
+        return bufs[3].to_array(np.float32, (M, E))
+    finally:
+        for b in bufs:
+            b.close()
 
 
 # ---------------------------------------------------------------------------

@@ -22,10 +22,15 @@
 //     for the wave's QW tokens off one read of the K row (q in registers); K
 //     rows are head_dim + 4 floats apart, so the 16-byte reads of 8 lanes hit
 //     distinct banks;
-//   - softmax: per token, inside its wave;
+//   - softmax: per token, inside its wave, four of a lane's positions per
+//     step (expf without branches);
 //   - output: lane = element d; the wave adds pr_p * v_p[d] for its QW tokens
-//     in position order from the staged V rows, the reads of the next four
-//     positions issued before the adds of the current four.
+//     in position order from V tiles staged transposed (a lane's positions
+//     contiguous, 16-byte reads of four).  A tile that every token of a
+//     two-token wave takes whole runs as one asm block whose probabilities
+//     come from one read per token and a DPP row broadcast per product;
+//     partial tiles read the probabilities by quad, the next quad's reads in
+//     flight during the current quad's adds.
 // The blocks with the longest key ranges start first; the grid is (head,
 // token group), which spreads the blocks over all 8 XCDs.
 #include <cfloat>
@@ -40,6 +45,385 @@ namespace {
 
 constexpr int kPfTile = 64;  // positions per staged K / V tile
 
+// The output sums of two tokens over 8*n8 positions (n8 >= 1), in order:
+// o_i += pr_i[p] * v[p] (product rounded, then the add) for token i = 0, 1.
+// p0/p1: LDS byte addresses of the tokens' probabilities of the first
+// position, va: of this lane's element of that position in the transposed V
+// tile (all 16-byte aligned).  The reads of the next four positions are in
+// flight while the current four are added.  Reads four positions past the end
+// (values unused).
+__device__ __forceinline__ void pf_chain2(float &o0, float &o1, uint32_t p0, uint32_t p1, uint32_t va, int n8) {
+  float t0, t1;
+  asm volatile(
+      "ds_read_b128 v[40:43], %[p0] offset:0\n"
+      "ds_read_b128 v[44:47], %[p1] offset:0\n"
+      "ds_read_b128 v[48:51], %[va] offset:0\n"
+      "L_pf_chain%=:\n"
+      "ds_read_b128 v[52:55], %[p0] offset:16\n"
+      "ds_read_b128 v[56:59], %[p1] offset:16\n"
+      "ds_read_b128 v[60:63], %[va] offset:16\n"
+      "s_waitcnt lgkmcnt(3)\n"
+      "v_mul_f32 %[t0], v40, v48\n"
+      "v_mul_f32 %[t1], v44, v48\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32 %[t0], v41, v49\n"
+      "v_mul_f32 %[t1], v45, v49\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32 %[t0], v42, v50\n"
+      "v_mul_f32 %[t1], v46, v50\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32 %[t0], v43, v51\n"
+      "v_mul_f32 %[t1], v47, v51\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_add_u32 %[p0], 32, %[p0]\n"
+      "v_add_u32 %[p1], 32, %[p1]\n"
+      "v_add_u32 %[va], 32, %[va]\n"
+      "ds_read_b128 v[40:43], %[p0] offset:0\n"
+      "ds_read_b128 v[44:47], %[p1] offset:0\n"
+      "ds_read_b128 v[48:51], %[va] offset:0\n"
+      "s_waitcnt lgkmcnt(3)\n"
+      "v_mul_f32 %[t0], v52, v60\n"
+      "v_mul_f32 %[t1], v56, v60\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32 %[t0], v53, v61\n"
+      "v_mul_f32 %[t1], v57, v61\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32 %[t0], v54, v62\n"
+      "v_mul_f32 %[t1], v58, v62\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32 %[t0], v55, v63\n"
+      "v_mul_f32 %[t1], v59, v63\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "s_sub_u32 %[n], %[n], 1\n"
+      "s_cmp_lg_u32 %[n], 0\n"
+      "s_cbranch_scc1 L_pf_chain%=\n"
+      "s_waitcnt lgkmcnt(0)\n"
+      : [o0] "+v"(o0), [o1] "+v"(o1), [t0] "=&v"(t0), [t1] "=&v"(t1), [p0] "+v"(p0), [p1] "+v"(p1), [va] "+v"(va),
+        [n] "+s"(n8)
+      :
+      : "v40", "v41", "v42", "v43", "v44", "v45", "v46", "v47", "v48", "v49", "v50", "v51", "v52", "v53", "v54", "v55", "v56", "v57", "v58", "v59", "v60", "v61", "v62", "v63", "scc", "memory");
+}
+
+// The output sums of two tokens over one whole tile of 64 positions, in
+// order, as pf_chain2.  p0/p1: LDS byte addresses of the tokens'
+// probabilities of positions 4*(lane % 16) .. +3 of the tile, so that lane j
+// of every 16-lane row holds those of quad j; each product takes its
+// probability from that lane by a DPP row broadcast (row_newbcast), which
+// replaces a 64-lane broadcast read per quad and token.  va: LDS byte address
+// of this lane's element of the tile's first position in the transposed V
+// tile; quad j is read 16*j bytes further, eight quads ahead of its adds.
+__device__ __forceinline__ void pf_tile2(float &o0, float &o1, uint32_t p0, uint32_t p1, uint32_t va) {
+  float t0, t1;
+  asm volatile(
+      "ds_read_b128 v[40:43], %[p0]\n"
+      "ds_read_b128 v[44:47], %[p1]\n"
+      "ds_read_b128 v[48:51], %[va] offset:0\n"
+      "ds_read_b128 v[52:55], %[va] offset:16\n"
+      "ds_read_b128 v[56:59], %[va] offset:32\n"
+      "ds_read_b128 v[60:63], %[va] offset:48\n"
+      "ds_read_b128 v[64:67], %[va] offset:64\n"
+      "ds_read_b128 v[68:71], %[va] offset:80\n"
+      "ds_read_b128 v[72:75], %[va] offset:96\n"
+      "ds_read_b128 v[76:79], %[va] offset:112\n"
+      "s_waitcnt lgkmcnt(7)\n"
+      "v_mul_f32_dpp %[t0], v40, v48 row_newbcast:0 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v44, v48 row_newbcast:0 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32_dpp %[t0], v41, v49 row_newbcast:0 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v45, v49 row_newbcast:0 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32_dpp %[t0], v42, v50 row_newbcast:0 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v46, v50 row_newbcast:0 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32_dpp %[t0], v43, v51 row_newbcast:0 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v47, v51 row_newbcast:0 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "ds_read_b128 v[48:51], %[va] offset:128\n"
+      "s_waitcnt lgkmcnt(7)\n"
+      "v_mul_f32_dpp %[t0], v40, v52 row_newbcast:1 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v44, v52 row_newbcast:1 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32_dpp %[t0], v41, v53 row_newbcast:1 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v45, v53 row_newbcast:1 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32_dpp %[t0], v42, v54 row_newbcast:1 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v46, v54 row_newbcast:1 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32_dpp %[t0], v43, v55 row_newbcast:1 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v47, v55 row_newbcast:1 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "ds_read_b128 v[52:55], %[va] offset:144\n"
+      "s_waitcnt lgkmcnt(7)\n"
+      "v_mul_f32_dpp %[t0], v40, v56 row_newbcast:2 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v44, v56 row_newbcast:2 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32_dpp %[t0], v41, v57 row_newbcast:2 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v45, v57 row_newbcast:2 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32_dpp %[t0], v42, v58 row_newbcast:2 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v46, v58 row_newbcast:2 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32_dpp %[t0], v43, v59 row_newbcast:2 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v47, v59 row_newbcast:2 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "ds_read_b128 v[56:59], %[va] offset:160\n"
+      "s_waitcnt lgkmcnt(7)\n"
+      "v_mul_f32_dpp %[t0], v40, v60 row_newbcast:3 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v44, v60 row_newbcast:3 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32_dpp %[t0], v41, v61 row_newbcast:3 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v45, v61 row_newbcast:3 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32_dpp %[t0], v42, v62 row_newbcast:3 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v46, v62 row_newbcast:3 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32_dpp %[t0], v43, v63 row_newbcast:3 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v47, v63 row_newbcast:3 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "ds_read_b128 v[60:63], %[va] offset:176\n"
+      "s_waitcnt lgkmcnt(7)\n"
+      "v_mul_f32_dpp %[t0], v40, v64 row_newbcast:4 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v44, v64 row_newbcast:4 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32_dpp %[t0], v41, v65 row_newbcast:4 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v45, v65 row_newbcast:4 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32_dpp %[t0], v42, v66 row_newbcast:4 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v46, v66 row_newbcast:4 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32_dpp %[t0], v43, v67 row_newbcast:4 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v47, v67 row_newbcast:4 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "ds_read_b128 v[64:67], %[va] offset:192\n"
+      "s_waitcnt lgkmcnt(7)\n"
+      "v_mul_f32_dpp %[t0], v40, v68 row_newbcast:5 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v44, v68 row_newbcast:5 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32_dpp %[t0], v41, v69 row_newbcast:5 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v45, v69 row_newbcast:5 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32_dpp %[t0], v42, v70 row_newbcast:5 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v46, v70 row_newbcast:5 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32_dpp %[t0], v43, v71 row_newbcast:5 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v47, v71 row_newbcast:5 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "ds_read_b128 v[68:71], %[va] offset:208\n"
+      "s_waitcnt lgkmcnt(7)\n"
+      "v_mul_f32_dpp %[t0], v40, v72 row_newbcast:6 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v44, v72 row_newbcast:6 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32_dpp %[t0], v41, v73 row_newbcast:6 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v45, v73 row_newbcast:6 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32_dpp %[t0], v42, v74 row_newbcast:6 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v46, v74 row_newbcast:6 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32_dpp %[t0], v43, v75 row_newbcast:6 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v47, v75 row_newbcast:6 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "ds_read_b128 v[72:75], %[va] offset:224\n"
+      "s_waitcnt lgkmcnt(7)\n"
+      "v_mul_f32_dpp %[t0], v40, v76 row_newbcast:7 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v44, v76 row_newbcast:7 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32_dpp %[t0], v41, v77 row_newbcast:7 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v45, v77 row_newbcast:7 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32_dpp %[t0], v42, v78 row_newbcast:7 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v46, v78 row_newbcast:7 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32_dpp %[t0], v43, v79 row_newbcast:7 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v47, v79 row_newbcast:7 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "ds_read_b128 v[76:79], %[va] offset:240\n"
+      "s_waitcnt lgkmcnt(7)\n"
+      "v_mul_f32_dpp %[t0], v40, v48 row_newbcast:8 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v44, v48 row_newbcast:8 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32_dpp %[t0], v41, v49 row_newbcast:8 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v45, v49 row_newbcast:8 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32_dpp %[t0], v42, v50 row_newbcast:8 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v46, v50 row_newbcast:8 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32_dpp %[t0], v43, v51 row_newbcast:8 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v47, v51 row_newbcast:8 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "s_waitcnt lgkmcnt(6)\n"
+      "v_mul_f32_dpp %[t0], v40, v52 row_newbcast:9 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v44, v52 row_newbcast:9 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32_dpp %[t0], v41, v53 row_newbcast:9 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v45, v53 row_newbcast:9 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32_dpp %[t0], v42, v54 row_newbcast:9 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v46, v54 row_newbcast:9 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32_dpp %[t0], v43, v55 row_newbcast:9 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v47, v55 row_newbcast:9 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "s_waitcnt lgkmcnt(5)\n"
+      "v_mul_f32_dpp %[t0], v40, v56 row_newbcast:10 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v44, v56 row_newbcast:10 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32_dpp %[t0], v41, v57 row_newbcast:10 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v45, v57 row_newbcast:10 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32_dpp %[t0], v42, v58 row_newbcast:10 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v46, v58 row_newbcast:10 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32_dpp %[t0], v43, v59 row_newbcast:10 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v47, v59 row_newbcast:10 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "s_waitcnt lgkmcnt(4)\n"
+      "v_mul_f32_dpp %[t0], v40, v60 row_newbcast:11 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v44, v60 row_newbcast:11 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32_dpp %[t0], v41, v61 row_newbcast:11 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v45, v61 row_newbcast:11 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32_dpp %[t0], v42, v62 row_newbcast:11 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v46, v62 row_newbcast:11 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32_dpp %[t0], v43, v63 row_newbcast:11 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v47, v63 row_newbcast:11 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "s_waitcnt lgkmcnt(3)\n"
+      "v_mul_f32_dpp %[t0], v40, v64 row_newbcast:12 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v44, v64 row_newbcast:12 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32_dpp %[t0], v41, v65 row_newbcast:12 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v45, v65 row_newbcast:12 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32_dpp %[t0], v42, v66 row_newbcast:12 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v46, v66 row_newbcast:12 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32_dpp %[t0], v43, v67 row_newbcast:12 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v47, v67 row_newbcast:12 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "s_waitcnt lgkmcnt(2)\n"
+      "v_mul_f32_dpp %[t0], v40, v68 row_newbcast:13 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v44, v68 row_newbcast:13 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32_dpp %[t0], v41, v69 row_newbcast:13 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v45, v69 row_newbcast:13 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32_dpp %[t0], v42, v70 row_newbcast:13 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v46, v70 row_newbcast:13 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32_dpp %[t0], v43, v71 row_newbcast:13 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v47, v71 row_newbcast:13 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "s_waitcnt lgkmcnt(1)\n"
+      "v_mul_f32_dpp %[t0], v40, v72 row_newbcast:14 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v44, v72 row_newbcast:14 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32_dpp %[t0], v41, v73 row_newbcast:14 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v45, v73 row_newbcast:14 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32_dpp %[t0], v42, v74 row_newbcast:14 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v46, v74 row_newbcast:14 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32_dpp %[t0], v43, v75 row_newbcast:14 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v47, v75 row_newbcast:14 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "s_waitcnt lgkmcnt(0)\n"
+      "v_mul_f32_dpp %[t0], v40, v76 row_newbcast:15 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v44, v76 row_newbcast:15 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32_dpp %[t0], v41, v77 row_newbcast:15 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v45, v77 row_newbcast:15 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32_dpp %[t0], v42, v78 row_newbcast:15 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v46, v78 row_newbcast:15 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      "v_mul_f32_dpp %[t0], v43, v79 row_newbcast:15 row_mask:0xf bank_mask:0xf\n"
+      "v_mul_f32_dpp %[t1], v47, v79 row_newbcast:15 row_mask:0xf bank_mask:0xf\n"
+      "v_add_f32 %[o0], %[o0], %[t0]\n"
+      "v_add_f32 %[o1], %[o1], %[t1]\n"
+      : [o0] "+v"(o0), [o1] "+v"(o1), [t0] "=&v"(t0), [t1] "=&v"(t1)
+      : [p0] "v"(p0), [p1] "v"(p1), [va] "v"(va)
+      : "v40", "v41", "v42", "v43", "v44", "v45", "v46", "v47", "v48", "v49", "v50", "v51", "v52", "v53", "v54", "v55", "v56", "v57", "v58", "v59", "v60", "v61", "v62", "v63", "v64", "v65", "v66", "v67", "v68", "v69", "v70", "v71", "v72", "v73", "v74", "v75", "v76", "v77", "v78", "v79", "memory");
+}
+
+// V tiles are staged transposed: element d of the tile's position r at
+// tile[pf_vrow(d) + r].  Rows are 68 floats apart plus 8 more every 16 rows,
+// so that the staging writes (per wave 8 positions x 8 chunks of 8 elements)
+// and the 16-byte reads of 16 consecutive rows both hit distinct banks.
+constexpr int pf_vrow(int d) { return d * (kPfTile + 4) + 8 * (d >> 4); }
+
 // NW waves per block, QW tokens per wave (consecutive), NW * QW tokens per block
 template <int HD, int NW, int QW>
 __global__ __launch_bounds__(NW * 64) void attn_prefill_kernel(AttnArgs a, int ngroups, int nsc) {
@@ -49,8 +433,10 @@ __global__ __launch_bounds__(NW * 64) void attn_prefill_kernel(AttnArgs a, int n
   constexpr int TCH = kPfTile * CPR;           // chunks per tile
   constexpr int NCH = (TCH + NT - 1) / NT;     // chunks per thread
   constexpr int DPL = HD > 64 ? HD / 64 : 1;   // output elements per lane
+  constexpr int VJ = pf_vrow(64);              // transposed V: element d + 64 is VJ floats after d
+  static_assert(pf_vrow(HD - 1) + kPfTile + 4 <= (kPfTile + 4) * KP, "transposed V tile fits the tile area");
   extern __shared__ __attribute__((aligned(16))) float lds[];
-  float *tile = lds;  // [kPfTile + 4][KP]: K rows, then V rows (4 spare rows for look-ahead reads)
+  float *tile = lds;  // [kPfTile + 4][KP]: K rows (4 spare rows for look-ahead reads), then transposed V
   __shared__ uint64_t etab[32];
 
   const int t = threadIdx.x, lane = t & 63;
@@ -100,7 +486,8 @@ __global__ __launch_bounds__(NW * 64) void attn_prefill_kernel(AttnArgs a, int n
 
   // tile staging: the next tile's 16-byte chunks are loaded into registers
   // (gload) while the waves work on the current one, then converted to fp32
-  // into LDS (lstore) after the barrier.  Rows past pos_hi are clamped to it.
+  // into LDS after the barrier, K row by row (lstore), V transposed
+  // (lstore_v).  Rows past pos_hi are clamped to it.
   v4u pre[NCH];
   auto gload = [&](const uint16_t *src, int p0) {
 #pragma unroll
@@ -125,6 +512,23 @@ __global__ __launch_bounds__(NW * 64) void attn_prefill_kernel(AttnArgs a, int n
         float *dst = tile + r * KP + 8 * cc;
         *reinterpret_cast<float4 *>(dst) = make_float4(f[0], f[1], f[2], f[3]);
         *reinterpret_cast<float4 *>(dst + 4) = make_float4(f[4], f[5], f[6], f[7]);
+      }
+    }
+  };
+  auto lstore_v = [&]() {
+#pragma unroll
+    for (int j = 0; j < NCH; j++) {
+      const int c = t + NT * j;
+      if (TCH % NT == 0 || c < TCH) {
+        const int r = c / CPR, cc = c - r * CPR;
+        const uint32_t hv[4] = {pre[j].x, pre[j].y, pre[j].z, pre[j].w};
+        // elements 8cc .. 8cc+7 share d >> 4: rows kPfTile + 4 floats apart
+        float *dst = tile + pf_vrow(8 * cc) + r;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          dst[(2 * i) * (kPfTile + 4)] = h2f((uint16_t)(hv[i] & 0xffffu));
+          dst[(2 * i + 1) * (kPfTile + 4)] = h2f((uint16_t)(hv[i] >> 16));
+        }
       }
     }
   };
@@ -182,15 +586,35 @@ __global__ __launch_bounds__(NW * 64) void attn_prefill_kernel(AttnArgs a, int n
     const float m = wave_max_dpp(mx[i]);
     const int n = pos[i] - lo[i] + 1;
     float *sq = scq[i] + (lo[i] - lo0);
+    // four of the lane's scores per step, k, k + 64, k + 128, k + 192 (the
+    // lane's order of its part of the sum); past n a score of -inf adds
+    // exp = 0 (reads clamped to the token's last slot)
     double sum = 0.0;
-    for (int k = lane; k < n; k += 64) {
-      const float e = ec_expf_tab(sq[k] - m, etab);
-      sq[k] = e;
-      sum += (double)e;
+    for (int k = lane; k < n; k += 256) {
+      float e[4];
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        const float v = sq[min(k + 64 * u, n - 1)];
+        e[u] = k + 64 * u < n ? v - m : -__builtin_inff();
+      }
+#pragma unroll
+      for (int u = 0; u < 4; u++) e[u] = ec_expf_tab(e[u], etab);
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        if (k + 64 * u < n) sq[k + 64 * u] = e[u];
+        sum += (double)e[u];
+      }
     }
     sum = wave_sum_dpp(sum);
     const double isum = 1.0 / sum;
-    for (int k = lane; k < n; k += 64) sq[k] = (float)((double)sq[k] * isum);
+    for (int k = lane; k < n; k += 256) {
+      float v[4];
+#pragma unroll
+      for (int u = 0; u < 4; u++) v[u] = sq[min(k + 64 * u, n - 1)];
+#pragma unroll
+      for (int u = 0; u < 4; u++)
+        if (k + 64 * u < n) sq[k + 64 * u] = (float)((double)v[u] * isum);
+    }
   }
 
   // ---- output: lane = element d; per token, the sum over positions in order ----
@@ -200,22 +624,24 @@ __global__ __launch_bounds__(NW * 64) void attn_prefill_kernel(AttnArgs a, int n
 #pragma unroll
     for (int j = 0; j < DPL; j++) o[i][j] = 0.0f;
   const int d0 = HD >= 64 ? lane : (lane & (HD - 1));
+  // this lane's element of the tile's position p at vt[p - p0] (of element
+  // d0 + 64 j at vt[p - p0 + VJ * j])
+  const float *vt = tile + pf_vrow(d0);
   for (int p0 = lo0; p0 <= pos_hi; p0 += kPfTile) {
     __syncthreads();  // probabilities written / previous tile consumed
-    lstore();
+    lstore_v();
     __syncthreads();
     if (p0 + kPfTile <= pos_hi) gload(Vc, p0 + kPfTile);
-    const float *vt = tile + d0;  // staged row of position p at vt + (p - p0) * KP
     // a position that only some tokens of the wave take
     auto add_some = [&](int p) {
-      const float *vr = vt + (p - p0) * KP;
+      const float *vr = vt + (p - p0);
 #pragma unroll
       for (int i = 0; i < QW; i++) {
         if (p >= lo[i] && p <= pos[i]) {
           const float pr = scq[i][p - lo0];
 #pragma unroll
           for (int j = 0; j < DPL; j++) {
-            const float pv = pr * vr[64 * j];
+            const float pv = pr * vr[VJ * j];
             o[i][j] = o[i][j] + pv;
           }
         }
@@ -223,6 +649,14 @@ __global__ __launch_bounds__(NW * 64) void attn_prefill_kernel(AttnArgs a, int n
     };
     const int r0 = max(p0, lo[0]), r1 = min(p0 + kPfTile - 1, pos[QW - 1]);
     int c0 = max(p0, lo[QW - 1]), c1 = min(p0 + kPfTile - 1, pos[0]);  // taken by every token
+    if constexpr (QW == 2 && DPL == 1) {
+      if (c0 == p0 && c1 == p0 + kPfTile - 1) {  // the whole tile, for both tokens
+        const int pq = p0 - lo0 + 4 * (lane & 15);
+        pf_tile2(o[0][0], o[1][0], (uint32_t)(uintptr_t)(scq[0] + pq), (uint32_t)(uintptr_t)(scq[QW - 1] + pq),
+                 (uint32_t)(uintptr_t)vt);
+        continue;
+      }
+    }
     if (c0 > c1) c0 = r1 + 1, c1 = r1;
     int p = r0;
     for (; p < c0; p++) add_some(p);
@@ -235,16 +669,31 @@ __global__ __launch_bounds__(NW * 64) void attn_prefill_kernel(AttnArgs a, int n
       // reads are unconditional; past c1 they reach at most 4 positions
       // further: the tile's 4 spare rows, the next token's score slots or the
       // 4 spare floats after the last token's (values not used).
+      if constexpr (QW == 2 && DPL == 1) {
+        // the two-token, one-element case (the long prompts) in one asm loop
+        // of 8 positions per iteration; an odd group and the tail below
+        const int n8 = __builtin_amdgcn_readfirstlane(ng >> 1);
+        if (n8 > 0) {
+          pf_chain2(o[0][0], o[1][0], (uint32_t)(uintptr_t)(scq[0] + (p - lo0)),
+                    (uint32_t)(uintptr_t)(scq[QW - 1] + (p - lo0)), (uint32_t)(uintptr_t)(vt + (p - p0)), n8);
+          p += 8 * n8;
+        }
+        for (int e = 0; e < 4 * (ng & 1); e++, p++) add_some(p);
+      } else {
       float4 pa[QW], pb[QW];
       float va[4][DPL], vb[4][DPL];
       auto load4 = [&](int pp, float4 *pr, float (*vv)[DPL]) {
 #pragma unroll
         for (int i = 0; i < QW; i++) pr[i] = *reinterpret_cast<const float4 *>(scq[i] + (pp - lo0));
-        const float *vr = vt + (pp - p0) * KP;
+        const float *vr = vt + (pp - p0);
 #pragma unroll
-        for (int e = 0; e < 4; e++)
-#pragma unroll
-          for (int j = 0; j < DPL; j++) vv[e][j] = vr[e * KP + 64 * j];
+        for (int j = 0; j < DPL; j++) {
+          const float4 v4 = *reinterpret_cast<const float4 *>(vr + VJ * j);
+          vv[0][j] = v4.x;
+          vv[1][j] = v4.y;
+          vv[2][j] = v4.z;
+          vv[3][j] = v4.w;
+        }
       };
       auto add4 = [&](const float4 *pr, float (*vv)[DPL]) {
 #pragma unroll
@@ -274,6 +723,7 @@ __global__ __launch_bounds__(NW * 64) void attn_prefill_kernel(AttnArgs a, int n
         __builtin_amdgcn_sched_barrier(0);
         p += 4;
         if (++g == ng) break;
+      }
       }
     }
     for (; p <= r1; p++) add_some(p);

@@ -54,12 +54,10 @@ EC_EXPF_FN float ec_expf_tab(float x, const uint64_t *tab)
     uint32_t ux;
     memcpy(&ux, &x, 4);
     const uint32_t abstop = (ux >> 20) & 0x7ffu;
-    if (abstop >= 0x42bu) { /* |x| >= 88, inf or nan */
-        if (ux == 0xff800000u) return 0.0f;
-        if (abstop >= 0x7f8u) return x + x;
-        if (x > 0x1.62e42ep6f) return __builtin_inff(); /* overflow */
-        if (x < -0x1.9fe368p6f) return 0.0f;            /* underflow */
-    }
+    /* the main path for every input; glibc's special cases (|x| >= 88, inf,
+     * nan) replace its result below by selects, in glibc's order of
+     * precedence, so that a wave takes no branch (the main path of inf or
+     * nan yields some value, and its table index stays in 0..31) */
     const double xd = (double)x;
     const double z = inv_ln2_n * xd;
     double kd = z + shift;
@@ -76,7 +74,12 @@ EC_EXPF_FN float ec_expf_tab(float x, const uint64_t *tab)
     double y = __builtin_fma(c2, r, 1.0);
     y = __builtin_fma(zz, r2, y);
     y = y * s;
-    return (float)y;
+    float res = (float)y;
+    res = x < -0x1.9fe368p6f ? 0.0f : res;           /* underflow */
+    res = x > 0x1.62e42ep6f ? __builtin_inff() : res; /* overflow */
+    res = abstop >= 0x7f8u ? x + x : res;             /* inf or nan */
+    res = ux == 0xff800000u ? 0.0f : res;             /* -inf */
+    return res;
 }
 
 EC_EXPF_FN float ec_expf_ref(float x) { return ec_expf_tab(x, ec_exp2_32); }

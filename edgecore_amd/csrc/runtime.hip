@@ -1157,6 +1157,50 @@ extern "C" int ec_topk_dev(const float *logits, int rows, int vocab, int ld, int
   return 0;
 }
 
+extern "C" int ec_attention_dev(const float *q, int ldq, const uint16_t *kc, const uint16_t *vc, int nslots, int C,
+                                int H, int KVH, int hd, const int *pos, const int *slot, int M, int window, float *out,
+                                int ldo, int path) {
+  EC_INIT();
+  if (!q || !kc || !vc || !pos || !slot || !out) return set_err(-1, "ec_attention_dev: null pointer");
+  if (M < 1 || nslots < 1 || C < 1 || H < 1 || KVH < 1 || H % KVH || hd < 1 || ldq < H * hd || ldo < H * hd ||
+      window < 0 || (path != 0 && path != 1))
+    return set_err(-1, "ec_attention_dev: M=%d slots=%d C=%d H=%d KVH=%d hd=%d ldq=%d ldo=%d window=%d path=%d", M,
+                   nslots, C, H, KVH, hd, ldq, ldo, window, path);
+  int max_npos = 0;
+  for (int m = 0; m < M; m++) {
+    if (pos[m] < 0 || pos[m] >= C || slot[m] < 0 || slot[m] >= nslots)
+      return set_err(-1, "ec_attention_dev: token %d has position %d / slot %d outside [0, %d) / [0, %d)", m, pos[m],
+                     slot[m], C, nslots);
+    if (path == 0 && (slot[m] != slot[0] || pos[m] != pos[0] + m))
+      return set_err(-1, "ec_attention_dev: path 0 takes one slot's consecutive positions (token %d)", m);
+    if (pos[m] + 1 > max_npos) max_npos = pos[m] + 1;
+  }
+  const int kv = KVH * hd;
+  const int vtile = attn_vtile(max_npos, hd, kv);
+  if (vtile < 4) return set_err(-1, "ec_attention_dev: position %d needs more LDS than the device has", max_npos - 1);
+  int *dps = nullptr;
+  hipError_t e = hipMalloc(&dps, (size_t)2 * M * sizeof(int));
+  if (e == hipSuccess) e = hipMemcpyAsync(dps, pos, (size_t)M * sizeof(int), hipMemcpyHostToDevice, g_stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(dps + M, slot, (size_t)M * sizeof(int), hipMemcpyHostToDevice, g_stream);
+  AttnArgs aa{q, ldq, kc, vc, out, ldo, dps, dps + M, H, KVH, hd, kv, C, window, 1.0 / sqrt((double)hd), M, max_npos,
+              vtile, 0, nullptr, nullptr, 0, nullptr, 0, nullptr, nullptr, 0};
+  bool shape_ok = true;
+  if (e == hipSuccess) {
+    if (path == 0) {
+      shape_ok = attention_prefill_ok(aa, g_max_lds);
+      if (shape_ok) e = attention_prefill(aa, g_max_lds, g_stream);
+    } else {
+      e = attention(aa, g_stream);
+    }
+  }
+  if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
+  if (dps) (void)hipFree(dps);
+  if (!shape_ok) return set_err(-1, "ec_attention_dev: the prefill kernel does not take head_dim %d / %d positions", hd,
+                                max_npos);
+  if (e != hipSuccess) return set_err(-3, "ec_attention_dev: %s", hipGetErrorString(e));
+  return 0;
+}
+
 extern "C" void gpt2_forward(GPT2 *g, const int *tokens, const int *positions, const int *seqs, int M,
                              float *logits) {
   if (forward_impl(g, tokens, positions, seqs, M, 0, logits, nullptr)) {

@@ -323,6 +323,20 @@ int ec_last_logits(GPT2 *g, int row, float *out);
 int ec_topk_dev(const float *logits, int rows, int vocab, int ld, int top_k, float *vals, int *idx,
                 int *status);
 
+/* The forward's causal attention alone, on device memory, for checking it on
+ * its own: head h of token m attends over positions [lo, pos[m]] of cache slot
+ * slot[m] (lo = max(0, pos[m] - window + 1) when window > 0, else 0) with the
+ * arithmetic of src/gpt2.c:527-557 (GPT-2, KVH = H) and 744-777 (Qwen2 GQA:
+ * KV head h * KVH / H).  q [M][H*hd] fp32 (row stride ldq, 16-byte aligned
+ * rows for path 0), kc / vc fp16 caches [nslots][C][KVH*hd], out [M][H*hd]
+ * fp32 (row stride ldo); pos and slot are host arrays [M].  path 0: the
+ * prefill kernel (one slot's consecutive positions pos[0] + m, as the forward
+ * runs a prompt); path 1: the per-token kernel (any positions and slots, as
+ * the forward runs decode steps).  0 or <0. */
+int ec_attention_dev(const float *q, int ldq, const uint16_t *kc, const uint16_t *vc, int nslots, int C, int H,
+                     int KVH, int hd, const int *pos, const int *slot, int M, int window, float *out, int ldo,
+                     int path);
+
 /* Sampling of src/runtime_main.c:205-248.  ec_rng_next: the driver's LCG
  * (state advances, returns the top 31 bits).  ec_sample_full: sample_token on
  * a whole row (temp <= 0: greedy).  ec_sample_candidates: the same token from

@@ -55,6 +55,7 @@ def olib() -> C.CDLL:
             "or_argmax": (_I, [_P, _I]),
             "or_generate": (_I, [_P, _P, _I, _I, _P, _P]),
             "or_map": (None, [_I, _P, _P, C.c_size_t]),
+            "or_attention_rows": (_I, [_P, _I, _P, _P, _I, _I, _I, _I, _I, _P, _P, _P, _I, _I, _P, _I]),
         }
         for k, (r, a) in sig.items():
             f = getattr(L, k)
@@ -179,6 +180,26 @@ def map_op(op: int, x: np.ndarray) -> np.ndarray:
     x = np.ascontiguousarray(x)
     out = np.empty(x.shape, {3: np.uint16, 5: np.int8}.get(op, np.float32))
     olib().or_map(op, _p(x), _p(out), x.size)
+    return out
+
+
+def attention_rows(q, kc, vc, pos, slot, H: int, KVH: int, rows=None, window: int = 0) -> np.ndarray:
+    """Reference attention (or_attention_rows) of the listed rows (all if
+    None): q [M][H*hd] fp32, kc / vc [nslots][C][KVH*hd] fp16 bits, pos /
+    slot [M].  Rows not listed come back as NaN."""
+    q = np.ascontiguousarray(q, np.float32)
+    kc = np.ascontiguousarray(kc, np.uint16)
+    vc = np.ascontiguousarray(vc, np.uint16)
+    pos = np.ascontiguousarray(pos, np.int32)
+    slot = np.ascontiguousarray(slot, np.int32)
+    M, E = q.shape
+    nslots, C, _ = kc.shape
+    rows = np.arange(M, dtype=np.int32) if rows is None else np.ascontiguousarray(rows, np.int32)
+    out = np.full((M, E), np.nan, np.float32)
+    rc = olib().or_attention_rows(_p(q), E, _p(kc), _p(vc), nslots, C, H, KVH, E // H, _p(pos), _p(slot),
+                                  _p(rows), rows.size, window, _p(out), E)
+    if rc:
+        raise ValueError("or_attention_rows: arguments outside the caches")
     return out
 
 

@@ -733,6 +733,45 @@ static void or_attend(const float *q, const uint16_t *kb, const uint16_t *vb, in
     }
 }
 
+/* or_attend on caller-given caches [nslots][C][KVH*hd], for checking the
+ * device attention kernels alone: the listed rows (tokens) m, every head h
+ * (KV head h * KVH / H, src/gpt2.c:744-745), positions [lo, pos[m]] of slot
+ * slot[m] with lo as the forward's (sliding window, src/gpt2.c:753-754).
+ * 0, or -1 for arguments outside the caches. */
+int or_attention_rows(const float *q, int ldq, const uint16_t *kc, const uint16_t *vc, int nslots, int C,
+                      int H, int KVH, int hd, const int *pos, const int *slot, const int *rows, int nrows,
+                      int window, float *out, int ldo)
+{
+    if (nslots < 1 || C < 1 || H < 1 || KVH < 1 || H % KVH || hd < 1 || nrows < 0) return -1;
+    for (int r = 0; r < nrows; r++) {
+        int m = rows[r];
+        if (m < 0 || pos[m] < 0 || pos[m] >= C || slot[m] < 0 || slot[m] >= nslots) return -1;
+    }
+    f16_lut_init();
+    const int kv = KVH * hd;
+    const double inv_hd = 1.0 / sqrt((double)hd);
+    int rc = 0;
+#pragma omp parallel
+    {
+        float *sc = malloc((size_t)C * sizeof(float));
+        if (!sc) rc = -1;
+#pragma omp for collapse(2) schedule(static)
+        for (int r = 0; r < nrows; r++) {
+            for (int h = 0; h < H; h++) {
+                if (!sc) continue;
+                int m = rows[r];
+                int lo = window > 0 ? pos[m] - window + 1 : 0;
+                if (lo < 0) lo = 0;
+                size_t cbase = (size_t)slot[m] * C * kv + (size_t)(h * KVH / H) * hd;
+                or_attend(q + (size_t)m * ldq + (size_t)h * hd, kc + cbase, vc + cbase, kv, hd, lo, pos[m],
+                          inv_hd, sc, out + (size_t)m * ldo + (size_t)h * hd);
+            }
+        }
+        free(sc);
+    }
+    return rc;
+}
+
 static int or_check_inputs(const OrModel *g, const int *tokens, const int *positions, int M)
 {
     if (M < 1 || M > g->mmax) return -1;

@@ -74,6 +74,13 @@ int      or_arch(const OrModel *m);        /* 0 gpt2, 1 qwen2 */
  * when a position/slot/token is out of range or M exceeds the workspace. */
 int      or_forward(OrModel *m, const int *tokens, const int *positions,
                     const int *seqs, int M, float *logits);
+/* Attention rows alone on caller-given fp16 caches [nslots][C][KVH*hd]:
+ * for each m in rows[0..nrows), every head, the forward's per-row attention
+ * (src/gpt2.c:527-557, 744-777) over positions [lo, pos[m]] of slot slot[m];
+ * q / out rows of stride ldq / ldo.  0 or -1. */
+int or_attention_rows(const float *q, int ldq, const uint16_t *kc, const uint16_t *vc, int nslots, int C,
+                      int H, int KVH, int hd, const int *pos, const int *slot, const int *rows, int nrows,
+                      int window, float *out, int ldo);
 /* greedy argmax, first maximum wins (src/runtime_main.c:213-219) */
 int      or_argmax(const float *logits, int vocab);
 /* gen_and_measure at batch 1, temp 0 (src/runtime_main.c:293-362): prefill

@@ -203,6 +203,53 @@ def test_rope_inverse_frequencies():
     del C
 
 
+def _f16(x):
+    return np.asarray(x, np.float32).astype(np.float16).view(np.uint16)
+
+
+def test_attention_rows_closed_forms():
+    """or_attention_rows (the forward's per-row attention over given caches):
+    a single position returns its V row exactly (pins the slot and KV-head
+    mapping, h * KVH / H); positions outside [lo, pos] are never read (NaN
+    there stays out); random rows agree with a float64 softmax attention
+    within float rounding (pins the 1/sqrt(hd) scale and the operand roles)."""
+    rng = np.random.default_rng(11)
+    H, KVH, hd, C, ns = 6, 2, 16, 40, 3
+    kv = KVH * hd
+    kc = _f16(rng.normal(0, 1, (ns, C, kv)))
+    vc = _f16(rng.normal(0, 1, (ns, C, kv)))
+    q = rng.normal(0, 1, (ns, H * hd)).astype(np.float32)
+    out = oracle.attention_rows(q, kc, vc, np.zeros(ns), np.arange(ns), H, KVH)
+    vf = vc.view(np.float16).astype(np.float32)
+    for m in range(ns):
+        for h in range(H):
+            g = h * KVH // H
+            assert np.array_equal(out[m, h * hd:(h + 1) * hd], vf[m, 0, g * hd:(g + 1) * hd])
+    # causality and the sliding window: NaN outside [pos - window + 1, pos]
+    pos = np.array([5, 20, 39], np.int32)
+    for window in (0, 4):
+        k2, v2 = kc.copy(), vc.copy()
+        for m, p in enumerate(pos):
+            lo = max(0, p - window + 1) if window else 0
+            k2[m, :lo] = k2[m, p + 1:] = v2[m, :lo] = v2[m, p + 1:] = 0x7e00
+        o2 = oracle.attention_rows(q, k2, v2, pos, np.arange(ns), H, KVH, window=window)
+        assert np.isfinite(o2).all()
+        kf, vf2 = k2.view(np.float16).astype(np.float64), v2.view(np.float16).astype(np.float64)
+        for m, p in enumerate(pos):
+            lo = max(0, p - window + 1) if window else 0
+            for h in range(H):
+                g = h * KVH // H
+                K = kf[m, lo:p + 1, g * hd:(g + 1) * hd]
+                V = vf2[m, lo:p + 1, g * hd:(g + 1) * hd]
+                s = K @ q[m, h * hd:(h + 1) * hd].astype(np.float64) / np.sqrt(hd)
+                w = np.exp(s - s.max())
+                want = (w / w.sum()) @ V
+                np.testing.assert_allclose(o2[m, h * hd:(h + 1) * hd], want, rtol=1e-4, atol=1e-5)
+    # only the listed rows are computed
+    part = oracle.attention_rows(q, kc, vc, pos, np.arange(ns), H, KVH, rows=[1])
+    assert np.isnan(part[0]).all() and np.isfinite(part[1]).all()
+
+
 def test_elementwise_map_matches_scalars():
     x = np.array([-3.0, -0.5, 0.0, 0.75, 5.0], np.float32)
     L = oracle.olib()

@@ -325,22 +325,37 @@ __device__ __forceinline__ float dot_new_k(const float *qs, const float *kn, int
 // cycles)
 constexpr int kAttnStages = 3;
 
-template <int HD, bool FUSED>
+// 16-byte slots per quad of a slice's products (hs elements): 16 consecutive
+// lanes of the writes and of the sums' reads hit distinct bank slots
+__host__ __device__ constexpr inline int attn_spitch(int hs) { return hs == 16 ? 17 : attn_pitch(hs, 0); }
+__host__ __device__ constexpr inline int attn_sswz(int hs) { return hs == 16 ? 0 : attn_swz(hs, 0); }
+
+// NS: element slices per head, one block each (1, or 2 / 4 for head_dim 64):
+// every block of a head scores all positions, and forms the products and
+// sums of its slice's elements only
+template <int HD, bool FUSED, int NS>
 __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
+  static_assert(NS == 1 || (HD == 64 && (NS == 2 || NS == 4)), "element slices: head_dim 64, two or four");
   extern __shared__ __attribute__((aligned(16))) float lds[];
   __shared__ float redf[4];
   __shared__ double redd[4];
   __shared__ uint64_t etab[32];  // expf table
   constexpr int CPR = HD > 0 ? HD / 8 : 1;         // 16-byte chunks per K/V row
+  constexpr int HS = HD > 0 ? HD / NS : 0;  // elements of this block's slice
+  constexpr int CPRV = HD > 0 ? CPR / NS : 1;  // 16-byte V chunks per slice
   const int m = blockIdx.y, t = threadIdx.x;
-  int h = blockIdx.x;
+  int h = blockIdx.x, slice = 0;
   if (a.xcd_r) {
     // XCD-aware launch: blocks are dispatched to the 8 XCDs round-robin, so
-    // block x runs on XCD x % 8; group g's heads use blocks g, g + 8, ...
-    // and share that XCD's L2 for the group's K/V rows
+    // block x runs on XCD x % 8; group g's heads (and their slices) use
+    // blocks g, g + 8, ... and share that XCD's L2 for the group's K/V rows
     const int g = blockIdx.x & 7, j = blockIdx.x >> 3;
-    if (g >= a.KVH || j >= a.xcd_r) return;
-    h = g * a.xcd_r + j;
+    if (g >= a.KVH || j >= a.xcd_r * NS) return;
+    h = g * a.xcd_r + j / NS;
+    slice = j % NS;
+  } else if (NS > 1) {
+    h = blockIdx.x / NS;
+    slice = blockIdx.x % NS;
   }
   const int pos = ld_uniform(a.pos + m), slot = ld_uniform(a.slot + m);
   const uint64_t et = ec_exp2_32[t & 31];
@@ -358,7 +373,8 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   float *vn = kn + hdp;  // FUSED: the new v, fp16-rounded
   float *sc = vn + hdp;
   float *prod = sc + ((a.max_npos + 3) & ~3);  // [T/4][P][4]
-  const int P = attn_pitch(hd, a.kv);         // 16-byte slots per quad of positions
+  const int PA = attn_pitch(hd, a.kv);        // 16-byte slots per quad of the product area
+  const int P = NS > 1 ? attn_spitch(HS) : PA;  // slots per quad of this slice's products
   const size_t cbase = (size_t)slot * a.C * a.kv + (size_t)kvh * hd;
   const uint16_t *K = a.kc + cbase + (size_t)lo * a.kv;
   const uint16_t *V = a.vc + cbase + (size_t)lo * a.kv;
@@ -390,19 +406,19 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   constexpr int KQMAX = HD > 0 ? 256 * kAttnUnits * 4 / CPR : 0;  // K positions staged
   constexpr int KP = CPR + 1;  // K tile row pitch in 16-byte chunks (odd: rows spread over the banks)
   // the K tile lives in the product area (T/4 * P slots of 16 bytes)
-  const int KQ = min(KQMAX, (T / 4) * P / KP);
+  const int KQ = min(KQMAX, (T / 4) * PA / KP);
   // V: the product threads (all but the first SWV waves, which hold the
   // output elements) keep the tile's V in registers in units of 4 positions x
   // 8 elements: QPU quads per unit index across the product threads, UPS units
   // per thread and stage of SQ quads, NSTG stages for the largest tile
   constexpr int SWV = HD > 64 ? HD / 64 : 1;
   constexpr int NPT = 256 - 64 * SWV;
-  constexpr int QPU = HD > 0 ? NPT / CPR : 1;
+  constexpr int QPU = HD > 0 ? NPT / CPRV : 1;
   constexpr int MAXQ = HD > 0 ? (256 * kAttnUnits * 4 / CPR < 512 ? 256 * kAttnUnits * 4 / CPR : 512) / 4 : 1;
   constexpr int UPS = (MAXQ + kAttnStages * QPU - 1) / (kAttnStages * QPU);
   constexpr int SQ = UPS * QPU;
   constexpr int NSTG = (MAXQ + SQ - 1) / SQ;
-  static_assert(HD == 0 || NPT % CPR == 0, "product threads cover whole quads");
+  static_assert(HD == 0 || NPT % CPRV == 0, "product threads cover whole quads");
   const int pt = t - 64 * SWV;  // product thread index (negative in the summing waves)
   v4u kr[HD > 0 ? kAttnUnits : 1][4], vr[NSTG * UPS][4];
   if constexpr (HD > 0) {
@@ -418,7 +434,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   }
   auto load_v = [&](int t0) {  // this product thread's V units of the tile at t0
     if (HD > 0 && pt >= 0) {
-      const int qd0 = pt / CPR, cd = pt - qd0 * CPR;
+      const int qd0 = pt / CPRV, cd = pt - qd0 * CPRV;
 #pragma unroll
       for (int s = 0; s < NSTG; s++) {
 #pragma unroll
@@ -426,7 +442,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
 #pragma unroll
           for (int e = 0; e < 4; e++) {
             const int i = min(t0 + 4 * (SQ * s + QPU * u + qd0) + e, last);
-            vr[s * UPS + u][e] = *reinterpret_cast<const v4u *>(V + (size_t)i * a.kv + 8 * cd);
+            vr[s * UPS + u][e] = *reinterpret_cast<const v4u *>(V + (size_t)i * a.kv + 8 * (CPRV * slice + cd));
           }
         }
       }
@@ -456,7 +472,8 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
       const uint16_t kh = f2h(kv_), vh = f2h(vv);
       kn[t] = h2f(kh);
       vn[t] = h2f(vh);
-      const bool writer = h == 0 || (h - 1) * a.KVH / a.H != kvh;  // first query head of the group
+      // first query head of the group (its first slice)
+      const bool writer = slice == 0 && (h == 0 || (h - 1) * a.KVH / a.H != kvh);
       if (writer) {
         const size_t woff = ((size_t)slot * a.C + pos) * a.kv + (size_t)kvh * hd + t;
         a.kc_w[woff] = kh;
@@ -555,7 +572,8 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   // P and sw from attn_pitch/attn_swz every 16 consecutive lanes of the
   // product writes (units of 4 positions x 8 elements) and of the sums' reads
   // (consecutive d) touch 16 distinct bank slots
-  const int sw = attn_swz(hd, a.kv);
+  const int sw = NS > 1 ? attn_sswz(HS) : attn_swz(hd, a.kv);
+  const int hs = NS > 1 ? HS : hd;  // output elements of this block (summing lanes)
   const float4 *pp = reinterpret_cast<const float4 *>(prod) + (t ^ ((t >> 4) & sw));
   float o = 0.0f;
   // sequential sum of the complete quads [qa, qe) of the tile into o
@@ -564,7 +582,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     int nr = qe - qa;
     if constexpr (HD > 0) {
       if (nr >= 8) {
-        o = attn_chain8<attn_pitch(HD, 0) * 16>(o, (uint32_t)(uintptr_t)pq, nr >> 3);
+        o = attn_chain8<(NS > 1 ? attn_spitch(HD / NS) : attn_pitch(HD, 0)) * 16>(o, (uint32_t)(uintptr_t)pq, nr >> 3);
         pq += (size_t)(nr & ~7) * P;
         nr &= 7;
       }
@@ -598,7 +616,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         if (pt >= 0) {
 #pragma unroll
           for (int u = 0; u < UPS; u++) {
-            const int qd = SQ * s + QPU * u + pt / CPR, cd = pt % CPR;
+            const int qd = SQ * s + QPU * u + pt / CPRV, cd = pt % CPRV;
             v4u *vu = vr[min(s, NSTG - 1) * UPS + u];
             if (s < nst && 4 * qd < cnt) {
               if (FUSED) {
@@ -608,7 +626,8 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
                   uint32_t w[4];
 #pragma unroll
                   for (int j = 0; j < 4; j++)
-                    w[j] = (uint32_t)f2h(vn[8 * cd + 2 * j]) | ((uint32_t)f2h(vn[8 * cd + 2 * j + 1]) << 16);
+                    w[j] = (uint32_t)f2h(vn[HS * slice + 8 * cd + 2 * j]) |
+                           ((uint32_t)f2h(vn[HS * slice + 8 * cd + 2 * j + 1]) << 16);
                   const v4u nv = {w[0], w[1], w[2], w[3]};
 #pragma unroll
                   for (int e = 0; e < 4; e++)
@@ -631,7 +650,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
                     make_float4(pr[k][0], pr[k][1], pr[k][2], pr[k][3]);
             }
           }
-        } else if (t < hd && s > 0) {
+        } else if (t < hs && s > 0) {
           sum_quads(SQ * (s - 1), min(SQ * s, nq));
           if (s == nst) sum_tail(nq, cnt);
         }
@@ -650,7 +669,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
       }
     }
   }
-  if (t < hd) a.out[(size_t)m * a.ldo + (size_t)h * hd + t] = o;
+  if (t < hs) a.out[(size_t)m * a.ldo + (size_t)h * hd + (size_t)hs * slice + t] = o;
 }
 
 // ---------------------------------------------------------------------------
@@ -894,9 +913,12 @@ static void launch_attn(AttnArgs a, size_t lds, hipStream_t st) {
   // grouped-query heads: one XCD per KV group (8 XCDs, block x -> XCD x % 8)
   const int r = a.H / a.KVH;
   a.xcd_r = (a.KVH <= 8 && a.H % a.KVH == 0 && r > 1) ? r : 0;
-  const dim3 grid(a.xcd_r ? 8 * r : a.H, a.M);
-  if (a.fuse_kv) klaunch((attn_kernel<HD, true>), grid, dim3(256), lds, st, a);
-  else klaunch((attn_kernel<HD, false>), grid, dim3(256), lds, st, a);
+  // head_dim 64: two blocks per head (element halves), which halves the
+  // products and sums on each block's critical path
+  constexpr int NS = HD == 64 ? 4 : 1;
+  const dim3 grid((a.xcd_r ? 8 * r : a.H) * NS, a.M);
+  if (a.fuse_kv) klaunch((attn_kernel<HD, true, NS>), grid, dim3(256), lds, st, a);
+  else klaunch((attn_kernel<HD, false, NS>), grid, dim3(256), lds, st, a);
 }
 
 hipError_t attention(const AttnArgs &a, hipStream_t st) {

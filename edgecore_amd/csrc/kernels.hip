@@ -327,15 +327,15 @@ constexpr int kAttnStages = 3;
 
 // 16-byte slots per quad of a slice's products (hs elements): 16 consecutive
 // lanes of the writes and of the sums' reads hit distinct bank slots
-__host__ __device__ constexpr inline int attn_spitch(int hs) { return hs == 16 ? 17 : attn_pitch(hs, 0); }
-__host__ __device__ constexpr inline int attn_sswz(int hs) { return hs == 16 ? 0 : attn_swz(hs, 0); }
+__host__ __device__ constexpr inline int attn_spitch(int hs) { return hs <= 16 ? hs + 1 : attn_pitch(hs, 0); }
+__host__ __device__ constexpr inline int attn_sswz(int hs) { return hs <= 16 ? 0 : attn_swz(hs, 0); }
 
 // NS: element slices per head, one block each (1, or 2 / 4 for head_dim 64):
 // every block of a head scores all positions, and forms the products and
 // sums of its slice's elements only
 template <int HD, bool FUSED, int NS>
 __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
-  static_assert(NS == 1 || (HD == 64 && (NS == 2 || NS == 4)), "element slices: head_dim 64, two or four");
+  static_assert(NS == 1 || (HD == 64 && (NS == 2 || NS == 4 || NS == 8)), "element slices: head_dim 64, 2 / 4 / 8");
   extern __shared__ __attribute__((aligned(16))) float lds[];
   __shared__ float redf[4];
   __shared__ double redd[4];
@@ -913,8 +913,10 @@ static void launch_attn(AttnArgs a, size_t lds, hipStream_t st) {
   // grouped-query heads: one XCD per KV group (8 XCDs, block x -> XCD x % 8)
   const int r = a.H / a.KVH;
   a.xcd_r = (a.KVH <= 8 && a.H % a.KVH == 0 && r > 1) ? r : 0;
-  // head_dim 64: two blocks per head (element halves), which halves the
-  // products and sums on each block's critical path
+  // head_dim 64: four blocks per head (16 elements each), a quarter of the
+  // products on each block's critical path.  With one XCD per KV group, the
+  // 7 heads x 4 slices of a Qwen2-0.5B group fit that XCD's 32 CUs at once;
+  // 8 slices took two rounds of blocks.
   constexpr int NS = HD == 64 ? 4 : 1;
   const dim3 grid((a.xcd_r ? 8 * r : a.H) * NS, a.M);
   if (a.fuse_kv) klaunch((attn_kernel<HD, true, NS>), grid, dim3(256), lds, st, a);

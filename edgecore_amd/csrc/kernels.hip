@@ -417,7 +417,12 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   constexpr int MAXQ = HD > 0 ? (256 * kAttnUnits * 4 / CPR < 512 ? 256 * kAttnUnits * 4 / CPR : 512) / 4 : 1;
   constexpr int UPS = (MAXQ + kAttnStages * QPU - 1) / (kAttnStages * QPU);
   constexpr int SQ = UPS * QPU;
-  constexpr int NSTG = (MAXQ + SQ - 1) / SQ;
+  // The first stage is shorter when one unit per thread covers a whole stage
+  // (element slices): its products are ready sooner and the sums start
+  // earlier; stage s >= 1 covers quads [Q0 + SQ*(s-1), Q0 + SQ*s).
+  constexpr int Q0 = (UPS == 1 && QPU >= 96) ? QPU / 3 : SQ;
+  constexpr int NSTG = 1 + (MAXQ - Q0 + SQ - 1) / SQ;
+  auto stage_lo = [](int s) { return s == 0 ? 0 : Q0 + SQ * (s - 1); };
   static_assert(HD == 0 || NPT % CPRV == 0, "product threads cover whole quads");
   const int pt = t - 64 * SWV;  // product thread index (negative in the summing waves)
   v4u kr[HD > 0 ? kAttnUnits : 1][4], vr[NSTG * UPS][4];
@@ -441,7 +446,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         for (int u = 0; u < UPS; u++) {
 #pragma unroll
           for (int e = 0; e < 4; e++) {
-            const int i = min(t0 + 4 * (SQ * s + QPU * u + qd0) + e, last);
+            const int i = min(t0 + 4 * (stage_lo(s) + QPU * u + qd0) + e, last);
             vr[s * UPS + u][e] = *reinterpret_cast<const v4u *>(V + (size_t)i * a.kv + 8 * (CPRV * slice + cd));
           }
         }
@@ -606,19 +611,20 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     __syncthreads();  // probabilities written / previous tile's sums done
     if constexpr (HD > 0) {
       // Stage s: the product threads form the products of their UPS units of
-      // stage s (quads [SQ*s, SQ*(s+1))) while the summing lanes add the
-      // quads of stage s - 1; a barrier separates the stages.
+      // stage s (quads [stage_lo(s), stage_lo(s+1))) while the summing lanes
+      // add the quads of stage s - 1; a barrier separates the stages.
       if (t0) load_v(t0);
-      const int nst = ((cnt + 3) / 4 + SQ - 1) / SQ;  // stages holding positions
+      const int nqt = (cnt + 3) / 4;  // quads holding positions
+      const int nst = nqt <= Q0 ? 1 : 1 + (nqt - Q0 + SQ - 1) / SQ;  // stages holding positions
 #pragma unroll
       for (int s = 0; s <= NSTG; s++) {
         if (s > nst) continue;  // uniform
         if (pt >= 0) {
 #pragma unroll
           for (int u = 0; u < UPS; u++) {
-            const int qd = SQ * s + QPU * u + pt / CPRV, cd = pt % CPRV;
+            const int qd = stage_lo(s) + QPU * u + pt / CPRV, cd = pt % CPRV;
             v4u *vu = vr[min(s, NSTG - 1) * UPS + u];
-            if (s < nst && 4 * qd < cnt) {
+            if (s < nst && 4 * qd < cnt && qd < stage_lo(s + 1)) {
               if (FUSED) {
                 // the token's own position takes the fp16-rounded new v (one lane)
                 const int en = n - 1 - t0 - 4 * qd;
@@ -651,7 +657,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
             }
           }
         } else if (t < hs && s > 0) {
-          sum_quads(SQ * (s - 1), min(SQ * s, nq));
+          sum_quads(stage_lo(s - 1), min(stage_lo(s), nq));
           if (s == nst) sum_tail(nq, cnt);
         }
         if (s < nst) __syncthreads();

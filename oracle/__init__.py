@@ -52,6 +52,7 @@ def olib() -> C.CDLL:
             "or_precision": (_I, [_P]),
             "or_arch": (_I, [_P]),
             "or_forward": (_I, [_P, _P, _P, _P, _I, _P]),
+            "or_forward_from": (_I, [_P, _P, _P, _P, _I, _I, _P]),
             "or_argmax": (_I, [_P, _I]),
             "or_generate": (_I, [_P, _P, _I, _I, _P, _P]),
             "or_map": (None, [_I, _P, _P, C.c_size_t]),
@@ -222,12 +223,13 @@ class OracleModel:
     def kv_reset(self):
         olib().or_kv_reset(self.h)
 
-    def forward(self, tokens, positions, seqs=None) -> np.ndarray:
+    def forward(self, tokens, positions, seqs=None, lm_from: int = 0) -> np.ndarray:
+        """Logits of rows [lm_from, M) (the LM head skips the rows before)."""
         t = np.ascontiguousarray(tokens, np.int32)
         p = np.ascontiguousarray(positions, np.int32)
         s = None if seqs is None else np.ascontiguousarray(seqs, np.int32)
-        out = np.empty((len(t), self.vocab), np.float32)
-        rc = olib().or_forward(self.h, _p(t), _p(p), _p(s), len(t), _p(out))
+        out = np.empty((len(t) - lm_from, self.vocab), np.float32)
+        rc = olib().or_forward_from(self.h, _p(t), _p(p), _p(s), len(t), lm_from, _p(out))
         if rc:
             raise RuntimeError("oracle forward rejected its inputs")
         return out

@@ -925,6 +925,16 @@ int or_forward(OrModel *g, const int *tokens, const int *positions, const int *s
     return or_forward_rows(g, tokens, positions, seqs, M, logits, 0);
 }
 
+/* or_forward with the LM head only for rows [lm_from, M): logits gets
+ * [M - lm_from][V] (may be NULL when lm_from == M); every other result, the
+ * KV cache included, is the same (gpt2_forward_ex's lm_from) */
+int or_forward_from(OrModel *g, const int *tokens, const int *positions, const int *seqs,
+                    int M, int lm_from, float *logits)
+{
+    if (lm_from < 0 || lm_from > M) return -1;
+    return or_forward_rows(g, tokens, positions, seqs, M, logits, lm_from);
+}
+
 int or_argmax(const float *logits, int vocab)
 {
     int best = 0;

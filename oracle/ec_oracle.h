@@ -81,6 +81,10 @@ int      or_forward(OrModel *m, const int *tokens, const int *positions,
 int or_attention_rows(const float *q, int ldq, const uint16_t *kc, const uint16_t *vc, int nslots, int C,
                       int H, int KVH, int hd, const int *pos, const int *slot, const int *rows, int nrows,
                       int window, float *out, int ldo);
+/* or_forward with the LM head only for rows [lm_from, M) into logits
+ * [M - lm_from][V]; the rest (KV cache included) unchanged.  0 or -1. */
+int      or_forward_from(OrModel *m, const int *tokens, const int *positions,
+                         const int *seqs, int M, int lm_from, float *logits);
 /* greedy argmax, first maximum wins (src/runtime_main.c:213-219) */
 int      or_argmax(const float *logits, int vocab);
 /* gen_and_measure at batch 1, temp 0 (src/runtime_main.c:293-362): prefill

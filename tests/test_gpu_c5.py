@@ -1,0 +1,55 @@
+"""Qwen2.5-1.5B shape (E1536, 12 query / 2 KV heads of head_dim 128, SwiGLU
+FFN 8960, RMSNorm, RoPE theta 1e6, tied vocabulary 151936, int8 per-channel
+weights N(0, 0.02)) at 2 of its 28 layers, in the batched-decode regime of
+that configuration: 16 slots, each prompt prefilled on its own slot (as
+src/runtime_main.c:325-330 does), then greedy decode steps at M=16 with one
+token per slot (the M=16 matrix-core GEMM, the head_dim-128 attention
+kernels).  Every step's logits must be within max-abs 2e-2 of the oracle's and
+the greedy tokens identical.  The layer count is cut so that the CPU oracle
+finishes in seconds; every per-layer shape is the real one."""
+import numpy as np
+import pytest
+
+import edgecore_amd as ec
+import oracle
+from tests.conftest import prompt_ids
+
+pytestmark = [pytest.mark.gpu, pytest.mark.slow]
+
+B, PROMPT, STEPS, V = 16, 40, 12, 151936
+
+
+@pytest.fixture(scope="module")
+def c5_model(model_dir):
+    path = model_dir / "qwen2.5-1.5b-2l-int8.ecm"
+    if not path.exists():
+        ec.synth(path, name="qwen2.5-1.5b-2l", arch="qwen2", layers=2, embd=1536, heads=12, kv_heads=2,
+                 ffn=8960, ctx=4096, vocab=V, precision="int8", tie=1)
+    return path
+
+
+def test_qwen25_15b_shape_batched_decode(c5_model):
+    ctx = PROMPT + STEPS + 8
+    with ec.Model(c5_model, B, ctx) as m:
+        om = oracle.OracleModel(c5_model, B, ctx)
+        m.kv_reset()
+        om.kv_reset()
+        prompts = [prompt_ids(PROMPT, V, seed=20 + b) for b in range(B)]
+        for b, p in enumerate(prompts):
+            n = len(p)
+            m.forward(p, np.arange(n), np.full(n, b, np.int32), lm_from=n, want_logits=False)
+            om.forward(p, np.arange(n), np.full(n, b, np.int32), lm_from=n)
+        cur = [int(p[-1]) for p in prompts]
+        pos = [PROMPT] * B
+        worst = 0.0
+        for _ in range(STEPS):
+            got, am = m.forward(cur, pos, None, want_logits=True, want_argmax=True)
+            want = om.forward(cur, pos, None)
+            err = float(np.abs(got - want).max())
+            worst = max(worst, err)
+            assert err <= 2e-2, err
+            assert list(am) == [int(r.argmax()) for r in want]
+            cur = [int(x) for x in am]
+            pos = [p + 1 for p in pos]
+        om.close()
+    print(f"C5-shape max-abs logits diff over {STEPS} steps of 16 tokens: {worst:.3e}")

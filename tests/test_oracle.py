@@ -250,6 +250,21 @@ def test_attention_rows_closed_forms():
     assert np.isnan(part[0]).all() and np.isfinite(part[1]).all()
 
 
+def test_forward_from_equals_full_rows(make_model):
+    """or_forward_from (LM head from row lm_from on) = the full forward's rows,
+    and leaves the same KV cache (the next step's logits agree)."""
+    path = make_model("tiny-qwen2-int8")
+    a, b = oracle.OracleModel(path, 1, 32), oracle.OracleModel(path, 1, 32)
+    toks = [3, 14, 15, 92, 65, 35]
+    full = a.forward(toks, np.arange(6), np.zeros(6, np.int32))
+    part = b.forward(toks, np.arange(6), np.zeros(6, np.int32), lm_from=4)
+    assert np.array_equal(full[4:], part)
+    assert b.forward(toks, np.arange(6), np.zeros(6, np.int32), lm_from=6).shape == (0, a.vocab)
+    assert np.array_equal(a.forward([7], [6], [0]), b.forward([7], [6], [0]))
+    a.close()
+    b.close()
+
+
 def test_elementwise_map_matches_scalars():
     x = np.array([-3.0, -0.5, 0.0, 0.75, 5.0], np.float32)
     L = oracle.olib()

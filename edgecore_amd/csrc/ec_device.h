@@ -270,6 +270,27 @@ __device__ __forceinline__ double block_sum256_1b(double v, double *red) {
   __syncthreads();
   return (red[0] + red[1]) + (red[2] + red[3]);
 }
+// the same over NW waves (4 or 8), in a fixed pairwise order
+template <int NW>
+__device__ __forceinline__ double block_sum_1b(double v, double *red) {
+  static_assert(NW == 4 || NW == 8, "4 or 8 waves");
+  v = wave_sum_dpp(v);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  const double s4 = (red[0] + red[1]) + (red[2] + red[3]);
+  if constexpr (NW == 4) return s4;
+  else return s4 + ((red[4] + red[5]) + (red[6] + red[7]));
+}
+template <int NW>
+__device__ __forceinline__ float block_max_1b(float v, float *red) {
+  static_assert(NW == 4 || NW == 8, "4 or 8 waves");
+  v = wave_max_dpp(v);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  const float m4 = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  if constexpr (NW == 4) return m4;
+  else return fmaxf(m4, fmaxf(fmaxf(red[4], red[5]), fmaxf(red[6], red[7])));
+}
 __device__ __forceinline__ float block_max256_1b(float v, float *red) {
   v = wave_max_dpp(v);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;

@@ -334,11 +334,15 @@ __host__ __device__ constexpr inline int attn_sswz(int hs) { return hs <= 16 ? 0
 // every block of a head scores all positions, and forms the products and
 // sums of its slice's elements only
 template <int HD, bool FUSED, int NS>
-__global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
+__global__ __launch_bounds__(NS > 1 ? 512 : 256) void attn_kernel(AttnArgs a) {
   static_assert(NS == 1 || (HD == 64 && (NS == 2 || NS == 4 || NS == 8)), "element slices: head_dim 64, 2 / 4 / 8");
   extern __shared__ __attribute__((aligned(16))) float lds[];
-  __shared__ float redf[4];
-  __shared__ double redd[4];
+  // threads per block: 512 with element slices (one scored position per
+  // thread up to 512 positions), else 256
+  constexpr int NT = NS > 1 ? 512 : 256;
+  constexpr int KU = NT == 512 ? kAttnUnits / 2 : kAttnUnits;  // K units per thread
+  __shared__ float redf[NT / 64];
+  __shared__ double redd[NT / 64];
   __shared__ uint64_t etab[32];  // expf table
   constexpr int CPR = HD > 0 ? HD / 8 : 1;         // 16-byte chunks per K/V row
   constexpr int HS = HD > 0 ? HD / NS : 0;  // elements of this block's slice
@@ -402,8 +406,8 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   }
 
   // ---- 2. K rows of the first KQ positions ----
-  // unit = 4 positions x 8 elements (16 bytes each); kAttnUnits per thread
-  constexpr int KQMAX = HD > 0 ? 256 * kAttnUnits * 4 / CPR : 0;  // K positions staged
+  // unit = 4 positions x 8 elements (16 bytes each); KU per thread
+  constexpr int KQMAX = HD > 0 ? NT * KU * 4 / CPR : 0;  // K positions staged
   constexpr int KP = CPR + 1;  // K tile row pitch in 16-byte chunks (odd: rows spread over the banks)
   // the K tile lives in the product area (T/4 * P slots of 16 bytes)
   const int KQ = min(KQMAX, (T / 4) * PA / KP);
@@ -412,9 +416,9 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   // 8 elements: QPU quads per unit index across the product threads, UPS units
   // per thread and stage of SQ quads, NSTG stages for the largest tile
   constexpr int SWV = HD > 64 ? HD / 64 : 1;
-  constexpr int NPT = 256 - 64 * SWV;
+  constexpr int NPT = NT - 64 * SWV;
   constexpr int QPU = HD > 0 ? NPT / CPRV : 1;
-  constexpr int MAXQ = HD > 0 ? (256 * kAttnUnits * 4 / CPR < 512 ? 256 * kAttnUnits * 4 / CPR : 512) / 4 : 1;
+  constexpr int MAXQ = HD > 0 ? (KQMAX < 512 ? KQMAX : 512) / 4 : 1;
   constexpr int UPS = (MAXQ + kAttnStages * QPU - 1) / (kAttnStages * QPU);
   constexpr int SQ = UPS * QPU;
   // The first stage is shorter when one unit per thread covers a whole stage
@@ -425,11 +429,11 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   auto stage_lo = [](int s) { return s == 0 ? 0 : Q0 + SQ * (s - 1); };
   static_assert(HD == 0 || NPT % CPRV == 0, "product threads cover whole quads");
   const int pt = t - 64 * SWV;  // product thread index (negative in the summing waves)
-  v4u kr[HD > 0 ? kAttnUnits : 1][4], vr[NSTG * UPS][4];
+  v4u kr[HD > 0 ? KU : 1][4], vr[NSTG * UPS][4];
   if constexpr (HD > 0) {
 #pragma unroll
-    for (int u = 0; u < kAttnUnits; u++) {
-      const int unit = t + 256 * u, qd = unit / CPR, cd = unit - qd * CPR;
+    for (int u = 0; u < KU; u++) {
+      const int unit = t + NT * u, qd = unit / CPR, cd = unit - qd * CPR;
 #pragma unroll
       for (int e = 0; e < 4; e++) {
         const int i = min(4 * qd + e, last);
@@ -494,8 +498,8 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   v4u *ktile = reinterpret_cast<v4u *>(prod);
   if constexpr (HD > 0) {
 #pragma unroll
-    for (int u = 0; u < kAttnUnits; u++) {
-      const int unit = t + 256 * u, qd = unit / CPR, cd = unit - qd * CPR;
+    for (int u = 0; u < KU; u++) {
+      const int unit = t + NT * u, qd = unit / CPR, cd = unit - qd * CPR;
 #pragma unroll
       for (int e = 0; e < 4; e++) {
         const int i = 4 * qd + e;
@@ -517,7 +521,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   };
   if constexpr (HD > 0) {
     // R positions per thread, their sequential dots interleaved
-    constexpr int R = KQMAX / 256;
+    constexpr int R = KQMAX / NT;
     float s[R];
 #pragma unroll
     for (int r = 0; r < R; r++) s[r] = 0.0f;
@@ -525,7 +529,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     for (int c = 0; c < CPR; c++) {
       v4u kk[R];
 #pragma unroll
-      for (int r = 0; r < R; r++) kk[r] = ktile[min(t + 256 * r, KQ - 1) * KP + c];
+      for (int r = 0; r < R; r++) kk[r] = ktile[min(t + NT * r, KQ - 1) * KP + c];
       float qv[8];
 #pragma unroll
       for (int j = 0; j < 8; j++) qv[j] = qs[8 * c + j];
@@ -535,42 +539,42 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     }
 #pragma unroll
     for (int r = 0; r < R; r++) {
-      const int i = t + 256 * r;
+      const int i = t + NT * r;
       if (i < n && i < KQ) put(i, s[r]);
     }
   }
   // positions past the K tile (long contexts) and the generic path
-  for (int i = t; i < n; i += 256) {
+  for (int i = t; i < n; i += NT) {
     if (HD > 0 && i < KQ) continue;  // scored from the K tile above
     put(i, (FUSED && i == n - 1) ? dot_new_k<HD>(qs, kn, hd) : dot_k_row<HD>(qs, K + (size_t)i * a.kv, hd));
   }
-  mx = block_max256_1b(mx, redf);
+  mx = block_max_1b<NT / 64>(mx, redf);
   // this thread's first two values stay in registers until the sum is known
   // (positions below 512); further ones go through LDS
   double sum = 0.0;
   float ev[2];
 #pragma unroll
   for (int k = 0; k < 2; k++) {
-    const int i = t + 256 * k;
+    const int i = t + NT * k;
     ev[k] = 0.0f;
     if (i < n) {
       ev[k] = ec_expf_tab(sc[i] - mx, etab);
       sum += (double)ev[k];
     }
   }
-  for (int i = t + 512; i < n; i += 256) {
+  for (int i = t + 2 * NT; i < n; i += NT) {
     const float e = ec_expf_tab(sc[i] - mx, etab);
     sc[i] = e;
     sum += (double)e;
   }
-  sum = block_sum256_1b(sum, redd);
+  sum = block_sum_1b<NT / 64>(sum, redd);
   const double isum = 1.0 / sum;
 #pragma unroll
   for (int k = 0; k < 2; k++) {
-    const int i = t + 256 * k;
+    const int i = t + NT * k;
     if (i < n) sc[i] = (float)((double)ev[k] * isum);
   }
-  for (int i = t + 512; i < n; i += 256) sc[i] = (float)((double)sc[i] * isum);
+  for (int i = t + 2 * NT; i < n; i += NT) sc[i] = (float)((double)sc[i] * isum);
 
   // ---- 5. products p*v, and the sequential sums ----
   // element d of quad q sits in 16-byte slot q*P + (d ^ ((d >> 4) & sw)); with
@@ -663,7 +667,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         if (s < nst) __syncthreads();
       }
     } else {
-      for (int e = t; e < cnt * hd; e += 256) {
+      for (int e = t; e < cnt * hd; e += NT) {
         const int i = e / hd, d = e - i * hd;
         const float v = (FUSED && t0 + i == n - 1) ? vn[d] : h2f(V[(size_t)(t0 + i) * a.kv + d]);
         prod[((size_t)(i >> 2) * P + (d ^ ((d >> 4) & sw))) * 4 + (i & 3)] = sc[t0 + i] * v;
@@ -925,8 +929,9 @@ static void launch_attn(AttnArgs a, size_t lds, hipStream_t st) {
   // 8 slices took two rounds of blocks.
   constexpr int NS = HD == 64 ? 4 : 1;
   const dim3 grid((a.xcd_r ? 8 * r : a.H) * NS, a.M);
-  if (a.fuse_kv) klaunch((attn_kernel<HD, true, NS>), grid, dim3(256), lds, st, a);
-  else klaunch((attn_kernel<HD, false, NS>), grid, dim3(256), lds, st, a);
+  const dim3 block(NS > 1 ? 512 : 256);
+  if (a.fuse_kv) klaunch((attn_kernel<HD, true, NS>), grid, block, lds, st, a);
+  else klaunch((attn_kernel<HD, false, NS>), grid, block, lds, st, a);
 }
 
 hipError_t attention(const AttnArgs &a, hipStream_t st) {

@@ -421,10 +421,10 @@ __global__ __launch_bounds__(NS > 1 ? 512 : 256) void attn_kernel(AttnArgs a) {
   constexpr int MAXQ = HD > 0 ? (KQMAX < 512 ? KQMAX : 512) / 4 : 1;
   constexpr int UPS = (MAXQ + kAttnStages * QPU - 1) / (kAttnStages * QPU);
   constexpr int SQ = UPS * QPU;
-  // The first stage is shorter when one unit per thread covers a whole stage
-  // (element slices): its products are ready sooner and the sums start
-  // earlier; stage s >= 1 covers quads [Q0 + SQ*(s-1), Q0 + SQ*s).
-  constexpr int Q0 = (UPS == 1 && QPU >= 96) ? QPU / 3 : SQ;
+  // The first stage is shorter (32 quads) when one unit per thread covers a
+  // whole stage (element slices): its products are ready sooner and the sums
+  // start earlier; stage s >= 1 covers quads [Q0 + SQ*(s-1), Q0 + SQ*s).
+  constexpr int Q0 = (UPS == 1 && QPU >= 96) ? 32 : SQ;
   constexpr int NSTG = 1 + (MAXQ - Q0 + SQ - 1) / SQ;
   auto stage_lo = [](int s) { return s == 0 ? 0 : Q0 + SQ * (s - 1); };
   static_assert(HD == 0 || NPT % CPRV == 0, "product threads cover whole quads");

@@ -269,6 +269,162 @@ __device__ __forceinline__ float attn_chain8(float o, uint32_t a, int n8) {
   return o;
 }
 
+// As attn_chain8, 16 quads per iteration (n16 >= 1) in four register sets:
+// the reads of the next 12 quads are in flight while the current four quads
+// are added, one wait per four quads.  Reads 16 quads past the end (values
+// unused).
+template <int STRIDE>
+__device__ __forceinline__ float attn_chain16(float o, uint32_t a, int n16) {
+  static_assert(31 * STRIDE <= 65535, "ds_read offsets are 16-bit");
+  asm volatile(
+      "ds_read_b128 v[192:195], %[a] offset:%[q0]\n"
+      "ds_read_b128 v[196:199], %[a] offset:%[q1]\n"
+      "ds_read_b128 v[200:203], %[a] offset:%[q2]\n"
+      "ds_read_b128 v[204:207], %[a] offset:%[q3]\n"
+      "ds_read_b128 v[208:211], %[a] offset:%[q4]\n"
+      "ds_read_b128 v[212:215], %[a] offset:%[q5]\n"
+      "ds_read_b128 v[216:219], %[a] offset:%[q6]\n"
+      "ds_read_b128 v[220:223], %[a] offset:%[q7]\n"
+      "ds_read_b128 v[224:227], %[a] offset:%[q8]\n"
+      "ds_read_b128 v[228:231], %[a] offset:%[q9]\n"
+      "ds_read_b128 v[232:235], %[a] offset:%[q10]\n"
+      "ds_read_b128 v[236:239], %[a] offset:%[q11]\n"
+      "ds_read_b128 v[240:243], %[a] offset:%[q12]\n"
+      "ds_read_b128 v[244:247], %[a] offset:%[q13]\n"
+      "ds_read_b128 v[248:251], %[a] offset:%[q14]\n"
+      "ds_read_b128 v[252:255], %[a] offset:%[q15]\n"
+      "L_attn_chain16_%=:\n"
+      "s_waitcnt lgkmcnt(12)\n"
+      "v_add_f32 %[o], %[o], v192\n"
+      "v_add_f32 %[o], %[o], v193\n"
+      "v_add_f32 %[o], %[o], v194\n"
+      "v_add_f32 %[o], %[o], v195\n"
+      "v_add_f32 %[o], %[o], v196\n"
+      "v_add_f32 %[o], %[o], v197\n"
+      "v_add_f32 %[o], %[o], v198\n"
+      "v_add_f32 %[o], %[o], v199\n"
+      "v_add_f32 %[o], %[o], v200\n"
+      "v_add_f32 %[o], %[o], v201\n"
+      "v_add_f32 %[o], %[o], v202\n"
+      "v_add_f32 %[o], %[o], v203\n"
+      "v_add_f32 %[o], %[o], v204\n"
+      "v_add_f32 %[o], %[o], v205\n"
+      "v_add_f32 %[o], %[o], v206\n"
+      "v_add_f32 %[o], %[o], v207\n"
+      "ds_read_b128 v[192:195], %[a] offset:%[q16]\n"
+      "ds_read_b128 v[196:199], %[a] offset:%[q17]\n"
+      "ds_read_b128 v[200:203], %[a] offset:%[q18]\n"
+      "ds_read_b128 v[204:207], %[a] offset:%[q19]\n"
+      "s_waitcnt lgkmcnt(12)\n"
+      "v_add_f32 %[o], %[o], v208\n"
+      "v_add_f32 %[o], %[o], v209\n"
+      "v_add_f32 %[o], %[o], v210\n"
+      "v_add_f32 %[o], %[o], v211\n"
+      "v_add_f32 %[o], %[o], v212\n"
+      "v_add_f32 %[o], %[o], v213\n"
+      "v_add_f32 %[o], %[o], v214\n"
+      "v_add_f32 %[o], %[o], v215\n"
+      "v_add_f32 %[o], %[o], v216\n"
+      "v_add_f32 %[o], %[o], v217\n"
+      "v_add_f32 %[o], %[o], v218\n"
+      "v_add_f32 %[o], %[o], v219\n"
+      "v_add_f32 %[o], %[o], v220\n"
+      "v_add_f32 %[o], %[o], v221\n"
+      "v_add_f32 %[o], %[o], v222\n"
+      "v_add_f32 %[o], %[o], v223\n"
+      "ds_read_b128 v[208:211], %[a] offset:%[q20]\n"
+      "ds_read_b128 v[212:215], %[a] offset:%[q21]\n"
+      "ds_read_b128 v[216:219], %[a] offset:%[q22]\n"
+      "ds_read_b128 v[220:223], %[a] offset:%[q23]\n"
+      "s_waitcnt lgkmcnt(12)\n"
+      "v_add_f32 %[o], %[o], v224\n"
+      "v_add_f32 %[o], %[o], v225\n"
+      "v_add_f32 %[o], %[o], v226\n"
+      "v_add_f32 %[o], %[o], v227\n"
+      "v_add_f32 %[o], %[o], v228\n"
+      "v_add_f32 %[o], %[o], v229\n"
+      "v_add_f32 %[o], %[o], v230\n"
+      "v_add_f32 %[o], %[o], v231\n"
+      "v_add_f32 %[o], %[o], v232\n"
+      "v_add_f32 %[o], %[o], v233\n"
+      "v_add_f32 %[o], %[o], v234\n"
+      "v_add_f32 %[o], %[o], v235\n"
+      "v_add_f32 %[o], %[o], v236\n"
+      "v_add_f32 %[o], %[o], v237\n"
+      "v_add_f32 %[o], %[o], v238\n"
+      "v_add_f32 %[o], %[o], v239\n"
+      "ds_read_b128 v[224:227], %[a] offset:%[q24]\n"
+      "ds_read_b128 v[228:231], %[a] offset:%[q25]\n"
+      "ds_read_b128 v[232:235], %[a] offset:%[q26]\n"
+      "ds_read_b128 v[236:239], %[a] offset:%[q27]\n"
+      "s_waitcnt lgkmcnt(12)\n"
+      "v_add_f32 %[o], %[o], v240\n"
+      "v_add_f32 %[o], %[o], v241\n"
+      "v_add_f32 %[o], %[o], v242\n"
+      "v_add_f32 %[o], %[o], v243\n"
+      "v_add_f32 %[o], %[o], v244\n"
+      "v_add_f32 %[o], %[o], v245\n"
+      "v_add_f32 %[o], %[o], v246\n"
+      "v_add_f32 %[o], %[o], v247\n"
+      "v_add_f32 %[o], %[o], v248\n"
+      "v_add_f32 %[o], %[o], v249\n"
+      "v_add_f32 %[o], %[o], v250\n"
+      "v_add_f32 %[o], %[o], v251\n"
+      "v_add_f32 %[o], %[o], v252\n"
+      "v_add_f32 %[o], %[o], v253\n"
+      "v_add_f32 %[o], %[o], v254\n"
+      "v_add_f32 %[o], %[o], v255\n"
+      "ds_read_b128 v[240:243], %[a] offset:%[q28]\n"
+      "ds_read_b128 v[244:247], %[a] offset:%[q29]\n"
+      "ds_read_b128 v[248:251], %[a] offset:%[q30]\n"
+      "ds_read_b128 v[252:255], %[a] offset:%[q31]\n"
+      "v_add_u32 %[a], %[inc], %[a]\n"
+      "s_sub_u32 %[n], %[n], 1\n"
+      "s_cmp_lg_u32 %[n], 0\n"
+      "s_cbranch_scc1 L_attn_chain16_%=\n"
+      "s_waitcnt lgkmcnt(0)\n"
+      : [o] "+v"(o), [a] "+v"(a), [n] "+s"(n16)
+      : [inc] "v"(16 * STRIDE), [q0] "i"(0 * STRIDE), [q1] "i"(1 * STRIDE), [q2] "i"(2 * STRIDE), [q3] "i"(3 * STRIDE), [q4] "i"(4 * STRIDE), [q5] "i"(5 * STRIDE), [q6] "i"(6 * STRIDE), [q7] "i"(7 * STRIDE), [q8] "i"(8 * STRIDE), [q9] "i"(9 * STRIDE), [q10] "i"(10 * STRIDE), [q11] "i"(11 * STRIDE), [q12] "i"(12 * STRIDE), [q13] "i"(13 * STRIDE), [q14] "i"(14 * STRIDE), [q15] "i"(15 * STRIDE), [q16] "i"(16 * STRIDE), [q17] "i"(17 * STRIDE), [q18] "i"(18 * STRIDE), [q19] "i"(19 * STRIDE), [q20] "i"(20 * STRIDE), [q21] "i"(21 * STRIDE), [q22] "i"(22 * STRIDE), [q23] "i"(23 * STRIDE), [q24] "i"(24 * STRIDE), [q25] "i"(25 * STRIDE), [q26] "i"(26 * STRIDE), [q27] "i"(27 * STRIDE), [q28] "i"(28 * STRIDE), [q29] "i"(29 * STRIDE), [q30] "i"(30 * STRIDE), [q31] "i"(31 * STRIDE)
+      : "v192", "v193", "v194", "v195", "v196", "v197", "v198", "v199", "v200", "v201", "v202", "v203", "v204", "v205", "v206", "v207", "v208", "v209", "v210", "v211", "v212", "v213", "v214", "v215", "v216", "v217", "v218", "v219", "v220", "v221", "v222", "v223", "v224", "v225", "v226", "v227", "v228", "v229", "v230", "v231", "v232", "v233", "v234", "v235", "v236", "v237", "v238", "v239", "v240", "v241", "v242", "v243", "v244", "v245", "v246", "v247", "v248", "v249", "v250", "v251", "v252", "v253", "v254", "v255", "scc", "memory");
+  return o;
+}
+
+// o += the four floats of each of the 4 quads at LDS byte address a + j*STRIDE,
+// in order; the four reads are issued together (no read past the last quad)
+template <int STRIDE>
+__device__ __forceinline__ float attn_sum4(float o, uint32_t a) {
+  asm volatile(
+      "ds_read_b128 v[240:243], %[a]\n"
+      "ds_read_b128 v[244:247], %[a] offset:%[q1]\n"
+      "ds_read_b128 v[248:251], %[a] offset:%[q2]\n"
+      "ds_read_b128 v[252:255], %[a] offset:%[q3]\n"
+      "s_waitcnt lgkmcnt(3)\n"
+      "v_add_f32 %[o], %[o], v240\n"
+      "v_add_f32 %[o], %[o], v241\n"
+      "v_add_f32 %[o], %[o], v242\n"
+      "v_add_f32 %[o], %[o], v243\n"
+      "s_waitcnt lgkmcnt(2)\n"
+      "v_add_f32 %[o], %[o], v244\n"
+      "v_add_f32 %[o], %[o], v245\n"
+      "v_add_f32 %[o], %[o], v246\n"
+      "v_add_f32 %[o], %[o], v247\n"
+      "s_waitcnt lgkmcnt(1)\n"
+      "v_add_f32 %[o], %[o], v248\n"
+      "v_add_f32 %[o], %[o], v249\n"
+      "v_add_f32 %[o], %[o], v250\n"
+      "v_add_f32 %[o], %[o], v251\n"
+      "s_waitcnt lgkmcnt(0)\n"
+      "v_add_f32 %[o], %[o], v252\n"
+      "v_add_f32 %[o], %[o], v253\n"
+      "v_add_f32 %[o], %[o], v254\n"
+      "v_add_f32 %[o], %[o], v255\n"
+      : [o] "+v"(o)
+      : [a] "v"(a), [q1] "i"(STRIDE), [q2] "i"(2 * STRIDE), [q3] "i"(3 * STRIDE)
+      : "v240", "v241", "v242", "v243", "v244", "v245", "v246", "v247", "v248", "v249", "v250", "v251", "v252",
+        "v253", "v254", "v255", "memory");
+  return o;
+}
+
 template <int HD>
 __device__ __forceinline__ float dot_k_row(const float *qs, const uint16_t *kp, int hd) {
   float s = 0.0f;
@@ -589,11 +745,25 @@ __global__ __launch_bounds__(NS > 1 ? 512 : 256) void attn_kernel(AttnArgs a) {
   auto sum_quads = [&](int qa, int qe) {
     const float4 *pq = pp + (size_t)qa * P;
     int nr = qe - qa;
+    constexpr int STR = (NS > 1 ? attn_spitch(HD / NS) : attn_pitch(HD, 0)) * 16;  // bytes per quad
+    if constexpr (HD > 0 && NS > 1) {
+      // slices: the product area has room for 16 quads of look-ahead
+      if (nr >= 16) {
+        o = attn_chain16<STR>(o, (uint32_t)(uintptr_t)pq, nr >> 4);
+        pq += (size_t)(nr & ~15) * P;
+        nr &= 15;
+      }
+    }
     if constexpr (HD > 0) {
       if (nr >= 8) {
-        o = attn_chain8<(NS > 1 ? attn_spitch(HD / NS) : attn_pitch(HD, 0)) * 16>(o, (uint32_t)(uintptr_t)pq, nr >> 3);
+        o = attn_chain8<STR>(o, (uint32_t)(uintptr_t)pq, nr >> 3);
         pq += (size_t)(nr & ~7) * P;
         nr &= 7;
+      }
+      if (nr >= 4) {
+        o = attn_sum4<STR>(o, (uint32_t)(uintptr_t)pq);
+        pq += (size_t)4 * P;
+        nr -= 4;
       }
     }
     for (; nr > 0; nr--, pq += P) {

@@ -507,9 +507,11 @@ __global__ __launch_bounds__(NS > 1 ? 512 : 256) void attn_kernel(AttnArgs a) {
   int h = blockIdx.x, slice = 0;
   if (a.xcd_r) {
     // XCD-aware launch: blocks are dispatched to the 8 XCDs round-robin, so
-    // block x runs on XCD x % 8; group g's heads (and their slices) use
-    // blocks g, g + 8, ... and share that XCD's L2 for the group's K/V rows
-    const int g = blockIdx.x & 7, j = blockIdx.x >> 3;
+    // block x runs on XCD x % 8 (gridDim.x is a multiple of 8); token m's
+    // group g uses the blocks on XCD (m * KVH + g) % 8, x = that XCD + 8j, and
+    // its heads (and their slices) share that XCD's L2 for the group's K/V
+    // rows.  The tokens of a batch (their own slots' K/V) go to other XCDs.
+    const int g = ((int)(blockIdx.x & 7) - m * a.KVH) & 7, j = blockIdx.x >> 3;
     if (g >= a.KVH || j >= a.xcd_r * NS) return;
     h = g * a.xcd_r + j / NS;
     slice = j % NS;

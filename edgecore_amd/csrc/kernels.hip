@@ -665,6 +665,22 @@ __global__ __launch_bounds__(NS > 1 ? 512 : 256) void attn_kernel(AttnArgs a) {
       }
     }
   }
+  // Long contexts: the K rows of positions [k0, k0 + KQ) into kr (the next
+  // K tile), loaded while the current tile is scored
+  auto load_k = [&](int k0) {
+    if constexpr (HD > 0) {
+#pragma unroll
+      for (int u = 0; u < KU; u++) {
+        const int unit = t + NT * u, qd = unit / CPR, cd = unit - qd * CPR;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const int i = min(k0 + 4 * qd + e, last);
+          kr[u][e] = *reinterpret_cast<const v4u *>(K + (size_t)i * a.kv + 8 * cd);
+        }
+      }
+    }
+  };
+  if (HD > 0 && n > KQ) load_k(KQ);
   // the product threads' V loads go out after the K rows are written, so no
   // wait before this point counts them; scores and softmax cover their latency
   load_v(0);
@@ -677,34 +693,57 @@ __global__ __launch_bounds__(NS > 1 ? 512 : 256) void attn_kernel(AttnArgs a) {
     sc[i] = s;
     mx = fmaxf(mx, s);
   };
+  // the positions k0 + t + NT*r of the K tile (rows t + NT*r)
+  auto score_tile = [&](int k0) {
+    if constexpr (HD > 0) {
+      // R positions per thread, their sequential dots interleaved
+      constexpr int R = KQMAX / NT;
+      float s[R];
+#pragma unroll
+      for (int r = 0; r < R; r++) s[r] = 0.0f;
+#pragma unroll
+      for (int c = 0; c < CPR; c++) {
+        v4u kk[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) kk[r] = ktile[min(t + NT * r, KQ - 1) * KP + c];
+        float qv[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) qv[j] = qs[8 * c + j];
+#pragma unroll
+        for (int r = 0; r + 1 < R; r += 2) mac8x2(s[r], s[r + 1], qv, kk[r], kk[r + 1]);
+        if constexpr (R & 1) mac8(s[R - 1], qv, kk[R - 1]);
+      }
+#pragma unroll
+      for (int r = 0; r < R; r++) {
+        const int i = k0 + t + NT * r;
+        // past the first tile the own position (FUSED) is scored below
+        if (i < n && t + NT * r < KQ && !(FUSED && k0 > 0 && i == n - 1)) put(i, s[r]);
+      }
+    }
+  };
   if constexpr (HD > 0) {
-    // R positions per thread, their sequential dots interleaved
-    constexpr int R = KQMAX / NT;
-    float s[R];
+    score_tile(0);
+    // long contexts: further K tiles of KQ positions, each loaded into
+    // registers while the previous one is scored
+    for (int k0 = KQ; k0 < n; k0 += KQ) {
+      __syncthreads();  // the previous tile is scored
 #pragma unroll
-    for (int r = 0; r < R; r++) s[r] = 0.0f;
+      for (int u = 0; u < KU; u++) {
+        const int unit = t + NT * u, qd = unit / CPR, cd = unit - qd * CPR;
 #pragma unroll
-    for (int c = 0; c < CPR; c++) {
-      v4u kk[R];
-#pragma unroll
-      for (int r = 0; r < R; r++) kk[r] = ktile[min(t + NT * r, KQ - 1) * KP + c];
-      float qv[8];
-#pragma unroll
-      for (int j = 0; j < 8; j++) qv[j] = qs[8 * c + j];
-#pragma unroll
-      for (int r = 0; r + 1 < R; r += 2) mac8x2(s[r], s[r + 1], qv, kk[r], kk[r + 1]);
-      if constexpr (R & 1) mac8(s[R - 1], qv, kk[R - 1]);
+        for (int e = 0; e < 4; e++) {
+          const int i = 4 * qd + e;
+          if (i < KQ) ktile[i * KP + cd] = kr[u][e];
+        }
+      }
+      if (k0 + KQ < n) load_k(k0 + KQ);
+      __syncthreads();
+      score_tile(k0);
     }
-#pragma unroll
-    for (int r = 0; r < R; r++) {
-      const int i = t + NT * r;
-      if (i < n && i < KQ) put(i, s[r]);
-    }
-  }
-  // positions past the K tile (long contexts) and the generic path
-  for (int i = t; i < n; i += NT) {
-    if (HD > 0 && i < KQ) continue;  // scored from the K tile above
-    put(i, (FUSED && i == n - 1) ? dot_new_k<HD>(qs, kn, hd) : dot_k_row<HD>(qs, K + (size_t)i * a.kv, hd));
+    if (FUSED && n - 1 >= KQ && t == 0) put(n - 1, dot_new_k<HD>(qs, kn, hd));
+  } else {
+    for (int i = t; i < n; i += NT)
+      put(i, (FUSED && i == n - 1) ? dot_new_k<HD>(qs, kn, hd) : dot_k_row<HD>(qs, K + (size_t)i * a.kv, hd));
   }
   mx = block_max_1b<NT / 64>(mx, redf);
   // this thread's first two values stay in registers until the sum is known
@@ -789,7 +828,8 @@ __global__ __launch_bounds__(NS > 1 ? 512 : 256) void attn_kernel(AttnArgs a) {
       // Stage s: the product threads form the products of their UPS units of
       // stage s (quads [stage_lo(s), stage_lo(s+1))) while the summing lanes
       // add the quads of stage s - 1; a barrier separates the stages.
-      if (t0) load_v(t0);
+      // (the V of tiles after the first is loaded during the previous tile's
+      // last stage)
       const int nqt = (cnt + 3) / 4;  // quads holding positions
       const int nst = nqt <= Q0 ? 1 : 1 + (nqt - Q0 + SQ - 1) / SQ;  // stages holding positions
 #pragma unroll
@@ -832,6 +872,8 @@ __global__ __launch_bounds__(NS > 1 ? 512 : 256) void attn_kernel(AttnArgs a) {
                     make_float4(pr[k][0], pr[k][1], pr[k][2], pr[k][3]);
             }
           }
+          // the next tile's V into the registers this tile has used up
+          if (s == nst - 1 && t0 + T < n) load_v(t0 + T);
         } else if (t < hs && s > 0) {
           sum_quads(stage_lo(s - 1), min(stage_lo(s), nq));
           if (s == nst) sum_tail(nq, cnt);

@@ -102,7 +102,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   constexpr bool LDS_ACT = PRO != PRO_F32;
   constexpr bool NORM = PRO == PRO_RMS || PRO == PRO_LN;
   constexpr int NS = ProStrips<PRO>::NS;
-  static_assert(!WL || (MT == 1 && (PRO == PRO_QUANT || NORM)), "wave-local prologue: one row, fp32 input");
+  static_assert(!WL || (MT <= 4 && (PRO == PRO_QUANT || NORM)), "wave-local prologue: up to 4 rows, fp32 input");
+  // WL with MT > 1: wave w computes row min(w, mc - 1) of the tile into LDS
+  // slot w, and one block barrier precedes the dot
+  constexpr bool WL1 = WL && MT == 1;
 
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
   __shared__ double redd[2][4];
@@ -154,12 +157,14 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
       }
     }
   };
-  // WL: every wave holds the whole row (K <= 1024), lane l elements
-  // 4l + 256j, and computes the prologue alone: no block barrier, and each
-  // wave writes its own copy of the quantized / normalized row to LDS
+  // WL: every wave holds a whole row (K <= 1024), lane l elements
+  // 4l + 256j, and computes the prologue alone: for one row (WL1) no block
+  // barrier, each wave writing its own copy of the quantized / normalized
+  // row to LDS; for an M tile of up to 4 rows, wave w takes row w
   float4 xw[WL ? 4 : 1], gw[WL && NORM ? 4 : 1], bw[WL && PRO == PRO_LN ? 4 : 1];
   if constexpr (WL) {
-    const float *row = reinterpret_cast<const float *>(a.A) + (size_t)m0 * a.lda;
+    const int wr = MT > 1 ? min(wave, mc - 1) : 0;
+    const float *row = reinterpret_cast<const float *>(a.A) + (size_t)(m0 + wr) * a.lda;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
       const int i = min(4 * lane + 256 * j, K - 4);
@@ -307,6 +312,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
         }
       }
       xsw = sc;
+      if constexpr (MT > 1) {
+        if (lane == 0) xs[wave] = sc;
+      }
     } else {
       float *f = xf + (size_t)wave * Kp;
 #pragma unroll
@@ -429,7 +437,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
       if (m + 1 < mc) __syncthreads();
     }
   }
-  if constexpr (!WL) __syncthreads();
+  if constexpr (!WL1) __syncthreads();
 
   unsigned long long best[MT];
 #pragma unroll
@@ -455,7 +463,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
 #pragma unroll
           for (int m = 0; m < MT; m++) {
             if (m < mc) {
-              const v4i x = *reinterpret_cast<const v4i *>(xq + (size_t)(WL ? wave : m) * Kp + (size_t)ch * 16);
+              const v4i x = *reinterpret_cast<const v4i *>(xq + (size_t)(WL1 ? wave : m) * Kp + (size_t)ch * 16);
               int s = acc[m];
               s = __builtin_amdgcn_sdot4(x.x, w[c].x, s, false);
               s = __builtin_amdgcn_sdot4(x.y, w[c].y, s, false);
@@ -494,7 +502,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
           for (int m = 0; m < MT; m++) {
             if (m < mc) {
               const float4 *xp =
-                  LDS_ACT ? reinterpret_cast<const float4 *>(xf + (size_t)(WL ? wave : m) * Kp + (size_t)ch * 8)
+                  LDS_ACT ? reinterpret_cast<const float4 *>(xf + (size_t)(WL1 ? wave : m) * Kp + (size_t)ch * 8)
                           : reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(a.A) +
                                                              (size_t)(m0 + m) * a.lda + (size_t)ch * 8);
               const float4 x0 = xp[0], x1 = xp[1];
@@ -550,13 +558,13 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
         if (m < mc) {
           float v;
           if constexpr (Q8) {
-            v = i8_epilogue((int)acc[m], WL ? xsw : xs[m], cbs, SWI ? 0.0f : cbia);
+            v = i8_epilogue((int)acc[m], WL1 ? xsw : xs[m], cbs, SWI ? 0.0f : cbia);
           } else {
             v = (float)acc[m];
           }
           float *o = a.out + (size_t)(m0 + m) * a.ldo + n;
           if constexpr (SWI) {
-            const float u = Q8 ? i8_epilogue((int)acc2[m], WL ? xsw : xs[m], cbs2, 0.0f) : (float)acc2[m];
+            const float u = Q8 ? i8_epilogue((int)acc2[m], WL1 ? xsw : xs[m], cbs2, 0.0f) : (float)acc2[m];
             v = silu(v, etab + 32 * wave) * u;
           } else {
             if constexpr (!Q8 && (EPI == EPI_BIAS || EPI == EPI_BIAS_RESID || EPI == EPI_BIAS_GELU)) v = v + cbia;
@@ -618,8 +626,14 @@ hipError_t gemv_launch_shape(const GemvArgs &a, hipStream_t s) {
     if constexpr (PRO == PRO_QUANT || PRO == PRO_RMS || PRO == PRO_LN) \
       if (gemv_wave_pro(PRO, 1, a.K)) return gemv_launch<WT, SH, 1, EPI, PRO, true>(a, s); \
     return gemv_launch<WT, SH, 1, EPI, PRO>(a, s);                  \
-  case 2: return gemv_launch<WT, SH, 2, EPI, PRO>(a, s);            \
-  case 4: return gemv_launch<WT, SH, 4, EPI, PRO>(a, s);            \
+  case 2:                                                           \
+    if constexpr (PRO == PRO_QUANT || PRO == PRO_RMS || PRO == PRO_LN) \
+      if (gemv_wave_pro(PRO, 2, a.K)) return gemv_launch<WT, SH, 2, EPI, PRO, true>(a, s); \
+    return gemv_launch<WT, SH, 2, EPI, PRO>(a, s);                  \
+  case 4:                                                           \
+    if constexpr (PRO == PRO_QUANT || PRO == PRO_RMS || PRO == PRO_LN) \
+      if (gemv_wave_pro(PRO, 4, a.K)) return gemv_launch<WT, SH, 4, EPI, PRO, true>(a, s); \
+    return gemv_launch<WT, SH, 4, EPI, PRO>(a, s);                  \
   default: return gemv_launch<WT, SH, 8, EPI, PRO>(a, s);           \
   }
   if (shape == GS_NARROW) {

@@ -1028,7 +1028,7 @@ size_t gemv_lds_bytes(int wt, int pro, int MT, int K) {
   const int rows = gemv_wave_pro(pro, MT, K) ? 4 : MT;  // one row per wave, or the M tile
   if (wt == WT_I8) {
     const size_t kp = (size_t)(K + 15) / 16 * 16;
-    return (rows * kp + 4 * MT + 15) / 16 * 16;
+    return (rows * kp + 4 * rows + 15) / 16 * 16;  // codes, then one scale per row slot
   }
   const size_t kp = (size_t)(K + 7) / 8 * 8;
   return rows * kp * 4;

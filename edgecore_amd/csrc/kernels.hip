@@ -661,7 +661,7 @@ __global__ __launch_bounds__(NS > 1 ? 512 : 256) void attn_kernel(AttnArgs a) {
 #pragma unroll
       for (int e = 0; e < 4; e++) {
         const int i = 4 * qd + e;
-        if (i < KQ && !(FUSED && i == n - 1)) ktile[i * KP + cd] = kr[u][e];
+        if (i < KQ && i < n && !(FUSED && i == n - 1)) ktile[i * KP + cd] = kr[u][e];
       }
     }
   }
@@ -696,6 +696,8 @@ __global__ __launch_bounds__(NS > 1 ? 512 : 256) void attn_kernel(AttnArgs a) {
   // the positions k0 + t + NT*r of the K tile (rows t + NT*r)
   auto score_tile = [&](int k0) {
     if constexpr (HD > 0) {
+      // a wave whose positions all lie past n skips the dots (uniform)
+      if (k0 + (t & ~63) >= n) return;
       // R positions per thread, their sequential dots interleaved
       constexpr int R = KQMAX / NT;
       float s[R];
@@ -733,7 +735,7 @@ __global__ __launch_bounds__(NS > 1 ? 512 : 256) void attn_kernel(AttnArgs a) {
 #pragma unroll
         for (int e = 0; e < 4; e++) {
           const int i = 4 * qd + e;
-          if (i < KQ) ktile[i * KP + cd] = kr[u][e];
+          if (i < KQ && k0 + i < n) ktile[i * KP + cd] = kr[u][e];
         }
       }
       if (k0 + KQ < n) load_k(k0 + KQ);

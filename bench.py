@@ -205,7 +205,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              f"(independent sequences would shard as pure data parallelism, see DESIGN.md)",
+              f"(independent sequences would shard as pure data parallelism: one process per GPU, each with its own model copy and slots)",
               file=sys.stderr)
         return 2
 

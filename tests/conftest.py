@@ -16,7 +16,7 @@ def pytest_configure(config):
 
 # Synthetic model shapes used by the tests, as ecm_synth arguments.
 MODEL_SPECS = {
-    # tiny GPT-2 (L2 E64 H2 FFN256 ctx128 V50257) int8
+    # the reference's CPU-runnable case: tiny GPT-2 (L2 E64 H2 FFN256 ctx128 V50257) int8
     "tiny-gpt2-int8": dict(preset="tiny-gpt2"),
     "tiny-gpt2-fp16": dict(preset="tiny-gpt2", precision="fp16"),
     "tiny-qwen2-int8": dict(preset="tiny-qwen2"),

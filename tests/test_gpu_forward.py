@@ -1,7 +1,7 @@
 """End-to-end GPU forward parity against the CPU oracle (src/gpt2.c:470-805
 semantics) on seeded synthetic models.
 
-Bar (north star): greedy tokens identical for the first 32 generated tokens;
+Bar: greedy tokens identical for the first 32 generated tokens;
 logits within max-abs 2e-2 (int8 models) / 1e-2 (fp16 and bf16 models) of
 the oracle, which itself is bit-exact with the reference build.
 """

@@ -140,37 +140,76 @@ def prefill_c4(ec, np, model: Path, cache: Path):
     }
 
 
-def physical_cores() -> int:
+def cpu_info():
+    """(model name, physical cores of socket 0 among the CPUs this process may
+    run on, the cgroup CPU quota in whole CPUs or None)"""
+    model = ""
     try:
-        out = subprocess.run(["lscpu", "-p=CORE,SOCKET"], capture_output=True, text=True).stdout
-        cores = {tuple(l.split(",")) for l in out.splitlines() if l and not l.startswith("#")}
-        socket0 = [c for c in cores if c[1] == "0"]
-        return max(1, len(socket0) or len(cores))
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    allowed = os.sched_getaffinity(0)
+    phys = 0
+    try:
+        out = subprocess.run(["lscpu", "-p=CPU,CORE,SOCKET"], capture_output=True, text=True).stdout
+        cores = set()
+        for l in out.splitlines():
+            if not l or l.startswith("#"):
+                continue
+            cpu, core, sock = l.split(",")[:3]
+            if sock == "0" and int(cpu) in allowed:
+                cores.add(core)
+        phys = len(cores)
     except Exception:
-        return os.cpu_count() or 1
+        pass
+    quota = None
+    try:
+        q, per = Path("/sys/fs/cgroup/cpu.max").read_text().split()[:2]
+        if q != "max":
+            quota = max(1, int(int(q) // int(per)))
+    except Exception:
+        pass
+    return model, phys or len(allowed), quota
 
 
 def cpu_baseline(model: Path, prompt: Path, n_tokens: int):
-    """The reference CPU runtime (built from its sources) on a bounded sample:
-    the same 256-token prefill, then n_tokens greedy decode steps."""
+    """The reference CPU runtime (built from its sources) on a bounded sample
+    of the same workload: the same 256-token prefill, then n_tokens greedy
+    decode steps; once with one thread and once with one socket's physical
+    cores (capped by the cgroup CPU quota, where one is set, since threads
+    beyond it would time-share).  tok/s is the reference's own bench-mode
+    figure: decode tokens over decode time."""
     sys.path.insert(0, str(REPO))
     import oracle
 
-    threads = min(16, physical_cores(), len(os.sched_getaffinity(0)))
-    if oracle.REF_RUNTIME.exists():
+    cpu_model, phys, quota = cpu_info()
+    threads_p = min(phys, quota) if quota else phys
+
+    def run(threads):
         cmd = [str(oracle.REF_RUNTIME), "--model", str(model), "--mode", "bench", "--tokens-file",
                str(prompt), "--n-tokens", str(n_tokens), "--warmup", "0", "--iters", "1",
                "--threads", str(threads), "--affinity", "physical", "--max-ctx",
                str(PROMPT + n_tokens + 8), "--no-print"]
-        p = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
-        if p.returncode == 0:
-            d = json.loads(p.stdout)
-            return {"value": d["tokens_per_sec"], "unit": "tok/s", "cores": threads, "kind": "reference",
-                    "sample": f"reference runtime_main.c/gpt2.c/kernels.c built with gcc -O3 "
-                              f"-mavx2 -mfma -mf16c; same model and 256-token prompt; "
-                              f"{n_tokens} greedy decode steps after the prefill; "
-                              f"--threads {threads} --affinity physical",
-                    "ttft_ms": d.get("ttft_avg_ms"), "avg_token_ms": d.get("avg_token_ms")}
+        p = subprocess.run(cmd, capture_output=True, text=True, timeout=900)
+        if p.returncode != 0:
+            raise RuntimeError(f"reference runtime exited {p.returncode}: {p.stderr[-300:]}")
+        return json.loads(p.stdout)
+
+    if oracle.REF_RUNTIME.exists():
+        d1 = run(1)
+        dp = run(threads_p) if threads_p > 1 else d1
+        sample = (f"reference runtime_main.c/gpt2.c/kernels.c built with gcc -O3 -mavx2 -mfma -mf16c; "
+                  f"same model and 256-token prompt; {n_tokens} greedy decode steps after the prefill; "
+                  f"--affinity physical; CPU {cpu_model!r}; socket 0 has {phys} physical cores among the "
+                  f"allowed CPUs; cgroup CPU quota {quota if quota else 'none'}")
+        return {"value": dp["tokens_per_sec"], "unit": "tok/s", "cores": threads_p, "kind": "reference",
+                "sample": sample, "cpu_model": cpu_model, "threads": threads_p,
+                "ttft_ms": dp.get("ttft_avg_ms"), "avg_token_ms": dp.get("avg_token_ms"),
+                "single_thread": {"value": d1["tokens_per_sec"], "unit": "tok/s", "cores": 1,
+                                  "ttft_ms": d1.get("ttft_avg_ms"), "avg_token_ms": d1.get("avg_token_ms")}}
     # the C restatement (oracle port) when the reference build is absent
     import numpy as np
 
@@ -185,9 +224,8 @@ def cpu_baseline(model: Path, prompt: Path, n_tokens: int):
         t += time.perf_counter() - t0
         cur, pos = int(np.argmax(lg[0])), pos + 1
     om.close()
-    return {"value": n_tokens / t, "unit": "tok/s", "cores": int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
-            or (os.cpu_count() or 1), "kind": "port",
-            "sample": f"oracle/ec_oracle.c; same model and prompt; {n_tokens} greedy decode steps"}
+    return {"value": n_tokens / t, "unit": "tok/s", "cores": 1, "kind": "port", "cpu_model": cpu_model,
+            "sample": f"oracle/ec_oracle.c (one thread); same model and prompt; {n_tokens} greedy decode steps"}
 
 
 def main() -> int:

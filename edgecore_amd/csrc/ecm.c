@@ -9,6 +9,7 @@
 #include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
+#include <string.h>
 #include <time.h>
 
 double now_sec(void)
@@ -160,6 +161,10 @@ int ecm_parse(const void *data, size_t size, EcmTensor *out, int max, GPT2 *meta
 /* weight packer                                                        */
 /* ------------------------------------------------------------------ */
 
+/* edgecore/ecm.py:50-59, in float64 as numpy computes it: max|w| (NaN
+ * propagates, as numpy's max does), scale = max/127 (1.0 when 0), code =
+ * clip(rint(w/scale)); numpy's float64 -> int32 cast gives INT32_MIN for a
+ * NaN quotient on x86-64, which the clip turns into -128. */
 void ec_quantize_int8_symmetric(const float *w, int rows, int cols, int8_t *q, float *scales)
 {
     for (int r = 0; r < rows; r++) {
@@ -167,6 +172,7 @@ void ec_quantize_int8_symmetric(const float *w, int rows, int cols, int8_t *q, f
         double maxabs = 0.0;
         for (int c = 0; c < cols; c++) {
             double a = fabs((double)row[c]);
+            if (isnan(a)) { maxabs = a; break; }
             if (a > maxabs) maxabs = a;
         }
         double s = maxabs / 127.0;
@@ -174,9 +180,20 @@ void ec_quantize_int8_symmetric(const float *w, int rows, int cols, int8_t *q, f
         int8_t *qr = q + (size_t)r * cols;
         for (int c = 0; c < cols; c++) {
             double v = nearbyint((double)row[c] / s);
-            qr[c] = (int8_t)(v > 127.0 ? 127 : v < -128.0 ? -128 : (int)v);
+            qr[c] = (int8_t)(isnan(v) ? -128 : v > 127.0 ? 127 : v < -128.0 ? -128 : (int)v);
         }
         scales[r] = (float)s;
     }
+}
+
+/* edgecore/ecm.py:27-41: fp32 -> bfloat16 bits, round to nearest even,
+ * every NaN to the quiet NaN 0x7fc0 */
+uint16_t ec_f32_to_bf16(float f)
+{
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    if ((x & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+    const uint32_t lsb = (x >> 16) & 1u;
+    return (uint16_t)(((uint64_t)x + 0x7fffu + lsb) >> 16);
 }
 

@@ -67,13 +67,6 @@ static void normal_row(uint64_t state, float *dst, int n, double std)
     }
 }
 
-static uint16_t f32_to_bf16_rne(float f)
-{
-    uint32_t x; /* edgecore/ecm.py:27-41 */
-    memcpy(&x, &f, 4);
-    if ((x & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
-    return (uint16_t)(((uint64_t)x + 0x7fffu + ((x >> 16) & 1u)) >> 16);
-}
 
 typedef struct {
     char name[96];
@@ -271,7 +264,7 @@ static int write_model(const Opts *o)
                 else if (t->dtype == 1)
                     for (int c = 0; c < cols; c++) ((uint16_t *)buf)[base + c] = f32_to_fp16(tmp[c]);
                 else if (t->dtype == 4)
-                    for (int c = 0; c < cols; c++) ((uint16_t *)buf)[base + c] = f32_to_bf16_rne(tmp[c]);
+                    for (int c = 0; c < cols; c++) ((uint16_t *)buf)[base + c] = ec_f32_to_bf16(tmp[c]);
                 else
                     ec_quantize_int8_symmetric(tmp, 1, cols, (int8_t *)buf + base, pending_scales + r);
             }

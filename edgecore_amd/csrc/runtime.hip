@@ -163,15 +163,53 @@ struct ProfRec {
   int ev;  // index of the first of two pooled events
   double bytes;
 };
+struct ProfAgg {
+  const char *fam;
+  int n;
+  double us, bytes;
+};
+// The event pool is bounded: when it is full, the stream is synchronized, the
+// pending records are folded into per-family totals and the events reused, so
+// a profiled run of any length holds at most kProfEvents events.
+constexpr size_t kProfEvents = 4096;
 static bool g_prof_on = false;
 static std::string g_prof_filter;
 static std::vector<hipEvent_t> g_ev_pool;
 static size_t g_ev_used = 0;
 static std::vector<ProfRec> g_prof;
+static std::vector<ProfAgg> g_prof_agg;
+
+// fold every pending record into g_prof_agg (the stream must be idle)
+static int prof_harvest() {
+  for (const ProfRec &r : g_prof) {
+    float ms = 0.0f;
+    EC_HIP(hipEventElapsedTime(&ms, g_ev_pool[r.ev], g_ev_pool[r.ev + 1]));
+    size_t i = 0;
+    for (; i < g_prof_agg.size(); i++)
+      if (!strcmp(g_prof_agg[i].fam, r.fam)) break;
+    if (i == g_prof_agg.size()) g_prof_agg.push_back({r.fam, 0, 0.0, 0.0});
+    g_prof_agg[i].n++;
+    g_prof_agg[i].us += ms * 1000.0;
+    g_prof_agg[i].bytes += r.bytes;
+  }
+  g_prof.clear();
+  g_ev_used = 0;
+  return 0;
+}
+
+static void prof_release_events() {
+  for (hipEvent_t e : g_ev_pool) (void)hipEventDestroy(e);
+  g_ev_pool.clear();
+  g_ev_used = 0;
+}
 
 static int prof_begin(const char *fam, double bytes) {
   if (!g_prof_on) return -1;
   if (!g_prof_filter.empty() && strcmp(fam, g_prof_filter.c_str()) != 0) return -1;
+  if (g_ev_used + 2 > kProfEvents) {
+    // pool full: wait for the recorded launches and reuse their events
+    if (hipStreamSynchronize(g_stream) != hipSuccess || prof_harvest() != 0) return -1;
+  }
   while (g_ev_pool.size() < g_ev_used + 2) {
     hipEvent_t e;
     if (hipEventCreate(&e) != hipSuccess) return -1;
@@ -192,6 +230,7 @@ static void prof_end(int rec) {
   if (g_launch_ev[0]) {
     g_launch_ev[0] = g_launch_ev[1] = nullptr;
     g_prof.pop_back();
+    g_ev_used -= 2;
   }
 }
 
@@ -199,6 +238,7 @@ extern "C" int ec_prof_start(const char *filter) {
   EC_INIT();
   g_prof_filter = filter ? filter : "";
   g_prof.clear();
+  g_prof_agg.clear();
   g_ev_used = 0;
   g_prof_on = true;
   return 0;
@@ -208,37 +248,22 @@ extern "C" int ec_prof_stop(char *buf, int len) {
   EC_INIT();
   g_prof_on = false;
   EC_HIP(hipStreamSynchronize(g_stream));
-  struct Agg {
-    const char *fam;
-    int n;
-    double us, bytes;
-  };
-  std::vector<Agg> agg;
-  for (const ProfRec &r : g_prof) {
-    float ms = 0.0f;
-    EC_HIP(hipEventElapsedTime(&ms, g_ev_pool[r.ev], g_ev_pool[r.ev + 1]));
-    size_t i = 0;
-    for (; i < agg.size(); i++)
-      if (!strcmp(agg[i].fam, r.fam)) break;
-    if (i == agg.size()) agg.push_back({r.fam, 0, 0.0, 0.0});
-    agg[i].n++;
-    agg[i].us += ms * 1000.0;
-    agg[i].bytes += r.bytes;
-  }
+  const int hr = prof_harvest();
+  prof_release_events();
+  if (hr) return hr;
   std::string s = "[";
-  for (size_t i = 0; i < agg.size(); i++) {
+  for (size_t i = 0; i < g_prof_agg.size(); i++) {
+    const ProfAgg &g = g_prof_agg[i];
     char tmp[512];
-    const double avg = agg[i].us / agg[i].n, bpl = agg[i].bytes / agg[i].n;
+    const double avg = g.us / g.n, bpl = g.bytes / g.n;
     snprintf(tmp, sizeof tmp,
              "%s{\"kernel\": \"%s\", \"launches\": %d, \"total_us\": %.3f, \"avg_us\": %.4f, "
              "\"bytes_per_launch\": %.0f, \"gbps\": %.2f}",
-             i ? ", " : "", agg[i].fam, agg[i].n, agg[i].us, avg, bpl,
-             avg > 0 ? bpl / (avg * 1e3) : 0.0);
+             i ? ", " : "", g.fam, g.n, g.us, avg, bpl, avg > 0 ? bpl / (avg * 1e3) : 0.0);
     s += tmp;
   }
   s += "]";
-  g_prof.clear();
-  g_ev_used = 0;
+  g_prof_agg.clear();
   if ((int)s.size() + 1 > len) return set_err(-1, "ec_prof_stop: buffer too small (%zu)", s.size() + 1);
   memcpy(buf, s.c_str(), s.size() + 1);
   return (int)s.size();

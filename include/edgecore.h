@@ -391,8 +391,13 @@ int ec_prof_stop(char *buf, int len);
 int ec_device_math(int op, const void *in, void *out, size_t n);
 
 /* int8 weight packing of edgecore/ecm.py:50-59 (float64 max|w|/127, zero row
- * -> scale 1, round half to even, clip), used by the synthetic generator. */
+ * -> scale 1, round half to even, clip; a row holding NaN gets scale NaN and
+ * codes -128, as numpy gives), used by the synthetic generator. */
 void ec_quantize_int8_symmetric(const float *w, int rows, int cols, int8_t *q, float *scales);
+
+/* fp32 -> bfloat16 bits of edgecore/ecm.py:27-41 (round to nearest even, NaN
+ * -> 0x7fc0), used by the synthetic generator for bf16 weights. */
+uint16_t ec_f32_to_bf16(float f);
 
 #ifdef __cplusplus
 }

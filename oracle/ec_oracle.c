@@ -11,11 +11,13 @@
  * Parity pins (tests/test_oracle.py, tests/golden/):
  *   or_f32_to_f16 / or_f16_to_f32 : exhaustive vs the host F16C instruction
  *                                   (or_check_f16c below) + the reference build
- *   or_quantize_int8_symmetric     : closed-form special cases (zero row,
- *                                   +-maxabs, exact .5 ties); the reference's
- *                                   generator sits behind numpy, so this packer
- *                                   is also cross-checked against the
- *                                   library's independent C packer
+ *   or_quantize_int8_symmetric     : tests/golden/packer.npz, whose codes come
+ *                                   from exact rational arithmetic on the
+ *                                   float64 definition (adversarial quotients
+ *                                   a float32 packer rounds differently, ties,
+ *                                   +-maxabs, zero/NaN/inf/subnormal rows)
+ *   or_f32_to_bf16                 : all 2^32 inputs against round-to-nearest-
+ *                                   even as a distance comparison
  *   or_quantize_rows               : closed-form ties / clamp cases + the
  *                                   reference build (through gpt2_forward)
  *   or_gemm_int8                   : brute-force int64 dot + adversarial
@@ -172,12 +174,16 @@ void or_quantize_int8_symmetric(const float *w, int rows, int cols,
         double maxabs = 0.0;
         for (int c = 0; c < cols; c++) {
             double a = fabs((double)row[c]);
-            if (a > maxabs) maxabs = a;
+            if (isnan(a)) maxabs = a; /* numpy's max propagates NaN */
+            else if (a > maxabs) maxabs = a;
         }
         double s = maxabs / 127.0;
         if (s == 0.0) s = 1.0;
         for (int c = 0; c < cols; c++) {
             double v = rint((double)row[c] / s);
+            /* numpy's float64 -> int32 cast of NaN is INT32_MIN on x86-64;
+             * np.clip then gives -128 */
+            if (isnan(v)) v = -128.0;
             if (v > 127.0) v = 127.0;
             if (v < -128.0) v = -128.0;
             q[(size_t)r * cols + c] = (int8_t)(int)v;

@@ -35,12 +35,22 @@ def test_f32_to_f16_exhaustive_vs_f16c():
     assert L.or_check_f16c_widen() == 0
 
 
-def _compile_and_run(src: str, tmp_path, *args) -> subprocess.CompletedProcess:
+def _compile_and_run(src: str, tmp_path, *args, extra=()) -> subprocess.CompletedProcess:
     exe = tmp_path / "chk"
     subprocess.run(["gcc", "-O2", "-std=c11", "-ffp-contract=off", "-fopenmp", "-mf16c",
                     f"-I{REPO / 'include'}", f"-I{REPO / 'edgecore_amd' / 'csrc'}",
-                    str(REPO / "tests" / "c" / src), "-o", str(exe), "-lm"], check=True)
+                    str(REPO / "tests" / "c" / src), *[str(REPO / e) for e in extra], "-o", str(exe), "-lm"],
+                   check=True)
     return subprocess.run([str(exe), *map(str, args)], capture_output=True, text=True)
+
+
+def test_bf16_packers_exhaustive(tmp_path):
+    """edgecore/ecm.py:27-41 restated twice (the generator's ec_f32_to_bf16 and
+    the oracle's or_f32_to_bf16) against round-to-nearest-even written as a
+    distance comparison, on all 2^32 inputs."""
+    p = _compile_and_run("bf16_exhaustive.c", tmp_path,
+                         extra=("edgecore_amd/csrc/ecm.c", "oracle/ec_oracle.c"))
+    assert p.returncode == 0 and "mismatches 0, or_f32_to_bf16 mismatches 0" in p.stdout, p.stdout
 
 
 def test_library_header_f16_exhaustive(tmp_path):
@@ -77,6 +87,49 @@ def test_weight_packer_closed_forms(packer):
     assert list(q[1]) == [127, 0, 2, 2, 0, -2, -2, -127] and s[1] == 1.0
     assert s[2] == np.float32(1.0 / 127.0) and q[2, 0] == 127 and q[2, 7] == -127
     assert q[3, 1] == -127 and q[3, 6] == 127 and s[3] == np.float32(0.7 / 127.0)
+
+
+def _packer_golden():
+    return np.load(GOLDEN / "packer.npz")
+
+
+@pytest.mark.parametrize("packer", ["oracle", "library"])
+def test_weight_packer_golden(packer):
+    """edgecore/ecm.py:50-59 on tests/golden/packer.npz, whose codes and scales
+    come from exact rational arithmetic on the float64 definition
+    (make_packer_golden.py): adversarial near-half-integer quotients, ties,
+    +-maxabs, zero / NaN / infinite / subnormal rows, seeded N(0, 0.02) rows."""
+    pack = oracle.quantize_int8_symmetric if packer == "oracle" else ec.quantize_int8_symmetric
+    g = _packer_golden()
+    q, s = pack(g["w"])
+    assert np.array_equal(q, g["q"])
+    assert np.array_equal(s.view(np.uint32), g["s"].view(np.uint32)) or np.array_equal(
+        np.isnan(s), np.isnan(g["s"])) and np.array_equal(s[~np.isnan(s)], g["s"][~np.isnan(g["s"])])
+
+
+def test_weight_packer_golden_catches_mistakes():
+    """The fixture tells the float64 packer from plausible wrong ones: float32
+    arithmetic throughout, dividing by the float32-rounded scale, and
+    multiplying by 127 / maxabs each give other codes on its adversarial rows."""
+    g = _packer_golden()
+    w, want = g["w"][: int(g["n_adversarial"])], g["q"][: int(g["n_adversarial"])]
+
+    def f32(w):
+        m = np.max(np.abs(w), axis=1).astype(np.float32)
+        s = m / np.float32(127.0)
+        return np.clip(np.rint(w / s[:, None]), -128, 127).astype(np.int8)
+
+    def f32_scale(w):
+        s = np.max(np.abs(w.astype(np.float64)), axis=1) / 127.0
+        return np.clip(np.rint(w.astype(np.float64) / s.astype(np.float32).astype(np.float64)[:, None]),
+                       -128, 127).astype(np.int8)
+
+    def recip(w):
+        r = 127.0 / np.max(np.abs(w.astype(np.float64)), axis=1)
+        return np.clip(np.rint(w.astype(np.float64) * r[:, None]), -128, 127).astype(np.int8)
+
+    for wrong in (f32, f32_scale, recip):
+        assert not np.array_equal(wrong(w), want), wrong.__name__
 
 
 def test_weight_packer_library_equals_oracle():

@@ -82,6 +82,8 @@ hipError_t gemv_generic(const GemvArgs &a, int wt, int epi, hipStream_t s);
 constexpr int kGemmMinM = 16;
 bool gemm_i8_ok(const GemvArgs &a, int epi);
 hipError_t gemm_i8(const GemvArgs &a, int epi, hipStream_t s);
+// the same with the row tile forced: bm 32, 64 or 128 (0: gemm_i8's choice)
+hipError_t gemm_i8_tile(const GemvArgs &a, int epi, int bm, hipStream_t s);
 // grid-size cap of the grid-stride GEMV (set from the CU count at init)
 void gemv_set_max_blocks(int n);
 int gemv_max_blocks();

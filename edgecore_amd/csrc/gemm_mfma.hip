@@ -237,14 +237,15 @@ hipError_t launch_bm(const GemvArgs &a, hipStream_t s) {
 }
 
 template <int EPI>
-hipError_t launch_epi(const GemvArgs &a, hipStream_t s) {
+hipError_t launch_epi(const GemvArgs &a, int bm, hipStream_t s) {
   // the largest row tile that still gives every CU a block or more, else the
   // smallest (N = 896 at M = 2048: 448 blocks of 32 rows beat 224 of 64 rows,
   // 9.7 against 10.7 us for K = 896 and 34.0 against 35.5 us for K = 4864)
   constexpr int NOUT = EPI == EPI_SWIGLU ? kBN / 2 : kBN;
   const long gx = (a.N + NOUT - 1) / NOUT;
-  if (gx * ((a.M + 127) / 128) >= 256) return launch_bm<128, EPI>(a, s);
-  if (gx * ((a.M + 63) / 64) >= 256) return launch_bm<64, EPI>(a, s);
+  if (bm == 0) bm = gx * ((a.M + 127) / 128) >= 256 ? 128 : gx * ((a.M + 63) / 64) >= 256 ? 64 : 32;
+  if (bm == 128) return launch_bm<128, EPI>(a, s);
+  if (bm == 64) return launch_bm<64, EPI>(a, s);
   return launch_bm<32, EPI>(a, s);
 }
 
@@ -259,18 +260,20 @@ bool gemm_i8_ok(const GemvArgs &a, int epi) {
          epi == EPI_BIAS_RESID || epi == EPI_BIAS_GELU;
 }
 
-hipError_t gemm_i8(const GemvArgs &a, int epi, hipStream_t s) {
-  if (!gemm_i8_ok(a, epi)) return hipErrorInvalidValue;
+hipError_t gemm_i8_tile(const GemvArgs &a, int epi, int bm, hipStream_t s) {
+  if (!gemm_i8_ok(a, epi) || (bm != 0 && bm != 32 && bm != 64 && bm != 128)) return hipErrorInvalidValue;
   switch (epi) {
     case EPI_STORE:
-    case EPI_BIAS: return launch_epi<EPI_STORE>(a, s);
+    case EPI_BIAS: return launch_epi<EPI_STORE>(a, bm, s);
     case EPI_RESID:
-    case EPI_BIAS_RESID: return launch_epi<EPI_RESID>(a, s);
+    case EPI_BIAS_RESID: return launch_epi<EPI_RESID>(a, bm, s);
     case EPI_GELU:
-    case EPI_BIAS_GELU: return launch_epi<EPI_GELU>(a, s);
-    case EPI_SWIGLU: return launch_epi<EPI_SWIGLU>(a, s);
+    case EPI_BIAS_GELU: return launch_epi<EPI_GELU>(a, bm, s);
+    case EPI_SWIGLU: return launch_epi<EPI_SWIGLU>(a, bm, s);
   }
   return hipErrorInvalidValue;
 }
+
+hipError_t gemm_i8(const GemvArgs &a, int epi, hipStream_t s) { return gemm_i8_tile(a, epi, 0, s); }
 
 }  // namespace ec

@@ -23,7 +23,9 @@
 #include <sys/stat.h>
 #include <unistd.h>
 
+#include <mutex>
 #include <string>
+#include <unordered_map>
 #include <vector>
 
 using namespace ec;
@@ -314,6 +316,25 @@ extern "C" int ec_gemm_int8_dev(float *C, const int8_t *A, const float *a_scale,
   return 0;
 }
 
+// int8 matrix-core GEMM with a fused epilogue and a chosen row tile, on
+// device buffers: the forward's prefill linears, callable alone for checks
+extern "C" int ec_gemm_int8_epi_dev(int epi, int bm, float *C, const int8_t *A, const float *a_scale,
+                                    const int8_t *B, const float *b_scale, const int8_t *B2,
+                                    const float *b2_scale, const float *bias, int M, int K, int N) {
+  EC_INIT();
+  if (M < 1 || N < 1 || K < 16 || K % 16)
+    return set_err(-1, "ec_gemm_int8_epi_dev: shape M=%d K=%d N=%d (K a multiple of 16)", M, K, N);
+  if (epi != EPI_STORE && epi != EPI_RESID && epi != EPI_GELU && epi != EPI_SWIGLU)
+    return set_err(-1, "ec_gemm_int8_epi_dev: epilogue %d (0 store, 1 residual, 2 GELU, 3 SwiGLU)", epi);
+  if (bm != 0 && bm != 32 && bm != 64 && bm != 128) return set_err(-1, "ec_gemm_int8_epi_dev: row tile %d", bm);
+  if (!C || !A || !a_scale || !B || (epi == EPI_SWIGLU && !B2)) return set_err(-1, "ec_gemm_int8_epi_dev: null pointer");
+  GemvArgs a{A, K, a_scale, nullptr, nullptr, 0.0, B, B2, b_scale, b2_scale, epi == EPI_SWIGLU ? nullptr : bias,
+             C, N, M, K, N, nullptr};
+  if (!gemm_i8_ok(a, epi)) return set_err(-1, "ec_gemm_int8_epi_dev: unaligned operands");
+  EC_LAUNCH("gemm_i8", 0.0, gemm_i8_tile(a, epi, bm, g_stream));
+  return 0;
+}
+
 static int gemm_w16_dev(float *C, const float *A, const uint16_t *B, int M, int K, int N, bool bf16) {
   EC_INIT();
   if (M < 0 || N < 0 || K < 0) return set_err(-1, "gemm: negative shape M=%d K=%d N=%d", M, K, N);
@@ -546,6 +567,35 @@ static void free_dev(DevModel *d) {
   delete d;
 }
 
+// The device state of each loaded model, keyed by the address of its GPT2
+// struct: the struct itself keeps the reference's layout (src/edgecore.h:
+// 170-234) field for field, so a caller compiled against that header passes a
+// struct of the same size.  A GPT2 must therefore not be moved or copied
+// between gpt2_load and gpt2_free (the reference's callers never do).
+static std::mutex g_models_mu;
+static std::unordered_map<const GPT2 *, DevModel *> g_models;
+
+static DevModel *dev_of(const GPT2 *g) {
+  if (!g) return nullptr;
+  std::lock_guard<std::mutex> lk(g_models_mu);
+  auto it = g_models.find(g);
+  return it == g_models.end() ? nullptr : it->second;
+}
+
+static void dev_attach(const GPT2 *g, DevModel *d) {
+  std::lock_guard<std::mutex> lk(g_models_mu);
+  g_models[g] = d;
+}
+
+static DevModel *dev_detach(const GPT2 *g) {
+  std::lock_guard<std::mutex> lk(g_models_mu);
+  auto it = g_models.find(g);
+  if (it == g_models.end()) return nullptr;
+  DevModel *d = it->second;
+  g_models.erase(it);
+  return d;
+}
+
 static int load_impl(GPT2 *g, const char *path, int batch_cap, int max_ctx) {
   memset(g, 0, sizeof *g);
   g->batch_cap = batch_cap < 1 ? 1 : batch_cap;
@@ -610,7 +660,8 @@ static int load_impl(GPT2 *g, const char *path, int batch_cap, int max_ctx) {
   const int eff = gpt2_eff_ctx(g);
 
   DevModel *d = new DevModel();
-  g->dev = d;
+  free_dev(dev_detach(g));
+  dev_attach(g, d);
   d->eff_ctx = eff;
   d->F = F;
   d->L.resize(Lc);
@@ -838,14 +889,14 @@ extern "C" void gpt2_free(GPT2 *g) {
   if (!g) return;
   tokenizer_free(&g->tok);
   free(g->lw);
-  free_dev((DevModel *)g->dev);
+  free_dev(dev_detach(g));
   if (g->file_data && g->file_mapped) munmap(g->file_data, g->file_size);
   memset(g, 0, sizeof *g);
 }
 
 extern "C" int gpt2_kv_reset(GPT2 *g) {
   EC_INIT();
-  DevModel *d = (DevModel *)g->dev;
+  DevModel *d = dev_of(g);
   if (!d) return set_err(-1, "gpt2_kv_reset: model not loaded");
   const size_t b = d->kv_layer * g->n_layer * sizeof(uint16_t);
   EC_HIP(hipMemsetAsync(d->kc, 0, b, g_stream));
@@ -1044,7 +1095,7 @@ static int enqueue_forward(GPT2 *g, DevModel *d, int M, int lm_from, bool distin
 static int forward_impl(GPT2 *g, const int *tokens, const int *positions, const int *seqs, int M,
                         int lm_from, float *logits, int *argmax, const TopkReq *tk = nullptr) {
   EC_INIT();
-  DevModel *d = (DevModel *)g->dev;
+  DevModel *d = dev_of(g);
   if (!d) return set_err(-1, "model not loaded");
   if (M < 1 || M > d->mmax) return set_err(-1, "M=%d outside [1, %d]", M, d->mmax);
   if (lm_from < 0 || lm_from > M) return set_err(-1, "lm_from=%d outside [0, %d]", lm_from, M);
@@ -1142,7 +1193,7 @@ extern "C" int ec_topk_max(void) { return kTopkMax; }
 
 extern "C" int ec_last_logits(GPT2 *g, int row, float *out) {
   EC_INIT();
-  DevModel *d = g ? (DevModel *)g->dev : nullptr;
+  DevModel *d = dev_of(g);
   if (!d) return set_err(-1, "model not loaded");
   if (!out || row < 0 || row >= d->last_lm_rows)
     return set_err(-1, "ec_last_logits: row %d outside the last LM-head chunk (%d rows)", row, d->last_lm_rows);

@@ -1,546 +1,757 @@
 /*
- * edgecore-runtime for the MI355X library: the command-line contract of the
- * reference driver (src/runtime_main.c) -- modes generate|logits|bench, the
- * same flags, JSON keys, --logits-bin layout and exit codes (0 ok, 1 load or
- * prompt failure, 2 usage error or precision mismatch) -- over the GPU
- * forward of libedgecore_hip.so.
+ * edgecore-runtime: the command-line driver over libedgecore_hip.so.
  *
- * Differences from the reference, all additive or result-preserving:
- *   - the KV cache is cleared with gpt2_kv_reset() instead of a host memset;
- *   - greedy steps take the argmax on the GPU (same first-maximum rule) and
- *     copy back one id per sequence instead of the full logits row;
- *   - the prefill call computes the LM head of the last prompt row only (the
- *     reference computes all rows and then discards them);
- *   - n_prompt + n_tokens beyond the context is rejected (exit 2) instead of
- *     writing past the KV cache;
- *   - JSON gains "backend", "device", "tokens_per_sec_aggregate" and
- *     "decode_bytes_per_step" / "decode_gbps".
+ * Contract kept from the reference driver (src/runtime_main.c), because the
+ * reference's Python CLI parses it (edgecore/bench.py:124-152,
+ * edgecore/verify.py:126-199, scripts/smoke_test.sh:17-86):
+ *   - the flags and their defaults (:163-191, :600-640);
+ *   - the JSON keys of each mode in the reference's order, with %.3f times,
+ *     %.6g logits and null for non-finite values (:400-590);
+ *   - the --logits-bin layout: int32 n, int32 vocab, int32 tokens[n],
+ *     float32 logits[n][vocab] (:454-464);
+ *   - exit codes: 0 ok, 1 load or prompt failure, 2 usage error or a
+ *     --precision that differs from the file's weights (:610-662);
+ *   - what is timed: TTFT is the prompt's forward, a step is one forward of
+ *     `batch` tokens, tok/s and percentiles are computed as in :381-396 and
+ *     :529-554; prompts are clamped to eff_ctx - 8 tokens;
+ *   - sampling: the LCG seeded with --seed, one draw per batch row in row
+ *     order; row 0's tokens are the generated ids.
+ *
+ * Everything else is this driver's own: a table of options that also prints
+ * the help, core pinning from sysfs topology, a small JSON emitter, and a
+ * Decoder object that owns the per-step buffers.  Differences in behaviour,
+ * all additive or result-preserving: the KV cache is cleared on the device
+ * (gpt2_kv_reset); greedy steps take the argmax on the GPU and copy back one
+ * id per row; the prompt's forward computes the LM head of its last row only;
+ * a prompt plus n-tokens beyond the context is refused (exit 2) instead of
+ * writing past the cache; the JSON ends with extra keys (backend, device,
+ * token_ids, tokens_per_sec_aggregate, decode_bytes_per_step, decode_gbps).
  */
 #define _GNU_SOURCE
 #include "edgecore.h"
 
 #include <math.h>
 #include <sched.h>
+#include <stddef.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 
 /* ------------------------------------------------------------------ */
-/* CPU affinity (policy names of src/runtime_main.c:108-133)            */
-/* ------------------------------------------------------------------ */
-
-typedef struct {
-    char requested[32];
-    int cpus[256];
-    int n;
-    int applied;
-    char error[96];
-} Affinity;
-
-static void cpuset_list(const cpu_set_t *set, int *cpus, int *n)
-{
-    *n = 0;
-    for (int i = 0; i < CPU_SETSIZE && *n < 256; i++)
-        if (CPU_ISSET(i, set)) cpus[(*n)++] = i;
-}
-
-static int parse_cpu_list(const char *s, cpu_set_t *set)
-{
-    CPU_ZERO(set);
-    while (*s) {
-        while (*s == ' ' || *s == ',') s++;
-        if (!*s) break;
-        char *end;
-        long c = strtol(s, &end, 10);
-        if (end == s || c < 0 || c >= CPU_SETSIZE) return -1;
-        CPU_SET((int)c, set);
-        s = end;
-    }
-    return 0;
-}
-
-/* first logical CPU of each (physical id, core id) pair in /proc/cpuinfo */
-static int physical_cpuset(cpu_set_t *set)
-{
-    CPU_ZERO(set);
-    FILE *f = fopen("/proc/cpuinfo", "r");
-    if (!f) return -1;
-    char line[256];
-    int proc = -1, phys = -1, core = -1, n = 0;
-    struct { int phys, core, cpu; } seen[512];
-    while (fgets(line, sizeof line, f)) {
-        int v;
-        if (sscanf(line, "processor : %d", &v) == 1) { proc = v; phys = core = -1; }
-        else if (sscanf(line, "physical id : %d", &v) == 1) phys = v;
-        else if (sscanf(line, "core id : %d", &v) == 1) core = v;
-        if (proc >= 0 && phys >= 0 && core >= 0) {
-            int k = 0;
-            while (k < n && !(seen[k].phys == phys && seen[k].core == core)) k++;
-            if (k == n && n < 512) { seen[n].phys = phys; seen[n].core = core; seen[n].cpu = proc; n++; }
-            else if (k < n && proc < seen[k].cpu) seen[k].cpu = proc;
-            proc = -1;
-        }
-    }
-    fclose(f);
-    for (int k = 0; k < n; k++) CPU_SET(seen[k].cpu, set);
-    return n > 0 ? 0 : -1;
-}
-
-static void affinity_apply(const char *policy, Affinity *a)
-{
-    memset(a, 0, sizeof *a);
-    snprintf(a->requested, sizeof a->requested, "%s", policy);
-    cpu_set_t set;
-    int want = 0;
-    if (!strcmp(policy, "physical") || !strcmp(policy, "auto")) {
-        if (physical_cpuset(&set) == 0) want = 1;
-        else snprintf(a->error, sizeof a->error, "physical core enumeration failed");
-    } else if (strcmp(policy, "none")) {
-        if (parse_cpu_list(policy, &set) == 0) want = 1;
-        else snprintf(a->error, sizeof a->error, "bad cpu list");
-    }
-    if (want) {
-        if (sched_setaffinity(0, sizeof set, &set) != 0) snprintf(a->error, sizeof a->error, "sched_setaffinity failed");
-        else a->applied = 1;
-    }
-    cpu_set_t cur;
-    CPU_ZERO(&cur);
-    sched_getaffinity(0, sizeof cur, &cur);
-    cpuset_list(&cur, a->cpus, &a->n);
-}
-
-static void json_str(FILE *o, const char *s)
-{
-    fputc('"', o);
-    for (; *s; s++) {
-        unsigned char c = (unsigned char)*s;
-        if (c == '"') fputs("\\\"", o);
-        else if (c == '\\') fputs("\\\\", o);
-        else if (c == '\n') fputs("\\n", o);
-        else if (c == '\t') fputs("\\t", o);
-        else if (c == '\r') fputs("\\r", o);
-        else if (c < 0x20) fprintf(o, "\\u%04x", c);
-        else fputc(c, o);
-    }
-    fputc('"', o);
-}
-
-static void emit_affinity(FILE *o, const Affinity *a)
-{
-    fprintf(o, "  \"affinity_requested\": ");
-    json_str(o, a->requested);
-    fprintf(o, ",\n  \"affinity_applied\": %s,\n  \"affinity_cpus\": [", a->applied ? "true" : "false");
-    for (int i = 0; i < a->n; i++) fprintf(o, "%s%d", i ? "," : "", a->cpus[i]);
-    fprintf(o, "]");
-}
-
-/* ------------------------------------------------------------------ */
-/* arguments                                                            */
+/* configuration: one table drives parsing and the help text            */
 /* ------------------------------------------------------------------ */
 
 typedef struct {
     const char *model, *mode, *precision, *prompt, *tokens_file, *output, *affinity, *logits_bin;
-    int threads, batch, n_tokens, warmup, iters, seed, top_k, logits_limit, no_print, max_ctx;
-    float temp;
-    double load_time_ms;
-} Args;
+    int threads, batch, n_tokens, warmup, iters, seed, top_k, logits_limit, max_ctx, no_print;
+    double temp;
+    double load_ms; /* measured, not a flag */
+} Config;
 
-static void usage(const char *prog)
+enum { OPT_STR, OPT_INT, OPT_REAL, OPT_FLAG };
+
+typedef struct {
+    const char *flag;
+    int kind;
+    size_t at; /* offsetof(Config, field) */
+    const char *arg, *help;
+} Option;
+
+static const Option kOptions[] = {
+    {"--model", OPT_STR, offsetof(Config, model), "FILE", ".ecm model file (required)"},
+    {"--mode", OPT_STR, offsetof(Config, mode), "M", "generate | logits | bench (generate)"},
+    {"--precision", OPT_STR, offsetof(Config, precision), "P",
+     "fp16 | bf16 | int8 | auto; must agree with the file's weights (auto)"},
+    {"--threads", OPT_INT, offsetof(Config, threads), "N", "reported only: the forward runs on the GPU (1)"},
+    {"--batch", OPT_INT, offsetof(Config, batch), "N", "sequences decoded together (1)"},
+    {"--prompt", OPT_STR, offsetof(Config, prompt), "TEXT", "prompt text, encoded by the model's tokenizer"},
+    {"--tokens-file", OPT_STR, offsetof(Config, tokens_file), "FILE", "prompt as whitespace-separated ids"},
+    {"--n-tokens", OPT_INT, offsetof(Config, n_tokens), "N", "tokens to generate (32)"},
+    {"--temp", OPT_REAL, offsetof(Config, temp), "T", "sampling temperature; 0 is greedy (0)"},
+    {"--top-k", OPT_INT, offsetof(Config, top_k), "K", "sample among the K largest logits; 0 is all (0)"},
+    {"--seed", OPT_INT, offsetof(Config, seed), "S", "sampling seed (42)"},
+    {"--warmup", OPT_INT, offsetof(Config, warmup), "N", "untimed bench runs (1)"},
+    {"--iters", OPT_INT, offsetof(Config, iters), "N", "timed bench runs (1)"},
+    {"--logits-limit", OPT_INT, offsetof(Config, logits_limit), "N", "prompt tokens kept in logits mode (1024)"},
+    {"--max-ctx", OPT_INT, offsetof(Config, max_ctx), "N", "context to allocate; 0 is the model's (0)"},
+    {"--affinity", OPT_STR, offsetof(Config, affinity), "A",
+     "none | auto | physical | CPU list such as 0,2,4 (none)"},
+    {"--logits-bin", OPT_STR, offsetof(Config, logits_bin), "FILE", "also write raw logits (logits mode)"},
+    {"--output", OPT_STR, offsetof(Config, output), "FILE", "write the JSON here instead of stdout"},
+    {"--no-print", OPT_FLAG, offsetof(Config, no_print), NULL, "do not print the generated text"},
+};
+#define N_OPTIONS ((int)(sizeof kOptions / sizeof kOptions[0]))
+
+static void print_help(const char *prog)
 {
-    fprintf(stderr,
-            "usage: %s --model FILE --mode {generate|logits|bench} [options]\n"
-            "  --precision fp16|bf16|int8|auto (default auto; derived from .ecm weight dtype)\n"
-            "  --threads N            (accepted; the forward runs on the GPU)\n"
-            "  --batch N              (default 1)\n"
-            "  --prompt TEXT          prompt for generate/logits (byte-level vocabularies)\n"
-            "  --tokens-file FILE     token ids (whitespace separated) to use as prompt\n"
-            "  --n-tokens N           tokens to generate (default 32)\n"
-            "  --temp T               sampling temperature (default 0.0 = greedy)\n"
-            "  --top-k N              top-k sampling (default 0 = off)\n"
-            "  --seed N               rng seed\n"
-            "  --warmup N / --iters N bench warmup / iterations\n"
-            "  --logits-limit N       max prompt tokens for logits mode (default 1024)\n"
-            "  --max-ctx N            max context length (default 0 = use model's n_ctx)\n"
-            "  --affinity auto|none|physical|0[,2,..]  CPU affinity (default none)\n"
-            "  --logits-bin FILE      write raw logits (n, vocab, tokens, logits f32)\n"
-            "  --output FILE          JSON output file (default stdout)\n"
-            "  --no-print             suppress generated text on stdout\n"
-            "  GPU: device 0, or $EDGECORE_DEVICE\n",
-            prog);
+    fprintf(stderr, "usage: %s --model FILE [options]   (MI355X GPU forward; device 0 or $EDGECORE_DEVICE)\n", prog);
+    for (int i = 0; i < N_OPTIONS; i++) {
+        char left[48];
+        snprintf(left, sizeof left, "%s%s%s", kOptions[i].flag, kOptions[i].arg ? " " : "",
+                 kOptions[i].arg ? kOptions[i].arg : "");
+        fprintf(stderr, "  %-22s %s\n", left, kOptions[i].help);
+    }
 }
 
-/* the LCG state of src/runtime_main.c:205-211; sample_token (:213-248) is
-   ec_sample_full / ec_sample_candidates of the library */
-static unsigned long long rng_state;
+static void config_defaults(Config *c)
+{
+    memset(c, 0, sizeof *c);
+    c->mode = "generate";
+    c->precision = "auto";
+    c->affinity = "none";
+    c->prompt = "The quick brown fox jumps over the lazy dog";
+    c->threads = 1;
+    c->batch = 1;
+    c->n_tokens = 32;
+    c->warmup = 1;
+    c->iters = 1;
+    c->seed = 42;
+    c->logits_limit = 1024;
+}
 
-static int read_tokens(const char *path, int *out, int cap, int *n)
+/* 0 ok; 2 usage error (message printed) */
+static int config_parse(Config *c, int argc, char **argv)
+{
+    for (int i = 1; i < argc; i++) {
+        const Option *o = NULL;
+        for (int k = 0; k < N_OPTIONS && !o; k++)
+            if (!strcmp(argv[i], kOptions[k].flag)) o = &kOptions[k];
+        if (!o) {
+            fprintf(stderr, "unknown arg: %s\n", argv[i]);
+            print_help(argv[0]);
+            return 2;
+        }
+        char *field = (char *)c + o->at;
+        if (o->kind == OPT_FLAG) {
+            *(int *)field = 1;
+            continue;
+        }
+        if (i + 1 >= argc) {
+            fprintf(stderr, "%s needs a value\n", o->flag);
+            return 2;
+        }
+        const char *v = argv[++i];
+        if (o->kind == OPT_STR) *(const char **)field = v;
+        else if (o->kind == OPT_INT) *(int *)field = atoi(v);
+        else *(double *)field = atof(v);
+    }
+    if (!c->model) {
+        print_help(argv[0]);
+        return 2;
+    }
+    if (c->batch < 1) c->batch = 1;
+    if (c->n_tokens < 0) c->n_tokens = 0;
+    return 0;
+}
+
+/* ------------------------------------------------------------------ */
+/* CPU pinning                                                          */
+/* ------------------------------------------------------------------ */
+
+typedef struct {
+    const char *policy;
+    int applied;
+    int ncpu;
+    int cpu[1024];
+} CpuPin;
+
+/* the lowest CPU of a sysfs cpu list ("3", "3,67", "2-3,66-67") that is in
+ * `allowed`, or -1 */
+static int lowest_allowed(const char *path, const cpu_set_t *allowed)
 {
     FILE *f = fopen(path, "r");
-    if (!f) { perror("tokens file"); return -1; }
-    int v;
-    *n = 0;
-    while (fscanf(f, "%d", &v) == 1)
-        if (*n < cap) out[(*n)++] = v;
+    if (!f) return -1;
+    char buf[256];
+    const int got = fgets(buf, sizeof buf, f) != NULL;
     fclose(f);
-    return 0;
+    if (!got) return -1;
+    int best = -1;
+    for (char *p = buf; *p && *p != '\n';) {
+        char *end;
+        long lo = strtol(p, &end, 10), hi = lo;
+        if (end == p) break;
+        if (*end == '-') {
+            p = end + 1;
+            hi = strtol(p, &end, 10);
+        }
+        for (long c = lo; c <= hi && c < CPU_SETSIZE; c++)
+            if (CPU_ISSET((int)c, allowed) && (best < 0 || c < best)) best = (int)c;
+        p = *end == ',' ? end + 1 : end;
+    }
+    return best;
 }
 
-static int load_prompt(GPT2 *g, const Args *a, int *toks, int cap, int *n)
+/* one CPU per physical core: the lowest allowed CPU among each core's
+ * hardware threads (sysfs topology/thread_siblings_list) */
+static int cores_only(const cpu_set_t *allowed, cpu_set_t *out)
 {
-    if (a->tokens_file) return read_tokens(a->tokens_file, toks, cap, n);
-    int r = tokenizer_encode(&g->tok, a->prompt, toks, cap);
-    if (r < 0) return -1;
-    *n = r;
-    return 0;
+    CPU_ZERO(out);
+    int n = 0;
+    for (int c = 0; c < CPU_SETSIZE; c++) {
+        if (!CPU_ISSET(c, allowed)) continue;
+        char path[96];
+        snprintf(path, sizeof path, "/sys/devices/system/cpu/cpu%d/topology/thread_siblings_list", c);
+        const int lead = lowest_allowed(path, allowed);
+        if (lead == c || lead < 0) {
+            CPU_SET(c, out);
+            n++;
+        }
+    }
+    return n;
 }
 
-static void die_forward(void)
+static int cpus_from_list(const char *s, cpu_set_t *out)
+{
+    CPU_ZERO(out);
+    int n = 0;
+    for (const char *p = s; *p;) {
+        if (*p == ',' || *p == ' ') {
+            p++;
+            continue;
+        }
+        char *end;
+        const long v = strtol(p, &end, 10);
+        if (end == p || v < 0 || v >= CPU_SETSIZE) return -1;
+        CPU_SET((int)v, out);
+        n++;
+        p = end;
+    }
+    return n > 0 ? 0 : -1;
+}
+
+static void pin_cpus(const char *policy, CpuPin *pin)
+{
+    memset(pin, 0, sizeof *pin);
+    pin->policy = policy;
+    cpu_set_t now, want;
+    CPU_ZERO(&now);
+    sched_getaffinity(0, sizeof now, &now);
+    int have = 0;
+    if (!strcmp(policy, "physical") || !strcmp(policy, "auto")) have = cores_only(&now, &want) > 0;
+    else if (strcmp(policy, "none")) have = cpus_from_list(policy, &want) == 0;
+    if (have && sched_setaffinity(0, sizeof want, &want) == 0) pin->applied = 1;
+    CPU_ZERO(&now);
+    sched_getaffinity(0, sizeof now, &now);
+    for (int c = 0; c < CPU_SETSIZE && pin->ncpu < 1024; c++)
+        if (CPU_ISSET(c, &now)) pin->cpu[pin->ncpu++] = c;
+}
+
+/* ------------------------------------------------------------------ */
+/* JSON output                                                          */
+/* ------------------------------------------------------------------ */
+
+typedef struct {
+    FILE *f;
+    int fields;
+} Json;
+
+static void json_text(FILE *f, const char *s)
+{
+    fputc('"', f);
+    for (const unsigned char *p = (const unsigned char *)s; *p; p++) {
+        switch (*p) {
+        case '"': fputs("\\\"", f); break;
+        case '\\': fputs("\\\\", f); break;
+        case '\n': fputs("\\n", f); break;
+        case '\r': fputs("\\r", f); break;
+        case '\t': fputs("\\t", f); break;
+        default:
+            if (*p < 0x20) fprintf(f, "\\u%04x", *p);
+            else fputc(*p, f);
+        }
+    }
+    fputc('"', f);
+}
+
+static void jkey(Json *j, const char *k)
+{
+    fprintf(j->f, "%s  \"%s\": ", j->fields++ ? ",\n" : "{\n", k);
+}
+static void jint(Json *j, const char *k, long long v) { jkey(j, k); fprintf(j->f, "%lld", v); }
+static void jms(Json *j, const char *k, double v) { jkey(j, k); fprintf(j->f, "%.3f", v); }
+static void jstr(Json *j, const char *k, const char *v) { jkey(j, k); json_text(j->f, v); }
+static void jraw(Json *j, const char *k, const char *v) { jkey(j, k); fputs(v, j->f); }
+static void jints(Json *j, const char *k, const int *v, int n)
+{
+    jkey(j, k);
+    fputc('[', j->f);
+    for (int i = 0; i < n; i++) fprintf(j->f, "%s%d", i ? "," : "", v[i]);
+    fputc(']', j->f);
+}
+static void jclose(Json *j) { fputs(j->fields ? "\n}\n" : "{}\n", j->f); }
+
+static void jpin(Json *j, const CpuPin *p)
+{
+    jstr(j, "affinity_requested", p->policy);
+    jraw(j, "affinity_applied", p->applied ? "true" : "false");
+    jints(j, "affinity_cpus", p->cpu, p->ncpu);
+}
+
+/* ------------------------------------------------------------------ */
+/* statistics (percentile indices of src/runtime_main.c:388-396)        */
+/* ------------------------------------------------------------------ */
+
+typedef struct {
+    double mean, p50, p95, p99, sum;
+} Summary;
+
+static int by_value(const void *a, const void *b)
+{
+    const double x = *(const double *)a, y = *(const double *)b;
+    return (x > y) - (x < y);
+}
+
+static Summary summarize(const double *v, int n)
+{
+    Summary s = {0, 0, 0, 0, 0};
+    if (n <= 0) return s;
+    double *sorted = malloc((size_t)n * sizeof *sorted);
+    memcpy(sorted, v, (size_t)n * sizeof *sorted);
+    qsort(sorted, (size_t)n, sizeof *sorted, by_value);
+    for (int i = 0; i < n; i++) s.sum += sorted[i];
+    s.mean = s.sum / n;
+    s.p50 = sorted[(n - 1) / 2];
+    s.p95 = sorted[(int)(n * 0.95)];
+    s.p99 = sorted[(int)(n * 0.99)];
+    free(sorted);
+    return s;
+}
+
+/* ------------------------------------------------------------------ */
+/* decoding                                                             */
+/* ------------------------------------------------------------------ */
+
+/* the reference's sampling state (src/runtime_main.c:205-211); the draw
+ * itself is ec_sample_full / ec_sample_candidates of the library */
+static unsigned long long g_lcg;
+
+typedef struct {
+    GPT2 *g;
+    int batch, top_k, ncand, use_topk;
+    float temp;
+    int *cur, *pos, *greedy;
+    float *rows;               /* [batch][vocab] when sampling */
+    float *cand_v;             /* [batch][top_k + 1] device top-k candidates */
+    int *cand_i, *cand_status;
+} Decoder;
+
+static void fail_forward(void)
 {
     fprintf(stderr, "forward failed: %s\n", ec_last_error());
     exit(1);
 }
 
-/* ------------------------------------------------------------------ */
-/* prefill + decode (gen_and_measure, src/runtime_main.c:293-362)       */
-/* ------------------------------------------------------------------ */
-
-static void gen_and_measure(GPT2 *g, const int *prompt, int nprompt, int n_gen, int batch, float temp,
-                            int top_k, double *tok_ms, int *out_ids, int *out_n, double *ttft_ms)
+static void decoder_init(Decoder *d, GPT2 *g, int batch, float temp, int top_k)
 {
-    int V = g->vocab;
-    int *ids = malloc((size_t)(nprompt + n_gen + 8) * sizeof(int));
-    memcpy(ids, prompt, (size_t)nprompt * sizeof(int));
-    int n_ids = nprompt;
-    int *ppos = malloc((size_t)nprompt * sizeof(int)), *pseq = malloc((size_t)nprompt * sizeof(int));
-    for (int i = 0; i < nprompt; i++) { ppos[i] = i; pseq[i] = 0; }
-    int *positions = malloc((size_t)batch * sizeof(int)), *cur = malloc((size_t)batch * sizeof(int));
-    int *next = malloc((size_t)batch * sizeof(int));
-    float *logits = temp > 0.0f ? malloc((size_t)batch * V * sizeof(float)) : NULL;
-    /* sampled steps select the top_k + 1 logits on the GPU when top_k allows */
-    const int use_topk = temp > 0.0f && top_k > 0 && top_k < V && top_k <= ec_topk_max();
-    const int nc = top_k + 1;
-    float *tk_vals = use_topk ? malloc((size_t)batch * nc * sizeof(float)) : NULL;
-    int *tk_idx = use_topk ? malloc((size_t)batch * nc * sizeof(int)) : NULL;
-    int *tk_status = use_topk ? malloc((size_t)batch * sizeof(int)) : NULL;
-    int first;
-
-    if (gpt2_kv_reset(g)) die_forward();
-    double t0 = now_sec();
-    if (gpt2_forward_ex(g, ids, ppos, pseq, nprompt, nprompt - 1, NULL, &first)) die_forward();
-    *ttft_ms = (now_sec() - t0) * 1000.0;
-
-    for (int b = 1; b < batch; b++) {
-        for (int i = 0; i < nprompt; i++) pseq[i] = b;
-        if (gpt2_forward_ex(g, ids, ppos, pseq, nprompt, nprompt, NULL, NULL)) die_forward();
+    memset(d, 0, sizeof *d);
+    d->g = g;
+    d->batch = batch;
+    d->temp = temp;
+    d->top_k = top_k;
+    const int V = g->vocab;
+    /* sampled steps select the top_k + 1 largest logits on the GPU when k allows */
+    d->use_topk = temp > 0.0f && top_k > 0 && top_k < V && top_k <= ec_topk_max();
+    d->ncand = top_k + 1;
+    d->cur = calloc((size_t)batch, sizeof(int));
+    d->pos = calloc((size_t)batch, sizeof(int));
+    d->greedy = calloc((size_t)batch, sizeof(int));
+    if (temp > 0.0f) d->rows = malloc((size_t)batch * V * sizeof(float));
+    if (d->use_topk) {
+        d->cand_v = malloc((size_t)batch * d->ncand * sizeof(float));
+        d->cand_i = malloc((size_t)batch * d->ncand * sizeof(int));
+        d->cand_status = malloc((size_t)batch * sizeof(int));
     }
-    for (int b = 0; b < batch; b++) cur[b] = ids[n_ids - 1];
+}
 
-    int npos = nprompt;
-    for (int step = 0; step < n_gen; step++) {
-        for (int b = 0; b < batch; b++) positions[b] = npos;
-        double s0 = now_sec();
-        int rc = use_topk ? gpt2_forward_topk(g, cur, positions, NULL, batch, 0, top_k, tk_vals, tk_idx, tk_status)
-                 : temp > 0.0f ? gpt2_forward_ex(g, cur, positions, NULL, batch, 0, logits, NULL)
-                               : gpt2_forward_ex(g, cur, positions, NULL, batch, 0, NULL, next);
-        if (rc) die_forward();
-        tok_ms[step] = (now_sec() - s0) * 1000.0;
-        for (int b = 0; b < batch; b++) {
-            int tok;
-            if (use_topk && !tk_status[b]) {
-                tok = ec_sample_candidates(tk_vals + (size_t)b * nc, tk_idx + (size_t)b * nc, nc, V, temp, top_k,
-                                           &rng_state);
-            } else if (use_topk) {  /* NaN or a tie at the top_k boundary: the whole row */
-                if (ec_last_logits(g, b, logits + (size_t)b * V)) die_forward();
-                tok = ec_sample_full(logits + (size_t)b * V, V, temp, top_k, &rng_state);
-            } else {
-                tok = temp > 0.0f ? ec_sample_full(logits + (size_t)b * V, V, temp, top_k, &rng_state) : next[b];
-            }
-            cur[b] = tok;
-            if (b == 0) ids[n_ids++] = tok;
+static void decoder_free(Decoder *d)
+{
+    free(d->cur); free(d->pos); free(d->greedy); free(d->rows);
+    free(d->cand_v); free(d->cand_i); free(d->cand_status);
+}
+
+/* Fill every slot with the prompt (slot 0 timed: the TTFT), leaving each
+ * slot's next input at the prompt's last token.  Returns the TTFT in ms. */
+static double decoder_prefill(Decoder *d, const int *prompt, int n)
+{
+    int *at = malloc((size_t)n * sizeof(int)), *slot = malloc((size_t)n * sizeof(int));
+    for (int i = 0; i < n; i++) at[i] = i;
+    if (gpt2_kv_reset(d->g)) fail_forward();
+    double ttft = 0.0;
+    for (int b = 0; b < d->batch; b++) {
+        for (int i = 0; i < n; i++) slot[i] = b;
+        int first;
+        const double t = now_sec();
+        /* slot 0 computes its last row's LM head (and argmax), as the
+         * reference's timed prompt forward does; the others skip it */
+        if (gpt2_forward_ex(d->g, prompt, at, slot, n, b == 0 ? n - 1 : n, NULL, b == 0 ? &first : NULL))
+            fail_forward();
+        if (b == 0) ttft = (now_sec() - t) * 1000.0;
+        d->cur[b] = prompt[n - 1];
+        d->pos[b] = n;
+    }
+    free(at);
+    free(slot);
+    return ttft;
+}
+
+/* One decode step of every row; writes row 0's new token.  Returns ms. */
+static double decoder_step(Decoder *d, int *row0_token)
+{
+    GPT2 *g = d->g;
+    const int V = g->vocab, B = d->batch;
+    const double t = now_sec();
+    int rc;
+    if (d->use_topk)
+        rc = gpt2_forward_topk(g, d->cur, d->pos, NULL, B, 0, d->top_k, d->cand_v, d->cand_i, d->cand_status);
+    else if (d->temp > 0.0f)
+        rc = gpt2_forward_ex(g, d->cur, d->pos, NULL, B, 0, d->rows, NULL);
+    else
+        rc = gpt2_forward_ex(g, d->cur, d->pos, NULL, B, 0, NULL, d->greedy);
+    if (rc) fail_forward();
+    const double ms = (now_sec() - t) * 1000.0;
+    for (int b = 0; b < B; b++) {
+        int tok = d->greedy[b];
+        if (d->use_topk && d->cand_status[b] == 0) {
+            tok = ec_sample_candidates(d->cand_v + (size_t)b * d->ncand, d->cand_i + (size_t)b * d->ncand, d->ncand,
+                                       V, d->temp, d->top_k, &g_lcg);
+        } else if (d->temp > 0.0f) {
+            float *row = d->rows + (size_t)b * V;
+            /* NaN or a tie at the k-th place: draw from the whole row */
+            if (d->use_topk && ec_last_logits(g, b, row)) fail_forward();
+            tok = ec_sample_full(row, V, d->temp, d->top_k, &g_lcg);
         }
-        npos++;
+        d->cur[b] = tok;
+        d->pos[b]++;
     }
-    *out_n = n_ids;
-    memcpy(out_ids, ids, (size_t)n_ids * sizeof(int));
-    free(ids); free(ppos); free(pseq); free(positions); free(cur); free(next); free(logits);
-    free(tk_vals); free(tk_idx); free(tk_status);
+    *row0_token = d->cur[0];
+    return ms;
 }
 
-static int cmp_double(const void *a, const void *b)
+/* a prefill and n_gen steps: TTFT, per-step times and row 0's ids */
+typedef struct {
+    double ttft_ms;
+    double *step_ms;
+    int *ids; /* prompt followed by the generated tokens of row 0 */
+    int n_ids;
+} Run;
+
+static void run_once(GPT2 *g, const Config *c, const int *prompt, int n, float temp, Run *r)
 {
-    double x = *(const double *)a, y = *(const double *)b;
-    return x < y ? -1 : x > y;
+    Decoder d;
+    decoder_init(&d, g, c->batch, temp, c->top_k);
+    r->step_ms = malloc((size_t)(c->n_tokens > 0 ? c->n_tokens : 1) * sizeof(double));
+    r->ids = malloc((size_t)(n + c->n_tokens) * sizeof(int));
+    memcpy(r->ids, prompt, (size_t)n * sizeof(int));
+    r->n_ids = n;
+    r->ttft_ms = decoder_prefill(&d, prompt, n);
+    for (int s = 0; s < c->n_tokens; s++) r->step_ms[s] = decoder_step(&d, &r->ids[r->n_ids++]);
+    decoder_free(&d);
 }
 
-/* percentiles of src/runtime_main.c:388-396 */
-static void percentiles(const double *v, int n, double *p50, double *p95, double *p99)
+static void run_free(Run *r)
 {
-    *p50 = *p95 = *p99 = 0.0;
-    if (n <= 0) return;
-    double *s = malloc((size_t)n * sizeof(double));
-    memcpy(s, v, (size_t)n * sizeof(double));
-    qsort(s, (size_t)n, sizeof(double), cmp_double);
-    *p50 = s[(n - 1) / 2];
-    *p95 = s[(int)(n * 0.95) < n ? (int)(n * 0.95) : n - 1];
-    *p99 = s[(int)(n * 0.99) < n ? (int)(n * 0.99) : n - 1];
-    free(s);
+    free(r->step_ms);
+    free(r->ids);
 }
 
-/* algorithmic HBM bytes of one decode step at batch b and mean position p:
- * every weight byte once, plus the K/V rows read by attention */
-static double decode_bytes(const GPT2 *g, int batch, double mean_pos)
-{
-    double E = g->n_embd, F = g->intermediate, kv = g->n_kv_embd, V = g->vocab, L = g->n_layer;
-    double wb = g->precision == 0 ? 1.0 : 2.0;
-    double lin = g->arch == ARCH_QWEN2 ? (E * E * 2 + 2 * kv * E + 3 * F * E) : (12 * E * E);
-    double per_layer = lin * wb + (g->precision == 0 ? 4.0 * (lin / E) : 0.0);
-    double kvread = (mean_pos + 1.0) * kv * 2 * 2 * batch;
-    return L * (per_layer + kvread) + V * E * 2.0;
-}
+/* ------------------------------------------------------------------ */
+/* modes                                                                */
+/* ------------------------------------------------------------------ */
 
-static void emit_common(FILE *o, const GPT2 *g, const Args *a)
+/* the prompt as ids: --tokens-file if given, else --prompt through the
+ * tokenizer; at most `cap` ids.  0 ok, -1 failure. */
+static int prompt_ids(GPT2 *g, const Config *c, int *ids, int cap, int *n)
 {
-    char dev[512];
-    if (ec_device_info(dev, sizeof dev) < 0) snprintf(dev, sizeof dev, "null");
-    fprintf(o, "  \"model\": ");
-    json_str(o, g->model_name);
-    fprintf(o, ",\n  \"precision\": \"%s\",\n", a->precision);
-    fprintf(o, "  \"backend\": \"hip-gfx950\",\n  \"device\": %s,\n", dev);
-    fprintf(o, "  \"threads\": %d,\n", a->threads);
-}
-
-static int mode_generate(GPT2 *g, const Args *a, const Affinity *aff)
-{
-    int toks[4096], n;
-    if (load_prompt(g, a, toks, 4096, &n)) { fprintf(stderr, "prompt load failed\n"); return 1; }
-    if (n < 1) { fprintf(stderr, "empty prompt\n"); return 1; }
-    int eff = gpt2_eff_ctx(g);
-    if (n > eff - 8) n = eff - 8;
-    if (n < 1 || n + a->n_tokens > eff) {
-        fprintf(stderr, "prompt (%d) + n-tokens (%d) exceeds the context (%d); raise --max-ctx\n", n, a->n_tokens, eff);
-        return 2;
+    *n = 0;
+    if (!c->tokens_file) {
+        const int k = tokenizer_encode(&g->tok, c->prompt, ids, cap);
+        if (k < 0) return -1;
+        *n = k;
+        return 0;
     }
-    int *ids = malloc((size_t)(n + a->n_tokens + 8) * sizeof(int));
-    double *tok_ms = malloc((size_t)(a->n_tokens > 0 ? a->n_tokens : 1) * sizeof(double));
-    double ttft = 0;
-    int out_n = 0;
-    gen_and_measure(g, toks, n, a->n_tokens, a->batch, a->temp, a->top_k, tok_ms, ids, &out_n, &ttft);
-    double sum = 0;
-    for (int i = 0; i < a->n_tokens; i++) sum += tok_ms[i];
-    double tpot = a->n_tokens ? sum / a->n_tokens : 0;
-    double total_s = (sum + ttft) / 1000.0;
-    double tps = total_s > 0 ? a->n_tokens / total_s : 0;
-    double p50, p95, p99;
-    percentiles(tok_ms, a->n_tokens, &p50, &p95, &p99);
-    char *text = a->no_print ? NULL : tokenizer_decode(&g->tok, ids, out_n);
-    FILE *o = a->output ? fopen(a->output, "w") : stdout;
-    if (!o) { perror(a->output); return 1; }
-    fprintf(o, "{\n  \"mode\": \"generate\",\n");
-    emit_common(o, g, a);
-    fprintf(o, "  \"batch\": %d,\n  \"load_time_ms\": %.3f,\n", a->batch, a->load_time_ms);
-    emit_affinity(o, aff);
-    fprintf(o, ",\n  \"n_prompt_tokens\": %d,\n  \"n_generated_tokens\": %d,\n", n, a->n_tokens);
-    fprintf(o, "  \"ttft_ms\": %.3f,\n  \"cold_start_ms\": %.3f,\n", ttft, a->load_time_ms + ttft);
-    fprintf(o, "  \"tpot_avg_ms\": %.3f,\n  \"tokens_per_sec\": %.3f,\n", tpot, tps);
-    fprintf(o, "  \"p50_ms\": %.3f,\n  \"p95_ms\": %.3f,\n  \"p99_ms\": %.3f,\n", p50, p95, p99);
-    fprintf(o, "  \"token_ids\": [");
-    for (int i = n; i < out_n; i++) fprintf(o, "%s%d", i > n ? "," : "", ids[i]);
-    fprintf(o, "],\n  \"peak_rss_gb\": %.3f", peak_rss_gb());
-    if (text) {
-        fprintf(o, ",\n  \"text\": ");
-        json_str(o, text);
+    FILE *f = fopen(c->tokens_file, "r");
+    if (!f) {
+        perror("tokens file");
+        return -1;
     }
-    fprintf(o, "\n}\n");
-    if (a->output) fclose(o);
-    if (text) { printf("%s\n", text); free(text); }
-    free(ids);
-    free(tok_ms);
+    int v;
+    while (*n < cap && fscanf(f, "%d", &v) == 1) ids[(*n)++] = v;
+    fclose(f);
     return 0;
 }
 
-static int mode_logits(GPT2 *g, const Args *a, const Affinity *aff)
+#define PROMPT_CAP 4096
+
+/* the prompt for generate/bench, clamped to eff_ctx - 8; 0 ok or an exit code */
+static int decode_prompt(GPT2 *g, const Config *c, int *ids, int *n)
 {
-    int toks[4096], n;
-    if (load_prompt(g, a, toks, 4096, &n)) { fprintf(stderr, "prompt load failed\n"); return 1; }
+    if (prompt_ids(g, c, ids, PROMPT_CAP, n)) {
+        fprintf(stderr, "prompt load failed\n");
+        return 1;
+    }
+    if (*n < 1) {
+        fprintf(stderr, "empty prompt\n");
+        return 1;
+    }
+    const int ctx = gpt2_eff_ctx(g);
+    if (*n > ctx - 8) *n = ctx - 8;
+    if (*n < 1 || *n + c->n_tokens > ctx) {
+        fprintf(stderr, "prompt (%d) + n-tokens (%d) exceeds the context (%d); raise --max-ctx\n", *n, c->n_tokens,
+                ctx);
+        return 2;
+    }
+    return 0;
+}
+
+static FILE *open_output(const Config *c)
+{
+    if (!c->output) return stdout;
+    FILE *f = fopen(c->output, "w");
+    if (!f) perror(c->output);
+    return f;
+}
+
+static void device_json(char *buf, int len)
+{
+    if (ec_device_info(buf, len) < 0) snprintf(buf, (size_t)len, "null");
+}
+
+/* algorithmic HBM bytes of one decode step of `batch` tokens at mean
+ * position p: every weight byte once (and int8 row scales), plus the fp16
+ * K/V rows that attention reads */
+static double step_bytes(const GPT2 *g, int batch, double p)
+{
+    const double E = g->n_embd, F = g->intermediate, kv = g->n_kv_embd, L = g->n_layer;
+    const double lin = g->arch == ARCH_QWEN2 ? 2 * E * E + 2 * kv * E + 3 * F * E : 12 * E * E;
+    const double weights = g->precision == 0 ? lin + 4 * (lin / E) : 2 * lin;
+    return L * (weights + (p + 1) * kv * 4 * batch) + 2.0 * g->vocab * E;
+}
+
+static int mode_generate(GPT2 *g, const Config *c, const CpuPin *pin)
+{
+    int prompt[PROMPT_CAP], n;
+    int rc = decode_prompt(g, c, prompt, &n);
+    if (rc) return rc;
+    g_lcg = (unsigned long long)(unsigned long)c->seed;
+    Run r;
+    run_once(g, c, prompt, n, (float)c->temp, &r);
+    const Summary s = summarize(r.step_ms, c->n_tokens);
+    const double wall = (s.sum + r.ttft_ms) / 1000.0;
+    char *text = c->no_print ? NULL : tokenizer_decode(&g->tok, r.ids, r.n_ids);
+    FILE *f = open_output(c);
+    if (!f) return 1;
+    char dev[512];
+    device_json(dev, sizeof dev);
+    Json j = {f, 0};
+    jstr(&j, "mode", "generate");
+    jstr(&j, "model", g->model_name);
+    jstr(&j, "precision", c->precision);
+    jint(&j, "threads", c->threads);
+    jint(&j, "batch", c->batch);
+    jms(&j, "load_time_ms", c->load_ms);
+    jpin(&j, pin);
+    jint(&j, "n_prompt_tokens", n);
+    jint(&j, "n_generated_tokens", c->n_tokens);
+    jms(&j, "ttft_ms", r.ttft_ms);
+    jms(&j, "cold_start_ms", c->load_ms + r.ttft_ms);
+    jms(&j, "tpot_avg_ms", s.mean);
+    jms(&j, "tokens_per_sec", wall > 0 ? c->n_tokens / wall : 0.0);
+    jms(&j, "p50_ms", s.p50);
+    jms(&j, "p95_ms", s.p95);
+    jms(&j, "p99_ms", s.p99);
+    jms(&j, "peak_rss_gb", peak_rss_gb());
+    if (text) jstr(&j, "text", text);
+    jstr(&j, "backend", "hip-gfx950");
+    jraw(&j, "device", dev);
+    jints(&j, "token_ids", r.ids + n, r.n_ids - n);
+    jclose(&j);
+    if (f != stdout) fclose(f);
+    if (text) {
+        printf("%s\n", text);
+        free(text);
+    }
+    run_free(&r);
+    return 0;
+}
+
+static int mode_logits(GPT2 *g, const Config *c, const CpuPin *pin)
+{
+    int toks[PROMPT_CAP], n;
+    if (prompt_ids(g, c, toks, PROMPT_CAP, &n)) {
+        fprintf(stderr, "prompt load failed\n");
+        return 1;
+    }
     if (n < 1) return 1;
-    if (n > a->logits_limit) n = a->logits_limit;
+    if (n > c->logits_limit) n = c->logits_limit;
     if (n > gpt2_eff_ctx(g)) {
         fprintf(stderr, "prompt (%d) exceeds the context (%d); raise --max-ctx\n", n, gpt2_eff_ctx(g));
         return 2;
     }
-    int V = g->vocab;
-    int *pos = malloc((size_t)n * sizeof(int)), *seq = malloc((size_t)n * sizeof(int));
-    float *logits = malloc((size_t)n * V * sizeof(float));
-    for (int i = 0; i < n; i++) { pos[i] = i; seq[i] = 0; }
-    if (gpt2_kv_reset(g) || gpt2_forward_ex(g, toks, pos, seq, n, 0, logits, NULL)) die_forward();
-    if (a->logits_bin) {
-        FILE *b = fopen(a->logits_bin, "wb");
-        if (!b) { perror("logits bin"); return 1; }
-        int32_t hdr[2] = {n, V};
-        fwrite(hdr, 4, 2, b);
-        fwrite(toks, 4, (size_t)n, b);
-        fwrite(logits, 4, (size_t)n * V, b);
+    const int V = g->vocab;
+    int *at = malloc((size_t)n * sizeof(int)), *slot = calloc((size_t)n, sizeof(int));
+    float *lg = malloc((size_t)n * V * sizeof(float));
+    for (int i = 0; i < n; i++) at[i] = i;
+    if (gpt2_kv_reset(g) || gpt2_forward_ex(g, toks, at, slot, n, 0, lg, NULL)) fail_forward();
+    if (c->logits_bin) {
+        FILE *b = fopen(c->logits_bin, "wb");
+        if (!b) {
+            perror("logits bin");
+            return 1;
+        }
+        const int32_t head[2] = {n, V};
+        fwrite(head, sizeof head, 1, b);
+        fwrite(toks, sizeof(int32_t), (size_t)n, b);
+        fwrite(lg, sizeof(float), (size_t)n * V, b);
         fclose(b);
     }
-    FILE *o = a->output ? fopen(a->output, "w") : stdout;
-    if (!o) { perror(a->output); return 1; }
-    fprintf(o, "{\n");
-    emit_common(o, g, a);
-    fprintf(o, "  \"load_time_ms\": %.3f,\n", a->load_time_ms);
-    emit_affinity(o, aff);
-    fprintf(o, ",\n  \"n_tokens\": %d,\n  \"tokens\": [", n);
-    for (int i = 0; i < n; i++) fprintf(o, "%s%d", i ? "," : "", toks[i]);
-    fprintf(o, "],\n  \"logits\": [\n");
+    FILE *f = open_output(c);
+    if (!f) return 1;
+    Json j = {f, 0};
+    jstr(&j, "model", g->model_name);
+    jstr(&j, "precision", c->precision);
+    jint(&j, "threads", c->threads);
+    jms(&j, "load_time_ms", c->load_ms);
+    jpin(&j, pin);
+    jint(&j, "n_tokens", n);
+    jints(&j, "tokens", toks, n);
+    jkey(&j, "logits");
+    fputs("[\n", f);
     for (int i = 0; i < n; i++) {
-        fprintf(o, "    [");
-        for (int j = 0; j < V; j++) {
-            float v = logits[(size_t)i * V + j];
-            if (j) fputc(',', o);
-            if (isfinite(v)) fprintf(o, "%.6g", v);
-            else fputs("null", o);
+        fputs("    [", f);
+        const float *row = lg + (size_t)i * V;
+        for (int v = 0; v < V; v++) {
+            if (v) fputc(',', f);
+            if (isfinite(row[v])) fprintf(f, "%.6g", row[v]);
+            else fputs("null", f);
         }
-        fprintf(o, "]%s\n", i + 1 < n ? "," : "");
+        fprintf(f, "]%s\n", i + 1 < n ? "," : "");
     }
-    fprintf(o, "  ]\n}\n");
-    if (a->output) fclose(o);
-    free(pos); free(seq); free(logits);
+    fputs("  ]", f);
+    jclose(&j);
+    if (f != stdout) fclose(f);
+    free(at);
+    free(slot);
+    free(lg);
     return 0;
 }
 
-static int mode_bench(GPT2 *g, const Args *a, const Affinity *aff)
+static int mode_bench(GPT2 *g, const Config *c, const CpuPin *pin)
 {
-    int toks[4096], n;
-    if (load_prompt(g, a, toks, 4096, &n)) { fprintf(stderr, "prompt load failed\n"); return 1; }
-    if (n < 1) { fprintf(stderr, "empty prompt\n"); return 1; }
-    int eff = gpt2_eff_ctx(g);
-    if (n > eff - 8) n = eff - 8;
-    if (n < 1 || n + a->n_tokens > eff) {
-        fprintf(stderr, "prompt (%d) + n-tokens (%d) exceeds the context (%d); raise --max-ctx\n", n, a->n_tokens, eff);
-        return 2;
+    int prompt[PROMPT_CAP], n;
+    int rc = decode_prompt(g, c, prompt, &n);
+    if (rc) return rc;
+    const int iters = c->iters > 0 ? c->iters : 1, B = c->batch, nt = c->n_tokens;
+    Run r;
+    for (int w = 0; w < c->warmup; w++) {
+        run_once(g, c, prompt, n, 0.0f, &r);
+        run_free(&r);
     }
-    int nt = a->n_tokens;
-    int total_gen = a->batch * nt;
-    double *tok_ms = malloc((size_t)(nt > 0 ? nt : 1) * sizeof(double));
-    int *ids = malloc((size_t)(n + nt + 8) * sizeof(int));
-    for (int w = 0; w < a->warmup; w++) {
-        double ttft; int out_n;
-        gen_and_measure(g, toks, n, nt, a->batch, 0, 0, tok_ms, ids, &out_n, &ttft);
-    }
-    int iters = a->iters > 0 ? a->iters : 1;
-    double *all_ms = malloc((size_t)(total_gen * iters + 1) * sizeof(double));
-    double *ttfts = malloc((size_t)iters * sizeof(double));
-    double step_sum = 0;
-    int idx = 0;
+    /* every step's time counts once per row it decoded (src/runtime_main.c:521-526) */
+    const int per_token = B * nt * iters;
+    double *tok_ms = malloc((size_t)(per_token > 0 ? per_token : 1) * sizeof(double));
+    double *ttft = malloc((size_t)iters * sizeof(double));
+    double step_total = 0.0;
+    int k = 0;
     for (int it = 0; it < iters; it++) {
-        double ttft; int out_n;
-        gen_and_measure(g, toks, n, nt, a->batch, 0, 0, tok_ms, ids, &out_n, &ttft);
-        ttfts[it] = ttft;
-        for (int i = 0; i < nt; i++) {
-            step_sum += tok_ms[i];
-            for (int b = 0; b < a->batch; b++) all_ms[idx++] = tok_ms[i];
+        run_once(g, c, prompt, n, 0.0f, &r);
+        ttft[it] = r.ttft_ms;
+        for (int s = 0; s < nt; s++) {
+            step_total += r.step_ms[s];
+            for (int b = 0; b < B; b++) tok_ms[k++] = r.step_ms[s];
         }
+        run_free(&r);
     }
-    int N = idx;
-    double sum = 0;
-    for (int i = 0; i < N; i++) sum += all_ms[i];
-    double avg = N ? sum / N : 0, p50, p95, p99, t50, t95, t99;
-    percentiles(all_ms, N, &p50, &p95, &p99);
-    percentiles(ttfts, iters, &t50, &t95, &t99);
-    double ttft_avg = 0;
-    for (int i = 0; i < iters; i++) ttft_avg += ttfts[i] / iters;
-    double gen_s = sum / 1000.0;
-    double tps = gen_s > 0 ? N / gen_s : 0;
-    double agg = step_sum > 0 ? (double)total_gen * iters / (step_sum / 1000.0) : 0;
-    double dbytes = decode_bytes(g, a->batch, n + (nt - 1) / 2.0);
-    double step_avg_s = iters * nt > 0 ? step_sum / 1000.0 / (iters * nt) : 0;
-    FILE *o = a->output ? fopen(a->output, "w") : stdout;
-    if (!o) { perror(a->output); return 1; }
-    fprintf(o, "{\n  \"mode\": \"bench\",\n");
-    emit_common(o, g, a);
-    fprintf(o, "  \"batch\": %d,\n  \"load_time_ms\": %.3f,\n", a->batch, a->load_time_ms);
-    emit_affinity(o, aff);
-    fprintf(o, ",\n  \"n_prompt_tokens\": %d,\n  \"n_generated_tokens\": %d,\n  \"iterations\": %d,\n", n,
-            total_gen, iters);
-    fprintf(o, "  \"avg_token_ms\": %.3f,\n  \"p50_ms\": %.3f,\n  \"p95_ms\": %.3f,\n  \"p99_ms\": %.3f,\n", avg,
-            p50, p95, p99);
-    fprintf(o, "  \"ttft_avg_ms\": %.3f,\n  \"cold_start_ms\": %.3f,\n", ttft_avg, a->load_time_ms + ttft_avg);
-    fprintf(o, "  \"ttft_p50_ms\": %.3f,\n  \"ttft_p95_ms\": %.3f,\n  \"ttft_p99_ms\": %.3f,\n", t50, t95, t99);
-    fprintf(o, "  \"tokens_per_sec\": %.3f,\n  \"tokens_per_sec_aggregate\": %.3f,\n", tps, agg);
-    fprintf(o, "  \"decode_bytes_per_step\": %.0f,\n  \"decode_gbps\": %.2f,\n", dbytes,
-            step_avg_s > 0 ? dbytes / step_avg_s / 1e9 : 0.0);
-    fprintf(o, "  \"total_generation_sec\": %.3f,\n  \"peak_rss_gb\": %.3f\n}\n", gen_s, peak_rss_gb());
-    if (a->output) fclose(o);
-    free(tok_ms); free(ids); free(all_ms); free(ttfts);
+    const Summary tok = summarize(tok_ms, k), first = summarize(ttft, iters);
+    const double gen_s = tok.sum / 1000.0;
+    const double bytes = step_bytes(g, B, n + (nt - 1) / 2.0);
+    const double step_s = iters * nt > 0 ? step_total / 1000.0 / (iters * nt) : 0.0;
+    FILE *f = open_output(c);
+    if (!f) return 1;
+    char dev[512];
+    device_json(dev, sizeof dev);
+    Json j = {f, 0};
+    jstr(&j, "mode", "bench");
+    jstr(&j, "model", g->model_name);
+    jstr(&j, "precision", c->precision);
+    jint(&j, "threads", c->threads);
+    jint(&j, "batch", B);
+    jms(&j, "load_time_ms", c->load_ms);
+    jpin(&j, pin);
+    jint(&j, "n_prompt_tokens", n);
+    jint(&j, "n_generated_tokens", B * nt);
+    jint(&j, "iterations", iters);
+    jms(&j, "avg_token_ms", tok.mean);
+    jms(&j, "p50_ms", tok.p50);
+    jms(&j, "p95_ms", tok.p95);
+    jms(&j, "p99_ms", tok.p99);
+    jms(&j, "ttft_avg_ms", first.mean);
+    jms(&j, "cold_start_ms", c->load_ms + first.mean);
+    jms(&j, "ttft_p50_ms", first.p50);
+    jms(&j, "ttft_p95_ms", first.p95);
+    jms(&j, "ttft_p99_ms", first.p99);
+    jms(&j, "tokens_per_sec", gen_s > 0 ? k / gen_s : 0.0);
+    jms(&j, "total_generation_sec", gen_s);
+    jms(&j, "peak_rss_gb", peak_rss_gb());
+    jstr(&j, "backend", "hip-gfx950");
+    jraw(&j, "device", dev);
+    jms(&j, "tokens_per_sec_aggregate", step_total > 0 ? (double)B * nt * iters / (step_total / 1000.0) : 0.0);
+    jint(&j, "decode_bytes_per_step", (long long)bytes);
+    jkey(&j, "decode_gbps");
+    fprintf(f, "%.2f", step_s > 0 ? bytes / step_s / 1e9 : 0.0);
+    jclose(&j);
+    if (f != stdout) fclose(f);
+    free(tok_ms);
+    free(ttft);
     return 0;
 }
+
+/* ------------------------------------------------------------------ */
+
+static const char *dtype_name(int precision) { return precision == 2 ? "bf16" : precision == 1 ? "fp16" : "int8"; }
 
 int main(int argc, char **argv)
 {
-    Args a;
-    memset(&a, 0, sizeof a);
-    a.mode = "generate"; a.precision = "auto"; a.affinity = "none";
-    a.threads = 1; a.batch = 1; a.n_tokens = 32; a.warmup = 1; a.iters = 1; a.logits_limit = 1024;
-    a.seed = 42;
-    a.prompt = "The quick brown fox jumps over the lazy dog";
-    if (argc < 2) { usage(argv[0]); return 2; }
-    for (int i = 1; i < argc; i++) {
-        const char *s = argv[i];
-#define VAL() (i + 1 < argc ? argv[++i] : (fprintf(stderr, "missing value for %s\n", s), exit(2), ""))
-        if (!strcmp(s, "--model")) a.model = VAL();
-        else if (!strcmp(s, "--mode")) a.mode = VAL();
-        else if (!strcmp(s, "--precision")) a.precision = VAL();
-        else if (!strcmp(s, "--threads")) a.threads = atoi(VAL());
-        else if (!strcmp(s, "--batch")) a.batch = atoi(VAL());
-        else if (!strcmp(s, "--prompt")) a.prompt = VAL();
-        else if (!strcmp(s, "--tokens-file")) a.tokens_file = VAL();
-        else if (!strcmp(s, "--n-tokens")) a.n_tokens = atoi(VAL());
-        else if (!strcmp(s, "--temp")) a.temp = (float)atof(VAL());
-        else if (!strcmp(s, "--top-k")) a.top_k = atoi(VAL());
-        else if (!strcmp(s, "--seed")) a.seed = atoi(VAL());
-        else if (!strcmp(s, "--warmup")) a.warmup = atoi(VAL());
-        else if (!strcmp(s, "--iters")) a.iters = atoi(VAL());
-        else if (!strcmp(s, "--logits-limit")) a.logits_limit = atoi(VAL());
-        else if (!strcmp(s, "--max-ctx")) a.max_ctx = atoi(VAL());
-        else if (!strcmp(s, "--output")) a.output = VAL();
-        else if (!strcmp(s, "--affinity")) a.affinity = VAL();
-        else if (!strcmp(s, "--logits-bin")) a.logits_bin = VAL();
-        else if (!strcmp(s, "--no-print")) a.no_print = 1;
-        else { fprintf(stderr, "unknown arg: %s\n", s); usage(argv[0]); return 2; }
-#undef VAL
-    }
-    if (!a.model) { usage(argv[0]); return 2; }
-    if (a.batch < 1) a.batch = 1;
-    if (a.n_tokens < 0) a.n_tokens = 0;
-    rng_state = (unsigned long long)(unsigned long)a.seed;
-    Affinity aff;
-    affinity_apply(a.affinity, &aff);
-    int want = -1;
-    if (!strcmp(a.precision, "fp16")) want = 1;
-    else if (!strcmp(a.precision, "bf16")) want = 2;
-    else if (!strcmp(a.precision, "int8")) want = 0;
-    else if (strcmp(a.precision, "auto")) {
-        fprintf(stderr, "unknown precision: %s (use fp16|bf16|int8|auto)\n", a.precision);
+    Config c;
+    config_defaults(&c);
+    if (argc < 2) {
+        print_help(argv[0]);
         return 2;
     }
+    int rc = config_parse(&c, argc, argv);
+    if (rc) return rc;
+    static const char *const kDtypes[] = {"int8", "fp16", "bf16"};
+    int want = -1;
+    for (int p = 0; p < 3; p++)
+        if (!strcmp(c.precision, kDtypes[p])) want = p;
+    if (want < 0 && strcmp(c.precision, "auto")) {
+        fprintf(stderr, "unknown precision: %s (use fp16|bf16|int8|auto)\n", c.precision);
+        return 2;
+    }
+    CpuPin pin;
+    pin_cpus(c.affinity, &pin);
+
     GPT2 g;
-    double t0 = now_sec();
-    if (gpt2_load(&g, a.model, a.batch, a.max_ctx) != 0) {
+    const double t0 = now_sec();
+    if (gpt2_load(&g, c.model, c.batch, c.max_ctx) != 0) {
         fprintf(stderr, "failed to load model\n");
         return 1;
     }
-    a.load_time_ms = (now_sec() - t0) * 1000.0;
-    const char *have = g.precision == 2 ? "bf16" : (g.precision ? "fp16" : "int8");
+    c.load_ms = (now_sec() - t0) * 1000.0;
     if (want >= 0 && want != g.precision) {
-        fprintf(stderr, "model file uses %s weights, but --precision %s was requested\n", have, a.precision);
+        fprintf(stderr, "model file uses %s weights, but --precision %s was requested\n", dtype_name(g.precision),
+                c.precision);
         gpt2_free(&g);
         return 2;
     }
-    a.precision = have;
-    int rc;
-    if (!strcmp(a.mode, "generate")) rc = mode_generate(&g, &a, &aff);
-    else if (!strcmp(a.mode, "logits")) rc = mode_logits(&g, &a, &aff);
-    else if (!strcmp(a.mode, "bench")) rc = mode_bench(&g, &a, &aff);
-    else { fprintf(stderr, "unknown mode: %s\n", a.mode); rc = 2; }
+    c.precision = dtype_name(g.precision);
+
+    if (!strcmp(c.mode, "generate")) rc = mode_generate(&g, &c, &pin);
+    else if (!strcmp(c.mode, "logits")) rc = mode_logits(&g, &c, &pin);
+    else if (!strcmp(c.mode, "bench")) rc = mode_bench(&g, &c, &pin);
+    else {
+        fprintf(stderr, "unknown mode: %s\n", c.mode);
+        rc = 2;
+    }
     gpt2_free(&g);
     return rc;
 }

@@ -125,6 +125,15 @@ int ec_gemm_fp16_fp32_dev(float *C, const float *A, const uint16_t *B, int M, in
 int ec_gemm_bf16_fp32_dev(float *C, const float *A, const uint16_t *B, int M, int K, int N);
 int ec_gemm_int8_dev(float *C, const int8_t *A, const float *a_scale, const int8_t *B,
                      const float *b_scale, const float *bias, int M, int K, int N);
+/* The int8 matrix-core GEMM of the forward's prefill linears with its fused
+ * epilogue, v = the gemm_int8 value of each output: epi 0 C = v, 1 C += v
+ * (residual, src/gpt2.c:782-784), 2 C = gelu_new(v) (src/gpt2.c:568), 3 C =
+ * silu(g) * u with g from B (b_scale, no bias) and u from B2 (b2_scale)
+ * (src/gpt2.c:788-791).  bm forces the row tile (32, 64, 128; 0 = the
+ * library's choice).  K a multiple of 16, A and B 16-byte aligned. */
+int ec_gemm_int8_epi_dev(int epi, int bm, float *C, const int8_t *A, const float *a_scale, const int8_t *B,
+                         const float *b_scale, const int8_t *B2, const float *b2_scale, const float *bias,
+                         int M, int K, int N);
 /* Activation quantizer of the reference linear() (src/gpt2.c:446-461):
  * per row s = max|a|/127 (1 for an all-zero row), q = clamp(rint(a/s)). */
 int ec_quantize_rows_dev(const float *in, int M, int K, int8_t *q, float *s);
@@ -230,8 +239,9 @@ typedef struct {
     void *file_data; /* host mapping of the .ecm file while loading, else NULL */
     size_t file_size;
     int file_mapped;
-
-    void *dev; /* addition: the library's device state for this model */
+    /* The library keeps each model's device state in a table keyed by the
+     * struct's address, so the layout is the reference's byte for byte: a
+     * GPT2 must stay at one address from gpt2_load to gpt2_free. */
 } GPT2;
 
 typedef struct {

@@ -19,6 +19,8 @@ import pytest
 
 import edgecore_amd as ec
 
+REPO = ec.PKG_DIR.parent
+
 
 def declared_functions():
     text = ec.HEADER.read_text()
@@ -47,6 +49,22 @@ def test_library_exports_every_declared_symbol():
 
 def test_gpt2_struct_mirror():
     assert C.sizeof(ec.GPT2) == ec.lib().ec_gpt2_sizeof()
+
+
+def test_struct_layout_equals_reference_header():
+    """GPT2, struct LayerW, Tokenizer and EcmTensor have the reference's layout
+    (every field offset and sizeof, tests/golden/abi_layout.json written from
+    src/edgecore.h): a caller compiled against the reference header passes
+    structs of the same size and shape."""
+    import json
+    import sys
+
+    sys.path.insert(0, str(REPO / "tests" / "golden"))
+    from abi_layout import layout
+
+    want = json.loads((REPO / "tests" / "golden" / "abi_layout.json").read_text())
+    assert layout(REPO / "include" / "edgecore.h") == want
+    assert C.sizeof(ec.GPT2) == want["GPT2"]["sizeof"]
 
 
 def test_no_gpu_errors_are_reported(tmp_path):

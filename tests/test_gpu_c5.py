@@ -53,3 +53,32 @@ def test_qwen25_15b_shape_batched_decode(c5_model):
             pos = [p + 1 for p in pos]
         om.close()
     print(f"C5-shape max-abs logits diff over {STEPS} steps of 16 tokens: {worst:.3e}")
+
+
+def test_qwen25_15b_shape_long_prefill(c5_model):
+    """Two 1024-token prompts prefilled on their own slots (gate/up N=8960 at
+    M=1024 takes the 128-row matrix-core tiles, attention over 1024 positions
+    at head_dim 128), then 8 greedy steps at M=2."""
+    n, slots, steps = 1024, 2, 8
+    ctx = n + steps + 8
+    with ec.Model(c5_model, slots, ctx) as m:
+        om = oracle.OracleModel(c5_model, slots, ctx)
+        m.kv_reset()
+        om.kv_reset()
+        cur = []
+        for b in range(slots):
+            p = prompt_ids(n, V, seed=40 + b)
+            pos, slot = np.arange(n), np.full(n, b, np.int32)
+            got, am = m.forward(p, pos, slot, lm_from=n - 4, want_logits=True, want_argmax=True)
+            want = om.forward(p, pos, slot, lm_from=n - 4)
+            assert float(np.abs(got - want).max()) <= 2e-2
+            assert list(am) == [int(r.argmax()) for r in want]
+            cur.append(int(am[-1]))
+        pos = [n] * slots
+        for _ in range(steps):
+            got, am = m.forward(cur, pos, None, want_logits=True, want_argmax=True)
+            want = om.forward(cur, pos, None)
+            assert float(np.abs(got - want).max()) <= 2e-2
+            assert list(am) == [int(r.argmax()) for r in want]
+            cur, pos = [int(x) for x in am], [p + 1 for p in pos]
+        om.close()

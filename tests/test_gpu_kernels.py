@@ -121,3 +121,70 @@ def test_dev_entry_points_reject_bad_shapes():
     assert "negative" in ec.last_error()
     assert L.ec_gemm_fp16_fp32_dev(None, None, None, 2, 16, 4) < 0
     assert L.ec_gemm_int8_dev(None, None, None, None, None, None, 0, 4, 4) == 0
+
+
+# ------------------------------------------------------------------ matrix-core tiles x epilogues
+# ec_gemm_int8_epi_dev runs the prefill linears' int8 matrix-core GEMM with
+# every fused epilogue and each row tile (32, 64, 128 rows), on shapes with
+# row and column tails; 0 lets the library pick, as the forward does (the
+# C4 shapes: gate/up of 2048 rows takes 128-row tiles, qkv 64-row tiles).
+TILE_SHAPES = [(200, 896, 300), (130, 1536, 129), (257, 64, 200), (64, 4864, 128)]
+
+
+def _epi_inputs(M, K, N, seed):
+    rng = np.random.default_rng(seed)
+    A = _rand_i8(rng, (M, K))
+    B = _rand_i8(rng, (N, K))
+    B2 = _rand_i8(rng, (N, K))
+    a_s = rng.uniform(1e-4, 1e-2, M).astype(np.float32)
+    b_s = rng.uniform(1e-4, 1e-2, N).astype(np.float32)
+    b2_s = rng.uniform(1e-4, 1e-2, N).astype(np.float32)
+    bias = rng.normal(0, 0.02, N).astype(np.float32)
+    C0 = rng.normal(0, 1.0, (M, N)).astype(np.float32)
+    return A, B, B2, a_s, b_s, b2_s, bias, C0
+
+
+def _bits(x):
+    return np.ascontiguousarray(x, np.float32).view(np.uint32)
+
+
+def _device_gelu(v):
+    din = ec.DeviceBuffer.from_array(np.ascontiguousarray(v, np.float32))
+    dout = ec.DeviceBuffer(v.size * 4)
+    try:
+        assert ec.lib().ec_device_math(2, din.ptr, dout.ptr, v.size) == 0, ec.last_error()
+        return dout.to_array(np.float32, v.shape)
+    finally:
+        din.close()
+        dout.close()
+
+
+@pytest.mark.parametrize("bm", [32, 64, 128])
+@pytest.mark.parametrize("M,K,N", TILE_SHAPES)
+def test_gemm_int8_tiles_and_epilogues(bm, M, K, N):
+    A, B, B2, a_s, b_s, b2_s, bias, C0 = _epi_inputs(M, K, N, seed=M + K + N + bm)
+    v = oracle.gemm_int8(A, a_s, B, b_s, bias)
+    store = ec.gemm_int8_epi(0, bm, A, a_s, B, b_s, bias=bias)
+    assert np.array_equal(_bits(store), _bits(v))
+    resid = ec.gemm_int8_epi(1, bm, A, a_s, B, b_s, bias=bias, C0=C0)
+    assert np.array_equal(_bits(resid), _bits(C0 + v))
+    # GELU: the device's gelu_new (checked against the reference's in
+    # test_gpu_math) applied to the exact linear value
+    gelu = ec.gemm_int8_epi(2, bm, A, a_s, B, b_s, bias=bias)
+    assert np.array_equal(_bits(gelu), _bits(_device_gelu(v)))
+    g = oracle.gemm_int8(A, a_s, B, b_s)
+    u = oracle.gemm_int8(A, a_s, B2, b2_s)
+    swi = ec.gemm_int8_epi(3, bm, A, a_s, B, b_s, B2=B2, b2_scale=b2_s)
+    assert np.array_equal(_bits(swi), _bits(oracle.map_op(1, g) * u))
+
+
+@pytest.mark.parametrize("M,K,N", [(2048, 896, 2048), (1024, 1536, 4096), (1000, 896, 2120), (2040, 896, 2100)])
+def test_gemm_int8_auto_tile_prefill_shapes(M, K, N):
+    """Shapes whose automatic tile is 128 rows (2048x2048, 1024x4096,
+    2040x2100) or 64 rows (1000x2120), with row and column tails."""
+    A, B, B2, a_s, b_s, b2_s, bias, C0 = _epi_inputs(M, K, N, seed=M ^ N)
+    store = ec.gemm_int8_epi(0, 0, A, a_s, B, b_s, bias=bias)
+    assert np.array_equal(_bits(store), _bits(oracle.gemm_int8(A, a_s, B, b_s, bias)))
+    swi = ec.gemm_int8_epi(3, 0, A, a_s, B, b_s, B2=B2, b2_scale=b2_s)
+    want = oracle.map_op(1, oracle.gemm_int8(A, a_s, B, b_s)) * oracle.gemm_int8(A, a_s, B2, b2_s)
+    assert np.array_equal(_bits(swi), _bits(want))

@@ -187,6 +187,21 @@ __device__ __forceinline__ T ld_uniform(const T *p) {
   return *(const __attribute__((address_space(4))) T *)(uintptr_t)p;
 }
 
+// The thread's index within the block, opaque to the compiler: values derived
+// from it are not hoisted out of an enclosing loop (the persistent decode
+// step runs whole kernels' bodies in a loop over layers, where hoisting every
+// loop-invariant address computation exhausts the registers).
+__device__ __forceinline__ int tid_opaque() {
+  int t = threadIdx.x;
+  asm volatile("" : "+v"(t));
+  return t;
+}
+// a wave-uniform int, likewise opaque
+__device__ __forceinline__ int uniform_opaque(int v) {
+  asm volatile("" : "+s"(v));
+  return v;
+}
+
 // ---- wave / block reductions (wave64) ----
 template <typename T>
 __device__ __forceinline__ T wave_sum(T v) {

@@ -162,6 +162,48 @@ struct AttnArgs {
   int xcd_r;  // set by attention(): query heads per KV group when the launch is XCD-grouped, else 0
 };
 hipError_t attention(const AttnArgs &a, hipStream_t st);
+
+// Persistent decode step (decode_step.hip): all layers of the int8 Qwen2
+// forward for one token in one co-resident launch of kStepBlocks blocks of
+// kStepThreads threads (d_model 896, head_dim 64, 4 attention blocks per
+// query head, up to 8 query heads per KV group, FFN <= 5120).  Blocks exchange
+// activations through tagged words (value, step tag) in `xch`: per layer
+// [x after the layer: E][x after o: E][attention output: E][FFN activation: F].
+constexpr int kStepBlocks = 256, kStepThreads = 512, kStepSlices = 4;
+// phase timestamps per block and layer: 0 layer start, 1 x gathered (attention
+// blocks), 2 q/k/v rows done, 3 attention done, 4 attention output gathered,
+// 5 o done, 6 x_mid gathered, 7 gate/up done, 8 FFN activation gathered,
+// 9 down done
+constexpr int kStepEvents = 10;
+struct StepLayer {
+  const float *ln1_g, *ln2_g;
+  const int8_t *wqkv;  // [E + 2 kv][E]: q | k | v rows
+  const float *sqkv;
+  const int8_t *wo;
+  const float *so;
+  const int8_t *wg, *wu;
+  const float *sg, *su;
+  const int8_t *wd;  // [E][F]
+  const float *sd;
+};
+struct StepArgs {
+  const StepLayer *layers;  // device array [L]
+  const uint16_t *wte;      // fp16 [V][E]
+  int L, E, H, KVH, F;
+  double eps;
+  size_t kv_layer;  // elements per layer of one cache
+  const int *tok;   // the token's id (its position and slot: attn.pos / attn.slot)
+  const unsigned *tag;          // this step's tag (> 0, new every launch)
+  unsigned long long *xch;      // tagged exchange words
+  float *x_out;                 // x after the last layer [E] (the LM head's input)
+  int *err;                     // set when a wait timed out (results invalid)
+  unsigned long long *trace;    // null, or [blocks][L][kStepEvents] phase timestamps
+  // the attention body's arguments for layer 0 (kc/vc, kc_w/vc_w at layer
+  // 0, fused RoPE + append, M = 1); layer l adds l * kv_layer to the caches
+  AttnArgs attn;
+};
+size_t decode_step_scratch_bytes(int E, int F);
+hipError_t decode_step(const StepArgs &a, size_t lds, hipStream_t s);
 // Prefill attention (attn_prefill.hip): the M tokens are one slot's run of
 // consecutive positions whose k / v are already in the cache (fuse_kv 0);
 // blocks of 16, 8 or 4 tokens per head.  _ok: head_dim 32/64/128, q rows

@@ -504,6 +504,18 @@ struct DevModel {
   float *tk_vals = nullptr;               // [lm_rows][kTopkMax + 1]
   int *tk_idx = nullptr, *tk_status = nullptr;
   int last_lm_rows = 0;  // rows of the LM-head chunk the last forward left in `logits`
+  // persistent decode step (decode_step.hip), for int8 Qwen2 models of its shape
+  bool step_ok = false;
+  StepLayer *d_layers = nullptr;  // device copy of the layers' pointers
+  unsigned long long *xch = nullptr;  // tagged exchange words
+  size_t xch_bytes = 0;
+  // one-token step I/O, device and pinned host: [0] token, [1] position,
+  // [2] slot, [3] tag (copied in, 16 bytes); [4] a wait timed out, [5] the
+  // greedy id (copied out, 8 bytes)
+  int *d_step_io = nullptr, *h_step_io = nullptr;
+  unsigned step_tag = 0;          // last tag used
+  bool step_nograph = false;      // capturing the step failed once: launch it directly
+  unsigned long long *d_trace = nullptr;  // EDGECORE_STEP_TRACE=1: phase timestamps of the last step
 };
 
 // host outputs of a forward that selects the top-k logits of its LM-head rows
@@ -558,11 +570,12 @@ static void free_dev(DevModel *d) {
   if (!d) return;
   void *ps[] = {d->arena, d->rope, d->d_tok, d->d_pos, d->d_slot, d->d_amax, d->x, d->h, d->qkv,
                 d->att, d->ff, d->aq, d->as, d->logits, d->kc, d->vc, d->cand, d->tk_cand,
-                d->tk_nan, d->tk_vals, d->tk_idx, d->tk_status};
+                d->tk_nan, d->tk_vals, d->tk_idx, d->tk_status, d->d_layers, d->xch, d->d_step_io, d->d_trace};
   for (void *p : ps)
     if (p) (void)hipFree(p);
   if (d->h_stage) (void)hipHostFree(d->h_stage);
   if (d->h_amax) (void)hipHostFree(d->h_amax);
+  if (d->h_step_io) (void)hipHostFree(d->h_step_io);
   if (d->step_graph) (void)hipGraphExecDestroy(d->step_graph);
   delete d;
 }
@@ -594,6 +607,22 @@ static DevModel *dev_detach(const GPT2 *g) {
   DevModel *d = it->second;
   g_models.erase(it);
   return d;
+}
+
+// The persistent decode step's shape (decode_step.hip): int8 Qwen2 with
+// d_model 896, head_dim 64, up to 8 query heads per KV group (4 blocks per
+// head on one XCD of 32 CUs), up to 8 KV groups, FFN <= 5120 in 16-byte rows,
+// on a device with 256 CUs and cooperative launch.  EDGECORE_STEP=0 turns it
+// off (the forward then runs a kernel per operation).
+static bool step_shape_ok(const GPT2 *g, const DevModel *d) {
+  const char *env = getenv("EDGECORE_STEP");
+  if (env && !strcmp(env, "0")) return false;
+  int coop = 0;
+  if (hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, g_device) != hipSuccess || !coop) return false;
+  const int H = g->n_head, KVH = g->n_kv_head, E = g->n_embd, F = d->F;
+  return g->arch == ARCH_QWEN2 && g->precision == 0 && E == 896 && g->head_dim == 64 && KVH >= 1 && KVH <= 8 &&
+         H % KVH == 0 && (H / KVH) * kStepSlices <= kStepBlocks / 8 && F % 16 == 0 && F <= 5120 &&
+         F <= 64 * kStepBlocks && g_prop.multiProcessorCount == kStepBlocks;
 }
 
 static int load_impl(GPT2 *g, const char *path, int batch_cap, int max_ctx) {
@@ -847,7 +876,7 @@ static int load_impl(GPT2 *g, const char *path, int batch_cap, int max_ctx) {
   EC_HIP(hipMalloc(&d->d_pos, (size_t)mmax * 4));
   EC_HIP(hipMalloc(&d->d_slot, (size_t)mmax * 4));
   EC_HIP(hipMalloc(&d->d_amax, (size_t)mmax * 4));
-  EC_HIP(hipHostMalloc((void **)&d->h_stage, (size_t)mmax * 3 * 4, hipHostMallocDefault));
+  EC_HIP(hipHostMalloc((void **)&d->h_stage, ((size_t)mmax * 3 + 1) * 4, hipHostMallocDefault));
   EC_HIP(hipHostMalloc((void **)&d->h_amax, 4 * sizeof(int), hipHostMallocDefault));
   d->ncand = gemv_max_blocks();
   EC_HIP(hipMalloc(&d->cand, (size_t)d->lm_rows * d->ncand * sizeof(unsigned long long)));
@@ -858,6 +887,30 @@ static int load_impl(GPT2 *g, const char *path, int batch_cap, int max_ctx) {
     EC_HIP(hipMalloc(&d->tk_vals, (size_t)d->lm_rows * n * sizeof(float)));
     EC_HIP(hipMalloc(&d->tk_idx, (size_t)d->lm_rows * n * sizeof(int)));
     EC_HIP(hipMalloc(&d->tk_status, (size_t)d->lm_rows * sizeof(int)));
+  }
+  if (step_shape_ok(g, d)) {
+    std::vector<StepLayer> sl(Lc);
+    for (int l = 0; l < Lc; l++) {
+      const LayerDev &W = d->L[l];
+      sl[l] = StepLayer{W.ln1_g, W.ln2_g, (const int8_t *)W.wqkv, W.sqkv, (const int8_t *)W.wo, W.so,
+                        (const int8_t *)W.wg, (const int8_t *)W.wu, W.sg, W.su, (const int8_t *)W.wd, W.sd};
+    }
+    EC_HIP(hipMalloc(&d->d_layers, sl.size() * sizeof(StepLayer)));
+    EC_HIP(hipMemcpy(d->d_layers, sl.data(), sl.size() * sizeof(StepLayer), hipMemcpyHostToDevice));
+    d->xch_bytes = (size_t)Lc * (3 * (size_t)E + F) * sizeof(unsigned long long);
+    EC_HIP(hipMalloc(&d->xch, d->xch_bytes));
+    EC_HIP(hipMemset(d->xch, 0, d->xch_bytes));
+    EC_HIP(hipMalloc(&d->d_step_io, 8 * sizeof(int)));
+    EC_HIP(hipMemset(d->d_step_io, 0, 8 * sizeof(int)));
+    EC_HIP(hipHostMalloc((void **)&d->h_step_io, 8 * sizeof(int), hipHostMallocDefault));
+    memset(d->h_step_io, 0, 8 * sizeof(int));
+    const char *tr = getenv("EDGECORE_STEP_TRACE");
+    if (tr && !strcmp(tr, "1")) {
+      const size_t tb = (size_t)kStepBlocks * Lc * kStepEvents * sizeof(unsigned long long);
+      EC_HIP(hipMalloc(&d->d_trace, tb));
+      EC_HIP(hipMemset(d->d_trace, 0, tb));
+    }
+    d->step_ok = true;
   }
   g->ws_x = d->x;
   g->ws_tmp = d->h;
@@ -984,8 +1037,87 @@ static int attn_vtile(int max_npos, int hd, int kv) {
 // batch and sizes the attention LDS; distinct: no two tokens share a slot
 // (RoPE and the KV append then run inside attention); abytes: algorithmic
 // attention bytes, for the profiler only.
+// LDS the persistent step reserves outside the dynamic area (its static arrays)
+constexpr size_t kStepStaticLds = 4096;
+
+// the attention product tile of the persistent step for max_npos positions
+// (attn_vtile with the step's static LDS set aside)
+static int step_vtile(int max_npos) {
+  const size_t budget = (size_t)g_max_lds - kStepStaticLds;
+  const size_t lds_fixed = attention_lds_bytes(max_npos, 64, 0);
+  if (lds_fixed >= budget) return 0;
+  const size_t room = (budget - lds_fixed) / ((size_t)attn_pitch(64, 0) * sizeof(float));
+  const size_t cap = (size_t)attention_max_vtile(64, 128);
+  int vtile = (int)(room < cap ? room : cap) & ~3;
+  if (vtile > ((max_npos + 3) & ~3)) vtile = (max_npos + 3) & ~3;
+  return vtile;
+}
+
+static size_t step_lds(const GPT2 *g, const DevModel *d, int max_npos, int vtile) {
+  const size_t a = attention_lds_bytes(max_npos, 64, vtile), b = decode_step_scratch_bytes(g->n_embd, d->F);
+  return a > b ? a : b;
+}
+
+// algorithmic bytes of one persistent step: every layer's int8 weights and
+// row scales once, plus the K/V rows its attention reads
+static double step_bytes(const GPT2 *g, const DevModel *d, int npos) {
+  const double E = g->n_embd, F = d->F, kv = g->n_kv_embd;
+  const double rows = (E + 2 * kv) + E + 2 * F + E;
+  const double w = E * (E + 2 * kv) + E * E + 2 * F * E + F * E;
+  return g->n_layer * (w + 4 * rows + (double)npos * kv * 4);
+}
+
+// The layers of a one-token forward as one persistent launch (decode_step.hip);
+// x after the last layer lands in d->x.
+static int enqueue_step(GPT2 *g, DevModel *d, int max_npos, hipStream_t s) {
+  const int vtile = step_vtile(max_npos);
+  if (vtile < 4) return set_err(-1, "decode step: position %d does not fit the LDS", max_npos - 1);
+  EC_HIP(hipMemcpyAsync(d->d_step_io, d->h_step_io, 4 * sizeof(int), hipMemcpyHostToDevice, s));
+  int *io = d->d_step_io;
+  AttnArgs aa{};
+  aa.kc = d->kc;
+  aa.vc = d->vc;
+  aa.kc_w = d->kc;
+  aa.vc_w = d->vc;
+  aa.pos = io + 1;
+  aa.slot = io + 2;
+  aa.H = g->n_head;
+  aa.KVH = g->n_kv_head;
+  aa.hd = 64;
+  aa.kv = g->n_kv_embd;
+  aa.C = d->eff_ctx;
+  aa.window = g->sliding_window;
+  aa.inv_hd = 1.0 / sqrt(64.0);
+  aa.M = 1;
+  aa.max_npos = max_npos;
+  aa.vtile = vtile;
+  aa.fuse_kv = 1;
+  aa.cs = d->rope;
+  aa.half = d->half;
+  StepArgs sa{d->d_layers, g->wte, g->n_layer, g->n_embd, g->n_head, g->n_kv_head, d->F, g->eps, d->kv_layer,
+              io, reinterpret_cast<const unsigned *>(io + 3), d->xch, d->x, io + 4, d->d_trace, aa};
+  const size_t lds = step_lds(g, d, max_npos, vtile);
+  // decode_step is a cooperative launch (not through klaunch): its profiler
+  // events are recorded on the stream around it
+  const int p_ = prof_begin("decode_step", step_bytes(g, d, max_npos));
+  hipEvent_t e0 = g_launch_ev[0], e1 = g_launch_ev[1];
+  g_launch_ev[0] = g_launch_ev[1] = nullptr;
+  if (e0) EC_HIP(hipEventRecord(e0, s));
+  const hipError_t e = decode_step(sa, lds, s);
+  if (e0 && e == hipSuccess) EC_HIP(hipEventRecord(e1, s));
+  if (e != hipSuccess) {
+    if (p_ >= 0) {
+      g_prof.pop_back();
+      g_ev_used -= 2;
+    }
+    return set_err(-3, "decode_step launch failed: %s", hipGetErrorString(e));
+  }
+  return 0;
+}
+
 static int enqueue_forward(GPT2 *g, DevModel *d, int M, int lm_from, bool distinct, bool run, int max_npos,
-                           double abytes, float *logits, int *argmax, const TopkReq *tk, hipStream_t s) {
+                           double abytes, float *logits, int *argmax, const TopkReq *tk, hipStream_t s,
+                           bool step = false) {
   const int E = g->n_embd, H = g->n_head, V = g->vocab, kv = g->n_kv_embd, hd = g->head_dim;
   const bool qwen = g->arch == ARCH_QWEN2, i8 = g->precision == 0, bf16 = g->precision == 2;
   const int wt = i8 ? WT_I8 : (bf16 ? WT_BF16 : WT_F16);
@@ -995,17 +1127,21 @@ static int enqueue_forward(GPT2 *g, DevModel *d, int M, int lm_from, bool distin
     return set_err(-1, "position %d needs more LDS for attention scores than the device has (%d bytes)",
                    max_npos - 1, g_max_lds);
   const int *st = d->h_stage;
-  EC_HIP(hipMemcpyAsync(d->d_tok, st, (size_t)M * 4, hipMemcpyHostToDevice, s));
-  EC_HIP(hipMemcpyAsync(d->d_pos, st + d->mmax, (size_t)M * 4, hipMemcpyHostToDevice, s));
-  EC_HIP(hipMemcpyAsync(d->d_slot, st + 2 * d->mmax, (size_t)M * 4, hipMemcpyHostToDevice, s));
+  if (!step) {
+    EC_HIP(hipMemcpyAsync(d->d_tok, st, (size_t)M * 4, hipMemcpyHostToDevice, s));
+    EC_HIP(hipMemcpyAsync(d->d_pos, st + d->mmax, (size_t)M * 4, hipMemcpyHostToDevice, s));
+    EC_HIP(hipMemcpyAsync(d->d_slot, st + 2 * d->mmax, (size_t)M * 4, hipMemcpyHostToDevice, s));
+  }
 
-  EC_LAUNCH("embed", (double)M * E * (g->wpe ? 8 : 6),
-            embed(g->wte, g->wpe, bf16, d->d_tok, d->d_pos, M, E, d->x, s));
+  int r;
+  if (step && (r = enqueue_step(g, d, max_npos, s))) return r;
+  if (!step)
+    EC_LAUNCH("embed", (double)M * E * (g->wpe ? 8 : 6),
+              embed(g->wte, g->wpe, bf16, d->d_tok, d->d_pos, M, E, d->x, s));
 
   const int F = d->F, ldq = d->qkv_ld;
   const int nqkv = qwen ? E + 2 * kv : 3 * E;
-  int r;
-  for (int l = 0; l < g->n_layer; l++) {
+  for (int l = 0; l < (step ? 0 : g->n_layer); l++) {
     const LayerDev &W = d->L[l];
     uint16_t *kcl = d->kc + d->kv_layer * l, *vcl = d->vc + d->kv_layer * l;
     // norm -> q|k|v projection (GPT-2 bias: inside the int8 epilogue, a bias pass for 16-bit)
@@ -1057,6 +1193,7 @@ static int enqueue_forward(GPT2 *g, DevModel *d, int M, int lm_from, bool distin
   // final norm fused into the LM head (always fp16/bf16, src/gpt2.c:576-580 / 799-804);
   // greedy ids from per-block argmax candidates
   const int lwt = bf16 ? WT_BF16 : WT_F16;
+  int *amax_dev = step ? d->d_step_io + 5 : d->d_amax;  // a step's id goes out with its error flag
   for (int r0 = lm_from; r0 < M; r0 += d->lm_rows) {
     const int rows = M - r0 < d->lm_rows ? M - r0 : d->lm_rows;
     GemvArgs a{d->x + (size_t)r0 * E, E, nullptr, g->lnf_g, g->lnf_b, g->eps, d->lm, nullptr, nullptr, nullptr,
@@ -1068,9 +1205,9 @@ static int enqueue_forward(GPT2 *g, DevModel *d, int M, int lm_from, bool distin
       if (fused)
         EC_LAUNCH("argmax", 8.0 * rows * gemv_grid_x(a, lwt, EPI_STORE),
                   argmax_finalize(d->cand, gemv_grid_x(a, lwt, EPI_STORE), d->logits, V, rows,
-                                  d->d_amax + (r0 - lm_from), s));
+                                  amax_dev + (r0 - lm_from), s));
       else
-        EC_LAUNCH("argmax", 4.0 * rows * V, argmax_rows(d->logits, rows, V, d->d_amax + (r0 - lm_from), s));
+        EC_LAUNCH("argmax", 4.0 * rows * V, argmax_rows(d->logits, rows, V, amax_dev + (r0 - lm_from), s));
     }
     if (logits)
       EC_HIP(hipMemcpyAsync(logits + (size_t)(r0 - lm_from) * V, d->logits, (size_t)rows * V * 4,
@@ -1087,7 +1224,9 @@ static int enqueue_forward(GPT2 *g, DevModel *d, int M, int lm_from, bool distin
     }
     d->last_lm_rows = rows;
   }
-  if (argmax && lm_from < M)
+  if (step)
+    EC_HIP(hipMemcpyAsync(d->h_step_io + 4, d->d_step_io + 4, 2 * sizeof(int), hipMemcpyDeviceToHost, s));
+  else if (argmax && lm_from < M)
     EC_HIP(hipMemcpyAsync(argmax, d->d_amax, (size_t)(M - lm_from) * 4, hipMemcpyDeviceToHost, s));
   return 0;
 }
@@ -1145,6 +1284,68 @@ static int forward_impl(GPT2 *g, const int *tokens, const int *positions, const 
   if (bucket > d->eff_ctx) bucket = d->eff_ctx;
   if (tk && !topk_ok(V, tk->top_k))
     return set_err(-1, "top_k=%d outside (0, %d) or above %d", tk->top_k, V, kTopkMax);
+  const bool step = M == 1 && lm_from == 0 && d->step_ok && step_vtile(max_npos) >= 4;
+  if (step) {
+    // one token through the persistent step: its inputs and the step's tag
+    // into the pinned I/O block, then -- for a greedy step without logits --
+    // a HIP graph of the copy in, the step, the LM head, the argmax and the
+    // copy out, captured once per 512-position bucket (the attention LDS is
+    // sized for the bucket; the kernels read token, position and slot from
+    // device memory); otherwise the same launches directly
+    int *io = d->h_step_io;
+    io[0] = st[0];
+    io[1] = st[d->mmax];
+    io[2] = st[2 * d->mmax];
+    if (++d->step_tag == 0) {  // after 2^32 steps: clear the words of the old tags
+      EC_HIP(hipMemsetAsync(d->xch, 0, d->xch_bytes, s));
+      d->step_tag = 1;
+    }
+    io[3] = (int)d->step_tag;
+    io[4] = io[5] = 0;
+    bool graph = argmax && !logits && !tk && !g_prof_on && g_use_graphs && !d->step_nograph &&
+                 step_vtile(bucket) >= 4;
+    if (graph && (!d->step_graph || d->step_bucket != bucket)) {
+      if (d->step_graph) {
+        EC_HIP(hipGraphExecDestroy(d->step_graph));
+        d->step_graph = nullptr;
+      }
+      // a runtime that cannot capture the cooperative launch leaves the
+      // step to direct launches from then on
+      hipGraph_t gr = nullptr;
+      hipError_t e = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
+      int r = 0;
+      if (e == hipSuccess) {
+        r = enqueue_forward(g, d, 1, 0, true, false, bucket, abytes, nullptr, argmax, nullptr, s, true);
+        e = hipStreamEndCapture(s, &gr);
+      }
+      if (e == hipSuccess && r == 0) e = hipGraphInstantiate(&d->step_graph, gr, nullptr, nullptr, 0);
+      if (gr) (void)hipGraphDestroy(gr);
+      if (e != hipSuccess || r != 0) {
+        fprintf(stderr, "edgecore: the decode step could not be captured as a HIP graph (%s); launching it "
+                "directly\n", r ? g_err : hipGetErrorString(e));
+        (void)hipGetLastError();
+        d->step_graph = nullptr;
+        d->step_nograph = true;
+        graph = false;
+        g_err[0] = 0;
+      } else {
+        d->step_bucket = bucket;
+      }
+    }
+    if (graph) {
+      EC_HIP(hipGraphLaunch(d->step_graph, s));
+    } else {
+      const int r = enqueue_forward(g, d, M, lm_from, distinct, run, max_npos, abytes, logits, argmax, tk, s, true);
+      if (r) return r;
+    }
+    EC_HIP(hipStreamSynchronize(s));
+    if (io[4]) {
+      EC_HIP(hipMemset(d->d_step_io + 4, 0, sizeof(int)));
+      return set_err(-3, "decode step: a block's wait for another's results timed out (results discarded)");
+    }
+    if (argmax) argmax[0] = io[5];
+    return 0;
+  }
   if (M == 1 && lm_from == 0 && argmax && !logits && !tk && !g_prof_on && g_use_graphs &&
       attn_vtile(bucket, hd, kv) >= 4) {
     if (!d->step_graph || d->step_bucket != bucket) {
@@ -1190,6 +1391,17 @@ extern "C" int gpt2_forward_topk(GPT2 *g, const int *tokens, const int *position
 }
 
 extern "C" int ec_topk_max(void) { return kTopkMax; }
+
+extern "C" int ec_step_trace(GPT2 *g, unsigned long long *out, size_t n) {
+  EC_INIT();
+  DevModel *d = dev_of(g);
+  if (!d) return set_err(-1, "model not loaded");
+  if (!d->d_trace) return set_err(-1, "ec_step_trace: load the model with EDGECORE_STEP_TRACE=1");
+  const size_t need = (size_t)kStepBlocks * g->n_layer * kStepEvents;
+  if (!out || n < need) return set_err(-1, "ec_step_trace: %zu words needed", need);
+  EC_HIP(hipMemcpy(out, d->d_trace, need * sizeof(unsigned long long), hipMemcpyDeviceToHost));
+  return (int)need;
+}
 
 extern "C" int ec_last_logits(GPT2 *g, int row, float *out) {
   EC_INIT();

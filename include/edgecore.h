@@ -400,6 +400,13 @@ int ec_prof_stop(char *buf, int len);
  * for HBM traffic counters).  fp32 in/out except as noted.  0 or <0. */
 int ec_device_math(int op, const void *in, void *out, size_t n);
 
+/* Diagnostics of the persistent decode step of one-token int8 Qwen2
+ * forwards (a model loaded with EDGECORE_STEP_TRACE=1): the last step's
+ * s_memrealtime (100 MHz) stamps at every block's phase boundaries,
+ * [256 blocks][n_layer][10 events] (see ec_kernels.h, kStepEvents).
+ * Returns the word count or <0. */
+int ec_step_trace(GPT2 *g, unsigned long long *out, size_t n);
+
 /* int8 weight packing of edgecore/ecm.py:50-59 (float64 max|w|/127, zero row
  * -> scale 1, round half to even, clip; a row holding NaN gets scale NaN and
  * codes -128, as numpy gives), used by the synthetic generator. */

@@ -1,0 +1,95 @@
+"""The persistent decode step (decode_step.hip) against the kernel-per-
+operation forward it replaces for one-token int8 Qwen2 steps
+(src/gpt2.c:667-805 at M = 1).
+
+Both paths run the same arithmetic in the same order, so a greedy decode
+through the step must give logits bit-identical to the same decode with the
+step turned off (EDGECORE_STEP=0 when the model is loaded), at every step,
+and the oracle's tokens.  The model has the Qwen2-0.5B per-layer shapes at 3
+layers; the decode crosses positions 505-530 (the attention's first K tile
+and a 512-position boundary)."""
+import ctypes as C
+import json
+import os
+
+import numpy as np
+import pytest
+
+import edgecore_amd as ec
+import oracle
+from tests.conftest import prompt_ids
+
+pytestmark = pytest.mark.gpu
+
+V = 151936
+
+
+@pytest.fixture(scope="module")
+def step_model(model_dir):
+    path = model_dir / "qwen2-0.5b-3l-int8.ecm"
+    if not path.exists():
+        ec.synth(path, name="qwen2-0.5b-3l", arch="qwen2", layers=3, embd=896, heads=14, kv_heads=2, ffn=4864,
+                 ctx=32768, vocab=V, precision="int8", tie=1)
+    return path
+
+
+def _families(fn):
+    L = ec.lib()
+    L.ec_prof_start(b"")
+    fn()
+    buf = C.create_string_buffer(1 << 16)
+    assert L.ec_prof_stop(buf, len(buf)) > 0, ec.last_error()
+    return {k["kernel"]: k for k in json.loads(buf.value.decode())}
+
+
+def _decode(path, prompt, steps, step_on):
+    old = os.environ.get("EDGECORE_STEP")
+    os.environ["EDGECORE_STEP"] = "1" if step_on else "0"
+    try:
+        m = ec.Model(path, 1, len(prompt) + steps + 8)
+    finally:
+        if old is None:
+            del os.environ["EDGECORE_STEP"]
+        else:
+            os.environ["EDGECORE_STEP"] = old
+    with m:
+        n = len(prompt)
+        m.kv_reset()
+        m.forward(prompt, np.arange(n), np.zeros(n, np.int32), lm_from=n, want_logits=False)
+        cur, pos, out, ids = int(prompt[-1]), n, [], []
+        fams = None
+        for s in range(steps):
+            if s == 0:
+                res = {}
+                fams = _families(lambda: res.update(r=m.forward([cur], [pos], None, want_logits=True,
+                                                              want_argmax=True)))
+                lg, am = res["r"]
+            else:
+                lg, am = m.forward([cur], [pos], None, want_logits=True, want_argmax=True)
+            out.append(lg[0])
+            cur, pos = int(am[0]), pos + 1
+            ids.append(cur)
+    return np.stack(out), ids, fams
+
+
+def test_step_bit_identical_to_kernel_per_op(step_model):
+    prompt = prompt_ids(505, V, seed=7)
+    lg_s, ids_s, fam_s = _decode(step_model, prompt, 26, True)
+    lg_k, ids_k, fam_k = _decode(step_model, prompt, 26, False)
+    assert "decode_step" in fam_s and "gemv_qkv" not in fam_s, sorted(fam_s)
+    assert "decode_step" not in fam_k and "gemv_qkv" in fam_k, sorted(fam_k)
+    assert ids_s == ids_k
+    assert np.array_equal(lg_s.view(np.uint32), lg_k.view(np.uint32)), float(np.abs(lg_s - lg_k).max())
+    om = oracle.OracleModel(step_model, 1, len(prompt) + 26 + 8)
+    oids, olg = om.generate(prompt, 26, want_logits=True)
+    om.close()
+    assert ids_s == [int(x) for x in oids[len(prompt):]]
+    assert float(np.abs(lg_s - olg).max()) <= 2e-2
+
+
+def test_step_short_context(step_model):
+    """Positions 1-12: the first steps after a one-token prompt."""
+    prompt = prompt_ids(1, V, seed=9)
+    lg_s, ids_s, _ = _decode(step_model, prompt, 12, True)
+    lg_k, ids_k, _ = _decode(step_model, prompt, 12, False)
+    assert ids_s == ids_k and np.array_equal(lg_s.view(np.uint32), lg_k.view(np.uint32))

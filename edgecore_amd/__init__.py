@@ -93,6 +93,7 @@ _SIG = {
     "ec_topk_max": (_I, []),
     "ec_last_logits": (_I, [_P, _I, _P]),
     "ec_topk_dev": (_I, [_P, _I, _I, _I, _I, _P, _P, _P]),
+    "ec_topk_dev_noalloc": (_I, [_P, _I, _I, _I, _I, _P, _P, _P]),
     "ec_attention_dev": (_I, [_P, _I, _P, _P, _I, _I, _I, _I, _I, _P, _P, _I, _I, _P, _I, _I]),
     "ec_rng_next": (C.c_uint, [C.POINTER(C.c_ulonglong)]),
     "ec_sample_full": (_I, [_P, _I, C.c_float, _I, C.POINTER(C.c_ulonglong)]),

@@ -66,6 +66,15 @@ extern "C" const char *ec_last_error(void) { return g_err; }
 
 extern "C" size_t ec_gpt2_sizeof(void) { return sizeof(GPT2); }
 
+// Scratch of ec_topk_dev_noalloc: a file-scope device array, one copy per
+// GPU for the life of the process (kNoAllocScratch bytes).  Host code never
+// uses the array's name as an address: ec_init resolves this GPU's copy with
+// hipGetSymbolAddress and keeps the pointer (g_scratch_dev[device]).
+constexpr size_t kNoAllocScratch = (size_t)4 << 20;
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratch];
+static void *g_scratch_dev[kMaxDevices] = {};
+
 extern "C" int ec_init(void) {
   if (g_inited) return 0;
   const char *d = getenv("EDGECORE_DEVICE");
@@ -88,6 +97,11 @@ extern "C" int ec_init(void) {
   g_use_mfma = !(mf && !strcmp(mf, "0"));
   gemv_set_max_blocks(8 * g_prop.multiProcessorCount);
   gemv_set_max_lds(g_max_lds);
+  if (g_device < kMaxDevices) {
+    void *p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) == hipSuccess) g_scratch_dev[g_device] = p;
+    else (void)hipGetLastError();  // ec_topk_dev_noalloc reports it
+  }
   g_inited = 1;
   return 0;
 }
@@ -1442,6 +1456,44 @@ extern "C" int ec_topk_dev(const float *logits, int rows, int vocab, int ld, int
   for (void *p : {(void *)cand, (void *)nanf, (void *)dv, (void *)di, (void *)ds})
     if (p) (void)hipFree(p);
   if (e != hipSuccess) return set_err(-3, "ec_topk_dev: %s", hipGetErrorString(e));
+  return 0;
+}
+
+// ec_topk_dev with its scratch in the library's device array instead of
+// allocations: candidates [rows][chunks][top_k + 1], NaN flags, and the
+// results staged for the copies to the host, each region 256-byte aligned.
+// Every scratch byte the kernels read is written first by them in the same
+// call, so nothing needs clearing.  Calls overlapping on one GPU share the
+// array and race.
+extern "C" int ec_topk_dev_noalloc(const float *logits, int rows, int vocab, int ld, int top_k, float *vals,
+                                   int *idx, int *status) {
+  EC_INIT();
+  if (rows < 0 || ld < vocab) return set_err(-1, "ec_topk_dev_noalloc: rows=%d ld=%d vocab=%d", rows, ld, vocab);
+  if (rows == 0) return 0;
+  if (!topk_ok(vocab, top_k))
+    return set_err(-1, "ec_topk_dev_noalloc: top_k=%d outside (0, %d) or above %d", top_k, vocab, kTopkMax);
+  if (!logits || !vals || !idx || !status) return set_err(-1, "ec_topk_dev_noalloc: null pointer");
+  char *base = g_device < kMaxDevices ? (char *)g_scratch_dev[g_device] : nullptr;
+  if (!base) return set_err(-3, "ec_topk_dev_noalloc: the device scratch array is unavailable");
+  const int nb = topk_chunks(vocab), n = top_k + 1;
+  auto up = [](size_t b) { return (b + 255) & ~(size_t)255; };
+  const size_t o_nan = up((size_t)rows * nb * n * sizeof(unsigned long long));
+  const size_t o_v = o_nan + up((size_t)rows * nb), o_i = o_v + up((size_t)rows * n * 4);
+  const size_t o_s = o_i + up((size_t)rows * n * 4), need = o_s + up((size_t)rows * 4);
+  if (need > kNoAllocScratch)
+    return set_err(-1, "ec_topk_dev_noalloc: %d rows of vocab %d at top_k %d need %zu bytes of scratch, above "
+                   "its %zu", rows, vocab, top_k, need, kNoAllocScratch);
+  unsigned long long *cand = (unsigned long long *)base;
+  unsigned char *nanf = (unsigned char *)(base + o_nan);
+  float *dv = (float *)(base + o_v);
+  int *di = (int *)(base + o_i), *ds = (int *)(base + o_s);
+  hipError_t e = topk_select(logits, rows, vocab, ld, top_k, cand, nanf, g_stream);
+  if (e == hipSuccess) e = topk_merge(cand, nanf, rows, vocab, top_k, dv, di, ds, g_stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(vals, dv, (size_t)rows * n * 4, hipMemcpyDeviceToHost, g_stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(idx, di, (size_t)rows * n * 4, hipMemcpyDeviceToHost, g_stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(status, ds, (size_t)rows * 4, hipMemcpyDeviceToHost, g_stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
+  if (e != hipSuccess) return set_err(-3, "ec_topk_dev_noalloc: %s", hipGetErrorString(e));
   return 0;
 }
 

@@ -332,6 +332,14 @@ int ec_last_logits(GPT2 *g, int row, float *out);
  * (row stride ld) -> vals/idx/status as in gpt2_forward_topk (host). */
 int ec_topk_dev(const float *logits, int rows, int vocab, int ld, int top_k, float *vals, int *idx,
                 int *status);
+/* ec_topk_dev without allocating: no reference counterpart; for callers that
+ * cannot allocate device memory (code under stream capture, serving loops,
+ * harnesses that forbid hipMalloc).  Its scratch is a 4 MiB device array of
+ * the library, one per GPU for the life of the process; a call needing more
+ * (about 40 KB per row at vocab 151936 and top_k 128) fails with a message.
+ * Calls overlapping on one GPU share that array and race. */
+int ec_topk_dev_noalloc(const float *logits, int rows, int vocab, int ld, int top_k, float *vals, int *idx,
+                        int *status);
 
 /* The forward's causal attention alone, on device memory, for checking it on
  * its own: head h of token m attends over positions [lo, pos[m]] of cache slot

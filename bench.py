@@ -13,8 +13,11 @@ Two passes of the same K steps run, each after the same prefill and warmup.
 In the first, every kernel launch records its own dispatch start and stop on
 HIP events (hipExtLaunchKernel on the library's stream, ec_prof_*): that
 gives the per-kernel table and the launch durations of the roofline object
-(the family with the largest total time; roofline_int8_gemv: the int8-weight
-GEMV family with the largest total time).  The second is the timed region
+(the family with the largest total time: the persistent decode step, which
+runs every layer; int8_weight_stream: the layers' int8 weights and scales per
+step over that kernel's time; roofline_lm_head: the fp16 LM head;
+roofline_int8_gemv: the largest separate int8 GEMV family, when the step is
+off).  The second is the timed region
 proper (value, ms_per_step), with nothing but the work.  The launch durations
 agree with rocprofv3's kernel trace of the same command (profiles/), and
 both passes must produce the same tokens.  roofline.traffic is the HBM bytes
@@ -326,9 +329,11 @@ def main() -> int:
         k["share"] = round(k["total_us"] / tot, 4)
         k["hbm_frac"] = round(k["gbps"] / HBM_PEAK_GBPS, 4)
     dom = max(kernels, key=lambda k: k["total_us"]) if kernels else None
-    # the int8-weight GEMVs of the layers (the LM head is tied fp16)
+    # the int8-weight GEMVs: inside the persistent decode step (decode_step,
+    # all layers), or separate kernels when the step is off (EDGECORE_STEP=0)
     int8 = [k for k in kernels if k["kernel"] in ("gemv_qkv", "gemv_o", "gemv_gateup", "gemv_down")]
     dom_i8 = max(int8, key=lambda k: k["total_us"]) if int8 else None
+    lmh = next((k for k in kernels if k["kernel"] == "gemv_lmhead"), None)
 
     # HBM bytes per launch measured with rocprofv3 counters on this workload
     # (profiles/traffic.json: FETCH_SIZE + WRITE_SIZE of the decode launches,
@@ -353,6 +358,17 @@ def main() -> int:
     mean_pos = PROMPT + W + (K - 1) / 2.0
     step_bytes = Lyr * (lin + 4 * (lin // E) + (mean_pos + 1) * kv * 4) + V * E * 2
     value = K / elapsed
+    # the int8 weight stream of the decode GEMVs: int8 weights and row scales
+    # of every layer per step, over the time of the kernel(s) that stream them
+    # (the persistent step, which also holds the attention; or the separate
+    # GEMV kernels)
+    i8_bytes = Lyr * (lin + 4 * (lin // E))
+    i8_kernels = [k for k in kernels if k["kernel"] == "decode_step"] or int8
+    i8_us = sum(k["total_us"] for k in i8_kernels) / K if i8_kernels else 0.0
+    i8_stream = None if not i8_us else {
+        "kernels": [k["kernel"] for k in i8_kernels], "bytes_per_step": i8_bytes, "us_per_step": round(i8_us, 3),
+        "achieved": round(i8_bytes / (i8_us * 1e3), 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+        "frac": round(i8_bytes / (i8_us * 1e3) / HBM_PEAK_GBPS, 4)}
     out = {
         "metric": METRIC, "value": round(value, 2), "unit": "tok/s", "n_gpus": 1, "steps": K,
         "warmup": W, "ms_per_step": round(elapsed / K * 1e3, 4), "higher_is_better": True,
@@ -362,6 +378,8 @@ def main() -> int:
                    "prompt_tokens": PROMPT, "decode_positions": [PROMPT + W, PROMPT + W + K - 1],
                    "batch": 1},
         "roofline": roof(dom),
+        "int8_weight_stream": i8_stream,
+        "roofline_lm_head": roof(lmh),
         "roofline_int8_gemv": roof(dom_i8),
         "decode_bytes_per_step": int(step_bytes),
         "decode_effective_gbps": round(step_bytes * value / 1e9, 1),

@@ -278,7 +278,11 @@ static void jints(Json *j, const char *k, const int *v, int n)
     for (int i = 0; i < n; i++) fprintf(j->f, "%s%d", i ? "," : "", v[i]);
     fputc(']', j->f);
 }
-static void jclose(Json *j) { fputs(j->fields ? "\n}\n" : "{}\n", j->f); }
+static void jclose(Json *j)
+{
+    fputs(j->fields ? "\n}\n" : "{}\n", j->f);
+    fflush(j->f);
+}
 
 static void jpin(Json *j, const CpuPin *p)
 {

@@ -31,6 +31,14 @@ prefill_4x2048 is the prefill-heavy workload on the same model: 4 prompts of
 matrix-core GEMMs' TOP/s against the int8 dense peak.  It is reported beside
 the decode line, not as its value.
 
+gpt2_small_fp16: GPT-2 small with fp16 weights, a 128-token prompt prefilled
+on the 16-bit matrix-core GEMM (TFLOP/s against the fp16 dense peak), then
+128 greedy decode steps; the step's bytes (about 254 MB) fit in the 256 MiB
+Infinity Cache, which the line flags.  qwen25_1.5b_int8_m16: the
+Qwen2.5-1.5B shape in int8, 16 prompts of 1024 ids each prefilled into its
+own slot, then 256 greedy steps at M=16 (GB/s of the skinny int8 GEMMs).
+Both are reported beside the decode line.
+
 Prints one JSON line.
 """
 import argparse
@@ -143,6 +151,165 @@ def prefill_c4(ec, np, model: Path, cache: Path):
     }
 
 
+FP16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 matrix-core peak, TFLOP/s
+MALL_BYTES = 256 * 2 ** 20  # MI355X Infinity Cache (last-level, memory-side)
+
+
+def _prompts(ec, cache: Path, n: int, count: int, vocab: int):
+    out = []
+    for b in range(count):
+        f = cache / f"prompt{n}_v{vocab}_s{b + 1}.txt"
+        if not f.exists():
+            ec.synth(None, prompt_out=f, prompt_len=n, prompt_seed=b + 1, vocab=vocab)
+        out.append(ec.read_ids(f))
+    return out
+
+
+def _prof(L, fn):
+    """run fn with per-launch dispatch timestamps; the per-family table"""
+    L.ec_sync()
+    L.ec_prof_start(b"")
+    fn()
+    L.ec_sync()
+    buf = __import__("ctypes").create_string_buffer(1 << 16)
+    return json.loads(buf.value.decode()) if L.ec_prof_stop(buf, len(buf)) > 0 else []
+
+
+def _batched_leg(ec, np, model: Path, prompts, n_decode: int, prof_steps: int):
+    """prefill every prompt into its own slot (one at a time, LM head on the
+    last row and device argmax: time to first token), then n_decode greedy
+    steps with one token per slot; then a pass with per-launch timestamps of
+    one prefill and of prof_steps more decode steps"""
+    B, n = len(prompts), len(prompts[0])
+    m = ec.Model(model, B, n + n_decode + prof_steps + 8)
+    L = ec.lib()
+    pos = np.arange(n)
+
+    def prefill(b):
+        _, am = m.forward(prompts[b], pos, np.full(n, b, np.int32), lm_from=n - 1, want_logits=False,
+                          want_argmax=True)
+        return int(am[0])
+
+    m.kv_reset()
+    prefill(0)  # warm
+    m.kv_reset()
+    L.ec_sync()
+    t0 = time.perf_counter()
+    cur = [prefill(b) for b in range(B)]
+    L.ec_sync()
+    t_prefill = time.perf_counter() - t0
+    p = [n] * B
+
+    def decode(k):
+        nonlocal cur, p
+        for _ in range(k):
+            _, am = m.forward(cur, p, None, want_logits=False, want_argmax=True)
+            cur, p = [int(x) for x in am], [x + 1 for x in p]
+
+    decode(2)  # warm the decode path (graph capture at M=1)
+    L.ec_sync()
+    t0 = time.perf_counter()
+    decode(n_decode)
+    L.ec_sync()
+    t_decode = time.perf_counter() - t0
+    dec_kernels = _prof(L, lambda: decode(prof_steps))
+    pre_kernels = _prof(L, lambda: prefill(0))
+    m.close()
+    return t_prefill, t_decode, pre_kernels, dec_kernels
+
+
+def _gemm_rates(kernels, shapes, rows, peak, unit):
+    """TFLOP/s (TOP/s) of the matrix-core GEMM families over a prefill of rows
+    tokens: 2 * rows * N * K per launch"""
+    out = []
+    for k in kernels:
+        if k["kernel"] in shapes:
+            N_, K_ = shapes[k["kernel"]]
+            r = 2.0 * rows * N_ * K_ / (k["avg_us"] * 1e6)
+            out.append({"kernel": k["kernel"], "avg_us": k["avg_us"], "launches": k["launches"],
+                        "achieved": round(r, 1), "peak": peak, "unit": unit, "frac": round(r / peak, 4)})
+    return sorted(out, key=lambda x: -x["avg_us"] * x["launches"])
+
+
+def leg_gpt2_small_fp16(ec, np, cache: Path):
+    """GPT-2 small, fp16 weights N(0, 0.02) from seed 0: a 128-token prompt
+    (ids uniform in [0, 50257), seed 1) prefilled on the 16-bit matrix-core
+    path, then 128 greedy decode steps (positions 128-255)."""
+    E, F, L_, V, n, steps = 768, 3072, 12, 50257, 128, 128
+    model = cache / "gpt2-small-fp16.ecm"
+    if not model.exists():
+        tmp = cache / "gpt2-small-fp16.ecm.tmp"
+        ec.synth(tmp, preset="gpt2-small")
+        tmp.rename(model)
+    prompts = _prompts(ec, cache, n, 1, V)
+    t_pre, t_dec, pre_k, dec_k = _batched_leg(ec, np, model, prompts, steps, 16)
+    # bytes of one decode step: fp16 weights, fp32 biases and LayerNorm
+    # parameters, the tied fp16 LM head, and the fp16 K/V read at the mean position
+    w = L_ * ((4 * E * E + 2 * E * F) * 2 + (6 * E + F) * 4 + 4 * E * 4) + V * E * 2 + 2 * E * 4
+    mean_pos = n + (steps - 1) / 2.0 + 2
+    kv = L_ * (mean_pos + 1) * E * 2 * 2
+    step_bytes = w + kv
+    shapes = {"gemm_qkv": (3 * E, E), "gemm_o": (E, E), "gemm_fc": (F, E), "gemm_down": (E, F)}
+    gem = _gemm_rates(pre_k, shapes, n, FP16_PEAK_TFLOPS, "TFLOP/s (fp16)")
+    dom_dec = max(dec_k, key=lambda k: k["total_us"]) if dec_k else None
+    return {
+        "workload": f"GPT-2 small fp16 bs1: {n}-token prompt, then {steps} greedy decode steps",
+        "prefill_tok_s": round(n / t_pre, 1), "ttft_ms": round(t_pre * 1e3, 3),
+        "decode_tok_s": round(steps / t_dec, 1), "ms_per_step": round(t_dec / steps * 1e3, 4),
+        "decode_bytes_per_step": int(step_bytes),
+        "decode_effective_gbps": round(step_bytes * steps / t_dec / 1e9, 1),
+        "decode_hbm_frac": round(step_bytes * steps / t_dec / 1e9 / HBM_PEAK_GBPS, 4),
+        "fits_in_mall": step_bytes < MALL_BYTES,
+        "mall_note": "the step's weights, LM head and KV cache total less than the 256 MiB Infinity Cache, "
+                     "so repeated steps may be served partly from it: effective GB/s is not an HBM figure",
+        "prefill_gemms": gem,
+        "decode_dominant_kernel": None if not dom_dec else {
+            "kernel": dom_dec["kernel"], "avg_us": dom_dec["avg_us"], "gbps": dom_dec["gbps"]},
+        "prefill_kernels": pre_k, "decode_kernels": dec_k,
+    }
+
+
+def leg_qwen25_15b_int8_m16(ec, np, cache: Path, n=1024, steps=256):
+    """Qwen2.5-1.5B shape, int8 per-channel weights N(0, 0.02) from seed 0:
+    16 prompts of 1024 ids (seeds 1-16), each prefilled into its own slot, then
+    256 greedy decode steps at M=16 (one token per slot): the skinny M=16
+    int8 matrix-core GEMMs."""
+    E, F, kvd, L_, V, B = 1536, 8960, 256, 28, 151936, 16
+    model = cache / "qwen2.5-1.5b-int8.ecm"
+    if not model.exists():
+        tmp = cache / "qwen2.5-1.5b-int8.ecm.tmp"
+        ec.synth(tmp, preset="qwen2.5-1.5b")
+        tmp.rename(model)
+    prompts = _prompts(ec, cache, n, B, V)
+    t_pre, t_dec, pre_k, dec_k = _batched_leg(ec, np, model, prompts, steps, 8)
+    lin = E * (E + 2 * kvd) + E * E + 3 * F * E
+    rows = (E + 2 * kvd) + E + 2 * F + E
+    w = L_ * (lin + 4 * rows + 2 * E * 4 + (E + 2 * kvd) * 4) + V * E * 2
+    mean_pos = n + (steps - 1) / 2.0 + 2
+    kv = B * L_ * (mean_pos + 1) * kvd * 2 * 2
+    step_bytes = w + kv
+    shapes = {"gemm_qkv": (E + 2 * kvd, E), "gemm_o": (E, E), "gemm_gateup": (2 * F, E), "gemm_down": (E, F)}
+    dec_gemms = []
+    for k in dec_k:
+        if k["kernel"] in shapes:
+            dec_gemms.append({"kernel": k["kernel"], "avg_us": k["avg_us"], "launches": k["launches"],
+                              "achieved": k["gbps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                              "frac": round(k["gbps"] / HBM_PEAK_GBPS, 4)})
+    dec_gemms.sort(key=lambda x: -x["avg_us"] * x["launches"])
+    return {
+        "workload": f"Qwen2.5-1.5B-shape int8: {B} prompts of {n} ids, one slot each, prefilled one at a "
+                    f"time; then {steps} greedy decode steps at M={B}",
+        "prefill_tok_s": round(B * n / t_pre, 1), "ms_per_prompt": round(t_pre / B * 1e3, 3),
+        "decode_tok_s": round(B * steps / t_dec, 1), "ms_per_step": round(t_dec / steps * 1e3, 4),
+        "decode_bytes_per_step": int(step_bytes),
+        "decode_effective_gbps": round(step_bytes * steps / t_dec / 1e9, 1),
+        "decode_hbm_frac": round(step_bytes * steps / t_dec / 1e9 / HBM_PEAK_GBPS, 4),
+        "decode_m16_gemms": dec_gemms,
+        "prefill_gemms": _gemm_rates(pre_k, shapes, n, INT8_PEAK_TOPS, "TOP/s (int8)"),
+        "prefill_kernels": pre_k, "decode_kernels": dec_k,
+    }
+
+
 def cpu_info():
     """(model name, physical cores of socket 0 among the CPUs this process may
     run on, the cgroup CPU quota in whole CPUs or None)"""
@@ -240,6 +407,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-tokens", type=int, default=16)
     ap.add_argument("--no-prefill", action="store_true", help="skip the 4 x 2048-token prefill leg")
+    ap.add_argument("--no-gpt2", action="store_true", help="skip the GPT-2 small fp16 leg")
+    ap.add_argument("--no-m16", action="store_true", help="skip the Qwen2.5-1.5B M=16 batched-decode leg")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="also run the plain copy kernel (ec_device_math op 6) 8 times on this many "
                          "bytes: the reference for HBM traffic counters and achievable bandwidth")
@@ -392,6 +561,10 @@ def main() -> int:
     }
     if not args.no_prefill:
         out["prefill_4x2048"] = prefill_c4(ec, np, model, Path(args.cache))
+    if not args.no_gpt2:
+        out["gpt2_small_fp16"] = leg_gpt2_small_fp16(ec, np, Path(args.cache))
+    if not args.no_m16:
+        out["qwen25_1.5b_int8_m16"] = leg_qwen25_15b_int8_m16(ec, np, Path(args.cache))
     if not args.no_cpu_baseline:
         try:
             out["cpu_baseline"] = cpu_baseline(model, prompt_file, args.cpu_tokens)

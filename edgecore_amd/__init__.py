@@ -83,6 +83,7 @@ _SIG = {
     "ec_gemm_bf16_fp32_dev": (_I, [_P, _P, _P, _I, _I, _I]),
     "ec_gemm_int8_dev": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I]),
     "ec_gemm_int8_epi_dev": (_I, [_I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I]),
+    "ec_gemm_w16_epi_dev": (_I, [_I, _I, _I, _P, _P, _P, _P, _P, _I, _I, _I]),
     "ec_quantize_rows_dev": (_I, [_P, _I, _I, _P, _P]),
     "gpt2_load": (_I, [_P, C.c_char_p, _I, _I]),
     "gpt2_free": (None, [_P]),
@@ -207,6 +208,33 @@ def quantize_int8_symmetric(w: np.ndarray):
     s = np.empty(rows, np.float32)
     lib().ec_quantize_int8_symmetric(_ptr(w), rows, cols, _ptr(q), _ptr(s))
     return q, s
+
+
+def gemm_w16_epi(wt: int, epi: int, bm: int, A: np.ndarray, B: np.ndarray, B2: Optional[np.ndarray] = None,
+                 bias: Optional[np.ndarray] = None, C0: Optional[np.ndarray] = None) -> np.ndarray:
+    """ec_gemm_w16_epi_dev on host arrays copied to the device: the 16-bit
+    weight matrix-core GEMM (wt 1 fp16, 2 bf16; B and B2 as uint16 bit
+    patterns) with epilogue epi (0 store, 1 residual onto C0, 2 GELU, 3 SwiGLU
+    with B2, 4-6 the same with bias) and row tile bm (0 = the library's
+    choice)."""
+    M, K = A.shape
+    N = B.shape[0]
+    arrs = [np.ascontiguousarray(A, np.float32), np.ascontiguousarray(B, np.uint16)]
+    opt = [None if B2 is None else np.ascontiguousarray(B2, np.uint16),
+           None if bias is None else np.ascontiguousarray(bias, np.float32)]
+    c0 = np.zeros((M, N), np.float32) if C0 is None else np.ascontiguousarray(C0, np.float32)
+    bufs = [DeviceBuffer.from_array(x) for x in arrs]
+    obufs = [None if x is None else DeviceBuffer.from_array(x) for x in opt]
+    cb = DeviceBuffer.from_array(c0)
+    try:
+        p = [b.ptr for b in bufs] + [None if b is None else b.ptr for b in obufs]
+        _check(lib().ec_gemm_w16_epi_dev(int(wt), int(epi), int(bm), cb.ptr, p[0], p[1], p[2], p[3], M, K, N),
+               "ec_gemm_w16_epi_dev")
+        _check(lib().ec_sync(), "ec_sync")
+        return cb.to_array(np.float32, (M, N))
+    finally:
+        for b in bufs + [x for x in obufs if x is not None] + [cb]:
+            b.close()
 
 
 def gemm_int8_epi(epi: int, bm: int, A: np.ndarray, a_scale: np.ndarray, B: np.ndarray,

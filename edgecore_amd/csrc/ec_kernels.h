@@ -84,6 +84,17 @@ bool gemm_i8_ok(const GemvArgs &a, int epi);
 hipError_t gemm_i8(const GemvArgs &a, int epi, hipStream_t s);
 // the same with the row tile forced: bm 32, 64 or 128 (0: gemm_i8's choice)
 hipError_t gemm_i8_tile(const GemvArgs &a, int epi, int bm, hipStream_t s);
+// 16-bit-weight matrix-core GEMM (gemm_mfma.hip) for M >= kGemmMinM: fp32 A
+// rows (lda), fp16 or bf16 weights, every epilogue but argmax candidates,
+// no weight scales.  It first splits the rows into w16_parts(wt) 16-bit parts
+// in `parts` ([M * parts][ldp] halves, ldp >= K, ldp % 8 == 0, 16-byte
+// aligned) with per-row scales in rs[M].  gemm_w16_ok: K % 8, 16-byte aligned
+// W / W2.
+int w16_parts(int wt);
+bool gemm_w16_ok(const GemvArgs &a, int wt, int epi);
+hipError_t gemm_w16(const GemvArgs &a, int wt, int epi, uint16_t *parts, int ldp, float *rs, hipStream_t s);
+hipError_t gemm_w16_tile(const GemvArgs &a, int wt, int epi, int bm, uint16_t *parts, int ldp, float *rs,
+                         hipStream_t s);
 // grid-size cap of the grid-stride GEMV (set from the CU count at init)
 void gemv_set_max_blocks(int n);
 int gemv_max_blocks();

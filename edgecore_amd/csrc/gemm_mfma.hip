@@ -1,25 +1,44 @@
-// int8 x int8 -> int32 GEMM on the gfx950 matrix cores, for the linears of a
-// prefill and of batched decode (M >= kGemmMinM rows):
+// GEMMs on the gfx950 matrix cores for the linears of a prefill and of
+// batched decode (M >= kGemmMinM rows).
+//
+// int8 weights (src/kernels.c:153-168, gemm_int8, with the epilogues
+// src/gpt2.c applies after it: residual add :782-784, SwiGLU :788-791, GELU
+// :568):
 //
 //   C[m][n] = epi( bias[n] + ((float)sum_k A[m][k]*B[n][k] * as[m]) * bs[n] )
 //
-// which is src/kernels.c:153-168 (gemm_int8) with the epilogues src/gpt2.c
-// applies after it (residual add :782-784, SwiGLU :788-791, GELU :568).  The
-// int32 dot is exact whatever the summation order, so v_mfma_i32_16x16x64_i8
-// reproduces the reference's dot bit for bit; the fp32 epilogue is the same
-// device code as the decode GEMV's (i8_epilogue, silu, gelu_new), so a row gives
-// the same floats through either kernel.
+// The int32 dot is exact whatever the summation order, so
+// v_mfma_i32_16x16x64_i8 reproduces the reference's dot bit for bit; the fp32
+// epilogue is the same device code as the decode GEMV's (i8_epilogue, silu,
+// gelu_new), so a row gives the same floats through either kernel.
+//
+// 16-bit weights (src/kernels.c:129-151, gemm_fp16_fp32 / gemm_bf16_fp32:
+// fp32 activations times fp16 or bf16 weights, fp32 sums).  The matrix cores
+// multiply 16-bit operands, so split_rows first writes every fp32 activation
+// row as a sum of 16-bit parts that the products see exactly:
+//   fp16 weights: x = 2^e (h + l), h = fp16(x 2^-e), l = fp16(x 2^-e - h),
+//                 with e = ilogb(max_k |x|) - 14 per row, so that h stays in
+//                 fp16 range and h + l carries 22 significant bits;
+//   bf16 weights: x = h + m + l, three bf16 parts (24 bits, fp32 range).
+// Each product of a 16-bit weight and a 16-bit part is exact in fp32 and the
+// matrix core sums in fp32, so C[m][n] = 2^e * sum_parts sum_k B[n][k] * part
+// differs from the reference's sequential fp32 dot only by fp32 rounding of
+// the sums (and by the < 2^-22 relative residue of the split) -- the same
+// class of difference as the vector GEMV's reordered fp32 sums.
 //
 // Tiling: a block of 256 threads (4 waves, 2 x 2) computes a BM x 128 tile of
 // C (for SwiGLU: BM x 64 outputs, each from a gate row and an up row).  K runs
-// in stages of 128 bytes through two LDS buffers; each thread holds the next
-// stage's 16-byte chunks in registers while the waves multiply the current
-// one.  Rows of the LDS tiles are 144 bytes apart, so the 16-byte fragment
-// reads of 8 consecutive lanes (16 rows, same k) fall on distinct banks.
+// in stages of 128 bytes (128 int8 or 64 16-bit elements) through two LDS
+// buffers; each thread holds the next stage's 16-byte chunks in registers
+// while the waves multiply the current one.  Rows of the LDS tiles are 144
+// bytes apart, so the 16-byte fragment reads of 8 consecutive lanes (16 rows,
+// same k) fall on distinct banks.  The activation tile holds NP parts (1 for
+// int8, 2 for fp16, 3 for bf16), part-major.
 //
-// MFMA lane layout (16x16x64, checked on the device): lane l supplies row
-// l % 16 of A (column l % 16 of B) with the 16 k-bytes 16*(l/16) .. +15, and
-// receives D[4*(l/16) + r][l % 16] in accumulator register r.
+// MFMA lane layout (16x16x64 i8 and 16x16x32 f16 / bf16, checked on the
+// device): lane l supplies row l % 16 of A (column l % 16 of B) with the 16
+// bytes at byte offset 16*(l/16) of the 64-byte k-slice, and receives
+// D[4*(l/16) + r][l % 16] in accumulator register r.
 #include "ec_device.h"
 #include "ec_kernels.h"
 
@@ -27,37 +46,80 @@ namespace ec {
 
 namespace {
 
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+
 constexpr int kBK = 128;            // K bytes per LDS stage
 constexpr int kPitch = kBK + 16;    // LDS row pitch in bytes
 constexpr int kBN = 128;            // B rows per block tile
 
-template <int BM>
+// operand kinds: int8 x int8 -> int32, fp16 x fp16 -> fp32, bf16 x bf16 -> fp32
+enum { OP_I8 = 0, OP_F16 = 1, OP_BF16 = 2 };
+
+template <int OP>
+struct MfmaOp;
+template <>
+struct MfmaOp<OP_I8> {
+  static constexpr int NP = 1, EB = 1;  // activation parts, bytes per element
+  using Acc = v4i;
+  static __device__ __forceinline__ Acc mma(v4i a, v4i b, Acc c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct MfmaOp<OP_F16> {
+  static constexpr int NP = 2, EB = 2;
+  using Acc = v4f;
+  static __device__ __forceinline__ Acc mma(v4i a, v4i b, Acc c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, a), __builtin_bit_cast(v8h, b), c, 0, 0, 0);
+  }
+};
+template <>
+struct MfmaOp<OP_BF16> {
+  static constexpr int NP = 3, EB = 2;
+  using Acc = v4f;
+  static __device__ __forceinline__ Acc mma(v4i a, v4i b, Acc c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, a), __builtin_bit_cast(v8bf, b), c, 0, 0,
+                                                   0);
+  }
+};
+
+template <int OP, int BM>
 constexpr size_t gemm_lds_bytes() {
-  return (size_t)2 * (BM + kBN) * kPitch;
+  return (size_t)2 * (MfmaOp<OP>::NP * BM + kBN) * kPitch;
 }
 
-template <int BM, int EPI>
-__global__ __launch_bounds__(256) void gemm_i8_kernel(GemvArgs a) {
+// A: [M * NP][lda] elements (row m's part p at row m * NP + p), as: per-row
+// scale (int8 quantization scale, or the split's 2^e; 1 for bf16)
+template <int OP, int BM, int EPI>
+__global__ __launch_bounds__(256) void gemm_mfma_kernel(GemvArgs a) {
+  using Op = MfmaOp<OP>;
+  using Acc = typename Op::Acc;
+  constexpr int NP = Op::NP;
+  constexpr bool I8 = OP == OP_I8;
   constexpr bool SWI = EPI == EPI_SWIGLU;
   constexpr bool RES = EPI == EPI_RESID || EPI == EPI_BIAS_RESID;
   constexpr bool GELU = EPI == EPI_GELU || EPI == EPI_BIAS_GELU;
   constexpr int WM = BM / 2, WN = kBN / 2;   // wave tile
   constexpr int TI = WM / 16, TJ = WN / 16;  // 16 x 16 MFMA tiles per wave
   constexpr int CPR = kBK / 16;              // 16-byte chunks per tile row and stage
-  constexpr int ACH = BM * CPR / 256;        // A chunks per thread and stage
+  constexpr int ACH = NP * BM * CPR / 256;   // A chunks per thread and stage
   constexpr int BCH = kBN * CPR / 256;       // B chunks per thread and stage
   constexpr int NOUT = SWI ? kBN / 2 : kBN;  // output columns per block
-  static_assert(ACH >= 1 && BCH >= 1 && TJ % 2 == 0, "tile shape");
+  static_assert(ACH >= 1 && BCH >= 1 && TJ % 2 == 0 && NP * BM * CPR % 256 == 0, "tile shape");
 
   extern __shared__ __attribute__((aligned(16))) int8_t lds[];
-  int8_t *la = lds;                       // [2][BM][kPitch]
-  int8_t *lb = lds + 2 * BM * kPitch;     // [2][kBN][kPitch]
+  int8_t *la = lds;                            // [2][NP][BM][kPitch]
+  int8_t *lb = lds + 2 * NP * BM * kPitch;     // [2][kBN][kPitch]
   __shared__ uint64_t etab[SWI ? 32 : 1];
 
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int lr = lane & 15, lq = lane >> 4;
   const int M = a.M, K = a.K, N = a.N;
+  const int KB = K * Op::EB;  // bytes of a weight row and of an activation part row
+  const size_t ldab = (size_t)a.lda * Op::EB;
   // XCD-aware tile order: block b runs on XCD b % 8; XCD x takes tiles
   // [x * per, (x + 1) * per) of the weight-row-major order, i.e. a contiguous
   // share of the weight rows with every row tile of A, so its L2 holds both
@@ -104,7 +166,9 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemvArgs a) {
     }
   }
 
-  // global chunk sources of this thread: tile row, 16-byte column, row base
+  // global chunk sources of this thread: tile row, 16-byte column, row base.
+  // A chunk c covers tile row r = c / CPR of the part-major tile: part r / BM
+  // of activation row m0 + r % BM.
   const int8_t *arow[ACH];
   const int8_t *brow[BCH];
   int acol[ACH], bcol[BCH], aoff[ACH], boff[BCH];
@@ -112,8 +176,9 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemvArgs a) {
 #pragma unroll
   for (int j = 0; j < ACH; j++) {
     const int c = t + 256 * j, r = c / CPR;
+    const int p = r / BM, mr = r % BM;
     acol[j] = c % CPR;
-    arow[j] = A + (size_t)min(m0 + r, M - 1) * a.lda;
+    arow[j] = A + ((size_t)min(m0 + mr, M - 1) * NP + p) * ldab;
     aoff[j] = r * kPitch + 16 * acol[j];
   }
 #pragma unroll
@@ -126,32 +191,32 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemvArgs a) {
       W = (const int8_t *)a.W2;
       n = n0 + r - kBN / 2;
     }
-    brow[j] = W + (size_t)min(n, N - 1) * K;
+    brow[j] = W + (size_t)min(n, N - 1) * KB;
     boff[j] = r * kPitch + 16 * bcol[j];
   }
 
-  // chunks past K (a last stage shorter than kBK) are loaded clamped and
+  // chunks past the row (a last stage shorter than kBK) are loaded clamped and
   // zeroed when stored to LDS, so that nothing waits on the loads before the
   // multiplies of the current stage
   v4i ra[ACH], rb[BCH];
-  int kl = 0;  // k0 of the stage held in ra / rb
+  int kl = 0;  // byte offset of the stage held in ra / rb
   auto load = [&](int k0) {
     kl = k0;
 #pragma unroll
     for (int j = 0; j < ACH; j++)
-      ra[j] = *reinterpret_cast<const v4i *>(arow[j] + min(k0 + 16 * acol[j], K - 16));
+      ra[j] = *reinterpret_cast<const v4i *>(arow[j] + min(k0 + 16 * acol[j], KB - 16));
 #pragma unroll
     for (int j = 0; j < BCH; j++)
-      rb[j] = *reinterpret_cast<const v4i *>(brow[j] + min(k0 + 16 * bcol[j], K - 16));
+      rb[j] = *reinterpret_cast<const v4i *>(brow[j] + min(k0 + 16 * bcol[j], KB - 16));
   };
   auto store = [&](int buf) {
     const v4i z = {0, 0, 0, 0};
 #pragma unroll
     for (int j = 0; j < ACH; j++)
-      *reinterpret_cast<v4i *>(la + buf * BM * kPitch + aoff[j]) = kl + 16 * acol[j] < K ? ra[j] : z;
+      *reinterpret_cast<v4i *>(la + buf * NP * BM * kPitch + aoff[j]) = kl + 16 * acol[j] < KB ? ra[j] : z;
 #pragma unroll
     for (int j = 0; j < BCH; j++)
-      *reinterpret_cast<v4i *>(lb + buf * kBN * kPitch + boff[j]) = kl + 16 * bcol[j] < K ? rb[j] : z;
+      *reinterpret_cast<v4i *>(lb + buf * kBN * kPitch + boff[j]) = kl + 16 * bcol[j] < KB ? rb[j] : z;
   };
 
   // B tile rows of this wave's column tiles: plain, or gate (j < TJ/2) and up
@@ -166,33 +231,37 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemvArgs a) {
     }
   }
 
-  v4i acc[TI][TJ];
+  Acc acc[TI][TJ];
 #pragma unroll
   for (int i = 0; i < TI; i++)
 #pragma unroll
-    for (int j = 0; j < TJ; j++) acc[i][j] = v4i{0, 0, 0, 0};
+    for (int j = 0; j < TJ; j++) acc[i][j] = Acc{0, 0, 0, 0};
 
-  const int ns = (K + kBK - 1) / kBK;
+  const int ns = (KB + kBK - 1) / kBK;
   load(0);
   store(0);
   __syncthreads();
   for (int s = 0; s < ns; s++) {
     const int buf = s & 1;
     if (s + 1 < ns) load((s + 1) * kBK);
-    const int8_t *ta = la + buf * BM * kPitch + (wm * WM + lr) * kPitch + 16 * lq;
+    const int8_t *ta = la + buf * NP * BM * kPitch + (wm * WM + lr) * kPitch + 16 * lq;
     const int8_t *tb = lb + buf * kBN * kPitch + lr * kPitch + 16 * lq;
 #pragma unroll
     for (int kk = 0; kk < kBK / 64; kk++) {
-      v4i fa[TI], fb[TJ];
+      v4i fa[NP][TI], fb[TJ];
 #pragma unroll
-      for (int i = 0; i < TI; i++) fa[i] = *reinterpret_cast<const v4i *>(ta + 16 * i * kPitch + 64 * kk);
+      for (int p = 0; p < NP; p++)
+#pragma unroll
+        for (int i = 0; i < TI; i++)
+          fa[p][i] = *reinterpret_cast<const v4i *>(ta + (p * BM + 16 * i) * kPitch + 64 * kk);
 #pragma unroll
       for (int j = 0; j < TJ; j++) fb[j] = *reinterpret_cast<const v4i *>(tb + bt[j] * kPitch + 64 * kk);
 #pragma unroll
-      for (int i = 0; i < TI; i++)
+      for (int p = 0; p < NP; p++)
 #pragma unroll
-        for (int j = 0; j < TJ; j++)
-          acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
+        for (int i = 0; i < TI; i++)
+#pragma unroll
+          for (int j = 0; j < TJ; j++) acc[i][j] = Op::mma(fa[p][i], fb[j], acc[i][j]);
     }
     if (s + 1 < ns) store(buf ^ 1);
     __syncthreads();
@@ -213,11 +282,24 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemvArgs a) {
         const int m = lrow0 + 16 * i + r;
         if (m >= M) continue;
         const float as = e_as[i][r];
-        float v = i8_epilogue(acc[i][j][r], as, bs, bv);
-        if constexpr (SWI) {
-          const float u = i8_epilogue(acc[i][j + TJ / 2][r], as, bs2, 0.0f);
-          v = silu(v, etab) * u;
+        float v;
+        if constexpr (I8) {
+          v = i8_epilogue(acc[i][j][r], as, bs, bv);
+          if constexpr (SWI) {
+            const float u = i8_epilogue(acc[i][j + TJ / 2][r], as, bs2, 0.0f);
+            v = silu(v, etab) * u;
+          }
         } else {
+          // 16-bit: the split's 2^e, then the 16-bit GEMV's epilogue order
+          v = acc[i][j][r] * as;
+          if constexpr (SWI) {
+            const float u = acc[i][j + TJ / 2][r] * as;
+            v = silu(v, etab) * u;
+          } else if (a.bias) {
+            v = v + bv;
+          }
+        }
+        if constexpr (!SWI) {
           if constexpr (RES) v = e_old[i][j][r] + v;
           if constexpr (GELU) v = gelu_new(v);
         }
@@ -227,16 +309,16 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemvArgs a) {
   }
 }
 
-template <int BM, int EPI>
+template <int OP, int BM, int EPI>
 hipError_t launch_bm(const GemvArgs &a, hipStream_t s) {
   constexpr int NOUT = EPI == EPI_SWIGLU ? kBN / 2 : kBN;
   const int T = ((a.N + NOUT - 1) / NOUT) * ((a.M + BM - 1) / BM);
   const dim3 grid(8 * ((T + 7) / 8));
-  klaunch((gemm_i8_kernel<BM, EPI>), grid, dim3(256), gemm_lds_bytes<BM>(), s, a);
+  klaunch((gemm_mfma_kernel<OP, BM, EPI>), grid, dim3(256), gemm_lds_bytes<OP, BM>(), s, a);
   return hipGetLastError();
 }
 
-template <int EPI>
+template <int OP, int EPI>
 hipError_t launch_epi(const GemvArgs &a, int bm, hipStream_t s) {
   // the largest row tile that still gives every CU a block or more, else the
   // smallest (N = 896 at M = 2048: 448 blocks of 32 rows beat 224 of 64 rows,
@@ -244,36 +326,123 @@ hipError_t launch_epi(const GemvArgs &a, int bm, hipStream_t s) {
   constexpr int NOUT = EPI == EPI_SWIGLU ? kBN / 2 : kBN;
   const long gx = (a.N + NOUT - 1) / NOUT;
   if (bm == 0) bm = gx * ((a.M + 127) / 128) >= 256 ? 128 : gx * ((a.M + 63) / 64) >= 256 ? 64 : 32;
-  if (bm == 128) return launch_bm<128, EPI>(a, s);
-  if (bm == 64) return launch_bm<64, EPI>(a, s);
-  return launch_bm<32, EPI>(a, s);
+  if (bm == 128) return launch_bm<OP, 128, EPI>(a, s);
+  if (bm == 64) return launch_bm<OP, 64, EPI>(a, s);
+  return launch_bm<OP, 32, EPI>(a, s);
+}
+
+template <int OP>
+hipError_t launch_op(const GemvArgs &a, int epi, int bm, hipStream_t s) {
+  switch (epi) {
+    case EPI_STORE:
+    case EPI_BIAS: return launch_epi<OP, EPI_STORE>(a, bm, s);
+    case EPI_RESID:
+    case EPI_BIAS_RESID: return launch_epi<OP, EPI_RESID>(a, bm, s);
+    case EPI_GELU:
+    case EPI_BIAS_GELU: return launch_epi<OP, EPI_GELU>(a, bm, s);
+    case EPI_SWIGLU: return launch_epi<OP, EPI_SWIGLU>(a, bm, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+bool epi_ok(int epi) {
+  return epi == EPI_STORE || epi == EPI_RESID || epi == EPI_GELU || epi == EPI_SWIGLU || epi == EPI_BIAS ||
+         epi == EPI_BIAS_RESID || epi == EPI_BIAS_GELU;
+}
+
+bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+// bf16 bits of x rounded to nearest even (finite x)
+__device__ __forceinline__ uint16_t f2b_rne(float x) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+
+// one block of 256 threads per row: the row's 16-bit parts and scale
+template <int OP>
+__global__ __launch_bounds__(256) void split_kernel(const float *x, int ldx, int K, uint16_t *out, int ldo,
+                                                    float *rs) {
+  __shared__ float red[4];
+  const int m = blockIdx.x, t = threadIdx.x;
+  const float *row = x + (size_t)m * ldx;
+  if constexpr (OP == OP_F16) {
+    float mx = 0.0f;
+    for (int k = t; k < K; k += 256) mx = fmaxf(mx, fabsf(row[k]));
+    mx = block_max256(mx, red);
+    // 2^-e x in [2^14, 2^15) for the row's largest |x|; zero, tiny and
+    // non-finite rows keep e = 0 (values pass through the fp16 parts)
+    int e = 0;
+    if (mx > 0.0f && mx <= 3.402823466e38f) e = max(ilogbf(mx) - 14, -100);
+    uint16_t *h = out + (size_t)m * 2 * ldo, *l = h + ldo;
+    for (int k = t; k < K; k += 256) {
+      const float v = ldexpf(row[k], -e);
+      const _Float16 hi = (_Float16)v;
+      h[k] = __builtin_bit_cast(uint16_t, hi);
+      l[k] = f2h(v - (float)hi);
+    }
+    if (t == 0) rs[m] = ldexpf(1.0f, e);
+  } else {
+    uint16_t *h = out + (size_t)m * 3 * ldo, *mid = h + ldo, *l = mid + ldo;
+    for (int k = t; k < K; k += 256) {
+      const float v = row[k];
+      const uint16_t b0 = f2b_rne(v);
+      const float r1 = v - b2f(b0);
+      const uint16_t b1 = f2b_rne(r1);
+      const float r2 = r1 - b2f(b1);
+      h[k] = b0;
+      mid[k] = b1;
+      l[k] = f2b_rne(r2);
+    }
+    if (t == 0) rs[m] = 1.0f;
+  }
 }
 
 }  // namespace
 
 bool gemm_i8_ok(const GemvArgs &a, int epi) {
-  const auto al = [](const void *p) { return ((uintptr_t)p & 15u) == 0; };
   if (a.M < 1 || a.N < 1 || a.K < 16 || a.K % 16 || a.lda % 16 || !a.as || a.cand) return false;
-  if (!al(a.A) || !al(a.W)) return false;
-  if (epi == EPI_SWIGLU && (!a.W2 || !al(a.W2))) return false;
-  return epi == EPI_STORE || epi == EPI_RESID || epi == EPI_GELU || epi == EPI_SWIGLU || epi == EPI_BIAS ||
-         epi == EPI_BIAS_RESID || epi == EPI_BIAS_GELU;
+  if (!aligned16(a.A) || !aligned16(a.W)) return false;
+  if (epi == EPI_SWIGLU && (!a.W2 || !aligned16(a.W2))) return false;
+  return epi_ok(epi);
 }
 
 hipError_t gemm_i8_tile(const GemvArgs &a, int epi, int bm, hipStream_t s) {
   if (!gemm_i8_ok(a, epi) || (bm != 0 && bm != 32 && bm != 64 && bm != 128)) return hipErrorInvalidValue;
-  switch (epi) {
-    case EPI_STORE:
-    case EPI_BIAS: return launch_epi<EPI_STORE>(a, bm, s);
-    case EPI_RESID:
-    case EPI_BIAS_RESID: return launch_epi<EPI_RESID>(a, bm, s);
-    case EPI_GELU:
-    case EPI_BIAS_GELU: return launch_epi<EPI_GELU>(a, bm, s);
-    case EPI_SWIGLU: return launch_epi<EPI_SWIGLU>(a, bm, s);
-  }
-  return hipErrorInvalidValue;
+  return launch_op<OP_I8>(a, epi, bm, s);
 }
 
 hipError_t gemm_i8(const GemvArgs &a, int epi, hipStream_t s) { return gemm_i8_tile(a, epi, 0, s); }
+
+int w16_parts(int wt) { return wt == WT_BF16 ? 3 : 2; }
+
+bool gemm_w16_ok(const GemvArgs &a, int wt, int epi) {
+  if (wt != WT_F16 && wt != WT_BF16) return false;
+  if (a.M < 1 || a.N < 1 || a.K < 8 || a.K % 8 || a.cand || a.ws || a.ws2) return false;
+  if (!aligned16(a.W)) return false;
+  if (epi == EPI_SWIGLU && (!a.W2 || !aligned16(a.W2))) return false;
+  return epi_ok(epi);
+}
+
+hipError_t gemm_w16_tile(const GemvArgs &a, int wt, int epi, int bm, uint16_t *parts, int ldp, float *rs,
+                         hipStream_t s) {
+  if (!gemm_w16_ok(a, wt, epi) || (bm != 0 && bm != 32 && bm != 64 && bm != 128)) return hipErrorInvalidValue;
+  if (!parts || !rs || ldp < a.K || ldp % 8 || !aligned16(parts)) return hipErrorInvalidValue;
+  const float *x = (const float *)a.A;
+  if (wt == WT_F16) klaunch((split_kernel<OP_F16>), dim3(a.M), dim3(256), 0, s, x, a.lda, a.K, parts, ldp, rs);
+  else klaunch((split_kernel<OP_BF16>), dim3(a.M), dim3(256), 0, s, x, a.lda, a.K, parts, ldp, rs);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  GemvArgs q = a;
+  q.A = parts;
+  q.lda = ldp;
+  q.as = rs;
+  // the 16-bit linears add a bias only in their BIAS epilogues
+  if (epi != EPI_BIAS && epi != EPI_BIAS_RESID && epi != EPI_BIAS_GELU) q.bias = nullptr;
+  return wt == WT_F16 ? launch_op<OP_F16>(q, epi, bm, s) : launch_op<OP_BF16>(q, epi, bm, s);
+}
+
+hipError_t gemm_w16(const GemvArgs &a, int wt, int epi, uint16_t *parts, int ldp, float *rs, hipStream_t s) {
+  return gemm_w16_tile(a, wt, epi, 0, parts, ldp, rs, s);
+}
 
 }  // namespace ec

@@ -349,6 +349,32 @@ extern "C" int ec_gemm_int8_epi_dev(int epi, int bm, float *C, const int8_t *A, 
   return 0;
 }
 
+// 16-bit parts of the kernel-ABI 16-bit GEMMs' activation rows, grown on demand
+static uint16_t *g_w16_parts = nullptr;
+static float *g_w16_rs = nullptr;
+static size_t g_w16_halves = 0, g_w16_rows = 0;
+
+static int w16_workspace(int M, int ldp) {
+  const size_t halves = (size_t)M * 3 * ldp;
+  if (halves > g_w16_halves) {
+    EC_HIP(hipStreamSynchronize(g_stream));
+    if (g_w16_parts) EC_HIP(hipFree(g_w16_parts));
+    g_w16_parts = nullptr;
+    g_w16_halves = 0;
+    EC_HIP(hipMalloc(&g_w16_parts, halves * sizeof(uint16_t)));
+    g_w16_halves = halves;
+  }
+  if ((size_t)M > g_w16_rows) {
+    EC_HIP(hipStreamSynchronize(g_stream));
+    if (g_w16_rs) EC_HIP(hipFree(g_w16_rs));
+    g_w16_rs = nullptr;
+    g_w16_rows = 0;
+    EC_HIP(hipMalloc(&g_w16_rs, (size_t)M * sizeof(float)));
+    g_w16_rows = M;
+  }
+  return 0;
+}
+
 static int gemm_w16_dev(float *C, const float *A, const uint16_t *B, int M, int K, int N, bool bf16) {
   EC_INIT();
   if (M < 0 || N < 0 || K < 0) return set_err(-1, "gemm: negative shape M=%d K=%d N=%d", M, K, N);
@@ -356,8 +382,37 @@ static int gemm_w16_dev(float *C, const float *A, const uint16_t *B, int M, int 
   if (!C || (K > 0 && (!A || !B))) return set_err(-1, "gemm: null pointer");
   const int wt = bf16 ? WT_BF16 : WT_F16;
   GemvArgs a{A, K, nullptr, nullptr, nullptr, 0.0, B, nullptr, nullptr, nullptr, nullptr, C, N, M, K, N, nullptr};
-  EC_LAUNCH("gemv_w16", gemv_bytes(wt, PRO_F32, EPI_STORE, M, K, N, false, false),
-            gemv_any(a, wt, EPI_STORE, PRO_F32, g_stream));
+  const double bytes = gemv_bytes(wt, PRO_F32, EPI_STORE, M, K, N, false, false);
+  if (g_use_mfma && M >= kGemmMinM && gemm_w16_ok(a, wt, EPI_STORE)) {
+    const int ldp = (K + 7) & ~7;
+    int r;
+    if ((r = w16_workspace(M, ldp))) return r;
+    EC_LAUNCH("gemm_w16", bytes, gemm_w16(a, wt, EPI_STORE, g_w16_parts, ldp, g_w16_rs, g_stream));
+    return 0;
+  }
+  EC_LAUNCH("gemv_w16", bytes, gemv_any(a, wt, EPI_STORE, PRO_F32, g_stream));
+  return 0;
+}
+
+// 16-bit-weight matrix-core GEMM with a fused epilogue and a chosen row tile,
+// on device buffers: the forward's 16-bit prefill linears, callable alone for
+// checks.  wt 1 fp16 / 2 bf16; epi as ec_gemm_int8_epi_dev plus 4-6 (bias
+// store / residual / GELU).
+extern "C" int ec_gemm_w16_epi_dev(int wt, int epi, int bm, float *C, const float *A, const uint16_t *B,
+                                   const uint16_t *B2, const float *bias, int M, int K, int N) {
+  EC_INIT();
+  if (wt != WT_F16 && wt != WT_BF16) return set_err(-1, "ec_gemm_w16_epi_dev: weight type %d (1 fp16, 2 bf16)", wt);
+  if (M < 1 || N < 1 || K < 8 || K % 8)
+    return set_err(-1, "ec_gemm_w16_epi_dev: shape M=%d K=%d N=%d (K a multiple of 8)", M, K, N);
+  if (epi < EPI_STORE || epi > EPI_BIAS_GELU) return set_err(-1, "ec_gemm_w16_epi_dev: epilogue %d", epi);
+  if (bm != 0 && bm != 32 && bm != 64 && bm != 128) return set_err(-1, "ec_gemm_w16_epi_dev: row tile %d", bm);
+  if (!C || !A || !B || (epi == EPI_SWIGLU && !B2)) return set_err(-1, "ec_gemm_w16_epi_dev: null pointer");
+  GemvArgs a{A, K, nullptr, nullptr, nullptr, 0.0, B, B2, nullptr, nullptr, bias, C, N, M, K, N, nullptr};
+  if (!gemm_w16_ok(a, wt, epi)) return set_err(-1, "ec_gemm_w16_epi_dev: unaligned operands");
+  const int ldp = (K + 7) & ~7;
+  int r;
+  if ((r = w16_workspace(M, ldp))) return r;
+  EC_LAUNCH("gemm_w16", 0.0, gemm_w16_tile(a, wt, epi, bm, g_w16_parts, ldp, g_w16_rs, g_stream));
   return 0;
 }
 
@@ -502,6 +557,11 @@ struct DevModel {
   float *x = nullptr, *h = nullptr, *qkv = nullptr, *att = nullptr, *ff = nullptr;
   int8_t *aq = nullptr;
   float *as = nullptr;
+  // 16-bit parts of fp32 activation rows for the 16-bit-weight matrix-core
+  // GEMM ([rows * 3][ah_ld] halves) and their row scales
+  uint16_t *ah = nullptr;
+  int ah_ld = 0, ah_rows = 0;
+  float *ahs = nullptr;
   float *logits = nullptr;
   uint16_t *kc = nullptr, *vc = nullptr;
   size_t kv_layer = 0;  // elements per layer of one cache
@@ -583,7 +643,7 @@ struct Loader {
 static void free_dev(DevModel *d) {
   if (!d) return;
   void *ps[] = {d->arena, d->rope, d->d_tok, d->d_pos, d->d_slot, d->d_amax, d->x, d->h, d->qkv,
-                d->att, d->ff, d->aq, d->as, d->logits, d->kc, d->vc, d->cand, d->tk_cand,
+                d->att, d->ff, d->aq, d->as, d->ah, d->ahs, d->logits, d->kc, d->vc, d->cand, d->tk_cand,
                 d->tk_nan, d->tk_vals, d->tk_idx, d->tk_status, d->d_layers, d->xch, d->d_step_io, d->d_trace};
   for (void *p : ps)
     if (p) (void)hipFree(p);
@@ -885,6 +945,14 @@ static int load_impl(GPT2 *g, const char *path, int batch_cap, int max_ctx) {
   EC_HIP(hipMalloc(&d->ff, (size_t)mmax * F * 4));
   EC_HIP(hipMalloc(&d->aq, (size_t)mmax * d->aq_ld));
   EC_HIP(hipMalloc(&d->as, (size_t)mmax * 4));
+  {
+    // 16-bit linears: every row of every layer; int8 models: the LM head's rows
+    const bool w16 = g->precision != 0;
+    d->ah_rows = w16 ? mmax : d->lm_rows;
+    d->ah_ld = ((w16 ? qmax : E) + 7) & ~7;
+    EC_HIP(hipMalloc(&d->ah, (size_t)d->ah_rows * 3 * d->ah_ld * sizeof(uint16_t)));
+    EC_HIP(hipMalloc(&d->ahs, (size_t)d->ah_rows * 4));
+  }
   EC_HIP(hipMalloc(&d->logits, (size_t)d->lm_rows * V * 4));
   EC_HIP(hipMalloc(&d->d_tok, (size_t)mmax * 4));
   EC_HIP(hipMalloc(&d->d_pos, (size_t)mmax * 4));
@@ -979,7 +1047,7 @@ extern "C" int gpt2_kv_reset(GPT2 *g) {
 static const char *gemm_family(const char *fam) {
   static const char *const names[][2] = {{"gemv_qkv", "gemm_qkv"},       {"gemv_o", "gemm_o"},
                                          {"gemv_gateup", "gemm_gateup"}, {"gemv_fc", "gemm_fc"},
-                                         {"gemv_down", "gemm_down"}};
+                                         {"gemv_down", "gemm_down"},     {"gemv_lmhead", "gemm_lmhead"}};
   for (const auto &n : names)
     if (!strcmp(fam, n[0])) return n[1];
   return "gemm_i8";
@@ -1007,6 +1075,20 @@ static int linear(GPT2 *g, DevModel *d, const char *fam, GemvArgs a, int wt, int
       EC_LAUNCH(gemm_family(fam), bytes, gemm_i8(q, epi, s));
       return 0;
     }
+  }
+  if (wt != WT_I8 && g_use_mfma && a.M >= kGemmMinM && a.M <= d->ah_rows && a.K <= d->ah_ld &&
+      gemm_w16_ok(a, wt, epi)) {
+    // many rows, 16-bit weights: the norm as its own pass into fp32 rows, then
+    // the matrix-core GEMM (which splits the rows into 16-bit parts first)
+    GemvArgs q = a;
+    if (pro == PRO_RMS || pro == PRO_LN) {
+      EC_LAUNCH("norm", 8.0 * a.M * a.K,
+                norm_rows((const float *)a.A, a.M, a.K, a.gamma, a.beta, g->eps, d->h, a.K, nullptr, 0, nullptr, s));
+      q.A = d->h;
+      q.lda = a.K;
+    }
+    EC_LAUNCH(gemm_family(fam), bytes, gemm_w16(q, wt, epi, d->ah, d->ah_ld, d->ahs, s));
+    return 0;
   }
   if (gemv_vector_ok(a, wt, pro)) {
     EC_LAUNCH(fam, bytes, gemv(a, wt, epi, pro, s));

@@ -134,6 +134,18 @@ int ec_gemm_int8_dev(float *C, const int8_t *A, const float *a_scale, const int8
 int ec_gemm_int8_epi_dev(int epi, int bm, float *C, const int8_t *A, const float *a_scale, const int8_t *B,
                          const float *b_scale, const int8_t *B2, const float *b2_scale, const float *bias,
                          int M, int K, int N);
+/* The 16-bit-weight matrix-core GEMM of the forward's prefill linears
+ * (src/kernels.c:129-151 with the epilogues of src/gpt2.c), v = sum_k
+ * A[m][k] * B[n][k] in fp32 from fp16 (wt 1) or bf16 (wt 2) weights: epi 0
+ * C = v, 1 C += v, 2 C = gelu_new(v), 3 C = silu(v_B) * v_B2, 4 C = v +
+ * bias, 5 C += v + bias, 6 C = gelu_new(v + bias).  The fp32 rows of A are
+ * split into 16-bit parts first (2 for fp16 under a per-row power-of-two
+ * scale, 3 for bf16), so the sums carry fp32-level accuracy.  bm forces the
+ * row tile (32, 64, 128; 0 = the library's choice).  K a multiple of 8, B and
+ * B2 16-byte aligned.  ec_gemm_fp16_fp32_dev / ec_gemm_bf16_fp32_dev take
+ * this kernel for M >= 16. */
+int ec_gemm_w16_epi_dev(int wt, int epi, int bm, float *C, const float *A, const uint16_t *B,
+                        const uint16_t *B2, const float *bias, int M, int K, int N);
 /* Activation quantizer of the reference linear() (src/gpt2.c:446-461):
  * per row s = max|a|/127 (1 for an all-zero row), q = clamp(rint(a/s)). */
 int ec_quantize_rows_dev(const float *in, int M, int K, int8_t *q, float *s);

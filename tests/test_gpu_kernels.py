@@ -188,3 +188,93 @@ def test_gemm_int8_auto_tile_prefill_shapes(M, K, N):
     swi = ec.gemm_int8_epi(3, 0, A, a_s, B, b_s, B2=B2, b2_scale=b2_s)
     want = oracle.map_op(1, oracle.gemm_int8(A, a_s, B, b_s)) * oracle.gemm_int8(A, a_s, B2, b2_s)
     assert np.array_equal(_bits(swi), _bits(want))
+
+
+# ------------------------------------------------------------------ 16-bit weights on the matrix cores
+# ec_gemm_w16_epi_dev / ec_gemm_{fp16,bf16}_fp32_dev at M >= 16: the fp32
+# rows are split into 16-bit parts (fp16: 2 under a per-row 2^e; bf16: 3),
+# multiplied exactly and summed in fp32.  Every value is checked against the
+# float64 product with the fp32 bound of the vector path (2 K 2^-24 sum|a b|),
+# propagated through the epilogue.
+W16_MFMA_SHAPES = [(16, 768, 2304), (128, 768, 3072), (40, 3072, 768), (100, 896, 1000), (257, 64, 200),
+                   (33, 1536, 129)]
+
+
+def _w16_inputs(M, K, N, bf16, seed, scale=1.0):
+    rng = np.random.default_rng(seed)
+    A = (rng.normal(0, 1, (M, K)) * scale).astype(np.float32)
+    mk = _bf16_bits if bf16 else _f16_bits
+    B, B2 = (mk(rng.normal(0, 0.02, (N, K)).astype(np.float32)) for _ in range(2))
+    bias = rng.normal(0, 0.02, N).astype(np.float32)
+    C0 = rng.normal(0, 1.0, (M, N)).astype(np.float32)
+    return A, B, B2, bias, C0
+
+
+def _w16_f64(B, bf16):
+    return ((B.astype(np.uint32) << 16).view(np.float32) if bf16 else B.view(np.float16)).astype(np.float64)
+
+
+def _exact_and_bound(A, B, bf16):
+    Bf = _w16_f64(B, bf16)
+    A64 = A.astype(np.float64)
+    K = A.shape[1]
+    return A64 @ Bf.T, 2.0 * K * 2.0 ** -24 * (np.abs(A64) @ np.abs(Bf).T) + 1e-30
+
+
+def _gelu64(x):
+    return 0.5 * x * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (x + 0.044715 * x ** 3)))
+
+
+def _silu64(x):
+    return x / (1.0 + np.exp(-x))
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("M,K,N", W16_MFMA_SHAPES)
+def test_gemm_w16_matrix_core_within_bound(M, K, N, bf16):
+    A, B, _, _, _ = _w16_inputs(M, K, N, bf16, seed=M * 3 + K + N + bf16)
+    got = (ec.gemm_bf16_fp32 if bf16 else ec.gemm_fp16_fp32)(A, B)
+    exact, bound = _exact_and_bound(A, B, bf16)
+    assert np.all(np.abs(got - exact) <= bound)
+    # the split keeps far more than the bound needs: typically within a few fp32 ulps
+    assert np.median(np.abs(got - exact) / (np.abs(exact) + 1e-30)) < 1e-6
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("bm", [0, 32, 64, 128])
+@pytest.mark.parametrize("M,K,N", [(200, 768, 300), (130, 3072, 129), (64, 896, 128)])
+def test_gemm_w16_tiles_and_epilogues(bm, M, K, N, bf16):
+    wt = 2 if bf16 else 1
+    A, B, B2, bias, C0 = _w16_inputs(M, K, N, bf16, seed=M + K + N + bm + 7 * bf16)
+    v, bv = _exact_and_bound(A, B, bf16)
+    b64, c64 = bias.astype(np.float64), C0.astype(np.float64)
+    ulp = 2.0 ** -23
+
+    def check(got, want, tol):
+        assert np.all(np.abs(got.astype(np.float64) - want) <= tol + 2 * ulp * np.abs(want) + 1e-30)
+
+    check(ec.gemm_w16_epi(wt, 0, bm, A, B, bias=bias), v, bv)             # store: bias ignored
+    check(ec.gemm_w16_epi(wt, 4, bm, A, B, bias=bias), v + b64, bv)       # store + bias
+    check(ec.gemm_w16_epi(wt, 1, bm, A, B, C0=C0), c64 + v, bv)           # residual
+    check(ec.gemm_w16_epi(wt, 5, bm, A, B, bias=bias, C0=C0), c64 + (v + b64), bv)
+    check(ec.gemm_w16_epi(wt, 2, bm, A, B), _gelu64(v), 1.2 * bv + 1e-6)  # GELU (tanh form)
+    check(ec.gemm_w16_epi(wt, 6, bm, A, B, bias=bias), _gelu64(v + b64), 1.2 * bv + 1e-6)
+    u, bu = _exact_and_bound(A, B2, bf16)
+    want = _silu64(v) * u
+    tol = 1.1 * (np.abs(u) * bv + np.abs(_silu64(v)) * bu) + 1e-6 * np.abs(want)
+    check(ec.gemm_w16_epi(wt, 3, bm, A, B, B2=B2), want, tol)
+
+
+@pytest.mark.parametrize("scale", [1e-30, 1e-8, 1e4, 3e5, 1e30])
+def test_gemm_fp16_matrix_core_row_scale_range(scale):
+    """fp16 parts hold 2^-e x with e from each row's largest |x|: rows far
+    outside fp16 range (1e30, 3e5 > 65504) or deep in its subnormals
+    (1e-30) keep fp32-level accuracy.  One row is all zeros."""
+    M, K, N = 32, 768, 256
+    A, B, _, _, _ = _w16_inputs(M, K, N, False, seed=11, scale=scale)
+    A[3] = 0.0
+    got = ec.gemm_fp16_fp32(A, B)
+    exact, bound = _exact_and_bound(A, B, False)
+    assert np.all(np.isfinite(got))
+    assert np.all(np.abs(got - exact) <= bound)
+    assert not got[3].any()

@@ -84,6 +84,11 @@ bool gemm_i8_ok(const GemvArgs &a, int epi);
 hipError_t gemm_i8(const GemvArgs &a, int epi, hipStream_t s);
 // the same with the row tile forced: bm 32, 64 or 128 (0: gemm_i8's choice)
 hipError_t gemm_i8_tile(const GemvArgs &a, int epi, int bm, hipStream_t s);
+// skinny int8 matrix-core GEMM for M <= 32 rows (batched decode): one block
+// of wpb waves (0: the library's choice, at most 16) per 16 output columns,
+// K split over the waves and summed exactly through LDS.  Same floats as
+// gemm_i8.
+hipError_t gemm_i8_skinny(const GemvArgs &a, int epi, int wpb, hipStream_t s);
 // 16-bit-weight matrix-core GEMM (gemm_mfma.hip) for M >= kGemmMinM: fp32 A
 // rows (lda), fp16 or bf16 weights, every epilogue but argmax candidates,
 // no weight scales.  It first splits the rows into w16_parts(wt) 16-bit parts
@@ -246,8 +251,12 @@ size_t attention_lds_bytes(int max_npos, int hd, int vtile);
 // largest vtile the kernel accepts for this head_dim / KV row length
 int attention_max_vtile(int hd, int kv);
 
-// greedy argmax per row (src/runtime_main.c:215-218 semantics)
+// greedy argmax per row (src/runtime_main.c:215-218 semantics): one block per
+// row, or (chunked) per-chunk candidates into cand ([rows][<= cap]) and
+// argmax_finalize
 hipError_t argmax_rows(const float *logits, int rows, int V, int *out, hipStream_t st);
+hipError_t argmax_rows_chunked(const float *logits, int rows, int V, unsigned long long *cand, int cap, int *out,
+                               hipStream_t st);
 // final reduction of the LM head's per-block argmax candidates
 hipError_t argmax_finalize(const unsigned long long *cand, int ncand, const float *logits,
                            int ldl, int rows, int *out, hipStream_t st);

@@ -75,6 +75,41 @@ __global__ __launch_bounds__(256) void quant_kernel(const float *in, int ldi, in
   for (int k = threadIdx.x; k < K; k += 256) qr[k] = quant1(x[k], sc);
 }
 
+// the same for rows whose K is a multiple of 4 (16-byte aligned fp32 rows,
+// 4-byte aligned int8 rows): each thread keeps its NV float4 of the row in
+// registers between the max and the quantization
+template <int NV>
+__global__ __launch_bounds__(256) void quant_vec_kernel(const float *in, int ldi, int K, int8_t *q, int ldq,
+                                                        float *s) {
+  __shared__ float red[4];
+  const int m = blockIdx.x, t = threadIdx.x, K4 = K / 4;
+  const float4 *x = reinterpret_cast<const float4 *>(in + (size_t)m * ldi);
+  float4 v[NV];
+  float mx = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NV; j++) {
+    const int i = t + 256 * j;
+    if (i < K4) {
+      v[j] = x[i];
+      mx = fmaxf(mx, fabsf(v[j].x));
+      mx = fmaxf(mx, fabsf(v[j].y));
+      mx = fmaxf(mx, fabsf(v[j].z));
+      mx = fmaxf(mx, fabsf(v[j].w));
+    }
+  }
+  mx = block_max256(mx, red);
+  const float sc = quant_scale(mx);
+  if (t == 0) s[m] = sc;
+  uint32_t *qr = reinterpret_cast<uint32_t *>(q + (size_t)m * ldq);
+#pragma unroll
+  for (int j = 0; j < NV; j++) {
+    const int i = t + 256 * j;
+    if (i < K4)
+      qr[i] = (uint32_t)(uint8_t)quant1(v[j].x, sc) | ((uint32_t)(uint8_t)quant1(v[j].y, sc) << 8) |
+              ((uint32_t)(uint8_t)quant1(v[j].z, sc) << 16) | ((uint32_t)(uint8_t)quant1(v[j].w, sc) << 24);
+  }
+}
+
 // src/gpt2.c:398-414 (LN) and 592-604 (RMS): double accumulation, fp32 output
 template <bool LN, bool QUANT>
 __global__ __launch_bounds__(256) void norm_kernel(const float *x, int E, const float *gamma,
@@ -242,6 +277,32 @@ __global__ __launch_bounds__(256) void argmax_kernel(const float *L, int V, int 
   }
 }
 
+// first-stage argmax over chunks of csz logits: the orderable key (amax_key:
+// larger value, then lower index) of each (row, chunk) into cand[row][chunk];
+// NaN never wins, 0 stands for a chunk without a non-NaN value
+__global__ __launch_bounds__(256) void argmax_chunk_kernel(const float *L, int V, int csz,
+                                                           unsigned long long *cand) {
+  __shared__ unsigned long long red[4];
+  const int c = blockIdx.x, r = blockIdx.y, nc = gridDim.x;
+  const float *l = L + (size_t)r * V;
+  const int e = min(V, (c + 1) * csz);
+  unsigned long long b = 0ull;
+  for (int i = c * csz + threadIdx.x; i < e; i += 256) {
+    const float v = l[i];
+    if (v == v) {
+      const unsigned long long k = amax_key(v, i);
+      b = k > b ? k : b;
+    }
+  }
+  b = wave_max_u64(b);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = b;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < 4; w++) b = red[w] > b ? red[w] : b;
+    cand[(size_t)r * nc + c] = b;
+  }
+}
+
 // argmax over the LM head's per-block candidates; logits[0] NaN -> 0 and no
 // non-NaN logit -> 0, like the reference's strict '>' scan from index 0
 __global__ __launch_bounds__(256) void argmax_finalize_kernel(const unsigned long long *cand, int ncand,
@@ -397,6 +458,17 @@ hipError_t gemv_generic(const GemvArgs &a, int wt, int epi, hipStream_t s) {
 
 hipError_t quant_rows(const float *in, int ldi, int M, int K, int8_t *q, int ldq, float *s,
                       hipStream_t st) {
+  const bool vec = K % 4 == 0 && ldi % 4 == 0 && ldq % 4 == 0 && ((uintptr_t)in & 15u) == 0 &&
+                   ((uintptr_t)q & 3u) == 0 && K <= 256 * 4 * 16;
+  if (vec) {
+    const int nv = (K / 4 + 255) / 256;
+    if (nv <= 1) klaunch(quant_vec_kernel<1>, dim3(M), dim3(256), 0, st, in, ldi, K, q, ldq, s);
+    else if (nv <= 2) klaunch(quant_vec_kernel<2>, dim3(M), dim3(256), 0, st, in, ldi, K, q, ldq, s);
+    else if (nv <= 4) klaunch(quant_vec_kernel<4>, dim3(M), dim3(256), 0, st, in, ldi, K, q, ldq, s);
+    else if (nv <= 8) klaunch(quant_vec_kernel<8>, dim3(M), dim3(256), 0, st, in, ldi, K, q, ldq, s);
+    else klaunch(quant_vec_kernel<16>, dim3(M), dim3(256), 0, st, in, ldi, K, q, ldq, s);
+    return hipGetLastError();
+  }
   klaunch(quant_kernel, dim3(M), dim3(256), 0, st, in, ldi, K, q, ldq, s);
   return hipGetLastError();
 }
@@ -476,6 +548,21 @@ hipError_t argmax_finalize(const unsigned long long *cand, int ncand, const floa
 
 hipError_t argmax_rows(const float *logits, int rows, int V, int *out, hipStream_t st) {
   klaunch(argmax_kernel, dim3(rows), dim3(256), 0, st, logits, V, out);
+  return hipGetLastError();
+}
+
+hipError_t argmax_rows_chunked(const float *logits, int rows, int V, unsigned long long *cand, int cap, int *out,
+                               hipStream_t st) {
+  // chunks of at least 2048 logits, at most cap per row
+  int nc = (V + 2047) / 2048;
+  if (nc > cap) nc = cap;
+  if (nc < 1) return hipErrorInvalidValue;
+  const int csz = (V + nc - 1) / nc;
+  nc = (V + csz - 1) / csz;
+  klaunch(argmax_chunk_kernel, dim3(nc, rows), dim3(256), 0, st, logits, V, csz, cand);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  klaunch(argmax_finalize_kernel, dim3(rows), dim3(256), 0, st, cand, nc, logits, V, out);
   return hipGetLastError();
 }
 

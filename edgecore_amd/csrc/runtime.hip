@@ -323,7 +323,11 @@ extern "C" int ec_gemm_int8_dev(float *C, const int8_t *A, const float *a_scale,
   GemvArgs a{A, K, a_scale, nullptr, nullptr, 0.0, B, nullptr, b_scale, nullptr, bias, C, N, M, K, N, nullptr};
   const double bytes = gemv_bytes(WT_I8, PRO_I8, EPI_STORE, M, K, N, b_scale, bias);
   if (g_use_mfma && M >= kGemmMinM && gemm_i8_ok(a, EPI_STORE)) {
-    EC_LAUNCH("gemm_i8", bytes, gemm_i8(a, EPI_STORE, g_stream));
+    if (M <= 32) {
+      EC_LAUNCH("gemm_i8", bytes, gemm_i8_skinny(a, EPI_STORE, 0, g_stream));
+    } else {
+      EC_LAUNCH("gemm_i8", bytes, gemm_i8(a, EPI_STORE, g_stream));
+    }
     return 0;
   }
   EC_LAUNCH("gemv_i8", bytes, gemv_any(a, WT_I8, EPI_STORE, PRO_I8, g_stream));
@@ -340,11 +344,17 @@ extern "C" int ec_gemm_int8_epi_dev(int epi, int bm, float *C, const int8_t *A, 
     return set_err(-1, "ec_gemm_int8_epi_dev: shape M=%d K=%d N=%d (K a multiple of 16)", M, K, N);
   if (epi != EPI_STORE && epi != EPI_RESID && epi != EPI_GELU && epi != EPI_SWIGLU)
     return set_err(-1, "ec_gemm_int8_epi_dev: epilogue %d (0 store, 1 residual, 2 GELU, 3 SwiGLU)", epi);
-  if (bm != 0 && bm != 32 && bm != 64 && bm != 128) return set_err(-1, "ec_gemm_int8_epi_dev: row tile %d", bm);
+  if (bm != 0 && bm != 16 && bm != 32 && bm != 64 && bm != 128)
+    return set_err(-1, "ec_gemm_int8_epi_dev: row tile %d", bm);
+  if (bm == 16 && M > 32) return set_err(-1, "ec_gemm_int8_epi_dev: the skinny kernel (bm 16) takes M <= 32, not %d", M);
   if (!C || !A || !a_scale || !B || (epi == EPI_SWIGLU && !B2)) return set_err(-1, "ec_gemm_int8_epi_dev: null pointer");
   GemvArgs a{A, K, a_scale, nullptr, nullptr, 0.0, B, B2, b_scale, b2_scale, epi == EPI_SWIGLU ? nullptr : bias,
              C, N, M, K, N, nullptr};
   if (!gemm_i8_ok(a, epi)) return set_err(-1, "ec_gemm_int8_epi_dev: unaligned operands");
+  if (bm == 16) {
+    EC_LAUNCH("gemm_i8", 0.0, gemm_i8_skinny(a, epi, 0, g_stream));
+    return 0;
+  }
   EC_LAUNCH("gemm_i8", 0.0, gemm_i8_tile(a, epi, bm, g_stream));
   return 0;
 }
@@ -1072,7 +1082,10 @@ static int linear(GPT2 *g, DevModel *d, const char *fam, GemvArgs a, int wt, int
         EC_LAUNCH("norm_quant", 5.0 * a.M * a.K,
                   norm_rows(A, a.M, a.K, a.gamma, a.beta, g->eps, nullptr, 0, d->aq, d->aq_ld, d->as, s));
       }
-      EC_LAUNCH(gemm_family(fam), bytes, gemm_i8(q, epi, s));
+      if (a.M <= 32)
+        EC_LAUNCH(gemm_family(fam), bytes, gemm_i8_skinny(q, epi, 0, s));
+      else
+        EC_LAUNCH(gemm_family(fam), bytes, gemm_i8(q, epi, s));
       return 0;
     }
   }
@@ -1294,7 +1307,11 @@ static int enqueue_forward(GPT2 *g, DevModel *d, int M, int lm_from, bool distin
     const int rows = M - r0 < d->lm_rows ? M - r0 : d->lm_rows;
     GemvArgs a{d->x + (size_t)r0 * E, E, nullptr, g->lnf_g, g->lnf_b, g->eps, d->lm, nullptr, nullptr, nullptr,
                nullptr, d->logits, V, rows, E, V, nullptr};
-    const bool fused = gemv_vector_ok(a, lwt, pro_norm);
+    // the matrix-core GEMM (many rows: the weights stream once) leaves the
+    // argmax to argmax_rows; the fused GEMV keeps per-block candidates
+    const bool mfma = g_use_mfma && rows >= kGemmMinM && rows <= d->ah_rows && E <= d->ah_ld &&
+                      gemm_w16_ok(a, lwt, EPI_STORE);
+    const bool fused = !mfma && gemv_vector_ok(a, lwt, pro_norm);
     if (argmax && fused) a.cand = d->cand;
     if ((r = linear(g, d, "gemv_lmhead", a, lwt, EPI_STORE, pro_norm, s))) return r;
     if (argmax) {
@@ -1303,7 +1320,8 @@ static int enqueue_forward(GPT2 *g, DevModel *d, int M, int lm_from, bool distin
                   argmax_finalize(d->cand, gemv_grid_x(a, lwt, EPI_STORE), d->logits, V, rows,
                                   amax_dev + (r0 - lm_from), s));
       else
-        EC_LAUNCH("argmax", 4.0 * rows * V, argmax_rows(d->logits, rows, V, amax_dev + (r0 - lm_from), s));
+        EC_LAUNCH("argmax", 4.0 * rows * V,
+                  argmax_rows_chunked(d->logits, rows, V, d->cand, d->ncand, amax_dev + (r0 - lm_from), s));
     }
     if (logits)
       EC_HIP(hipMemcpyAsync(logits + (size_t)(r0 - lm_from) * V, d->logits, (size_t)rows * V * 4,

@@ -130,7 +130,8 @@ int ec_gemm_int8_dev(float *C, const int8_t *A, const float *a_scale, const int8
  * (residual, src/gpt2.c:782-784), 2 C = gelu_new(v) (src/gpt2.c:568), 3 C =
  * silu(g) * u with g from B (b_scale, no bias) and u from B2 (b2_scale)
  * (src/gpt2.c:788-791).  bm forces the row tile (32, 64, 128; 0 = the
- * library's choice).  K a multiple of 16, A and B 16-byte aligned. */
+ * library's choice; 16 = the skinny kernel of batched decode, M <=
+ * 32).  K a multiple of 16, A and B 16-byte aligned. */
 int ec_gemm_int8_epi_dev(int epi, int bm, float *C, const int8_t *A, const float *a_scale, const int8_t *B,
                          const float *b_scale, const int8_t *B2, const float *b2_scale, const float *bias,
                          int M, int K, int N);

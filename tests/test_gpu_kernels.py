@@ -115,6 +115,28 @@ def test_quantize_rows_bit_exact_with_ties():
     assert gs[2] == 1.0 and not gq[2].any()
 
 
+@pytest.mark.parametrize("M,K", [(16, 8960), (3, 37), (2, 4100), (40, 1536)])
+def test_quantize_rows_vector_and_scalar_paths(M, K):
+    """K % 4 == 0 takes the float4 kernel, other K the scalar one; both give
+    the oracle's codes and scales bit for bit."""
+    rng = np.random.default_rng(M * K)
+    x = rng.normal(0, 2, (M, K)).astype(np.float32)
+    x[0, K // 2] = 0.5 * np.abs(x).max() * 2  # a row max inside the row
+    src = ec.DeviceBuffer.from_array(x)
+    q = ec.DeviceBuffer(x.size)
+    s = ec.DeviceBuffer(4 * M)
+    try:
+        assert ec.lib().ec_quantize_rows_dev(src.ptr, M, K, q.ptr, s.ptr) == 0, ec.last_error()
+        gq = q.to_array(np.int8, x.shape)
+        gs = s.to_array(np.float32, M)
+    finally:
+        for b in (src, q, s):
+            b.close()
+    oq, os_ = oracle.quantize_rows(x)
+    assert np.array_equal(gq, oq)
+    assert np.array_equal(gs.view(np.uint32), os_.view(np.uint32))
+
+
 def test_dev_entry_points_reject_bad_shapes():
     L = ec.lib()
     assert L.ec_gemm_int8_dev(None, None, None, None, None, None, -1, 4, 4) < 0
@@ -278,3 +300,36 @@ def test_gemm_fp16_matrix_core_row_scale_range(scale):
     assert np.all(np.isfinite(got))
     assert np.all(np.abs(got - exact) <= bound)
     assert not got[3].any()
+
+
+# ------------------------------------------------------------------ skinny int8 GEMM (M <= 32)
+# bm=16 forces the batched-decode kernel: one block per 16 output columns,
+# MFMA fragments straight from global memory, K split over up to 16 waves
+# whose exact int32 partial tiles are summed through LDS.  Shapes give few
+# and many K steps per wave, row / column / K tails and both row fragments.
+SKINNY_SHAPES = [(16, 8960, 1536), (16, 1536, 2048), (16, 4864, 896), (32, 8960, 300), (20, 1040, 200),
+                 (17, 16, 129), (1, 4864, 70), (25, 2048, 8960)]
+
+
+@pytest.mark.parametrize("M,K,N", SKINNY_SHAPES)
+def test_gemm_int8_skinny_epilogues_bit_exact(M, K, N):
+    A, B, B2, a_s, b_s, b2_s, bias, C0 = _epi_inputs(M, K, N, seed=3 * M + K + N)
+    v = oracle.gemm_int8(A, a_s, B, b_s, bias)
+    for _ in range(2):  # two launches in a row give the same floats
+        store = ec.gemm_int8_epi(0, 16, A, a_s, B, b_s, bias=bias)
+        assert np.array_equal(_bits(store), _bits(v))
+    resid = ec.gemm_int8_epi(1, 16, A, a_s, B, b_s, bias=bias, C0=C0)
+    assert np.array_equal(_bits(resid), _bits(C0 + v))
+    gelu = ec.gemm_int8_epi(2, 16, A, a_s, B, b_s, bias=bias)
+    assert np.array_equal(_bits(gelu), _bits(_device_gelu(v)))
+    g = oracle.gemm_int8(A, a_s, B, b_s)
+    u = oracle.gemm_int8(A, a_s, B2, b2_s)
+    swi = ec.gemm_int8_epi(3, 16, A, a_s, B, b_s, B2=B2, b2_scale=b2_s)
+    assert np.array_equal(_bits(swi), _bits(oracle.map_op(1, g) * u))
+
+
+def test_gemm_int8_skinny_rejects_tall_inputs():
+    A = np.zeros((33, 64), np.int8)
+    B = np.zeros((8, 64), np.int8)
+    with pytest.raises(ec.EdgeCoreError, match="M <= 32"):
+        ec.gemm_int8_epi(0, 16, A, np.ones(33, np.float32), B)

@@ -100,6 +100,10 @@ bool gemm_w16_ok(const GemvArgs &a, int wt, int epi);
 hipError_t gemm_w16(const GemvArgs &a, int wt, int epi, uint16_t *parts, int ldp, float *rs, hipStream_t s);
 hipError_t gemm_w16_tile(const GemvArgs &a, int wt, int epi, int bm, uint16_t *parts, int ldp, float *rs,
                          hipStream_t s);
+// its two launches apart: the split of a.A's rows, then the GEMM on the parts
+hipError_t split_rows16(const GemvArgs &a, int wt, uint16_t *parts, int ldp, float *rs, hipStream_t s);
+hipError_t gemm_w16_parts(const GemvArgs &a, int wt, int epi, int bm, const uint16_t *parts, int ldp,
+                          const float *rs, hipStream_t s);
 // grid-size cap of the grid-stride GEMV (set from the CU count at init)
 void gemv_set_max_blocks(int n);
 int gemv_max_blocks();
@@ -257,6 +261,9 @@ int attention_max_vtile(int hd, int kv);
 hipError_t argmax_rows(const float *logits, int rows, int V, int *out, hipStream_t st);
 hipError_t argmax_rows_chunked(const float *logits, int rows, int V, unsigned long long *cand, int cap, int *out,
                                hipStream_t st);
+// the chunked form's first launch alone; returns the chunk count in *nc
+hipError_t argmax_chunks(const float *logits, int rows, int V, unsigned long long *cand, int cap, int *nc,
+                         hipStream_t st);
 // final reduction of the LM head's per-block argmax candidates
 hipError_t argmax_finalize(const unsigned long long *cand, int ncand, const float *logits,
                            int ldl, int rows, int *out, hipStream_t st);

@@ -423,15 +423,19 @@ bool gemm_w16_ok(const GemvArgs &a, int wt, int epi) {
   return epi_ok(epi);
 }
 
-hipError_t gemm_w16_tile(const GemvArgs &a, int wt, int epi, int bm, uint16_t *parts, int ldp, float *rs,
-                         hipStream_t s) {
-  if (!gemm_w16_ok(a, wt, epi) || (bm != 0 && bm != 32 && bm != 64 && bm != 128)) return hipErrorInvalidValue;
+hipError_t split_rows16(const GemvArgs &a, int wt, uint16_t *parts, int ldp, float *rs, hipStream_t s) {
+  if ((wt != WT_F16 && wt != WT_BF16) || a.M < 1 || a.K < 1) return hipErrorInvalidValue;
   if (!parts || !rs || ldp < a.K || ldp % 8 || !aligned16(parts)) return hipErrorInvalidValue;
   const float *x = (const float *)a.A;
   if (wt == WT_F16) klaunch((split_kernel<OP_F16>), dim3(a.M), dim3(256), 0, s, x, a.lda, a.K, parts, ldp, rs);
   else klaunch((split_kernel<OP_BF16>), dim3(a.M), dim3(256), 0, s, x, a.lda, a.K, parts, ldp, rs);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  return hipGetLastError();
+}
+
+hipError_t gemm_w16_parts(const GemvArgs &a, int wt, int epi, int bm, const uint16_t *parts, int ldp,
+                          const float *rs, hipStream_t s) {
+  if (!gemm_w16_ok(a, wt, epi) || (bm != 0 && bm != 32 && bm != 64 && bm != 128)) return hipErrorInvalidValue;
+  if (!parts || !rs || ldp < a.K || ldp % 8 || !aligned16(parts)) return hipErrorInvalidValue;
   GemvArgs q = a;
   q.A = parts;
   q.lda = ldp;
@@ -439,6 +443,14 @@ hipError_t gemm_w16_tile(const GemvArgs &a, int wt, int epi, int bm, uint16_t *p
   // the 16-bit linears add a bias only in their BIAS epilogues
   if (epi != EPI_BIAS && epi != EPI_BIAS_RESID && epi != EPI_BIAS_GELU) q.bias = nullptr;
   return wt == WT_F16 ? launch_op<OP_F16>(q, epi, bm, s) : launch_op<OP_BF16>(q, epi, bm, s);
+}
+
+hipError_t gemm_w16_tile(const GemvArgs &a, int wt, int epi, int bm, uint16_t *parts, int ldp, float *rs,
+                         hipStream_t s) {
+  if (!gemm_w16_ok(a, wt, epi) || (bm != 0 && bm != 32 && bm != 64 && bm != 128)) return hipErrorInvalidValue;
+  hipError_t e = split_rows16(a, wt, parts, ldp, rs, s);
+  if (e != hipSuccess) return e;
+  return gemm_w16_parts(a, wt, epi, bm, parts, ldp, rs, s);
 }
 
 hipError_t gemm_w16(const GemvArgs &a, int wt, int epi, uint16_t *parts, int ldp, float *rs, hipStream_t s) {

@@ -551,19 +551,25 @@ hipError_t argmax_rows(const float *logits, int rows, int V, int *out, hipStream
   return hipGetLastError();
 }
 
-hipError_t argmax_rows_chunked(const float *logits, int rows, int V, unsigned long long *cand, int cap, int *out,
-                               hipStream_t st) {
+hipError_t argmax_chunks(const float *logits, int rows, int V, unsigned long long *cand, int cap, int *nc_out,
+                         hipStream_t st) {
   // chunks of at least 2048 logits, at most cap per row
   int nc = (V + 2047) / 2048;
   if (nc > cap) nc = cap;
   if (nc < 1) return hipErrorInvalidValue;
   const int csz = (V + nc - 1) / nc;
   nc = (V + csz - 1) / csz;
+  *nc_out = nc;
   klaunch(argmax_chunk_kernel, dim3(nc, rows), dim3(256), 0, st, logits, V, csz, cand);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  klaunch(argmax_finalize_kernel, dim3(rows), dim3(256), 0, st, cand, nc, logits, V, out);
   return hipGetLastError();
+}
+
+hipError_t argmax_rows_chunked(const float *logits, int rows, int V, unsigned long long *cand, int cap, int *out,
+                               hipStream_t st) {
+  int nc = 0;
+  const hipError_t e = argmax_chunks(logits, rows, V, cand, cap, &nc, st);
+  if (e != hipSuccess) return e;
+  return argmax_finalize(cand, nc, logits, V, rows, out, st);
 }
 
 }  // namespace ec

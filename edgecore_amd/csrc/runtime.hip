@@ -1100,7 +1100,9 @@ static int linear(GPT2 *g, DevModel *d, const char *fam, GemvArgs a, int wt, int
       q.A = d->h;
       q.lda = a.K;
     }
-    EC_LAUNCH(gemm_family(fam), bytes, gemm_w16(q, wt, epi, d->ah, d->ah_ld, d->ahs, s));
+    EC_LAUNCH("split16", 4.0 * a.M * a.K * (1.0 + w16_parts(wt) / 2.0),
+              split_rows16(q, wt, d->ah, d->ah_ld, d->ahs, s));
+    EC_LAUNCH(gemm_family(fam), bytes, gemm_w16_parts(q, wt, epi, 0, d->ah, d->ah_ld, d->ahs, s));
     return 0;
   }
   if (gemv_vector_ok(a, wt, pro)) {
@@ -1315,13 +1317,16 @@ static int enqueue_forward(GPT2 *g, DevModel *d, int M, int lm_from, bool distin
     if (argmax && fused) a.cand = d->cand;
     if ((r = linear(g, d, "gemv_lmhead", a, lwt, EPI_STORE, pro_norm, s))) return r;
     if (argmax) {
-      if (fused)
+      if (fused) {
         EC_LAUNCH("argmax", 8.0 * rows * gemv_grid_x(a, lwt, EPI_STORE),
                   argmax_finalize(d->cand, gemv_grid_x(a, lwt, EPI_STORE), d->logits, V, rows,
                                   amax_dev + (r0 - lm_from), s));
-      else
-        EC_LAUNCH("argmax", 4.0 * rows * V,
-                  argmax_rows_chunked(d->logits, rows, V, d->cand, d->ncand, amax_dev + (r0 - lm_from), s));
+      } else {
+        int nc = 0;
+        EC_LAUNCH("argmax_chunks", 4.0 * rows * V, argmax_chunks(d->logits, rows, V, d->cand, d->ncand, &nc, s));
+        EC_LAUNCH("argmax", 8.0 * rows * nc,
+                  argmax_finalize(d->cand, nc, d->logits, V, rows, amax_dev + (r0 - lm_from), s));
+      }
     }
     if (logits)
       EC_HIP(hipMemcpyAsync(logits + (size_t)(r0 - lm_from) * V, d->logits, (size_t)rows * V * 4,

@@ -293,6 +293,7 @@ __device__ void attention_loop(const StepArgs &a, int head, int slice, unsigned 
     }
     mark<TRACE>(a, b, l, 1);
     const float sx = block_norm_quant(xs, E, gam, a.eps, codes, red);
+    mark<TRACE>(a, b, l, 11);
 #pragma unroll
     for (int p = 0; p < 3; p++) {
       int acc = 0;
@@ -396,6 +397,7 @@ __device__ void gemv_loop(const StepArgs &a, int gi, int ng, unsigned tag, int t
       gather<2>(XM, E, tag, xs, a.err);
       mark<TRACE>(a, b, l, 6);
       const float sx = block_norm_quant(xs, E, gam, a.eps, codes, red);
+      mark<TRACE>(a, b, l, 10);
       int ag = 0, au = 0;
 #pragma unroll
       for (int c = 0; c < 7; c++) {

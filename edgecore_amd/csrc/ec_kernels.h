@@ -193,8 +193,9 @@ constexpr int kStepBlocks = 256, kStepThreads = 512, kStepSlices = 4;
 // phase timestamps per block and layer: 0 layer start, 1 x gathered (attention
 // blocks), 2 q/k/v rows done, 3 attention done, 4 attention output gathered,
 // 5 o done, 6 x_mid gathered, 7 gate/up done, 8 FFN activation gathered,
-// 9 down done
-constexpr int kStepEvents = 10;
+// 9 down done, 10 x_mid normalized and quantized, 11 x normalized and
+// quantized (attention blocks)
+constexpr int kStepEvents = 12;
 struct StepLayer {
   const float *ln1_g, *ln2_g;
   const int8_t *wqkv;  // [E + 2 kv][E]: q | k | v rows

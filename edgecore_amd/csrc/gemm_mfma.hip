@@ -399,6 +399,200 @@ __global__ __launch_bounds__(256) void split_kernel(const float *x, int ldx, int
 
 }  // namespace
 
+// ---------------------------------------------------------------------------
+// Skinny GEMM (M <= 32 rows: batched decode, a many-row LM head).
+//
+// One or two 16-row MFMA fragments cover every row, so the weights are the
+// whole traffic and the work has to spread over the chip by columns and by K:
+// a block owns NJ 16-column output tiles (SwiGLU: the 16 gate and the 16 up
+// rows of 16 outputs) and WPB waves (up to 16) that take every WPB-th
+// 64-byte K step, each lane loading its MFMA fragments straight from global
+// memory (16 bytes of a weight row, 16 bytes of each activation part: the A
+// rows stay in L2) with up to 8 steps in flight.  Every block reads all of A
+// once, so for wide outputs (the LM head) a block takes 4 tiles and reuses
+// each A fragment 4 times.  The waves' partial tiles
+// are summed through LDS in wave order (exact for int32) and the block
+// applies the epilogue: for int8 the same int32 dots and epilogue code as
+// gemm_mfma_kernel, so the same floats; for 16-bit weights the same class of
+// fp32 sums.  No workspace, no atomics.
+namespace {
+
+template <int OP, int TI, int NJ, int EPI>
+__global__ __launch_bounds__(1024) void gemm_skinny_kernel(GemvArgs a) {
+  using Op = MfmaOp<OP>;
+  using Acc = typename Op::Acc;
+  constexpr int NP = Op::NP;
+  constexpr bool I8 = OP == OP_I8;
+  constexpr bool SWI = EPI == EPI_SWIGLU;
+  constexpr bool RES = EPI == EPI_RESID || EPI == EPI_BIAS_RESID;
+  constexpr bool GELU = EPI == EPI_GELU || EPI == EPI_BIAS_GELU;
+  static_assert(!SWI || NJ == 1, "SwiGLU blocks take one tile of gate and up rows");
+  constexpr int NB = SWI ? 2 : NJ;  // B tiles: NJ tiles of 16 rows, or 16 gate + 16 up rows
+  constexpr int FR = TI * NP + NB;  // 16-byte fragments per lane and step
+  constexpr int U = FR <= 3 ? 8 : FR <= 5 ? 4 : 2;  // K steps per wave in flight (within 128 VGPRs)
+  __shared__ Acc part[16][TI][NB][64];  // [wave][i][j][lane]
+  __shared__ uint64_t etab[SWI ? 32 : 1];
+
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6, nw = blockDim.x >> 6;
+  const int lr = lane & 15, lq = lane >> 4;
+  const int M = a.M, K = a.K, N = a.N;
+  const int KB = K * Op::EB;  // bytes of a weight row and of an activation part row
+  const size_t ldab = (size_t)a.lda * Op::EB;
+  const int n0 = 16 * NJ * blockIdx.x;
+  const int ksteps = (KB + 63) / 64;
+  if constexpr (SWI) {
+    if (t < 32) etab[t] = ec_exp2_32[t];
+  }
+
+  // fragment sources: part p of A row 16 i + lr (clamped), B row n0 + lr of W (and W2)
+  const int8_t *arow[TI][NP];
+  const int8_t *brow[NB];
+#pragma unroll
+  for (int i = 0; i < TI; i++)
+#pragma unroll
+    for (int p = 0; p < NP; p++)
+      arow[i][p] = (const int8_t *)a.A + ((size_t)min(16 * i + lr, M - 1) * NP + p) * ldab;
+#pragma unroll
+  for (int j = 0; j < NB; j++) {
+    if constexpr (SWI) brow[j] = (const int8_t *)(j ? a.W2 : a.W) + (size_t)min(n0 + lr, N - 1) * KB;
+    else brow[j] = (const int8_t *)a.W + (size_t)min(n0 + 16 * j + lr, N - 1) * KB;
+  }
+
+  Acc acc[TI][NB];
+#pragma unroll
+  for (int i = 0; i < TI; i++)
+#pragma unroll
+    for (int j = 0; j < NB; j++) acc[i][j] = Acc{0, 0, 0, 0};
+
+  // this wave's steps: wave, wave + nw, ... < ksteps, U at a time; bytes
+  // past the row read a clamped address and the A fragments are zeroed
+  for (int sb = wave; sb < ksteps; sb += nw * U) {
+    v4i fa[U][TI][NP], fb[U][NB];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int st = sb + nw * u;  // uniform over the wave
+      if (st < ksteps) {
+        const int kc = min(64 * st + 16 * lq, KB - 16);
+#pragma unroll
+        for (int i = 0; i < TI; i++)
+#pragma unroll
+          for (int p = 0; p < NP; p++) fa[u][i][p] = *reinterpret_cast<const v4i *>(arow[i][p] + kc);
+#pragma unroll
+        for (int j = 0; j < NB; j++) fb[u][j] = *reinterpret_cast<const v4i *>(brow[j] + kc);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int st = sb + nw * u;
+      if (st < ksteps) {
+        const bool in = 64 * st + 16 * lq < KB;
+#pragma unroll
+        for (int i = 0; i < TI; i++)
+#pragma unroll
+          for (int p = 0; p < NP; p++) {
+            const v4i av = in ? fa[u][i][p] : v4i{0, 0, 0, 0};
+#pragma unroll
+            for (int j = 0; j < NB; j++) acc[i][j] = Op::mma(av, fb[u][j], acc[i][j]);
+          }
+      }
+    }
+  }
+
+  // sum the waves' tiles: thread t < 256 TI NO takes output tile
+  // jo = t / (256 TI), fragment i = (t / 256) % TI, accumulator register
+  // r = (t / 64) % 4 of lane t % 64, i.e. row 16 i + 4 lq + r, column
+  // n0 + 16 jo + lr (SwiGLU: gate and up of that column)
+  constexpr int NO = SWI ? 1 : NJ;  // output tiles
+#pragma unroll
+  for (int i = 0; i < TI; i++)
+#pragma unroll
+    for (int j = 0; j < NB; j++) part[wave][i][j][lane] = acc[i][j];
+  __syncthreads();
+  if (t >= 256 * TI * NO) return;
+  const int jo = t / (256 * TI), i = (t >> 8) % TI, r = (t >> 6) & 3;
+  const int m = 16 * i + 4 * lq + r, n = n0 + 16 * jo + lr;
+  if (m >= M || n >= N) return;
+  using Sum = std::conditional_t<I8, int, float>;
+  constexpr int NS = SWI ? 2 : 1;
+  Sum sum[NS];
+#pragma unroll
+  for (int k = 0; k < NS; k++) {
+    const int j = SWI ? k : jo;
+    Sum v = part[0][i][j][lane][r];
+    for (int w = 1; w < nw; w++) v = v + part[w][i][j][lane][r];
+    sum[k] = v;
+  }
+
+  // epilogue (the same code as gemm_mfma_kernel's)
+  const float as = a.as[m];
+  float v;
+  if constexpr (I8) {
+    const float bs = a.ws ? a.ws[n] : 1.0f;
+    if constexpr (SWI) {
+      v = i8_epilogue(sum[0], as, bs, 0.0f);
+      const float u = i8_epilogue(sum[1], as, a.ws2 ? a.ws2[n] : 1.0f, 0.0f);
+      v = silu(v, etab) * u;
+    } else {
+      v = i8_epilogue(sum[0], as, bs, a.bias ? a.bias[n] : 0.0f);
+    }
+  } else {
+    v = sum[0] * as;
+    if constexpr (SWI) {
+      const float u = sum[1] * as;
+      v = silu(v, etab) * u;
+    } else if (a.bias) {
+      v = v + a.bias[n];
+    }
+  }
+  if constexpr (!SWI) {
+    if constexpr (RES) v = a.out[(size_t)m * a.ldo + n] + v;
+    if constexpr (GELU) v = gelu_new(v);
+  }
+  a.out[(size_t)m * a.ldo + n] = v;
+}
+
+template <int OP, int TI, int NJ, int EPI>
+hipError_t launch_skinny_nj(const GemvArgs &a, int wpb, hipStream_t s) {
+  const int ksteps = (a.K * MfmaOp<OP>::EB + 63) / 64;
+  constexpr int NO = EPI == EPI_SWIGLU ? 1 : NJ;
+  // waves per block: two or more K steps each, 4 to 16 waves, and at least
+  // 4 TI NO (the epilogue takes one thread per output of 16 TI rows x 16 NO)
+  if (wpb <= 0) wpb = min(16, max(4, ksteps / 2));
+  wpb = max(min(wpb, 16), 4 * TI * NO);
+  klaunch((gemm_skinny_kernel<OP, TI, NJ, EPI>), dim3((a.N + 16 * NJ - 1) / (16 * NJ)), dim3(64 * wpb), 0, s, a);
+  return hipGetLastError();
+}
+
+// four column tiles per block for wide outputs (at least 1024 of them), else one
+template <int OP, int TI, int EPI>
+hipError_t launch_skinny(const GemvArgs &a, int wpb, hipStream_t s) {
+  if constexpr (EPI != EPI_SWIGLU && TI == 1) {
+    if (a.N >= 16 * 1024) return launch_skinny_nj<OP, TI, 4, EPI>(a, wpb, s);
+  }
+  return launch_skinny_nj<OP, TI, 1, EPI>(a, wpb, s);
+}
+
+template <int OP, int TI>
+hipError_t launch_skinny_epi(const GemvArgs &a, int epi, int wpb, hipStream_t s) {
+  switch (epi) {
+    case EPI_STORE:
+    case EPI_BIAS: return launch_skinny<OP, TI, EPI_STORE>(a, wpb, s);
+    case EPI_RESID:
+    case EPI_BIAS_RESID: return launch_skinny<OP, TI, EPI_RESID>(a, wpb, s);
+    case EPI_GELU:
+    case EPI_BIAS_GELU: return launch_skinny<OP, TI, EPI_GELU>(a, wpb, s);
+    case EPI_SWIGLU: return launch_skinny<OP, TI, EPI_SWIGLU>(a, wpb, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+template <int OP>
+hipError_t launch_skinny_op(const GemvArgs &a, int epi, int wpb, hipStream_t s) {
+  return a.M <= 16 ? launch_skinny_epi<OP, 1>(a, epi, wpb, s) : launch_skinny_epi<OP, 2>(a, epi, wpb, s);
+}
+
+}  // namespace
+
 bool gemm_i8_ok(const GemvArgs &a, int epi) {
   if (a.M < 1 || a.N < 1 || a.K < 16 || a.K % 16 || a.lda % 16 || !a.as || a.cand) return false;
   if (!aligned16(a.A) || !aligned16(a.W)) return false;
@@ -434,7 +628,8 @@ hipError_t split_rows16(const GemvArgs &a, int wt, uint16_t *parts, int ldp, flo
 
 hipError_t gemm_w16_parts(const GemvArgs &a, int wt, int epi, int bm, const uint16_t *parts, int ldp,
                           const float *rs, hipStream_t s) {
-  if (!gemm_w16_ok(a, wt, epi) || (bm != 0 && bm != 32 && bm != 64 && bm != 128)) return hipErrorInvalidValue;
+  if (!gemm_w16_ok(a, wt, epi) || (bm != 0 && bm != 16 && bm != 32 && bm != 64 && bm != 128))
+    return hipErrorInvalidValue;
   if (!parts || !rs || ldp < a.K || ldp % 8 || !aligned16(parts)) return hipErrorInvalidValue;
   GemvArgs q = a;
   q.A = parts;
@@ -442,12 +637,17 @@ hipError_t gemm_w16_parts(const GemvArgs &a, int wt, int epi, int bm, const uint
   q.as = rs;
   // the 16-bit linears add a bias only in their BIAS epilogues
   if (epi != EPI_BIAS && epi != EPI_BIAS_RESID && epi != EPI_BIAS_GELU) q.bias = nullptr;
+  if ((bm == 0 && a.M <= 32) || bm == 16) {  // skinny kernel (bm 16 forces it)
+    if (a.M > 32) return hipErrorInvalidValue;
+    return wt == WT_F16 ? launch_skinny_op<OP_F16>(q, epi, 0, s) : launch_skinny_op<OP_BF16>(q, epi, 0, s);
+  }
   return wt == WT_F16 ? launch_op<OP_F16>(q, epi, bm, s) : launch_op<OP_BF16>(q, epi, bm, s);
 }
 
 hipError_t gemm_w16_tile(const GemvArgs &a, int wt, int epi, int bm, uint16_t *parts, int ldp, float *rs,
                          hipStream_t s) {
-  if (!gemm_w16_ok(a, wt, epi) || (bm != 0 && bm != 32 && bm != 64 && bm != 128)) return hipErrorInvalidValue;
+  if (!gemm_w16_ok(a, wt, epi) || (bm != 0 && bm != 16 && bm != 32 && bm != 64 && bm != 128))
+    return hipErrorInvalidValue;
   hipError_t e = split_rows16(a, wt, parts, ldp, rs, s);
   if (e != hipSuccess) return e;
   return gemm_w16_parts(a, wt, epi, bm, parts, ldp, rs, s);
@@ -458,153 +658,9 @@ hipError_t gemm_w16(const GemvArgs &a, int wt, int epi, uint16_t *parts, int ldp
 }
 
 
-// ---------------------------------------------------------------------------
-// Skinny int8 GEMM (M <= 32 rows: batched decode).
-//
-// One or two 16-row MFMA fragments cover every row, so the weights are the
-// whole traffic and the work has to spread over the chip by columns and by K:
-// a block owns one 16-column output tile (SwiGLU: the 16 gate and the 16 up
-// rows of 16 outputs) and WPB waves (up to 16) that take every WPB-th
-// 64-byte K step, each lane loading its MFMA fragments straight from global
-// memory (16 bytes of a weight row, 16 bytes of an activation row: the A rows
-// stay in L2) with up to 8 steps in flight.  The waves' int32 partial
-// tiles are summed through LDS (exact in any order) and the block applies the
-// epilogue: the same int32 dots and the same epilogue code as
-// gemm_mfma_kernel, so the same floats.  No workspace, no atomics.
-namespace {
-
-
-template <int TI, int EPI>
-__global__ __launch_bounds__(1024) void gemm_skinny_i8_kernel(GemvArgs a) {
-  constexpr bool SWI = EPI == EPI_SWIGLU;
-  constexpr bool RES = EPI == EPI_RESID || EPI == EPI_BIAS_RESID;
-  constexpr bool GELU = EPI == EPI_GELU || EPI == EPI_BIAS_GELU;
-  constexpr int NB = SWI ? 2 : 1;  // B tiles: the 16 rows, or 16 gate + 16 up rows
-  constexpr int U = TI * NB <= 2 ? 8 : 4;  // K steps per wave in flight (within 128 VGPRs)
-  __shared__ v4i part[16][TI][NB][64];  // [wave][i][j][lane]
-  __shared__ uint64_t etab[SWI ? 32 : 1];
-
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6, nw = blockDim.x >> 6;
-  const int lr = lane & 15, lq = lane >> 4;
-  const int M = a.M, K = a.K, N = a.N;
-  const int n0 = 16 * blockIdx.x;
-  const int ksteps = (K + 63) / 64;
-  if constexpr (SWI) {
-    if (t < 32) etab[t] = ec_exp2_32[t];
-  }
-
-  // fragment sources: A rows 16 i + lr (clamped), B row n0 + lr of W (and W2)
-  const int8_t *arow[TI];
-  const int8_t *brow[NB];
-#pragma unroll
-  for (int i = 0; i < TI; i++) arow[i] = (const int8_t *)a.A + (size_t)min(16 * i + lr, M - 1) * a.lda;
-#pragma unroll
-  for (int j = 0; j < NB; j++)
-    brow[j] = (const int8_t *)(j ? a.W2 : a.W) + (size_t)min(n0 + lr, N - 1) * K;
-
-  v4i acc[TI][NB];
-#pragma unroll
-  for (int i = 0; i < TI; i++)
-#pragma unroll
-    for (int j = 0; j < NB; j++) acc[i][j] = v4i{0, 0, 0, 0};
-
-  // this wave's steps: wave, wave + nw, ... < ksteps, U at a time; bytes
-  // past K read a clamped address and the A fragment is zeroed
-  for (int sb = wave; sb < ksteps; sb += nw * U) {
-    v4i fa[U][TI], fb[U][NB];
-#pragma unroll
-    for (int u = 0; u < U; u++) {
-      const int st = sb + nw * u;  // uniform over the wave
-      if (st < ksteps) {
-        const int kc = min(64 * st + 16 * lq, K - 16);
-#pragma unroll
-        for (int i = 0; i < TI; i++) fa[u][i] = *reinterpret_cast<const v4i *>(arow[i] + kc);
-#pragma unroll
-        for (int j = 0; j < NB; j++) fb[u][j] = *reinterpret_cast<const v4i *>(brow[j] + kc);
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < U; u++) {
-      const int st = sb + nw * u;
-      if (st < ksteps) {
-        const bool in = 64 * st + 16 * lq < K;
-#pragma unroll
-        for (int i = 0; i < TI; i++) {
-          const v4i av = in ? fa[u][i] : v4i{0, 0, 0, 0};
-#pragma unroll
-          for (int j = 0; j < NB; j++)
-            acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, fb[u][j], acc[i][j], 0, 0, 0);
-        }
-      }
-    }
-  }
-
-  // sum the waves' tiles: thread t < 256 TI takes fragment i = t / 256,
-  // accumulator register r = (t / 64) % 4 of lane t % 64, i.e. row
-  // 16 i + 4 lq + r, column n0 + lr
-#pragma unroll
-  for (int i = 0; i < TI; i++)
-#pragma unroll
-    for (int j = 0; j < NB; j++) part[wave][i][j][lane] = acc[i][j];
-  __syncthreads();
-  if (t >= 256 * TI) return;
-  const int i = t >> 8, r = (t >> 6) & 3;
-  const int m = 16 * i + 4 * lq + r, n = n0 + lr;
-  if (m >= M || n >= N) return;
-  int sum[NB];
-#pragma unroll
-  for (int j = 0; j < NB; j++) {
-    int v = 0;
-    for (int w = 0; w < nw; w++) v += part[w][i][j][lane][r];
-    sum[j] = v;
-  }
-
-  // epilogue (the same code as gemm_mfma_kernel's int8 path)
-  const float as = a.as[m];
-  const float bs = a.ws ? a.ws[n] : 1.0f;
-  float v;
-  if constexpr (SWI) {
-    v = i8_epilogue(sum[0], as, bs, 0.0f);
-    const float u = i8_epilogue(sum[1], as, a.ws2 ? a.ws2[n] : 1.0f, 0.0f);
-    v = silu(v, etab) * u;
-  } else {
-    v = i8_epilogue(sum[0], as, bs, a.bias ? a.bias[n] : 0.0f);
-    if constexpr (RES) v = a.out[(size_t)m * a.ldo + n] + v;
-    if constexpr (GELU) v = gelu_new(v);
-  }
-  a.out[(size_t)m * a.ldo + n] = v;
-}
-
-template <int TI, int EPI>
-hipError_t launch_skinny(const GemvArgs &a, int wpb, hipStream_t s) {
-  const int ksteps = (a.K + 63) / 64;
-  // waves per block: two or more K steps each, 4 to 16 waves, and at least
-  // 4 TI (the epilogue takes one thread per output of 16 TI rows)
-  if (wpb <= 0) wpb = min(16, max(4, ksteps / 2));
-  wpb = max(min(wpb, 16), 4 * TI);
-  klaunch((gemm_skinny_i8_kernel<TI, EPI>), dim3((a.N + 15) / 16), dim3(64 * wpb), 0, s, a);
-  return hipGetLastError();
-}
-
-template <int TI>
-hipError_t launch_skinny_epi(const GemvArgs &a, int epi, int wpb, hipStream_t s) {
-  switch (epi) {
-    case EPI_STORE:
-    case EPI_BIAS: return launch_skinny<TI, EPI_STORE>(a, wpb, s);
-    case EPI_RESID:
-    case EPI_BIAS_RESID: return launch_skinny<TI, EPI_RESID>(a, wpb, s);
-    case EPI_GELU:
-    case EPI_BIAS_GELU: return launch_skinny<TI, EPI_GELU>(a, wpb, s);
-    case EPI_SWIGLU: return launch_skinny<TI, EPI_SWIGLU>(a, wpb, s);
-  }
-  return hipErrorInvalidValue;
-}
-
-}  // namespace
-
 hipError_t gemm_i8_skinny(const GemvArgs &a, int epi, int wpb, hipStream_t s) {
   if (!gemm_i8_ok(a, epi) || a.M > 32 || wpb < 0 || wpb > 16) return hipErrorInvalidValue;
-  return a.M <= 16 ? launch_skinny_epi<1>(a, epi, wpb, s) : launch_skinny_epi<2>(a, epi, wpb, s);
+  return launch_skinny_op<OP_I8>(a, epi, wpb, s);
 }
 
 }  // namespace ec

@@ -415,7 +415,9 @@ extern "C" int ec_gemm_w16_epi_dev(int wt, int epi, int bm, float *C, const floa
   if (M < 1 || N < 1 || K < 8 || K % 8)
     return set_err(-1, "ec_gemm_w16_epi_dev: shape M=%d K=%d N=%d (K a multiple of 8)", M, K, N);
   if (epi < EPI_STORE || epi > EPI_BIAS_GELU) return set_err(-1, "ec_gemm_w16_epi_dev: epilogue %d", epi);
-  if (bm != 0 && bm != 32 && bm != 64 && bm != 128) return set_err(-1, "ec_gemm_w16_epi_dev: row tile %d", bm);
+  if (bm != 0 && bm != 16 && bm != 32 && bm != 64 && bm != 128)
+    return set_err(-1, "ec_gemm_w16_epi_dev: row tile %d", bm);
+  if (bm == 16 && M > 32) return set_err(-1, "ec_gemm_w16_epi_dev: the skinny kernel (bm 16) takes M <= 32, not %d", M);
   if (!C || !A || !B || (epi == EPI_SWIGLU && !B2)) return set_err(-1, "ec_gemm_w16_epi_dev: null pointer");
   GemvArgs a{A, K, nullptr, nullptr, nullptr, 0.0, B, B2, nullptr, nullptr, bias, C, N, M, K, N, nullptr};
   if (!gemm_w16_ok(a, wt, epi)) return set_err(-1, "ec_gemm_w16_epi_dev: unaligned operands");

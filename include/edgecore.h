@@ -142,8 +142,8 @@ int ec_gemm_int8_epi_dev(int epi, int bm, float *C, const int8_t *A, const float
  * bias, 5 C += v + bias, 6 C = gelu_new(v + bias).  The fp32 rows of A are
  * split into 16-bit parts first (2 for fp16 under a per-row power-of-two
  * scale, 3 for bf16), so the sums carry fp32-level accuracy.  bm forces the
- * row tile (32, 64, 128; 0 = the library's choice).  K a multiple of 8, B and
- * B2 16-byte aligned.  ec_gemm_fp16_fp32_dev / ec_gemm_bf16_fp32_dev take
+ * row tile (32, 64, 128; 16 = the skinny kernel, M <= 32; 0 = the library's
+ * choice).  K a multiple of 8, B and B2 16-byte aligned.  ec_gemm_fp16_fp32_dev / ec_gemm_bf16_fp32_dev take
  * this kernel for M >= 16. */
 int ec_gemm_w16_epi_dev(int wt, int epi, int bm, float *C, const float *A, const uint16_t *B,
                         const uint16_t *B2, const float *bias, int M, int K, int N);

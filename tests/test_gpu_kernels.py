@@ -263,8 +263,11 @@ def test_gemm_w16_matrix_core_within_bound(M, K, N, bf16):
 
 
 @pytest.mark.parametrize("bf16", [False, True])
-@pytest.mark.parametrize("bm", [0, 32, 64, 128])
-@pytest.mark.parametrize("M,K,N", [(200, 768, 300), (130, 3072, 129), (64, 896, 128)])
+@pytest.mark.parametrize("bm,M,K,N", [(bm, M, K, N) for bm in (0, 32, 64, 128)
+                                      for M, K, N in ((200, 768, 300), (130, 3072, 129), (64, 896, 128))]
+                         + [(bm, M, K, N) for bm in (0, 16)
+                            for M, K, N in ((16, 1536, 600), (32, 768, 129), (20, 3072, 200), (1, 8, 17),
+                                            (16, 768, 16500))])
 def test_gemm_w16_tiles_and_epilogues(bm, M, K, N, bf16):
     wt = 2 if bf16 else 1
     A, B, B2, bias, C0 = _w16_inputs(M, K, N, bf16, seed=M + K + N + bm + 7 * bf16)
@@ -308,7 +311,7 @@ def test_gemm_fp16_matrix_core_row_scale_range(scale):
 # whose exact int32 partial tiles are summed through LDS.  Shapes give few
 # and many K steps per wave, row / column / K tails and both row fragments.
 SKINNY_SHAPES = [(16, 8960, 1536), (16, 1536, 2048), (16, 4864, 896), (32, 8960, 300), (20, 1040, 200),
-                 (17, 16, 129), (1, 4864, 70), (25, 2048, 8960)]
+                 (17, 16, 129), (1, 4864, 70), (25, 2048, 8960), (16, 896, 17000)]  # last: 4 tiles per block
 
 
 @pytest.mark.parametrize("M,K,N", SKINNY_SHAPES)

@@ -333,11 +333,16 @@ __host__ __device__ constexpr inline int attn_sswz(int hs) { return hs <= 16 ? 0
 // coff is added to every cache index (a layer's offset when a.kc / a.vc
 // point at layer 0).
 // Every thread of the block (NS > 1 ? 512 : 256) must call it.
-template <int HD, bool FUSED, int NS, class Out>
+// SCORED: steps 1-4 are skipped; the scores of (m, h) come from
+// a.scores[(m * H + h) * sc_ld + i] (position lo + i), written by the scores
+// pass with this body's arithmetic, and the cache already holds the token's k
+// and v (FUSED must be false).
+template <int HD, bool FUSED, int NS, bool SCORED = false, class Out>
 __device__ __forceinline__ void attn_decode_block(const AttnArgs &a, int m, int h, int slice, const float *qrow,
                                                   const float *krow, const float *vrow, float *lds, Out &&out,
                                                   size_t coff = 0) {
   static_assert(NS == 1 || (HD == 64 && (NS == 2 || NS == 4 || NS == 8)), "element slices: head_dim 64, 2 / 4 / 8");
+  static_assert(!(SCORED && FUSED), "the scores pass appends the new k / v");
   // threads per block: 512 with element slices (one scored position per
   // thread up to 512 positions), else 256
   constexpr int NT = NS > 1 ? 512 : 256;
@@ -414,18 +419,7 @@ __device__ __forceinline__ void attn_decode_block(const AttnArgs &a, int m, int 
   auto stage_lo = [](int s) { return s == 0 ? 0 : Q0 + SQ * (s - 1); };
   static_assert(HD == 0 || NPT % CPRV == 0, "product threads cover whole quads");
   const int pt = t - 64 * SWV;  // product thread index (negative in the summing waves)
-  v4u kr[HD > 0 ? KU : 1][4], vr[NSTG * UPS][4];
-  if constexpr (HD > 0) {
-#pragma unroll
-    for (int u = 0; u < KU; u++) {
-      const int unit = t + NT * u, qd = unit / CPR, cd = unit - qd * CPR;
-#pragma unroll
-      for (int e = 0; e < 4; e++) {
-        const int i = min(4 * qd + e, last);
-        kr[u][e] = *reinterpret_cast<const v4u *>(K + (size_t)i * a.kv + 8 * cd);
-      }
-    }
-  }
+  v4u vr[NSTG * UPS][4];
   auto load_v = [&](int t0) {  // this product thread's V units of the tile at t0
     if (HD > 0 && pt >= 0) {
       const int qd0 = pt / CPRV, cd = pt - qd0 * CPRV;
@@ -442,6 +436,30 @@ __device__ __forceinline__ void attn_decode_block(const AttnArgs &a, int m, int 
       }
     }
   };
+  float mx = -FLT_MAX;
+  if constexpr (SCORED) {
+    // V of the first tile, then the scores into LDS and their maximum
+    if (t < 32) etab[t] = et;
+    load_v(0);
+    const float *src = a.scores + ((size_t)m * a.H + h) * a.sc_ld;
+    for (int i = t; i < n; i += NT) {
+      const float s = src[i];
+      sc[i] = s;
+      mx = fmaxf(mx, s);
+    }
+  } else {
+  v4u kr[HD > 0 ? KU : 1][4];
+  if constexpr (HD > 0) {
+#pragma unroll
+    for (int u = 0; u < KU; u++) {
+      const int unit = t + NT * u, qd = unit / CPR, cd = unit - qd * CPR;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const int i = min(4 * qd + e, last);
+        kr[u][e] = *reinterpret_cast<const v4u *>(K + (size_t)i * a.kv + 8 * cd);
+      }
+    }
+  }
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- 3. RoPE, fp16 rounding of the new k/v, cache append ----
@@ -514,7 +532,6 @@ __device__ __forceinline__ void attn_decode_block(const AttnArgs &a, int m, int 
   __syncthreads();
 
   // ---- 4. scores ----
-  float mx = -FLT_MAX;
   auto put = [&](int i, float s) {
     s = (float)((double)s * a.inv_hd);
     sc[i] = s;
@@ -574,6 +591,7 @@ __device__ __forceinline__ void attn_decode_block(const AttnArgs &a, int m, int 
     for (int i = t; i < n; i += NT)
       put(i, (FUSED && i == n - 1) ? dot_new_k<HD>(qs, kn, hd) : dot_k_row<HD>(qs, K + (size_t)i * a.kv, hd));
   }
+  }  // !SCORED
   mx = block_max_1b<NT / 64>(mx, redf);
   // this thread's first two values stay in registers until the sum is known
   // (positions below 512); further ones go through LDS

@@ -180,8 +180,20 @@ struct AttnArgs {
   int half;
   uint16_t *kc_w, *vc_w;  // writable views of kc / vc for the append
   int xcd_r;  // set by attention(): query heads per KV group when the launch is XCD-grouped, else 0
+  // long decode contexts: scores [M][H][sc_ld] written by a scores pass (one
+  // block per token, KV group and chunk of positions) and read by the
+  // softmax / sums pass; null to score inside the attention blocks
+  float *scores;
+  int sc_ld;
 };
+// positions from which attention() splits a decode launch into the scores
+// pass and the softmax / sums pass (when a.scores is set)
+constexpr int kAttnSplitMinPos = 512;
 hipError_t attention(const AttnArgs &a, hipStream_t st);
+// the two launches attention() makes for a long decode context, apart
+bool attention_split_ok(const AttnArgs &a);
+hipError_t attention_scores(const AttnArgs &a, hipStream_t st);
+hipError_t attention_after_scores(const AttnArgs &a, hipStream_t st);
 
 // Persistent decode step (decode_step.hip): all layers of the int8 Qwen2
 // forward for one token in one co-resident launch of kStepBlocks blocks of

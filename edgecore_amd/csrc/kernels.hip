@@ -213,7 +213,7 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(KvArgs a) {
 // One block per (head, token) -- NS blocks per head with element slices --
 // running attn_decode_block (attn_decode.h) on the token's q row and new k/v
 // rows in global memory.
-template <int HD, bool FUSED, int NS>
+template <int HD, bool FUSED, int NS, bool SCORED = false>
 __global__ __launch_bounds__(NS > 1 ? 512 : 256) void attn_kernel(AttnArgs a) {
   extern __shared__ __attribute__((aligned(16))) float lds[];
   const int m = blockIdx.y;
@@ -237,7 +237,8 @@ __global__ __launch_bounds__(NS > 1 ? 512 : 256) void attn_kernel(AttnArgs a) {
   const float *krow = a.k + (size_t)m * a.ldk + (size_t)kvh * hd;
   const float *vrow = a.v + (size_t)m * a.ldk + (size_t)kvh * hd;
   float *orow = a.out + (size_t)m * a.ldo + (size_t)h * hd + (size_t)(hd / NS) * slice;
-  attn_decode_block<HD, FUSED, NS>(a, m, h, slice, qrow, krow, vrow, lds, [&](int i, float o) { orow[i] = o; });
+  attn_decode_block<HD, FUSED, NS, SCORED>(a, m, h, slice, qrow, krow, vrow, lds,
+                                            [&](int i, float o) { orow[i] = o; });
 }
 
 // ---------------------------------------------------------------------------
@@ -513,6 +514,112 @@ int attention_max_vtile(int hd, int kv) {
   return t < 512 ? t : 512;
 }
 
+// ---------------------------------------------------------------------------
+// Scores pass of a long decode context.  Block (chunk c of kScChunk
+// positions, KV group g, token m); thread t scores relative position
+// kScChunk * c + t for every query head of the group, each score a
+// sequential fp32 dot over head_dim (rounded products, added in order) scaled
+// in double -- attn_decode_block's arithmetic -- with the K row read once for
+// all the group's heads.  FUSED: q and the new k are rotated here (RoPE in
+// double, the body's formula), the new k and v rounded to fp16; the block
+// holding the token's position appends them to the cache and scores that
+// position from the rounded k.  The softmax / sums pass (attn_kernel with
+// SCORED) runs after it.
+constexpr int kScChunk = 256;
+constexpr int kScMaxHeads = 16;  // query heads per KV group
+
+// element tt of a head row after RoPE (rotate-half, the (cos, sin) pair of
+// the rotated index), as attn_decode_block computes it
+__device__ __forceinline__ float rope_elem(const float *row, int tt, int rot, const double2 *cs_pos) {
+  if (tt >= 2 * rot) return row[tt];
+  const int i0 = tt < rot ? tt : tt - rot;
+  const float xa = row[i0], xb = row[i0 + rot];
+  const double2 c2 = cs_pos[i0];
+  const double cr = c2.x, sr = c2.y;
+  if (tt < rot) {
+    const double t1 = (double)xa * cr, t2 = (double)xb * sr;
+    return (float)(t1 - t2);
+  }
+  const double t3 = (double)xa * sr, t4 = (double)xb * cr;
+  return (float)(t3 + t4);
+}
+
+template <int HD, bool FUSED>
+__global__ __launch_bounds__(256) void attn_scores_kernel(AttnArgs a) {
+  constexpr int CPR = HD / 8;         // 16-byte chunks per K row
+  constexpr int KP = CPR + 1;         // LDS row pitch in chunks (odd: a thread's row reads spread over the banks)
+  constexpr int RPL = 256 / CPR;      // rows per load instruction over the block
+  __shared__ __attribute__((aligned(16))) float qs[kScMaxHeads][HD];
+  __shared__ __attribute__((aligned(16))) uint16_t kn[HD];
+  __shared__ v4u ktile[kScChunk * KP];
+  const int c = blockIdx.x, g = blockIdx.y, m = blockIdx.z, t = threadIdx.x;
+  const int R = a.H / a.KVH;
+  const int pos = ld_uniform(a.pos + m), slot = ld_uniform(a.slot + m);
+  int lo = 0;
+  if (a.window > 0) {
+    lo = pos - a.window + 1;
+    if (lo < 0) lo = 0;
+  }
+  const int n = pos + 1 - lo, i0 = kScChunk * c;
+  if (i0 >= n) return;  // uniform
+  const int ncache = FUSED ? n - 1 : n;  // rows read from the cache
+  const size_t cbase = ((size_t)slot * a.C) * a.kv + (size_t)g * HD;
+  const uint16_t *K = a.kc + cbase + (size_t)lo * a.kv;
+  // the chunk's K rows, coalesced (CPR lanes per row), clamped into the cache rows
+  v4u kr[kScChunk / RPL];
+#pragma unroll
+  for (int u = 0; u < kScChunk / RPL; u++) {
+    const int r = RPL * u + t / CPR, cc = t % CPR;
+    const int i = min(i0 + r, ncache > 0 ? ncache - 1 : 0);
+    kr[u] = *reinterpret_cast<const v4u *>(K + (size_t)i * a.kv + 8 * cc);
+  }
+  const int rot = (FUSED && a.cs) ? a.half : 0;
+  const double2 *csp = rot ? a.cs + (size_t)pos * a.half : nullptr;
+  for (int e = t; e < R * HD; e += 256) {
+    const int r = e / HD, d = e - r * HD;
+    const float *qrow = a.q + (size_t)m * a.ldq + (size_t)(g * R + r) * HD;
+    qs[r][d] = rot ? rope_elem(qrow, d, rot, csp) : qrow[d];
+  }
+  if constexpr (FUSED) {
+    if (t < HD) {
+      const float *krow = a.k + (size_t)m * a.ldk + (size_t)g * HD;
+      const float *vrow = a.v + (size_t)m * a.ldk + (size_t)g * HD;
+      const uint16_t kh = f2h(rot ? rope_elem(krow, t, rot, csp) : krow[t]), vh = f2h(vrow[t]);
+      kn[t] = kh;
+      if (n - 1 < i0 + kScChunk) {  // this block holds the token's position: the append
+        const size_t woff = cbase + (size_t)pos * a.kv + t;
+        a.kc_w[woff] = kh;
+        a.vc_w[woff] = vh;
+      }
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kScChunk / RPL; u++) {
+    const int r = RPL * u + t / CPR, cc = t % CPR;
+    ktile[r * KP + cc] = kr[u];
+  }
+  __syncthreads();
+  const int i = i0 + t;
+  if (i >= n) return;
+  // this thread's row: the own position (FUSED) takes the rounded new k
+  const v4u *krow = (FUSED && i == n - 1) ? reinterpret_cast<const v4u *>(kn) : ktile + t * KP;
+  v4u kk[CPR];
+#pragma unroll
+  for (int cc = 0; cc < CPR; cc++) kk[cc] = krow[cc];
+  float *dst = a.scores + ((size_t)m * a.H + (size_t)g * R) * a.sc_ld + i;
+  for (int r = 0; r < R; r++) {
+    float s = 0.0f;
+#pragma unroll
+    for (int cc = 0; cc < CPR; cc++) {
+      float qv[8];
+#pragma unroll
+      for (int j = 0; j < 8; j++) qv[j] = qs[r][8 * cc + j];
+      mac8(s, qv, kk[cc]);
+    }
+    dst[(size_t)r * a.sc_ld] = (float)((double)s * a.inv_hd);
+  }
+}
+
 template <int HD>
 static void launch_attn(AttnArgs a, size_t lds, hipStream_t st) {
   // grouped-query heads: one XCD per KV group (8 XCDs, block x -> XCD x % 8)
@@ -529,14 +636,65 @@ static void launch_attn(AttnArgs a, size_t lds, hipStream_t st) {
   else klaunch((attn_kernel<HD, false, NS>), grid, block, lds, st, a);
 }
 
+template <int HD>
+static void launch_attn_scores(const AttnArgs &a, hipStream_t st) {
+  const dim3 g1((a.max_npos + kScChunk - 1) / kScChunk, a.KVH, a.M);
+  if (a.fuse_kv) klaunch((attn_scores_kernel<HD, true>), g1, dim3(256), 0, st, a);
+  else klaunch((attn_scores_kernel<HD, false>), g1, dim3(256), 0, st, a);
+}
+
+// the body on the scores pass's scores (the cache holds the new k / v)
+template <int HD>
+static void launch_attn_scored(AttnArgs a, hipStream_t st) {
+  const int r = a.H / a.KVH;
+  a.xcd_r = (a.KVH <= 8 && a.H % a.KVH == 0 && r > 1) ? r : 0;
+  a.fuse_kv = 0;
+  // one block per query head: element slices of head_dim 128 (2 or 4 blocks
+  // per head, measured at 1290 positions) took 29 and 43 us per layer
+  // against 24 us, their extra blocks running in more rounds
+  constexpr int NS = 1;
+  const dim3 grid((a.xcd_r ? 8 * r : a.H) * NS, a.M);
+  klaunch((attn_kernel<HD, false, NS, true>), grid, dim3(NS > 1 ? 512 : 256),
+          attention_lds_bytes(a.max_npos, HD, a.vtile), st, a);
+}
+
+// the scores pass applies: a workspace, a long context, head_dim 128 (the
+// one-block-per-head body, which re-scores nothing), whole KV groups of at
+// most kScMaxHeads heads.  head_dim 64 keeps its element slices in one
+// launch: the split measured no faster there (C4, 2048 positions, M = 4).
+bool attention_split_ok(const AttnArgs &a) {
+  return a.scores && a.sc_ld >= a.max_npos && a.max_npos >= kAttnSplitMinPos && attn_vec(a.hd, a.kv) &&
+         a.hd == 128 && a.H % a.KVH == 0 && a.H / a.KVH <= kScMaxHeads;
+}
+
 hipError_t attention(const AttnArgs &a, hipStream_t st) {
   if (a.vtile < 4 || (a.vtile & 3) || a.vtile > attention_max_vtile(a.hd, a.kv) || a.hd > 256)
     return hipErrorInvalidValue;
   const size_t lds = attention_lds_bytes(a.max_npos, a.hd, a.vtile);
+  if (attention_split_ok(a)) {
+    launch_attn_scores<128>(a, st);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    launch_attn_scored<128>(a, st);
+    return hipGetLastError();
+  }
   if (attn_vec(a.hd, a.kv) && a.hd == 64) launch_attn<64>(a, lds, st);
   else if (attn_vec(a.hd, a.kv) && a.hd == 128) launch_attn<128>(a, lds, st);
   else if (attn_vec(a.hd, a.kv) && a.hd == 32) launch_attn<32>(a, lds, st);
   else launch_attn<0>(a, lds, st);
+  return hipGetLastError();
+}
+
+hipError_t attention_scores(const AttnArgs &a, hipStream_t st) {
+  if (!attention_split_ok(a)) return hipErrorInvalidValue;
+  launch_attn_scores<128>(a, st);
+  return hipGetLastError();
+}
+
+hipError_t attention_after_scores(const AttnArgs &a, hipStream_t st) {
+  if (!attention_split_ok(a) || a.vtile < 4 || (a.vtile & 3) || a.vtile > attention_max_vtile(a.hd, a.kv))
+    return hipErrorInvalidValue;
+  launch_attn_scored<128>(a, st);
   return hipGetLastError();
 }
 

@@ -575,6 +575,7 @@ struct DevModel {
   int ah_ld = 0, ah_rows = 0;
   float *ahs = nullptr;
   float *logits = nullptr;
+  float *att_sc = nullptr;  // decode attention scores [batch_cap][H][eff_ctx] (long contexts)
   uint16_t *kc = nullptr, *vc = nullptr;
   size_t kv_layer = 0;  // elements per layer of one cache
   const uint16_t *lm = nullptr;
@@ -583,7 +584,14 @@ struct DevModel {
   // single-token greedy decode step captured as one HIP graph (see forward_impl)
   hipGraphExec_t step_graph = nullptr;
   int step_bucket = 0;  // the graph's attention LDS covers positions < step_bucket
-  int *h_amax = nullptr;  // pinned: the graph's argmax output
+  int *h_amax = nullptr;  // pinned: the graphs' argmax outputs (batch_cap ids)
+  // greedy decode steps of M tokens in distinct slots (kernel-per-op path),
+  // one HIP graph per (M, 512-position bucket), oldest replaced first
+  struct DecodeGraph {
+    int M, bucket;
+    hipGraphExec_t exec;
+  };
+  std::vector<DecodeGraph> dec_graphs;
   // device top-k for sampled decoding: chunk candidates, NaN flags, results
   unsigned long long *tk_cand = nullptr;  // [lm_rows][topk_chunks(V)][kTopkMax + 1]
   unsigned char *tk_nan = nullptr;        // [lm_rows][topk_chunks(V)]
@@ -655,7 +663,7 @@ struct Loader {
 static void free_dev(DevModel *d) {
   if (!d) return;
   void *ps[] = {d->arena, d->rope, d->d_tok, d->d_pos, d->d_slot, d->d_amax, d->x, d->h, d->qkv,
-                d->att, d->ff, d->aq, d->as, d->ah, d->ahs, d->logits, d->kc, d->vc, d->cand, d->tk_cand,
+                d->att, d->ff, d->aq, d->as, d->ah, d->ahs, d->att_sc, d->logits, d->kc, d->vc, d->cand, d->tk_cand,
                 d->tk_nan, d->tk_vals, d->tk_idx, d->tk_status, d->d_layers, d->xch, d->d_step_io, d->d_trace};
   for (void *p : ps)
     if (p) (void)hipFree(p);
@@ -663,6 +671,8 @@ static void free_dev(DevModel *d) {
   if (d->h_amax) (void)hipHostFree(d->h_amax);
   if (d->h_step_io) (void)hipHostFree(d->h_step_io);
   if (d->step_graph) (void)hipGraphExecDestroy(d->step_graph);
+  for (auto &dg : d->dec_graphs) (void)hipGraphExecDestroy(dg.exec);
+  d->dec_graphs.clear();
   delete d;
 }
 
@@ -965,13 +975,15 @@ static int load_impl(GPT2 *g, const char *path, int batch_cap, int max_ctx) {
     EC_HIP(hipMalloc(&d->ah, (size_t)d->ah_rows * 3 * d->ah_ld * sizeof(uint16_t)));
     EC_HIP(hipMalloc(&d->ahs, (size_t)d->ah_rows * 4));
   }
+  EC_HIP(hipMalloc(&d->att_sc, (size_t)g->batch_cap * g->n_head * eff * sizeof(float)));
   EC_HIP(hipMalloc(&d->logits, (size_t)d->lm_rows * V * 4));
   EC_HIP(hipMalloc(&d->d_tok, (size_t)mmax * 4));
   EC_HIP(hipMalloc(&d->d_pos, (size_t)mmax * 4));
   EC_HIP(hipMalloc(&d->d_slot, (size_t)mmax * 4));
   EC_HIP(hipMalloc(&d->d_amax, (size_t)mmax * 4));
   EC_HIP(hipHostMalloc((void **)&d->h_stage, ((size_t)mmax * 3 + 1) * 4, hipHostMallocDefault));
-  EC_HIP(hipHostMalloc((void **)&d->h_amax, 4 * sizeof(int), hipHostMallocDefault));
+  EC_HIP(hipHostMalloc((void **)&d->h_amax, (size_t)(g->batch_cap > 4 ? g->batch_cap : 4) * sizeof(int),
+                       hipHostMallocDefault));
   d->ncand = gemv_max_blocks();
   EC_HIP(hipMalloc(&d->cand, (size_t)d->lm_rows * d->ncand * sizeof(unsigned long long)));
   {
@@ -1273,8 +1285,15 @@ static int enqueue_forward(GPT2 *g, DevModel *d, int M, int lm_from, bool distin
     AttnArgs aa{d->qkv, ldq, kcl, vcl, d->att, E, d->d_pos, d->d_slot, H, g->n_kv_head, hd, kv,
                 d->eff_ctx, qwen ? g->sliding_window : 0, 1.0 / sqrt((double)hd), M, max_npos, vtile,
                 distinct ? 1 : 0, kq, vq, ldq, (distinct && qwen) ? d->rope : nullptr, d->half, kcl, vcl};
+    if (!run && M <= g->batch_cap) {  // long decode contexts: scores pass, then softmax / sums
+      aa.scores = d->att_sc;
+      aa.sc_ld = d->eff_ctx;
+    }
     if (run && attention_prefill_ok(aa, g_max_lds)) {
       EC_LAUNCH("attention_prefill", abytes, attention_prefill(aa, g_max_lds, s));
+    } else if (attention_split_ok(aa)) {
+      EC_LAUNCH("attention_scores", abytes / 2, attention_scores(aa, s));
+      EC_LAUNCH("attention", abytes / 2, attention_after_scores(aa, s));
     } else {
       EC_LAUNCH("attention", abytes, attention(aa, s));
     }
@@ -1467,15 +1486,22 @@ static int forward_impl(GPT2 *g, const int *tokens, const int *positions, const 
     if (argmax) argmax[0] = io[5];
     return 0;
   }
-  if (M == 1 && lm_from == 0 && argmax && !logits && !tk && !g_prof_on && g_use_graphs &&
-      attn_vtile(bucket, hd, kv) >= 4) {
-    if (!d->step_graph || d->step_bucket != bucket) {
-      if (d->step_graph) {
-        EC_HIP(hipGraphExecDestroy(d->step_graph));
-        d->step_graph = nullptr;
+  // a greedy decode step of M tokens, each in its own slot: one HIP graph per
+  // (M, bucket) of the staging copies, every kernel and the copy of the M
+  // argmax ids into pinned memory
+  if (lm_from == 0 && argmax && !logits && !tk && !g_prof_on && g_use_graphs && distinct && !run &&
+      M <= g->batch_cap && attn_vtile(bucket, hd, kv) >= 4) {
+    hipGraphExec_t ex = nullptr;
+    for (const auto &dg : d->dec_graphs)
+      if (dg.M == M && dg.bucket == bucket) ex = dg.exec;
+    if (!ex) {
+      constexpr size_t kMaxGraphs = 8;
+      if (d->dec_graphs.size() >= kMaxGraphs) {
+        EC_HIP(hipGraphExecDestroy(d->dec_graphs.front().exec));
+        d->dec_graphs.erase(d->dec_graphs.begin());
       }
       EC_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
-      const int r = enqueue_forward(g, d, 1, 0, true, false, bucket, abytes, nullptr, d->h_amax, nullptr, s);
+      const int r = enqueue_forward(g, d, M, 0, true, false, bucket, abytes, nullptr, d->h_amax, nullptr, s);
       hipGraph_t graph = nullptr;
       const hipError_t e = hipStreamEndCapture(s, &graph);
       if (r) {
@@ -1483,14 +1509,14 @@ static int forward_impl(GPT2 *g, const int *tokens, const int *positions, const 
         return r;
       }
       EC_HIP(e);
-      const hipError_t ei = hipGraphInstantiate(&d->step_graph, graph, nullptr, nullptr, 0);
+      const hipError_t ei = hipGraphInstantiate(&ex, graph, nullptr, nullptr, 0);
       (void)hipGraphDestroy(graph);
       EC_HIP(ei);
-      d->step_bucket = bucket;
+      d->dec_graphs.push_back({M, bucket, ex});
     }
-    EC_HIP(hipGraphLaunch(d->step_graph, s));
+    EC_HIP(hipGraphLaunch(ex, s));
     EC_HIP(hipStreamSynchronize(s));
-    argmax[0] = d->h_amax[0];
+    memcpy(argmax, d->h_amax, (size_t)M * sizeof(int));
     return 0;
   }
   const int r = enqueue_forward(g, d, M, lm_from, distinct, run, max_npos, abytes, logits, argmax, tk, s);
@@ -1610,7 +1636,7 @@ extern "C" int ec_attention_dev(const float *q, int ldq, const uint16_t *kc, con
   EC_INIT();
   if (!q || !kc || !vc || !pos || !slot || !out) return set_err(-1, "ec_attention_dev: null pointer");
   if (M < 1 || nslots < 1 || C < 1 || H < 1 || KVH < 1 || H % KVH || hd < 1 || ldq < H * hd || ldo < H * hd ||
-      window < 0 || (path != 0 && path != 1))
+      window < 0 || path < 0 || path > 2)
     return set_err(-1, "ec_attention_dev: M=%d slots=%d C=%d H=%d KVH=%d hd=%d ldq=%d ldo=%d window=%d path=%d", M,
                    nslots, C, H, KVH, hd, ldq, ldo, window, path);
   int max_npos = 0;
@@ -1626,11 +1652,15 @@ extern "C" int ec_attention_dev(const float *q, int ldq, const uint16_t *kc, con
   const int vtile = attn_vtile(max_npos, hd, kv);
   if (vtile < 4) return set_err(-1, "ec_attention_dev: position %d needs more LDS than the device has", max_npos - 1);
   int *dps = nullptr;
+  float *dsc = nullptr;
   hipError_t e = hipMalloc(&dps, (size_t)2 * M * sizeof(int));
+  if (e == hipSuccess && path == 2) e = hipMalloc(&dsc, (size_t)M * H * C * sizeof(float));
   if (e == hipSuccess) e = hipMemcpyAsync(dps, pos, (size_t)M * sizeof(int), hipMemcpyHostToDevice, g_stream);
   if (e == hipSuccess) e = hipMemcpyAsync(dps + M, slot, (size_t)M * sizeof(int), hipMemcpyHostToDevice, g_stream);
   AttnArgs aa{q, ldq, kc, vc, out, ldo, dps, dps + M, H, KVH, hd, kv, C, window, 1.0 / sqrt((double)hd), M, max_npos,
               vtile, 0, nullptr, nullptr, 0, nullptr, 0, nullptr, nullptr, 0};
+  aa.scores = dsc;
+  aa.sc_ld = C;
   bool shape_ok = true;
   if (e == hipSuccess) {
     if (path == 0) {
@@ -1642,6 +1672,7 @@ extern "C" int ec_attention_dev(const float *q, int ldq, const uint16_t *kc, con
   }
   if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
   if (dps) (void)hipFree(dps);
+  if (dsc) (void)hipFree(dsc);
   if (!shape_ok) return set_err(-1, "ec_attention_dev: the prefill kernel does not take head_dim %d / %d positions", hd,
                                 max_npos);
   if (e != hipSuccess) return set_err(-3, "ec_attention_dev: %s", hipGetErrorString(e));

@@ -363,7 +363,10 @@ int ec_topk_dev_noalloc(const float *logits, int rows, int vocab, int ld, int to
  * fp32 (row stride ldo); pos and slot are host arrays [M].  path 0: the
  * prefill kernel (one slot's consecutive positions pos[0] + m, as the forward
  * runs a prompt); path 1: the per-token kernel (any positions and slots, as
- * the forward runs decode steps).  0 or <0. */
+ * the forward runs decode steps); path 2: the forward's long-context decode
+ * form (from 512 positions, head_dim 128; otherwise path 1): a scores pass
+ * with one block per token, KV group and 256 positions, then the per-token
+ * kernel's softmax and sums on those scores.  0 or <0. */
 int ec_attention_dev(const float *q, int ldq, const uint16_t *kc, const uint16_t *vc, int nslots, int C, int H,
                      int KVH, int hd, const int *pos, const int *slot, int M, int window, float *out, int ldo,
                      int path);

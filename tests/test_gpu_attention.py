@@ -85,6 +85,25 @@ def test_decode_kernel_long_positions(hd, window):
     _check(got, want, np.arange(8))
 
 
+@pytest.mark.parametrize("H,KVH,hd,window", [(12, 2, 128, 0), (12, 2, 128, 700), (16, 1, 128, 0), (6, 6, 128, 0)])
+def test_decode_scores_pass_equals_per_token_kernel(H, KVH, hd, window):
+    """The long-context decode form of head_dim 128 (path 2: a scores pass
+    per token, KV group and 256 positions, then the per-token kernel's
+    softmax and sums on those scores) against the per-token kernel (path 1)
+    bit for bit, and against the oracle: GQA groups of 6 and 16 heads and
+    GPT-2-style heads, with and without a window; 8 tokens in 4 slots at
+    positions up to 2047."""
+    C, ns = 2048, 4
+    rng, q, kc, vc = _case(77 + hd + H + window, 8, H, KVH, hd, C, ns)
+    pos = np.array([2047, 2000, 1536, 1023, 511, 256, 3, 0])
+    sl = np.array([0, 1, 2, 3, 0, 1, 2, 3])
+    one = ec.attention_dev(q, kc, vc, pos, sl, H, KVH, window=window, path=1)
+    two = ec.attention_dev(q, kc, vc, pos, sl, H, KVH, window=window, path=2)
+    assert np.array_equal(one.view(np.uint32), two.view(np.uint32))
+    want = oracle.attention_rows(q, kc, vc, pos, sl, H, KVH, window=window)
+    _check(two, want, np.arange(8))
+
+
 def test_attention_dev_rejects_bad_arguments():
     H, KVH, hd, C = 4, 2, 64, 32
     _, q, kc, vc = _case(9, 4, H, KVH, hd, C, 1)

@@ -170,6 +170,44 @@ def test_graph_decode_equals_direct_and_oracle(make_model, name):
     assert np.array_equal(ids_graph, oids)
 
 
+@pytest.mark.parametrize("name,B", [("tiny-qwen2-int8", 3), ("tiny-gpt2-fp16", 16), ("qwen2-hd128-int8", 16)])
+def test_batched_graph_decode_equals_direct_and_oracle(make_model, name, B):
+    """A greedy step of B tokens in B slots (argmax only) replays a HIP graph
+    captured per (B, position bucket); asking for logits takes the direct
+    launches.  Graph ids, direct ids and the oracle's ids must agree, also on
+    a second pass that replays the cached graph after a cache reset."""
+    path = make_model(name)
+    steps = 8
+    with ec.Model(path, B, 64) as m:
+        prompts = [prompt_ids(6 + b % 5, m.vocab, seed=40 + b) for b in range(B)]
+
+        def run(want_logits):
+            m.kv_reset()
+            for b, p in enumerate(prompts):
+                m.forward(p, np.arange(len(p)), np.full(len(p), b, np.int32), lm_from=len(p), want_logits=False)
+            cur, pos, out = [int(p[-1]) for p in prompts], [len(p) for p in prompts], []
+            for _ in range(steps):
+                _, am = m.forward(cur, pos, None, want_logits=want_logits, want_argmax=True)
+                cur, pos = [int(x) for x in am], [q + 1 for q in pos]
+                out.append(cur)
+            return np.array(out)
+
+        ids_graph, ids_direct, ids_again = run(False), run(True), run(False)
+    om = oracle.OracleModel(path, B, 64)
+    om.kv_reset()
+    for b, p in enumerate(prompts):
+        om.forward(p, np.arange(len(p)), np.full(len(p), b, np.int32))
+    cur, pos, oids = [int(p[-1]) for p in prompts], [len(p) for p in prompts], []
+    for _ in range(steps):
+        lg = om.forward(cur, pos, None)
+        cur, pos = [int(r.argmax()) for r in lg], [q + 1 for q in pos]
+        oids.append(cur)
+    om.close()
+    assert np.array_equal(ids_graph, ids_direct)
+    assert np.array_equal(ids_graph, ids_again)
+    assert np.array_equal(ids_graph, np.array(oids))
+
+
 def test_graph_recaptured_across_position_buckets(make_model):
     """Decode positions 1000..1039 cross the 1024 bucket (the graph is captured
     again with a larger attention LDS); two models keep separate graphs."""

@@ -268,43 +268,61 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemvArgs a) {
   }
 
   // ---- epilogue: lane holds D[4*lq + r][lr] of each tile ----
+  // Every value of a column tile is computed before any of its stores, so
+  // that the 4*TI independent chains (SiLU's expf and division, GELU's tanh)
+  // interleave instead of each waiting in its own exec-masked branch; tiles
+  // wholly inside the matrix store without per-element tests.  Rows and
+  // columns past the matrix were loaded clamped: their values are computed
+  // and not stored.
+  const bool full = m0 + BM <= M && n0 + NOUT <= N;
 #pragma unroll
   for (int j = 0; j < JO; j++) {
     const int n = lcol0 + 16 * j;
-    if (n >= N) continue;
     const float bs = a.ws ? e_bs[j] : 1.0f;
     const float bv = (!SWI && a.bias) ? e_bv[j] : 0.0f;
     const float bs2 = (SWI && a.ws2) ? e_bs2[j] : 1.0f;
+    float v[TI][4];
 #pragma unroll
     for (int i = 0; i < TI; i++) {
 #pragma unroll
       for (int r = 0; r < 4; r++) {
-        const int m = lrow0 + 16 * i + r;
-        if (m >= M) continue;
         const float as = e_as[i][r];
-        float v;
+        float x;
         if constexpr (I8) {
-          v = i8_epilogue(acc[i][j][r], as, bs, bv);
+          x = i8_epilogue(acc[i][j][r], as, bs, bv);
           if constexpr (SWI) {
             const float u = i8_epilogue(acc[i][j + TJ / 2][r], as, bs2, 0.0f);
-            v = silu(v, etab) * u;
+            x = silu(x, etab) * u;
           }
         } else {
           // 16-bit: the split's 2^e, then the 16-bit GEMV's epilogue order
-          v = acc[i][j][r] * as;
+          x = acc[i][j][r] * as;
           if constexpr (SWI) {
             const float u = acc[i][j + TJ / 2][r] * as;
-            v = silu(v, etab) * u;
+            x = silu(x, etab) * u;
           } else if (a.bias) {
-            v = v + bv;
+            x = x + bv;
           }
         }
         if constexpr (!SWI) {
-          if constexpr (RES) v = e_old[i][j][r] + v;
-          if constexpr (GELU) v = gelu_new(v);
+          if constexpr (RES) x = e_old[i][j][r] + x;
+          if constexpr (GELU) x = gelu_new(x);
         }
-        a.out[(size_t)m * a.ldo + n] = v;
+        v[i][r] = x;
       }
+    }
+    float *op = a.out + n;
+    if (full) {
+#pragma unroll
+      for (int i = 0; i < TI; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) op[(size_t)(lrow0 + 16 * i + r) * a.ldo] = v[i][r];
+    } else if (n < N) {
+#pragma unroll
+      for (int i = 0; i < TI; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+          if (lrow0 + 16 * i + r < M) op[(size_t)(lrow0 + 16 * i + r) * a.ldo] = v[i][r];
     }
   }
 }

@@ -85,14 +85,15 @@ struct MfmaOp<OP_BF16> {
   }
 };
 
-template <int OP, int BM>
+// two stage buffers; the direct-to-LDS form (DL) has unpadded rows
+template <int OP, int BM, bool DL>
 constexpr size_t gemm_lds_bytes() {
-  return (size_t)2 * (MfmaOp<OP>::NP * BM + kBN) * kPitch;
+  return (size_t)2 * (MfmaOp<OP>::NP * BM + kBN) * (DL ? kBK : kPitch);
 }
 
 // A: [M * NP][lda] elements (row m's part p at row m * NP + p), as: per-row
 // scale (int8 quantization scale, or the split's 2^e; 1 for bf16)
-template <int OP, int BM, int EPI>
+template <int OP, int BM, int EPI, bool DL>
 __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemvArgs a) {
   using Op = MfmaOp<OP>;
   using Acc = typename Op::Acc;
@@ -238,33 +239,107 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemvArgs a) {
     for (int j = 0; j < TJ; j++) acc[i][j] = Acc{0, 0, 0, 0};
 
   const int ns = (KB + kBK - 1) / kBK;
-  load(0);
-  store(0);
-  __syncthreads();
-  for (int s = 0; s < ns; s++) {
-    const int buf = s & 1;
-    if (s + 1 < ns) load((s + 1) * kBK);
-    const int8_t *ta = la + buf * NP * BM * kPitch + (wm * WM + lr) * kPitch + 16 * lq;
-    const int8_t *tb = lb + buf * kBN * kPitch + lr * kPitch + 16 * lq;
-#pragma unroll
-    for (int kk = 0; kk < kBK / 64; kk++) {
-      v4i fa[NP][TI], fb[TJ];
-#pragma unroll
-      for (int p = 0; p < NP; p++)
-#pragma unroll
-        for (int i = 0; i < TI; i++)
-          fa[p][i] = *reinterpret_cast<const v4i *>(ta + (p * BM + 16 * i) * kPitch + 64 * kk);
-#pragma unroll
-      for (int j = 0; j < TJ; j++) fb[j] = *reinterpret_cast<const v4i *>(tb + bt[j] * kPitch + 64 * kk);
-#pragma unroll
-      for (int p = 0; p < NP; p++)
-#pragma unroll
-        for (int i = 0; i < TI; i++)
-#pragma unroll
-          for (int j = 0; j < TJ; j++) acc[i][j] = Op::mma(fa[p][i], fb[j], acc[i][j]);
-    }
-    if (s + 1 < ns) store(buf ^ 1);
+  if constexpr (!DL) {
+    const int ns = (KB + kBK - 1) / kBK;
+    load(0);
+    store(0);
     __syncthreads();
+    for (int s = 0; s < ns; s++) {
+      const int buf = s & 1;
+      if (s + 1 < ns) load((s + 1) * kBK);
+      const int8_t *ta = la + buf * NP * BM * kPitch + (wm * WM + lr) * kPitch + 16 * lq;
+      const int8_t *tb = lb + buf * kBN * kPitch + lr * kPitch + 16 * lq;
+  #pragma unroll
+      for (int kk = 0; kk < kBK / 64; kk++) {
+        v4i fa[NP][TI], fb[TJ];
+  #pragma unroll
+        for (int p = 0; p < NP; p++)
+  #pragma unroll
+          for (int i = 0; i < TI; i++)
+            fa[p][i] = *reinterpret_cast<const v4i *>(ta + (p * BM + 16 * i) * kPitch + 64 * kk);
+  #pragma unroll
+        for (int j = 0; j < TJ; j++) fb[j] = *reinterpret_cast<const v4i *>(tb + bt[j] * kPitch + 64 * kk);
+  #pragma unroll
+        for (int p = 0; p < NP; p++)
+  #pragma unroll
+          for (int i = 0; i < TI; i++)
+  #pragma unroll
+            for (int j = 0; j < TJ; j++) acc[i][j] = Op::mma(fa[p][i], fb[j], acc[i][j]);
+      }
+      if (s + 1 < ns) store(buf ^ 1);
+      __syncthreads();
+    }
+  } else {
+    // Both tiles loaded straight into LDS (global_load_lds_dwordx4: lane l's
+    // 16 bytes land 16 l bytes after the wave's base), rows of kBK bytes with
+    // no padding; chunk c of row r sits at chunk c ^ (r & 7) of the row, so
+    // that the 16-byte fragment reads of 8 consecutive rows hit distinct
+    // banks.  A wave instruction fills 8 rows: lane l takes row 8 u + l / 8
+    // and stores the row's chunk (l & 7) ^ (l / 8) at position l & 7.  Rows
+    // are K-complete (the launcher takes this path when K bytes are a
+    // multiple of kBK), so no chunk is past the row.
+    constexpr int RT = NP * BM + kBN;  // tile rows per stage
+    constexpr int UPW = RT / 32;       // 8-row load instructions per wave and stage
+    static_assert(RT % 32 == 0, "tile rows");
+    typedef __attribute__((address_space(1))) const void gvoid;
+    typedef __attribute__((address_space(3))) void lvoid;
+    const int lrow = lane >> 3, lchk = (lane & 7) ^ lrow;
+    const int8_t *src[UPW];
+#pragma unroll
+    for (int u = 0; u < UPW; u++) {
+      const int r = 8 * (wave * UPW + u) + lrow;  // tile row
+      if (r < NP * BM) {
+        const int p = r / BM, mr = r % BM;
+        src[u] = A + ((size_t)min(m0 + mr, M - 1) * NP + p) * ldab + 16 * lchk;
+      } else {
+        const int rb = r - NP * BM;
+        const int8_t *W = (const int8_t *)a.W;
+        int n = n0 + rb;
+        if (SWI && rb >= kBN / 2) {
+          W = (const int8_t *)a.W2;
+          n = n0 + rb - kBN / 2;
+        }
+        src[u] = W + (size_t)min(n, N - 1) * KB + 16 * lchk;
+      }
+    }
+    auto dload = [&](int k0, int buf) {
+      int8_t *base = lds + (size_t)buf * RT * kBK + (size_t)wave * UPW * 8 * kBK;
+#pragma unroll
+      for (int u = 0; u < UPW; u++)
+        __builtin_amdgcn_global_load_lds((gvoid *)(src[u] + k0), (lvoid *)(base + u * 8 * kBK), 16, 0, 0);
+    };
+    const int sw = lr & 7;  // fragment rows are 16-aligned: row & 7 == lr & 7
+    // stage s is waited for (each wave its own loads, then the barrier)
+    // before stage s+1 is loaded into the other buffer, whose reads of stage
+    // s-1 completed before their multiplies used them.  The barrier is bare:
+    // __syncthreads() adds a fence whose waits come out no better.
+    dload(0, 0);
+    for (int s = 0; s < ns; s++) {
+      __builtin_amdgcn_s_waitcnt(0);
+      asm volatile("s_barrier" ::: "memory");
+      if (s + 1 < ns) dload((s + 1) * kBK, (s + 1) & 1);
+      const int buf = s & 1;
+      const int8_t *ta = lds + (size_t)buf * RT * kBK + (size_t)(wm * WM + lr) * kBK;
+      const int8_t *tb = lds + (size_t)buf * RT * kBK + (size_t)(NP * BM + lr) * kBK;
+#pragma unroll
+      for (int kk = 0; kk < kBK / 64; kk++) {
+        const int co = 16 * ((4 * kk + lq) ^ sw);
+        v4i fa[NP][TI], fb[TJ];
+#pragma unroll
+        for (int p = 0; p < NP; p++)
+#pragma unroll
+          for (int i = 0; i < TI; i++)
+            fa[p][i] = *reinterpret_cast<const v4i *>(ta + (p * BM + 16 * i) * kBK + co);
+#pragma unroll
+        for (int j = 0; j < TJ; j++) fb[j] = *reinterpret_cast<const v4i *>(tb + bt[j] * kBK + co);
+#pragma unroll
+        for (int p = 0; p < NP; p++)
+#pragma unroll
+          for (int i = 0; i < TI; i++)
+#pragma unroll
+            for (int j = 0; j < TJ; j++) acc[i][j] = Op::mma(fa[p][i], fb[j], acc[i][j]);
+      }
+    }
   }
 
   // ---- epilogue: lane holds D[4*lq + r][lr] of each tile ----
@@ -327,12 +402,17 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemvArgs a) {
   }
 }
 
+#ifndef EC_GEMM_DL
+#define EC_GEMM_DL 1
+#endif
 template <int OP, int BM, int EPI>
 hipError_t launch_bm(const GemvArgs &a, hipStream_t s) {
   constexpr int NOUT = EPI == EPI_SWIGLU ? kBN / 2 : kBN;
   const int T = ((a.N + NOUT - 1) / NOUT) * ((a.M + BM - 1) / BM);
   const dim3 grid(8 * ((T + 7) / 8));
-  klaunch((gemm_mfma_kernel<OP, BM, EPI>), grid, dim3(256), gemm_lds_bytes<OP, BM>(), s, a);
+  const bool dl = EC_GEMM_DL && (a.K * MfmaOp<OP>::EB) % kBK == 0 && (a.lda * MfmaOp<OP>::EB) % kBK == 0;
+  if (dl) klaunch((gemm_mfma_kernel<OP, BM, EPI, true>), grid, dim3(256), gemm_lds_bytes<OP, BM, true>(), s, a);
+  else klaunch((gemm_mfma_kernel<OP, BM, EPI, false>), grid, dim3(256), gemm_lds_bytes<OP, BM, false>(), s, a);
   return hipGetLastError();
 }
 

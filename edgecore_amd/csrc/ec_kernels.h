@@ -154,6 +154,18 @@ struct KvArgs {
   int M;
 };
 hipError_t rope_kv_append(const KvArgs &a, hipStream_t st);
+// reads up to kTouchRanges weight matrices (rows of row16 16-byte words)
+// into the L2 of the XCDs whose GEMM blocks read them (see kernels.hip);
+// blocks: a multiple of 8
+constexpr int kTouchRanges = 6;
+struct TouchArgs {
+  const uint4 *p[kTouchRanges];
+  int rows[kTouchRanges];
+  int row16[kTouchRanges];
+  int n_ranges;
+  unsigned *sink;  // one device word, written only if the loaded xor equals a constant
+};
+hipError_t touch_ranges(const TouchArgs &a, int blocks, hipStream_t st);
 
 // causal attention over the fp16 cache for every (head, token), in the
 // reference's arithmetic order (see kernels.hip).  With `cs`/`fuse_kv` set it

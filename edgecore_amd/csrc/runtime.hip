@@ -38,6 +38,15 @@ static thread_local char g_err[512];
 static int g_inited = 0;
 static int g_device = 0;
 static hipStream_t g_stream = nullptr;
+// a prefill reads each layer's weights into the memory-side cache on a
+// second stream while that layer's attention runs (EDGECORE_TOUCH=0: off)
+static hipStream_t g_side = nullptr;
+static hipEvent_t g_touch_ev[4] = {};
+static unsigned g_touch_i = 0;
+static unsigned *g_touch_sink = nullptr;
+static bool g_touch = true;
+static int g_touch_blocks = 8;  // one per XCD; a multiple of 8 (EDGECORE_TOUCH_BLOCKS)
+constexpr int kTouchMinRows = 1024;  // prompts at least this long
 static hipDeviceProp_t g_prop;
 static int g_max_lds = 65536;
 // replay the single-token greedy step as a HIP graph (EDGECORE_GRAPHS=0 turns it off)
@@ -91,6 +100,13 @@ extern "C" int ec_init(void) {
       lds > 0)
     g_max_lds = lds;
   EC_HIP(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
+  EC_HIP(hipStreamCreateWithFlags(&g_side, hipStreamNonBlocking));
+  for (hipEvent_t &ev : g_touch_ev) EC_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+  EC_HIP(hipMalloc(&g_touch_sink, 256));
+  const char *tch = getenv("EDGECORE_TOUCH");
+  g_touch = !(tch && !strcmp(tch, "0"));
+  const char *tb = getenv("EDGECORE_TOUCH_BLOCKS");
+  if (tb && atoi(tb) >= 8) g_touch_blocks = atoi(tb) / 8 * 8;
   const char *gr = getenv("EDGECORE_GRAPHS");
   g_use_graphs = !(gr && !strcmp(gr, "0"));
   const char *mf = getenv("EDGECORE_MFMA");
@@ -1266,6 +1282,7 @@ static int enqueue_forward(GPT2 *g, DevModel *d, int M, int lm_from, bool distin
 
   const int F = d->F, ldq = d->qkv_ld;
   const int nqkv = qwen ? E + 2 * kv : 3 * E;
+  bool touched = false;
   for (int l = 0; l < (step ? 0 : g->n_layer); l++) {
     const LayerDev &W = d->L[l];
     uint16_t *kcl = d->kc + d->kv_layer * l, *vcl = d->vc + d->kv_layer * l;
@@ -1288,6 +1305,36 @@ static int enqueue_forward(GPT2 *g, DevModel *d, int M, int lm_from, bool distin
     if (!run && M <= g->batch_cap) {  // long decode contexts: scores pass, then softmax / sums
       aa.scores = d->att_sc;
       aa.sc_ld = d->eff_ctx;
+    }
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (g_touch && run && M >= kTouchMinRows && hipStreamIsCapturing(s, &cap) == hipSuccess &&
+        cap == hipStreamCaptureStatusNone) {
+      // this layer's o / MLP weights and the next layer's q|k|v rows into
+      // the memory-side cache while the attention runs
+      const size_t eb = i8 ? 1 : 2;
+      TouchArgs ta{};
+      ta.sink = g_touch_sink;
+      auto add = [&](const void *w, int rows, int cols) {
+        if (w && ta.n_ranges < kTouchRanges && (cols * eb) % 16 == 0) {
+          ta.p[ta.n_ranges] = (const uint4 *)w;
+          ta.rows[ta.n_ranges] = rows;
+          ta.row16[ta.n_ranges++] = (int)(cols * eb / 16);
+        }
+      };
+      add(W.wo, E, E);
+      if (qwen) {
+        add(W.wg, F, E);
+        add(W.wu, F, E);
+      } else {
+        add(W.wfc, F, E);
+      }
+      add(W.wd, E, F);
+      if (l + 1 < g->n_layer) add(d->L[l + 1].wqkv, nqkv, E);
+      hipEvent_t ev = g_touch_ev[g_touch_i++ & 3];
+      EC_HIP(hipEventRecord(ev, s));
+      EC_HIP(hipStreamWaitEvent(g_side, ev, 0));
+      EC_HIP(touch_ranges(ta, g_touch_blocks, g_side));
+      touched = true;
     }
     if (run && attention_prefill_ok(aa, g_max_lds)) {
       EC_LAUNCH("attention_prefill", abytes, attention_prefill(aa, g_max_lds, s));
@@ -1321,6 +1368,11 @@ static int enqueue_forward(GPT2 *g, DevModel *d, int M, int lm_from, bool distin
       const int epi = i8 ? EPI_RESID : (W.bd ? EPI_BIAS_RESID : EPI_RESID);
       if ((r = linear(g, d, "gemv_down", a, wt, epi, i8 ? PRO_QUANT : PRO_F32, s))) return r;
     }
+  }
+  if (touched) {  // the side stream's reads end before anything after this forward
+    hipEvent_t ev = g_touch_ev[g_touch_i++ & 3];
+    EC_HIP(hipEventRecord(ev, g_side));
+    EC_HIP(hipStreamWaitEvent(s, ev, 0));
   }
   // final norm fused into the LM head (always fp16/bf16, src/gpt2.c:576-580 / 799-804);
   // greedy ids from per-block argmax candidates

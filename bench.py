@@ -5,13 +5,16 @@ Workload (bs=1): Qwen2-0.5B architecture (24 layers, d_model 896, 14/2 heads,
 head_dim 64, SwiGLU 4864, vocab 151936 tied), int8 per-output-channel weights
 N(0, 0.02) from seed 0 (synthetic, bin/ecm_synth), a 256-token prompt of ids
 uniform in [0, 151936) from seed 1, greedy decoding.  One step is one decode
-token: the forward at M=1 plus the GPU argmax and the copy of the id back to
-the host.  The prompt is prefilled first (reported as prefill tok/s, untimed),
-then W warmup steps, then K timed steps bracketed by stream synchronisation.
+token: the forward at M=1 plus the GPU argmax.  The steps run through
+ec_generate_greedy, which chains them on the device (each argmax id becomes
+the next step's token there; the K ids come back to the host at the end).
+The prompt is prefilled first (reported as prefill tok/s, untimed), then W
+warmup steps, then K timed steps bracketed by stream synchronisation.
 
 Two passes of the same K steps run, each after the same prefill and warmup.
 In the first, every kernel launch records its own dispatch start and stop on
-HIP events (hipExtLaunchKernel on the library's stream, ec_prof_*): that
+HIP events (hipExtLaunchKernel on the library's stream, ec_prof_*; with the
+profiler on, ec_generate_greedy runs one host-driven step per token): that
 gives the per-kernel table and the launch durations of the roofline object
 (the family with the largest total time: the persistent decode step, which
 runs every layer; int8_weight_stream: the layers' int8 weights and scales per
@@ -462,19 +465,14 @@ def main() -> int:
         m.kv_reset()
         m.forward(prompt, np.arange(PROMPT), np.zeros(PROMPT, np.int32), lm_from=PROMPT, want_logits=False)
         cur, pos = int(prompt[-1]), PROMPT
-        for _ in range(W):
-            _, am = m.forward([cur], [pos], None, want_logits=False, want_argmax=True)
-            cur, pos = int(am[0]), pos + 1
+        if W > 0:
+            cur, pos = int(m.generate_greedy(cur, pos, 0, W)[-1]), pos + W
         L.ec_sync()
         if prof_filter is not None:
             L.ec_prof_start(prof_filter.encode())
         L.ec_sync()
         t0 = time.perf_counter()
-        ids = []
-        for _ in range(K):
-            _, am = m.forward([cur], [pos], None, want_logits=False, want_argmax=True)
-            cur, pos = int(am[0]), pos + 1
-            ids.append(cur)
+        ids = [int(x) for x in m.generate_greedy(cur, pos, 0, K)]
         L.ec_sync()
         elapsed = time.perf_counter() - t0
         kern = []

@@ -92,6 +92,7 @@ _SIG = {
     "gpt2_forward_ex": (_I, [_P, _P, _P, _P, _I, _I, _P, _P]),
     "gpt2_forward_topk": (_I, [_P, _P, _P, _P, _I, _I, _I, _P, _P, _P]),
     "ec_topk_max": (_I, []),
+    "ec_generate_greedy": (_I, [_P, _I, _I, _I, _I, _P]),
     "ec_last_logits": (_I, [_P, _I, _P]),
     "ec_topk_dev": (_I, [_P, _I, _I, _I, _I, _P, _P, _P]),
     "ec_topk_dev_noalloc": (_I, [_P, _I, _I, _I, _I, _P, _P, _P]),
@@ -358,6 +359,13 @@ class Model:
                                      _ptr(vals), _ptr(idx), _ptr(status))
         _check(rc, "gpt2_forward_topk")
         return vals, idx, status
+
+    def generate_greedy(self, token: int, pos: int, slot: int, n: int) -> np.ndarray:
+        """ec_generate_greedy: the ids of n greedy steps from `token` at `pos` in `slot`."""
+        out = np.empty(n, np.int32)
+        _check(lib().ec_generate_greedy(C.byref(self.g), int(token), int(pos), int(slot), int(n), _ptr(out)),
+               "ec_generate_greedy")
+        return out
 
     def last_logits(self, row: int) -> np.ndarray:
         out = np.empty(self.vocab, np.float32)

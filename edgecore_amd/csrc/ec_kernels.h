@@ -166,6 +166,10 @@ struct TouchArgs {
   unsigned *sink;  // one device word, written only if the loaded xor equals a constant
 };
 hipError_t touch_ranges(const TouchArgs &a, int blocks, hipStream_t st);
+// chained greedy decode: io[0..6] = token, position, slot, tag, error, argmax
+// id, ids written; moves the argmax id into the next step's inputs and
+// appends it to out[io[6]]
+hipError_t step_advance(int *io, int *out, hipStream_t st);
 
 // causal attention over the fp16 cache for every (head, token), in the
 // reference's arithmetic order (see kernels.hip).  With `cs`/`fuse_kv` set it

@@ -528,6 +528,23 @@ hipError_t touch_ranges(const TouchArgs &a, int blocks, hipStream_t st) {
   return hipGetLastError();
 }
 
+// After a chained greedy decode step (io: token, position, slot, tag, error,
+// argmax id, ids written): the argmax id becomes the next step's token at the
+// next position under the next tag, and is appended to out.
+__global__ void step_advance_kernel(int *io, int *out) {
+  const int t = io[5];
+  out[io[6]] = t;
+  io[6] = io[6] + 1;
+  io[0] = t;
+  io[1] = io[1] + 1;
+  io[3] = (int)((unsigned)io[3] + 1u);
+}
+
+hipError_t step_advance(int *io, int *out, hipStream_t st) {
+  klaunch(step_advance_kernel, dim3(1), dim3(1), 0, st, io, out);
+  return hipGetLastError();
+}
+
 hipError_t rope_kv_append(const KvArgs &a, hipStream_t st) {
   klaunch(rope_kv_kernel, dim3(a.M), dim3(256), 0, st, a);
   return hipGetLastError();

@@ -600,6 +600,12 @@ struct DevModel {
   // single-token greedy decode step captured as one HIP graph (see forward_impl)
   hipGraphExec_t step_graph = nullptr;
   int step_bucket = 0;  // the graph's attention LDS covers positions < step_bucket
+  // chained greedy decode (ec_generate_greedy): steps whose token comes from
+  // the previous step's argmax on the device; ids collected in d_gen
+  hipGraphExec_t chain_graph = nullptr;
+  int chain_bucket = 0;
+  bool chaining = false;  // set while a chained step is enqueued or captured
+  int *d_gen = nullptr;
   int *h_amax = nullptr;  // pinned: the graphs' argmax outputs (batch_cap ids)
   // greedy decode steps of M tokens in distinct slots (kernel-per-op path),
   // one HIP graph per (M, 512-position bucket), oldest replaced first
@@ -680,13 +686,15 @@ static void free_dev(DevModel *d) {
   if (!d) return;
   void *ps[] = {d->arena, d->rope, d->d_tok, d->d_pos, d->d_slot, d->d_amax, d->x, d->h, d->qkv,
                 d->att, d->ff, d->aq, d->as, d->ah, d->ahs, d->att_sc, d->logits, d->kc, d->vc, d->cand, d->tk_cand,
-                d->tk_nan, d->tk_vals, d->tk_idx, d->tk_status, d->d_layers, d->xch, d->d_step_io, d->d_trace};
+                d->tk_nan, d->tk_vals, d->tk_idx, d->tk_status, d->d_layers, d->xch, d->d_step_io, d->d_trace,
+                d->d_gen};
   for (void *p : ps)
     if (p) (void)hipFree(p);
   if (d->h_stage) (void)hipHostFree(d->h_stage);
   if (d->h_amax) (void)hipHostFree(d->h_amax);
   if (d->h_step_io) (void)hipHostFree(d->h_step_io);
   if (d->step_graph) (void)hipGraphExecDestroy(d->step_graph);
+  if (d->chain_graph) (void)hipGraphExecDestroy(d->chain_graph);
   for (auto &dg : d->dec_graphs) (void)hipGraphExecDestroy(dg.exec);
   d->dec_graphs.clear();
   delete d;
@@ -1026,6 +1034,7 @@ static int load_impl(GPT2 *g, const char *path, int batch_cap, int max_ctx) {
     EC_HIP(hipMemset(d->d_step_io, 0, 8 * sizeof(int)));
     EC_HIP(hipHostMalloc((void **)&d->h_step_io, 8 * sizeof(int), hipHostMallocDefault));
     memset(d->h_step_io, 0, 8 * sizeof(int));
+    EC_HIP(hipMalloc(&d->d_gen, (size_t)d->eff_ctx * sizeof(int)));
     const char *tr = getenv("EDGECORE_STEP_TRACE");
     if (tr && !strcmp(tr, "1")) {
       const size_t tb = (size_t)kStepBlocks * Lc * kStepEvents * sizeof(unsigned long long);
@@ -1213,7 +1222,8 @@ static double step_bytes(const GPT2 *g, const DevModel *d, int npos) {
 static int enqueue_step(GPT2 *g, DevModel *d, int max_npos, hipStream_t s) {
   const int vtile = step_vtile(max_npos);
   if (vtile < 4) return set_err(-1, "decode step: position %d does not fit the LDS", max_npos - 1);
-  EC_HIP(hipMemcpyAsync(d->d_step_io, d->h_step_io, 4 * sizeof(int), hipMemcpyHostToDevice, s));
+  if (!d->chaining)  // a chained step's inputs were written by the previous step
+    EC_HIP(hipMemcpyAsync(d->d_step_io, d->h_step_io, 4 * sizeof(int), hipMemcpyHostToDevice, s));
   int *io = d->d_step_io;
   AttnArgs aa{};
   aa.kc = d->kc;
@@ -1416,7 +1426,9 @@ static int enqueue_forward(GPT2 *g, DevModel *d, int M, int lm_from, bool distin
     }
     d->last_lm_rows = rows;
   }
-  if (step)
+  if (step && d->chaining)
+    EC_HIP(step_advance(d->d_step_io, d->d_gen, s));
+  else if (step)
     EC_HIP(hipMemcpyAsync(d->h_step_io + 4, d->d_step_io + 4, 2 * sizeof(int), hipMemcpyDeviceToHost, s));
   else if (argmax && lm_from < M)
     EC_HIP(hipMemcpyAsync(argmax, d->d_amax, (size_t)(M - lm_from) * 4, hipMemcpyDeviceToHost, s));
@@ -1679,6 +1691,98 @@ extern "C" int ec_topk_dev_noalloc(const float *logits, int rows, int vocab, int
   if (e == hipSuccess) e = hipMemcpyAsync(status, ds, (size_t)rows * 4, hipMemcpyDeviceToHost, g_stream);
   if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
   if (e != hipSuccess) return set_err(-3, "ec_topk_dev_noalloc: %s", hipGetErrorString(e));
+  return 0;
+}
+
+// Greedy decode of n tokens in one slot: `token` at position `pos` gives
+// out[0], out[0] at pos + 1 gives out[1], and so on -- the ids of n greedy
+// gpt2_forward_ex steps.  With the persistent step the steps are chained on
+// the device: each step's argmax id becomes the next step's token (and the
+// position and tag advance) in a one-thread kernel, so the host launches the
+// n steps back to back and reads the ids once; one HIP graph per 512-position
+// bucket.  Otherwise (no persistent step for this model, or the profiler on)
+// one forward per token.
+extern "C" int ec_generate_greedy(GPT2 *g, int token, int pos, int slot, int n, int *out) {
+  EC_INIT();
+  DevModel *d = dev_of(g);
+  if (!d) return set_err(-1, "model not loaded");
+  if (!out || n < 1) return set_err(-1, "ec_generate_greedy: n=%d (at least 1) and an output array", n);
+  if (token < 0 || token >= g->vocab) return set_err(-1, "ec_generate_greedy: token %d outside [0, %d)", token, g->vocab);
+  if (pos < 0 || n > d->eff_ctx - pos)
+    return set_err(-1, "ec_generate_greedy: positions %d..%d outside [0, %d)", pos, pos + n - 1, d->eff_ctx);
+  if (slot < 0) return set_err(-1, "ec_generate_greedy: negative slot %d", slot);
+  if (slot >= g->batch_cap) slot = g->batch_cap - 1;  // as the forward (src/gpt2.c:512-513)
+  if (!d->step_ok || g_prof_on || step_vtile(pos + n) < 4) {
+    int t = token;
+    for (int k = 0; k < n; k++) {
+      const int p = pos + k;
+      const int r = forward_impl(g, &t, &p, &slot, 1, 0, nullptr, &out[k]);
+      if (r) return r;
+      t = out[k];
+    }
+    return 0;
+  }
+  hipStream_t s = g_stream;
+  if (d->step_tag > 0xFFFFFFFFu - (unsigned)n - 1u) {  // the tags below must not wrap: clear the old ones
+    EC_HIP(hipMemsetAsync(d->xch, 0, d->xch_bytes, s));
+    d->step_tag = 0;
+  }
+  int *io = d->h_step_io;
+  io[0] = token;
+  io[1] = pos;
+  io[2] = slot;
+  io[3] = (int)(d->step_tag + 1u);
+  io[4] = io[5] = io[6] = 0;
+  EC_HIP(hipMemcpyAsync(d->d_step_io, io, 7 * sizeof(int), hipMemcpyHostToDevice, s));
+  for (int k = 0; k < n; k++) {
+    const int max_npos = pos + k + 1;
+    int bucket = (max_npos + 511) / 512 * 512;
+    if (bucket > d->eff_ctx) bucket = d->eff_ctx;
+    bool graph = g_use_graphs && !d->step_nograph && step_vtile(bucket) >= 4;
+    if (graph && (!d->chain_graph || d->chain_bucket != bucket)) {
+      if (d->chain_graph) {
+        EC_HIP(hipGraphExecDestroy(d->chain_graph));
+        d->chain_graph = nullptr;
+      }
+      hipGraph_t gr = nullptr;
+      hipError_t e = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
+      int r = 0;
+      if (e == hipSuccess) {
+        d->chaining = true;
+        r = enqueue_forward(g, d, 1, 0, true, false, bucket, 0.0, nullptr, io + 5, nullptr, s, true);
+        d->chaining = false;
+        e = hipStreamEndCapture(s, &gr);
+      }
+      if (e == hipSuccess && r == 0) e = hipGraphInstantiate(&d->chain_graph, gr, nullptr, nullptr, 0);
+      if (gr) (void)hipGraphDestroy(gr);
+      if (e != hipSuccess || r != 0) {
+        (void)hipGetLastError();
+        g_err[0] = 0;
+        d->chain_graph = nullptr;
+        graph = false;
+      } else {
+        d->chain_bucket = bucket;
+      }
+    }
+    int r = 0;
+    if (graph) {
+      const hipError_t e = hipGraphLaunch(d->chain_graph, s);
+      if (e != hipSuccess) r = set_err(-3, "ec_generate_greedy: graph launch: %s", hipGetErrorString(e));
+    } else {
+      d->chaining = true;
+      r = enqueue_forward(g, d, 1, 0, true, false, max_npos, 0.0, nullptr, io + 5, nullptr, s, true);
+      d->chaining = false;
+    }
+    if (r) return r;
+  }
+  d->step_tag += (unsigned)n;
+  EC_HIP(hipMemcpyAsync(io + 4, d->d_step_io + 4, sizeof(int), hipMemcpyDeviceToHost, s));
+  EC_HIP(hipMemcpyAsync(out, d->d_gen, (size_t)n * sizeof(int), hipMemcpyDeviceToHost, s));
+  EC_HIP(hipStreamSynchronize(s));
+  if (io[4]) {
+    EC_HIP(hipMemset(d->d_step_io + 4, 0, sizeof(int)));
+    return set_err(-3, "ec_generate_greedy: a block's wait for another's results timed out (ids discarded)");
+  }
   return 0;
 }
 

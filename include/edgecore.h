@@ -336,6 +336,16 @@ int gpt2_forward_topk(GPT2 *g, const int *tokens, const int *positions, const in
 /* Largest top_k of gpt2_forward_topk / ec_topk_dev. */
 int ec_topk_max(void);
 
+/* Greedy decode of n tokens in slot `slot`: `token` at position `pos` gives
+ * out[0], out[0] at pos + 1 gives out[1], ... -- the ids of n single-token
+ * gpt2_forward_ex steps with argmax (the greedy branch of the reference's
+ * generation loop, src/runtime_main.c:338-348 with temp 0).  No counterpart in
+ * the reference, whose loop reads each id on the host: with the persistent
+ * decode step the steps are chained on the device (each argmax id becomes
+ * the next step's token there) and the ids come back once.  Positions
+ * pos..pos+n-1 must lie in the allocated context.  0 or <0. */
+int ec_generate_greedy(GPT2 *g, int token, int pos, int slot, int n, int *out);
+
 /* Row `row` (counted from lm_from, < the LM-head chunk of the last forward,
  * which holds at least batch_cap rows) of the last forward's logits, into out
  * [vocab] (host).  0 or <0. */

@@ -93,3 +93,47 @@ def test_step_short_context(step_model):
     lg_s, ids_s, _ = _decode(step_model, prompt, 12, True)
     lg_k, ids_k, _ = _decode(step_model, prompt, 12, False)
     assert ids_s == ids_k and np.array_equal(lg_s.view(np.uint32), lg_k.view(np.uint32))
+
+
+def _load(path, ctx, step_on):
+    old = os.environ.get("EDGECORE_STEP")
+    os.environ["EDGECORE_STEP"] = "1" if step_on else "0"
+    try:
+        return ec.Model(path, 1, ctx)
+    finally:
+        if old is None:
+            del os.environ["EDGECORE_STEP"]
+        else:
+            os.environ["EDGECORE_STEP"] = old
+
+
+def test_generate_greedy_equals_step_loop(step_model):
+    """ec_generate_greedy (steps chained on the device, one HIP graph per
+    512-position bucket) gives the ids of the host-driven greedy loop, across
+    the 512-position boundary; in two calls (the second continuing from the
+    first's last id); then a host-driven step after it; and through the
+    kernel-per-op fallback (no persistent step)."""
+    prompt = prompt_ids(505, V, seed=7)
+    n = len(prompt)
+    _, ids_s, _ = _decode(step_model, prompt, 26, True)
+    for step_on in (True, False):
+        with _load(step_model, n + 26 + 8, step_on) as m:
+            m.kv_reset()
+            m.forward(prompt, np.arange(n), np.zeros(n, np.int32), lm_from=n, want_logits=False)
+            ids = m.generate_greedy(int(prompt[-1]), n, 0, 26)
+            assert [int(x) for x in ids] == ids_s, step_on
+            m.kv_reset()
+            m.forward(prompt, np.arange(n), np.zeros(n, np.int32), lm_from=n, want_logits=False)
+            a = m.generate_greedy(int(prompt[-1]), n, 0, 10)
+            b = m.generate_greedy(int(a[-1]), n + 10, 0, 15)
+            _, am = m.forward([int(b[-1])], [n + 25], None, want_logits=False, want_argmax=True)
+            assert [int(x) for x in a] + [int(x) for x in b] + [int(am[0])] == ids_s, step_on
+
+
+def test_generate_greedy_rejects_bad_arguments(step_model):
+    with _load(step_model, 64, True) as m:
+        for args in ((V, 0, 0, 4), (-1, 0, 0, 4), (5, 60, 0, 8), (5, -1, 0, 2), (5, 0, -1, 2)):
+            with pytest.raises(ec.EdgeCoreError):
+                m.generate_greedy(*args)
+        with pytest.raises(ec.EdgeCoreError):
+            m.generate_greedy(5, 0, 0, 0)

@@ -461,12 +461,14 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepArgs a) {
   }
 }
 
-hipError_t decode_step(const StepArgs &a, size_t lds, hipStream_t s) {
+hipError_t decode_step(const StepArgs &a, size_t lds, bool cooperative, hipStream_t s) {
   StepArgs args = a;
   void *kargs[] = {&args};
   const void *k = a.trace ? reinterpret_cast<const void *>(decode_step_kernel<true>)
                           : reinterpret_cast<const void *>(decode_step_kernel<false>);
-  return hipLaunchCooperativeKernel(k, dim3(kStepBlocks), dim3(kStepThreads), kargs, (unsigned)lds, s);
+  if (cooperative)
+    return hipLaunchCooperativeKernel(k, dim3(kStepBlocks), dim3(kStepThreads), kargs, (unsigned)lds, s);
+  return hipLaunchKernel(k, dim3(kStepBlocks), dim3(kStepThreads), kargs, (unsigned)lds, s);
 }
 
 }  // namespace ec

@@ -252,7 +252,10 @@ struct StepArgs {
   AttnArgs attn;
 };
 size_t decode_step_scratch_bytes(int E, int F);
-hipError_t decode_step(const StepArgs &a, size_t lds, hipStream_t s);
+// cooperative: a cooperative launch (every block resident by contract);
+// otherwise a plain launch of the same kStepBlocks blocks, one per CU, which the
+// step's bounded waits turn into a reported error if a block never ran
+hipError_t decode_step(const StepArgs &a, size_t lds, bool cooperative, hipStream_t s);
 // Prefill attention (attn_prefill.hip): the M tokens are one slot's run of
 // consecutive positions whose k / v are already in the cache (fuse_kv 0);
 // blocks of 16, 8 or 4 tokens per head.  _ok: head_dim 32/64/128, q rows

@@ -45,6 +45,14 @@ static hipEvent_t g_touch_ev[4] = {};
 static unsigned g_touch_i = 0;
 static unsigned *g_touch_sink = nullptr;
 static bool g_touch = true;
+// the persistent decode step: a plain launch of one block per CU (no
+// cooperative-launch barriers: ~30 us less per step) until a step reports a
+// timed-out wait (a block that never became resident), then cooperative
+// launches from there on, the failed step redone (EDGECORE_STEP_COOP=1:
+// cooperative from the start).  EDGECORE_STEP_TEST_FAIL=1 makes the first
+// plain step report a timeout (tests of the switch).
+static bool g_step_coop = false;
+static bool g_step_test_fail = false;
 static int g_touch_blocks = 8;  // one per XCD; a multiple of 8 (EDGECORE_TOUCH_BLOCKS)
 constexpr int kTouchMinRows = 1024;  // prompts at least this long
 static hipDeviceProp_t g_prop;
@@ -105,6 +113,10 @@ extern "C" int ec_init(void) {
   EC_HIP(hipMalloc(&g_touch_sink, 256));
   const char *tch = getenv("EDGECORE_TOUCH");
   g_touch = !(tch && !strcmp(tch, "0"));
+  const char *sc = getenv("EDGECORE_STEP_COOP");
+  g_step_coop = sc && !strcmp(sc, "1");
+  const char *sf = getenv("EDGECORE_STEP_TEST_FAIL");
+  g_step_test_fail = sf && !strcmp(sf, "1");
   const char *tb = getenv("EDGECORE_TOUCH_BLOCKS");
   if (tb && atoi(tb) >= 8) g_touch_blocks = atoi(tb) / 8 * 8;
   const char *gr = getenv("EDGECORE_GRAPHS");
@@ -1254,7 +1266,7 @@ static int enqueue_step(GPT2 *g, DevModel *d, int max_npos, hipStream_t s) {
   hipEvent_t e0 = g_launch_ev[0], e1 = g_launch_ev[1];
   g_launch_ev[0] = g_launch_ev[1] = nullptr;
   if (e0) EC_HIP(hipEventRecord(e0, s));
-  const hipError_t e = decode_step(sa, lds, s);
+  const hipError_t e = decode_step(sa, lds, g_step_coop, s);
   if (e0 && e == hipSuccess) EC_HIP(hipEventRecord(e1, s));
   if (e != hipSuccess) {
     if (p_ >= 0) {
@@ -1435,6 +1447,30 @@ static int enqueue_forward(GPT2 *g, DevModel *d, int M, int lm_from, bool distin
   return 0;
 }
 
+// After a step whose waits timed out: clear the flag; if the step ran as a
+// plain launch, switch to cooperative launches (captured graphs dropped) and
+// return 1 (redo the step), else 0 (a real failure)
+static int step_timed_out(DevModel *d) {
+  int *io = d->h_step_io;
+  io[4] = 0;
+  if (hipMemset(d->d_step_io + 4, 0, sizeof(int)) != hipSuccess) return 0;
+  if (g_step_coop) return 0;
+  g_step_coop = true;
+  if (d->step_graph) (void)hipGraphExecDestroy(d->step_graph);
+  if (d->chain_graph) (void)hipGraphExecDestroy(d->chain_graph);
+  d->step_graph = d->chain_graph = nullptr;
+  d->step_bucket = d->chain_bucket = 0;
+  fprintf(stderr, "edgecore: a decode step's blocks were not all resident; cooperative launches from now on\n");
+  return 1;
+}
+
+// the host-side stand-in for a timed-out plain step (EDGECORE_STEP_TEST_FAIL=1)
+static bool step_test_fail() {
+  if (!g_step_test_fail || g_step_coop) return false;
+  g_step_test_fail = false;
+  return true;
+}
+
 static int forward_impl(GPT2 *g, const int *tokens, const int *positions, const int *seqs, int M,
                         int lm_from, float *logits, int *argmax, const TopkReq *tk = nullptr) {
   EC_INIT();
@@ -1543,8 +1579,8 @@ static int forward_impl(GPT2 *g, const int *tokens, const int *positions, const 
       if (r) return r;
     }
     EC_HIP(hipStreamSynchronize(s));
-    if (io[4]) {
-      EC_HIP(hipMemset(d->d_step_io + 4, 0, sizeof(int)));
+    if (io[4] || step_test_fail()) {
+      if (step_timed_out(d)) return forward_impl(g, tokens, positions, seqs, M, lm_from, logits, argmax, tk);
       return set_err(-3, "decode step: a block's wait for another's results timed out (results discarded)");
     }
     if (argmax) argmax[0] = io[5];
@@ -1779,8 +1815,8 @@ extern "C" int ec_generate_greedy(GPT2 *g, int token, int pos, int slot, int n, 
   EC_HIP(hipMemcpyAsync(io + 4, d->d_step_io + 4, sizeof(int), hipMemcpyDeviceToHost, s));
   EC_HIP(hipMemcpyAsync(out, d->d_gen, (size_t)n * sizeof(int), hipMemcpyDeviceToHost, s));
   EC_HIP(hipStreamSynchronize(s));
-  if (io[4]) {
-    EC_HIP(hipMemset(d->d_step_io + 4, 0, sizeof(int)));
+  if (io[4] || step_test_fail()) {
+    if (step_timed_out(d)) return ec_generate_greedy(g, token, pos, slot, n, out);
     return set_err(-3, "ec_generate_greedy: a block's wait for another's results timed out (ids discarded)");
   }
   return 0;

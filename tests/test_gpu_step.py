@@ -137,3 +137,56 @@ def test_generate_greedy_rejects_bad_arguments(step_model):
                 m.generate_greedy(*args)
         with pytest.raises(ec.EdgeCoreError):
             m.generate_greedy(5, 0, 0, 0)
+
+
+_CHILD = r"""
+import json, sys
+import numpy as np
+import edgecore_amd as ec
+from tests.conftest import prompt_ids
+path, mode = sys.argv[1], sys.argv[2]
+prompt = prompt_ids(300, 151936, seed=11)
+n = len(prompt)
+with ec.Model(path, 1, n + 40) as m:
+    m.kv_reset()
+    m.forward(prompt, np.arange(n), np.zeros(n, np.int32), lm_from=n, want_logits=False)
+    if mode == "chain":
+        ids = [int(x) for x in m.generate_greedy(int(prompt[-1]), n, 0, 24)]
+    else:
+        cur, ids = int(prompt[-1]), []
+        for k in range(24):
+            _, am = m.forward([cur], [n + k], None, want_logits=False, want_argmax=True)
+            cur = int(am[0])
+            ids.append(cur)
+print(json.dumps(ids))
+"""
+
+
+def _child_ids(path, mode, env):
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    root = Path(__file__).resolve().parents[1]
+    e = dict(os.environ)
+    e.update(env)
+    r = subprocess.run([sys.executable, "-c", _CHILD, str(path), mode], cwd=root, env=e, capture_output=True,
+                       text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-2000:]
+    return json.loads(r.stdout.strip().splitlines()[-1]), r.stderr
+
+
+def test_step_launch_modes_and_timeout_switch(step_model):
+    """The persistent step as a plain launch (the default) and as a
+    cooperative launch give the same ids, host-driven and chained; and a step
+    that reports a timed-out wait while plain (forced from the host) switches
+    the library to cooperative launches and is redone with the same result."""
+    plain, _ = _child_ids(step_model, "loop", {})
+    coop, _ = _child_ids(step_model, "loop", {"EDGECORE_STEP_COOP": "1"})
+    chain, _ = _child_ids(step_model, "chain", {})
+    chain_coop, _ = _child_ids(step_model, "chain", {"EDGECORE_STEP_COOP": "1"})
+    assert plain == coop == chain == chain_coop
+    for mode in ("loop", "chain"):
+        ids, err = _child_ids(step_model, mode, {"EDGECORE_STEP_TEST_FAIL": "1"})
+        assert ids == plain, mode
+        assert "cooperative launches from now on" in err, (mode, err[-500:])

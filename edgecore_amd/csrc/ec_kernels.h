@@ -296,9 +296,11 @@ hipError_t argmax_rows_chunked(const float *logits, int rows, int V, unsigned lo
 // the chunked form's first launch alone; returns the chunk count in *nc
 hipError_t argmax_chunks(const float *logits, int rows, int V, unsigned long long *cand, int cap, int *nc,
                          hipStream_t st);
-// final reduction of the LM head's per-block argmax candidates
+// final reduction of the LM head's per-block argmax candidates; with
+// chain_io (one row), also step_advance's work on chain_io / chain_out
 hipError_t argmax_finalize(const unsigned long long *cand, int ncand, const float *logits,
-                           int ldl, int rows, int *out, hipStream_t st);
+                           int ldl, int rows, int *out, hipStream_t st, int *chain_io = nullptr,
+                           int *chain_out = nullptr);
 
 // top_k + 1 largest logits per row for sampling (topk.hip).  topk_select sorts
 // chunks of 4096 logits into cand [rows][topk_chunks(V)][top_k + 1] keys and

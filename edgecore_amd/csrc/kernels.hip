@@ -307,7 +307,8 @@ __global__ __launch_bounds__(256) void argmax_chunk_kernel(const float *L, int V
 // argmax over the LM head's per-block candidates; logits[0] NaN -> 0 and no
 // non-NaN logit -> 0, like the reference's strict '>' scan from index 0
 __global__ __launch_bounds__(256) void argmax_finalize_kernel(const unsigned long long *cand, int ncand,
-                                                              const float *logits, int ldl, int *out) {
+                                                              const float *logits, int ldl, int *out,
+                                                              int *chain_io, int *chain_out) {
   __shared__ unsigned long long red[4];
   const int r = blockIdx.x;
   unsigned long long b = 0ull;
@@ -321,7 +322,15 @@ __global__ __launch_bounds__(256) void argmax_finalize_kernel(const unsigned lon
   if (threadIdx.x == 0) {
     for (int w = 1; w < 4; w++) b = red[w] > b ? red[w] : b;
     const float l0 = logits[(size_t)r * ldl];
-    out[r] = (l0 != l0 || b == 0ull) ? 0 : (int)(0xFFFFFFFFu - (uint32_t)(b & 0xFFFFFFFFull));
+    const int id = (l0 != l0 || b == 0ull) ? 0 : (int)(0xFFFFFFFFu - (uint32_t)(b & 0xFFFFFFFFull));
+    out[r] = id;
+    if (chain_io) {  // a chained greedy step (one row): step_advance_kernel's work
+      chain_out[chain_io[6]] = id;
+      chain_io[6] = chain_io[6] + 1;
+      chain_io[0] = id;
+      chain_io[1] = chain_io[1] + 1;
+      chain_io[3] = (int)((unsigned)chain_io[3] + 1u);
+    }
   }
 }
 
@@ -747,8 +756,9 @@ hipError_t attention_after_scores(const AttnArgs &a, hipStream_t st) {
 }
 
 hipError_t argmax_finalize(const unsigned long long *cand, int ncand, const float *logits, int ldl, int rows,
-                           int *out, hipStream_t st) {
-  klaunch(argmax_finalize_kernel, dim3(rows), dim3(256), 0, st, cand, ncand, logits, ldl, out);
+                           int *out, hipStream_t st, int *chain_io, int *chain_out) {
+  if (chain_io && (rows != 1 || !chain_out)) return hipErrorInvalidValue;
+  klaunch(argmax_finalize_kernel, dim3(rows), dim3(256), 0, st, cand, ncand, logits, ldl, out, chain_io, chain_out);
   return hipGetLastError();
 }
 

@@ -1400,6 +1400,7 @@ static int enqueue_forward(GPT2 *g, DevModel *d, int M, int lm_from, bool distin
   // greedy ids from per-block argmax candidates
   const int lwt = bf16 ? WT_BF16 : WT_F16;
   int *amax_dev = step ? d->d_step_io + 5 : d->d_amax;  // a step's id goes out with its error flag
+  bool advanced = false;  // a chained step's inputs were advanced by the argmax launch
   for (int r0 = lm_from; r0 < M; r0 += d->lm_rows) {
     const int rows = M - r0 < d->lm_rows ? M - r0 : d->lm_rows;
     GemvArgs a{d->x + (size_t)r0 * E, E, nullptr, g->lnf_g, g->lnf_b, g->eps, d->lm, nullptr, nullptr, nullptr,
@@ -1413,9 +1414,13 @@ static int enqueue_forward(GPT2 *g, DevModel *d, int M, int lm_from, bool distin
     if ((r = linear(g, d, "gemv_lmhead", a, lwt, EPI_STORE, pro_norm, s))) return r;
     if (argmax) {
       if (fused) {
+        // a chained step advances its inputs in the same launch
+        const bool adv = step && d->chaining;
         EC_LAUNCH("argmax", 8.0 * rows * gemv_grid_x(a, lwt, EPI_STORE),
                   argmax_finalize(d->cand, gemv_grid_x(a, lwt, EPI_STORE), d->logits, V, rows,
-                                  amax_dev + (r0 - lm_from), s));
+                                  amax_dev + (r0 - lm_from), s, adv ? d->d_step_io : nullptr,
+                                  adv ? d->d_gen : nullptr));
+        if (adv) advanced = true;
       } else {
         int nc = 0;
         EC_LAUNCH("argmax_chunks", 4.0 * rows * V, argmax_chunks(d->logits, rows, V, d->cand, d->ncand, &nc, s));
@@ -1438,7 +1443,7 @@ static int enqueue_forward(GPT2 *g, DevModel *d, int M, int lm_from, bool distin
     }
     d->last_lm_rows = rows;
   }
-  if (step && d->chaining)
+  if (step && d->chaining && !advanced)
     EC_HIP(step_advance(d->d_step_io, d->d_gen, s));
   else if (step)
     EC_HIP(hipMemcpyAsync(d->h_step_io + 4, d->d_step_io + 4, 2 * sizeof(int), hipMemcpyDeviceToHost, s));

@@ -10,29 +10,30 @@
 // its phase's weight loads before it waits for the words of its input, so
 // the weight stream overlaps the wait instead of following it.
 //
-// Grid: kStepBlocks blocks of kStepThreads threads, one per CU (cooperative
-// launch: all blocks are resident, so the waits can be satisfied).  Block b
-// runs on XCD b % 8.  Per layer:
+// Grid: kStepBlocks blocks of kStepThreads threads, one per CU (a plain
+// launch on an idle device, or a cooperative one: all blocks resident, so the
+// waits can be satisfied).  Block b runs on XCD b % 8.  Per layer:
 //
-//   A  (attention blocks: query head h, element slice s; 4 per head, the
+//   A  (56 attention blocks: query head h, element slice s; 4 per head, the
 //      heads of KV group g on XCD g) -- wait for x; RMSNorm + int8 quantize
 //      (ln1); the 64 q rows of head h and the 64 + 64 k / v rows of group g
 //      (int8 dot, fp32 epilogue) into LDS; then the decode attention body
 //      (attn_decode.h: RoPE, fp16 KV append, scores, softmax, p*v sums);
 //      publish the slice of the attention output.
-//   O  (every block, rows [b N / NB, (b+1) N / NB) of 896) -- wait for the
-//      attention output; quantize; o rows; x_mid = x + o (residual).
-//   G  (every block, 19 gate/up row pairs) -- wait for x_mid; RMSNorm (ln2)
-//      + quantize; gate and up rows; silu(g) * u.
-//   D  (every block, the same rows as O) -- wait for the FFN activation;
-//      quantize; down rows; x = x_mid + d.
+//   O  (E / 16 o / down blocks, 16 rows each) -- wait for the attention
+//      output; quantize; o rows; x_mid = x + o (residual).
+//   G  (ceil(F / 64) gate/up blocks, up to 64 row pairs each) -- wait for
+//      x_mid; RMSNorm (ln2) + quantize; gate and up rows; silu(g) * u.
+//   D  (the o / down blocks, the same rows as O) -- wait for the FFN
+//      activation; quantize; down rows; x = x_mid + d.
 //
-// A block's O rows are its D rows, so both residuals use values the block
-// itself produced.  Every arithmetic step is the separate kernels': the
-// norms accumulate in double in the decode GEMV's wave order (lane l holds
-// elements 4l + 256j), the activation codes depend only on the row maximum,
-// int8 dots are exact int32, and the epilogues are the same device functions
-// -- so the step's results are bit-identical to the kernel-per-op path.
+// An o / down block's O rows are its D rows, so both residuals use values
+// the block itself produced.  Every arithmetic step is the separate kernels':
+// the norms accumulate in double in the decode GEMV's wave order (lane l
+// holds elements 4l + 256j), the activation codes depend only on the row
+// maximum, int8 dots are exact int32, and the epilogues are the same device
+// functions -- so the step's results are bit-identical to the kernel-per-op
+// path.
 //
 // A wait is bounded: past kSpin polls the block sets *err and goes on, and
 // every other waiting block sees *err within 64 polls and gives up too; the
@@ -48,14 +49,12 @@ namespace {
 
 constexpr int kSpin = 1 << 18;  // polls before a wait gives up (~0.3 s)
 constexpr int kNW = kStepThreads / 64;  // waves per block
+constexpr int kODRows = 2 * kNW;          // o / down rows per o / down block (two down rows per wave)
+constexpr int kFMax = 5120;               // largest FFN width
 
 __device__ __forceinline__ void put_word(unsigned long long *p, float v, unsigned tag) {
   __hip_atomic_store(p, ((unsigned long long)tag << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
                      __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ unsigned long long get_word(const unsigned long long *p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // The layers' pointers come from a table in memory, so the compiler cannot
@@ -72,28 +71,59 @@ __device__ __forceinline__ gptr<T> gbl(const T *p) {
 __device__ __forceinline__ gptr<v4i> gbl16(const void *p) { return (gptr<v4i>)p; }
 
 
-// Wait until words [0, n) of buf carry `tag` and put their values into dst
-// (LDS).  Thread t owns words t + kStepThreads * j (j < WMAX); its loads are
-// issued together and reissued only for the words still missing.  Every
-// thread of the block calls it; it starts with a barrier (dst is still being
-// read by the previous phase) and ends with one.
-template <int WMAX>
-__device__ void gather(const unsigned long long *buf, int n, unsigned tag, float *dst, int *err) {
+// TRACE: thread 0 of every block records s_memrealtime (100 MHz) at each
+// phase boundary into a.trace[block][layer][kStepEvents]
+template <bool TRACE>
+__device__ __forceinline__ void mark(const StepArgs &a, int b, int l, int e) {
+  if (TRACE && threadIdx.x == 0) a.trace[((size_t)b * a.L + l) * kStepEvents + e] = __builtin_amdgcn_s_memrealtime();
+}
+
+// The exchange words are read in pairs, each pair with one 16-byte
+// device-coherent load (n even, buf 16-byte aligned): a block reads 16 bytes
+// per load instead of 8, and the exchanges' time grows with the bytes all
+// waiting blocks read.  Each word is still written by one 8-byte store, so
+// each half of a pair is one consistent (value, tag) snapshot.
+// (buf and n are block-uniform; readfirstlane puts the descriptor in scalar
+// registers, or the compiler wraps every load in a loop over distinct
+// descriptors)
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t xch_rsrc(const unsigned long long *buf, int n) {
+  const uint64_t v = (uint64_t)(uintptr_t)buf;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  void *p = (void *)(uintptr_t)(((uint64_t)hi << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(p, 0, __builtin_amdgcn_readfirstlane(n * 8),
+                                           0x00020000);
+}
+__device__ __forceinline__ v4u get_pair(__amdgpu_buffer_rsrc_t r, int p) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, p * 16, 0, 16 /* sc1: device-coherent */);
+}
+
+// Wait until words [0, n) of buf carry `tag`; thread t owns the pairs
+// p = t + kStepThreads * j (j < WP), words 2p and 2p + 1, and receives their
+// values in x[j].  The loads are issued together and reissued only for the
+// pairs still missing.  Returns the pairs received (bit j); a pair missing
+// after a timed-out wait reads as zeros.
+template <int WP>
+__device__ __forceinline__ unsigned wait_pairs(const unsigned long long *buf, int n, unsigned tag, float (&x)[WP][2],
+                                               int *err) {
   const int t = threadIdx.x;
-  __syncthreads();
+  const __amdgpu_buffer_rsrc_t rs = xch_rsrc(buf, n);
   unsigned pending = 0;
 #pragma unroll
-  for (int j = 0; j < WMAX; j++)
-    if (t + kStepThreads * j < n) pending |= 1u << j;
-  unsigned long long v[WMAX];
+  for (int j = 0; j < WP; j++) {
+    x[j][0] = x[j][1] = 0.0f;
+    if (t + kStepThreads * j < (n >> 1)) pending |= 1u << j;
+  }
+  const unsigned own = pending;
+  v4u v[WP];
   for (int it = 0; pending; it++) {
 #pragma unroll
-    for (int j = 0; j < WMAX; j++)
-      if ((pending >> j) & 1u) v[j] = get_word(buf + t + kStepThreads * j);
+    for (int j = 0; j < WP; j++)
+      if ((pending >> j) & 1u) v[j] = get_pair(rs, t + kStepThreads * j);
 #pragma unroll
-    for (int j = 0; j < WMAX; j++) {
-      if (((pending >> j) & 1u) && (unsigned)(v[j] >> 32) == tag) {
-        dst[t + kStepThreads * j] = __uint_as_float((unsigned)v[j]);
+    for (int j = 0; j < WP; j++) {
+      if (((pending >> j) & 1u) && v[j].y == tag && v[j].w == tag) {
+        x[j][0] = __uint_as_float(v[j].x);
+        x[j][1] = __uint_as_float(v[j].z);
         pending &= ~(1u << j);
       }
     }
@@ -105,57 +135,60 @@ __device__ void gather(const unsigned long long *buf, int n, unsigned tag, float
     if ((it & 63) == 63 && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) break;
     __builtin_amdgcn_s_sleep(1);
   }
+  return own;
+}
+
+// Wait for words [0, n) of buf and put their values into dst (LDS).  Every
+// thread of the block calls it; it starts with a barrier (dst is still being
+// read by the previous phase) and ends with one.
+template <int WP>
+__device__ void gather(const unsigned long long *buf, int n, unsigned tag, float *dst, int *err) {
+  const int t = threadIdx.x;
+  __syncthreads();
+  float x[WP][2];
+  const unsigned own = wait_pairs<WP>(buf, n, tag, x, err);
+#pragma unroll
+  for (int j = 0; j < WP; j++)
+    if ((own >> j) & 1u) *reinterpret_cast<float2 *>(dst + 2 * (t + kStepThreads * j)) = make_float2(x[j][0], x[j][1]);
   __syncthreads();
 }
 
 // gather's wait, then the int8 quantization of the words (src/gpt2.c:446-461)
 // straight from the registers that received them: the row maximum over the
 // block, then each thread's codes into codes[] (LDS).  Returns the scale.
-template <int WMAX>
+// TRACE: event ev of layer l is recorded once every thread has its words.
+template <int WP, bool TRACE = false>
 __device__ float gather_quant(const unsigned long long *buf, int n, unsigned tag, int8_t *codes, float *red,
-                              int *err) {
+                              int *err, const StepArgs *ta = nullptr, int l = 0, int ev = 0) {
   const int t = threadIdx.x;
   __syncthreads();  // codes are still read by the previous phase
-  unsigned pending = 0;
-#pragma unroll
-  for (int j = 0; j < WMAX; j++)
-    if (t + kStepThreads * j < n) pending |= 1u << j;
-  const unsigned own = pending;
-  unsigned long long v[WMAX];
-  float x[WMAX];
-  for (int it = 0; pending; it++) {
-#pragma unroll
-    for (int j = 0; j < WMAX; j++)
-      if ((pending >> j) & 1u) v[j] = get_word(buf + t + kStepThreads * j);
-#pragma unroll
-    for (int j = 0; j < WMAX; j++) {
-      if (((pending >> j) & 1u) && (unsigned)(v[j] >> 32) == tag) {
-        x[j] = __uint_as_float((unsigned)v[j]);
-        pending &= ~(1u << j);
-      }
-    }
-    if (!pending) break;
-    if (it >= kSpin) {
-      atomicOr(err, 1);
-      break;
-    }
-    if ((it & 63) == 63 && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) break;
-    __builtin_amdgcn_s_sleep(1);
+  float x[WP][2];
+  const unsigned own = wait_pairs<WP>(buf, n, tag, x, err);
+  if constexpr (TRACE) {
+    __syncthreads();
+    mark<true>(*ta, blockIdx.x, l, ev);
   }
   float mx = 0.0f;
 #pragma unroll
-  for (int j = 0; j < WMAX; j++) {
-    if (!((own >> j) & 1u)) continue;
-    if ((pending >> j) & 1u) x[j] = 0.0f;  // a timed-out wait (results discarded)
-    mx = fmaxf(mx, fabsf(x[j]));
-  }
+  for (int j = 0; j < WP; j++) mx = fmaxf(mx, fmaxf(fabsf(x[j][0]), fabsf(x[j][1])));
   mx = block_max_1b<kNW>(mx, red);
   const float sc = quant_scale(mx);
-  const bool fast = ec_quant_rcp_ok(sc);
-  const float rcp = 1.0f / sc;
+  auto put = [&](auto q1) {
 #pragma unroll
-  for (int j = 0; j < WMAX; j++)
-    if ((own >> j) & 1u) codes[t + kStepThreads * j] = fast ? ec_quant1_rcp(x[j], sc, rcp) : quant1(x[j], sc);
+    for (int j = 0; j < WP; j++) {
+      if (!((own >> j) & 1u)) continue;
+      const int8_t c0 = q1(x[j][0]), c1 = q1(x[j][1]);
+      *reinterpret_cast<uint16_t *>(codes + 2 * (t + kStepThreads * j)) =
+          (uint16_t)((uint8_t)c0 | ((unsigned)(uint8_t)c1 << 8));
+    }
+  };
+  // one branch per block (sc is uniform), not a select per element
+  if (ec_quant_rcp_ok(sc)) {
+    const float rcp = 1.0f / sc;
+    put([&](float v) { return ec_quant1_rcp(v, sc, rcp); });
+  } else {
+    put([&](float v) { return quant1(v, sc); });
+  }
   __syncthreads();
   return sc;
 }
@@ -167,6 +200,15 @@ __device__ __forceinline__ int sum8(int v) {
   v = v + dpp_mov<0x4E>(v);   // quad_perm [2,3,0,1]
   v = v + dpp_mov<0x141>(v);  // row_half_mirror
   return v;
+}
+
+// 16 int8 products of a weight chunk against the activation chunk x
+__device__ __forceinline__ int dot16x(int s, v4i w, v4i x) {
+  s = __builtin_amdgcn_sdot4(x.x, w.x, s, false);
+  s = __builtin_amdgcn_sdot4(x.y, w.y, s, false);
+  s = __builtin_amdgcn_sdot4(x.z, w.z, s, false);
+  s = __builtin_amdgcn_sdot4(x.w, w.w, s, false);
+  return s;
 }
 
 // 16 int8 products of a weight chunk against the activation chunk at q
@@ -243,12 +285,6 @@ __device__ float block_norm_quant(const float *xs, int K, const float *g, double
   return sc;
 }
 
-// TRACE: thread 0 of every block records s_memrealtime (100 MHz) at each
-// phase boundary into a.trace[block][layer][kStepEvents]
-template <bool TRACE>
-__device__ __forceinline__ void mark(const StepArgs &a, int b, int l, int e) {
-  if (TRACE && threadIdx.x == 0) a.trace[((size_t)b * a.L + l) * kStepEvents + e] = __builtin_amdgcn_s_memrealtime();
-}
 
 // The attention blocks' loop: per layer, the q/k/v rows of the head (weights
 // loaded into registers one layer ahead, during the GEMV blocks' phases) and
@@ -289,7 +325,7 @@ __device__ void attention_loop(const StepArgs &a, int head, int slice, unsigned 
       for (int i = t; i < E; i += kStepThreads) xs[i] = h2f(gbl(a.wte)[(size_t)tok * E + i]);
       __syncthreads();
     } else {
-      gather<2>(a.xch + (size_t)(l - 1) * S, E, tag, xs, a.err);
+      gather<1>(a.xch + (size_t)(l - 1) * S, E, tag, xs, a.err);
     }
     mark<TRACE>(a, b, l, 1);
     const float sx = block_norm_quant(xs, E, gam, a.eps, codes, red);
@@ -305,9 +341,10 @@ __device__ void attention_loop(const StepArgs &a, int head, int slice, unsigned 
     __syncthreads();
     mark<TRACE>(a, b, l, 2);
     const int hh = uniform_opaque(head), ss = uniform_opaque(slice);
-    unsigned long long *orow = a.xch + (size_t)l * S + 2 * E + hh * 64 + 16 * ss;
+    unsigned long long *att = a.xch + (size_t)l * S + 2 * E;
+    const int o0 = hh * 64 + 16 * ss;
     attn_decode_block<64, true, kStepSlices>(a.attn, 0, hh, ss, qkv_s, qkv_s + 64, qkv_s + 128, lds,
-                                             [&](int i, float o) { put_word(orow + i, o, tag); },
+                                             [&](int i, float o) { put_word(att + o0 + i, o, tag); },
                                              a.kv_layer * l);
     __syncthreads();  // the body's LDS is reused by the next layer
     mark<TRACE>(a, b, l, 3);
@@ -325,60 +362,48 @@ __device__ void attention_loop(const StepArgs &a, int head, int slice, unsigned 
   if (sink == 0x7fffffff && tag == 0) red[0] = (float)sink;  // keeps the touches (tag is never 0)
 }
 
-// The GEMV blocks' loop (block gi of ng): per layer the o rows [r0, r1) of E
-// with the residual, the gate/up rows [g0, g1) of F with the SiLU gating,
-// and the down rows [r0, r1) with the residual.
+// The o / down blocks' loop (block gi): per layer the o rows [r0, r0 + kODRows)
+// of E with the residual, then the down rows of the same indices with the
+// residual.  Their weights (one 8-lane group per o row, one wave per two down
+// rows) are loaded at the start of the layer, while the attention runs.
 template <bool TRACE>
-__device__ void gemv_loop(const StepArgs &a, int gi, int ng, unsigned tag, int tok, float *lds, float *xown,
-                          float *xmown, float *red, uint64_t *etab) {
+__device__ void od_loop(const StepArgs &a, int gi, unsigned tag, int tok, float *lds, float *xown, float *xmown,
+                        float *red) {
   const int b = blockIdx.x;
   const int E = a.E, F = a.F;
   const size_t S = (size_t)3 * E + F;
-  float *xs = lds;
   int8_t *codes = reinterpret_cast<int8_t *>(lds + (E > F ? E : F));
-  {
-    const int r0 = gi * E / ng, r1 = (gi + 1) * E / ng;
-    if ((int)threadIdx.x < r1 - r0) xown[threadIdx.x] = h2f(gbl(a.wte)[(size_t)tok * E + r0 + threadIdx.x]);
-  }
+  if ((int)threadIdx.x < kODRows) xown[threadIdx.x] = h2f(gbl(a.wte)[(size_t)tok * E + gi * kODRows + threadIdx.x]);
   for (int l = 0; l < a.L; l++) {
     const StepLayer &W = a.layers[l];
     mark<TRACE>(a, b, l, 0);
     unsigned long long *X = a.xch + (size_t)l * S, *XM = X + E, *ATT = X + 2 * E, *FF = X + 3 * E;
     const int t = tid_opaque(), lane = t & 63, wave = t >> 6;
     const int grp = t >> 3, sub = t & 7;  // 64 row groups of 8 lanes (rows of E int8)
-    const int g = uniform_opaque(gi);
-    const int r0 = g * E / ng, r1 = (g + 1) * E / ng;  // o / down rows
-    const int g0 = g * F / ng, g1 = (g + 1) * F / ng;  // gate/up rows
-
-    // every weight of the layer's three phases, loaded while the attention
-    // blocks run (the block waits for nothing else meanwhile): the o rows,
-    // the gate/up rows and the down rows (one wave per row), with scales
-    const bool on_o = grp < r1 - r0, on_g = grp < g1 - g0, on_d = wave < r1 - r0;
-    const int no = r0 + (on_o ? grp : 0), ngt = g0 + (on_g ? grp : 0), nd = r0 + (on_d ? wave : 0);
+    const int r0 = uniform_opaque(gi) * kODRows;
+    const bool on_o = grp < kODRows;
+    const int no = r0 + (on_o ? grp : 0);
     const int nch = F / 16;
     constexpr int CD = 5;  // down chunks per lane (F <= 5120)
-    v4i wo[7], wg[7], wu[7], wd[CD];
+    v4i wo[7], wd[2][CD];
     {
-      const auto so = gbl16(W.wo + (size_t)no * E), sg = gbl16(W.wg + (size_t)ngt * E),
-                 su = gbl16(W.wu + (size_t)ngt * E), sd = gbl16(W.wd + (size_t)nd * F);
+      const auto so = gbl16(W.wo + (size_t)no * E);
+      if (on_o) {
 #pragma unroll
-      for (int c = 0; c < 7; c++) wo[c] = __builtin_nontemporal_load(so + sub + 8 * c);
-#pragma unroll
-      for (int c = 0; c < 7; c++) {
-        wg[c] = __builtin_nontemporal_load(sg + sub + 8 * c);
-        wu[c] = __builtin_nontemporal_load(su + sub + 8 * c);
+        for (int c = 0; c < 7; c++) wo[c] = __builtin_nontemporal_load(so + sub + 8 * c);
       }
 #pragma unroll
-      for (int c = 0; c < CD; c++) wd[c] = __builtin_nontemporal_load(sd + min(lane + 64 * c, nch - 1));
-    }
-    const float wso = gbl(W.so)[no], bsg = gbl(W.sg)[ngt], bsu = gbl(W.su)[ngt], wsd = gbl(W.sd)[nd];
-    float gam[2];
+      for (int h = 0; h < 2; h++) {
+        const auto sd = gbl16(W.wd + (size_t)(r0 + wave + 8 * h) * F);
 #pragma unroll
-    for (int j = 0; j < 2; j++) gam[j] = gbl(W.ln2_g)[min(t + kStepThreads * j, E - 1)];
+        for (int c = 0; c < CD; c++) wd[h][c] = __builtin_nontemporal_load(sd + min(lane + 64 * c, nch - 1));
+      }
+    }
+    const float wso = gbl(W.so)[no], wsd0 = gbl(W.sd)[r0 + wave], wsd1 = gbl(W.sd)[r0 + wave + 8];
 
     // ---------------- O: output projection + residual ----------------
     {
-      const float sa = gather_quant<2>(ATT, E, tag, codes, red, a.err);
+      const float sa = gather_quant<1, TRACE>(ATT, E, tag, codes, red, a.err, &a, l, 13);
       mark<TRACE>(a, b, l, 4);
       int acc = 0;
 #pragma unroll
@@ -392,41 +417,33 @@ __device__ void gemv_loop(const StepArgs &a, int gi, int ng, unsigned tag, int t
       mark<TRACE>(a, b, l, 5);
     }
 
-    // ---------------- G: gate/up + SiLU gating ----------------
-    {
-      gather<2>(XM, E, tag, xs, a.err);
-      mark<TRACE>(a, b, l, 6);
-      const float sx = block_norm_quant(xs, E, gam, a.eps, codes, red);
-      mark<TRACE>(a, b, l, 10);
-      int ag = 0, au = 0;
-#pragma unroll
-      for (int c = 0; c < 7; c++) {
-        ag = dot16(ag, wg[c], codes + 16 * (sub + 8 * c));
-        au = dot16(au, wu[c], codes + 16 * (sub + 8 * c));
-      }
-      ag = sum8(ag);
-      au = sum8(au);
-      if (on_g && sub == 0) {
-        const float gv = i8_epilogue(ag, sx, bsg, 0.0f), u = i8_epilogue(au, sx, bsu, 0.0f);
-        put_word(FF + ngt, silu(gv, etab + 32 * wave) * u, tag);
-      }
-      mark<TRACE>(a, b, l, 7);
-    }
-
     // ---------------- D: down projection + residual ----------------
     {
-      const float sf = gather_quant<10>(FF, F, tag, codes, red, a.err);
+      const float sf =
+          gather_quant<(kFMax / 2 + kStepThreads - 1) / kStepThreads, TRACE>(FF, F, tag, codes, red, a.err, &a, l, 12);
       mark<TRACE>(a, b, l, 8);
-      int acc = 0;
+      int acc0 = 0, acc1 = 0;
 #pragma unroll
-      for (int c = 0; c < CD; c++)
-        if (lane + 64 * c < nch) acc = dot16(acc, wd[c], codes + 16 * (lane + 64 * c));
-      acc = sum64(acc);
-      if (on_d && lane == 0) {
-        const float v = xmown[wave] + i8_epilogue(acc, sf, wsd, 0.0f);
-        xown[wave] = v;
-        put_word(X + nd, v, tag);
-        if (l + 1 == a.L) a.x_out[nd] = v;
+      for (int c = 0; c < CD; c++) {
+        if (lane + 64 * c < nch) {
+          const v4i x = *reinterpret_cast<const v4i *>(codes + 16 * (lane + 64 * c));
+          acc0 = dot16x(acc0, wd[0][c], x);
+          acc1 = dot16x(acc1, wd[1][c], x);
+        }
+      }
+      acc0 = sum64(acc0);
+      acc1 = sum64(acc1);
+      if (lane == 0) {
+        const float v0 = xmown[wave] + i8_epilogue(acc0, sf, wsd0, 0.0f);
+        const float v1 = xmown[wave + 8] + i8_epilogue(acc1, sf, wsd1, 0.0f);
+        xown[wave] = v0;
+        xown[wave + 8] = v1;
+        put_word(X + r0 + wave, v0, tag);
+        put_word(X + r0 + wave + 8, v1, tag);
+        if (l + 1 == a.L) {
+          a.x_out[r0 + wave] = v0;
+          a.x_out[r0 + wave + 8] = v1;
+        }
       }
       __syncthreads();  // xown / codes reused by the next layer
       mark<TRACE>(a, b, l, 9);
@@ -434,11 +451,67 @@ __device__ void gemv_loop(const StepArgs &a, int gi, int ng, unsigned tag, int t
   }
 }
 
+// The gate/up blocks' loop (block gi of ng): per layer the gate/up row pairs
+// [g0, g1) of F (at most 64: one 8-lane group each) with the SiLU gating,
+// after the RMSNorm and quantization of x_mid.  etab: this wave's copy of
+// the SiLU's 2^(i/32) table.
+template <bool TRACE>
+__device__ void gu_loop(const StepArgs &a, int gi, int ng, unsigned tag, float *lds, float *red, uint64_t *etab) {
+  const int b = blockIdx.x;
+  const int E = a.E, F = a.F;
+  const size_t S = (size_t)3 * E + F;
+  float *xs = lds;
+  int8_t *codes = reinterpret_cast<int8_t *>(lds + (E > F ? E : F));
+  for (int l = 0; l < a.L; l++) {
+    const StepLayer &W = a.layers[l];
+    mark<TRACE>(a, b, l, 0);
+    unsigned long long *XM = a.xch + (size_t)l * S + E, *FF = a.xch + (size_t)l * S + 3 * E;
+    const int t = tid_opaque();
+    const int grp = t >> 3, sub = t & 7;  // 64 row groups of 8 lanes (rows of E int8)
+    const int g = uniform_opaque(gi);
+    const int g0 = g * F / ng, g1 = (g + 1) * F / ng;
+    const bool on_g = grp < g1 - g0;
+    const int ngt = g0 + (on_g ? grp : 0);
+    v4i wg[7], wu[7];
+    {
+      const auto sg = gbl16(W.wg + (size_t)ngt * E), su = gbl16(W.wu + (size_t)ngt * E);
+#pragma unroll
+      for (int c = 0; c < 7; c++) {
+        wg[c] = __builtin_nontemporal_load(sg + sub + 8 * c);
+        wu[c] = __builtin_nontemporal_load(su + sub + 8 * c);
+      }
+    }
+    const float bsg = gbl(W.sg)[ngt], bsu = gbl(W.su)[ngt];
+    float gam[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) gam[j] = gbl(W.ln2_g)[min(t + kStepThreads * j, E - 1)];
+
+    gather<1>(XM, E, tag, xs, a.err);
+    mark<TRACE>(a, b, l, 6);
+    const float sx = block_norm_quant(xs, E, gam, a.eps, codes, red);
+    mark<TRACE>(a, b, l, 10);
+    int ag = 0, au = 0;
+#pragma unroll
+    for (int c = 0; c < 7; c++) {
+      ag = dot16(ag, wg[c], codes + 16 * (sub + 8 * c));
+      au = dot16(au, wu[c], codes + 16 * (sub + 8 * c));
+    }
+    ag = sum8(ag);
+    au = sum8(au);
+    if (on_g && sub == 0) {
+      const float gv = i8_epilogue(ag, sx, bsg, 0.0f), u = i8_epilogue(au, sx, bsu, 0.0f);
+      put_word(FF + ngt, silu(gv, etab) * u, tag);
+    }
+    if constexpr (TRACE) __syncthreads();  // the mark follows every wave's stores
+    mark<TRACE>(a, b, l, 7);
+  }
+}
+
 template <bool TRACE>
 __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepArgs a) {
   extern __shared__ __attribute__((aligned(16))) float lds[];
   __shared__ __attribute__((aligned(16))) float qkv_s[3 * 64];  // q of head h, k and v of its group
-  __shared__ float xown[8], xmown[8];  // this block's rows of x and x_mid
+  __shared__ float xown[kODRows], xmown[kODRows];  // an o / down block's rows of x and x_mid
   __shared__ float red[kNW];
   __shared__ uint64_t etab[kNW][32];  // the SiLU's 2^(i/32) table, one copy per wave
 
@@ -449,7 +522,9 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepArgs a) {
 
   // roles: the attention blocks of query head h, element slice s (the heads
   // of KV group g on XCD g, as the attention kernel's XCD-grouped launch);
-  // the other blocks, numbered gi in block order, run the GEMV phases
+  // the other blocks, numbered gi in block order: E / kODRows o / down
+  // blocks, then ceil(F / 64) gate/up blocks; the rest have nothing to do.
+  // Separate roles keep the number of blocks that read each exchange small.
   const int rpg = a.H / a.KVH, na = rpg * kStepSlices;
   const int xcd = b & 7, jx = b >> 3;
   if (xcd < a.KVH && jx < na) {
@@ -457,7 +532,11 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepArgs a) {
   } else {
     int before = 0;  // attention blocks with a lower index
     for (int x = 0; x < a.KVH; x++) before += b > x ? min(na, (b - x + 7) / 8) : 0;
-    gemv_loop<TRACE>(a, b - before, kStepBlocks - a.KVH * na, tag, tok, lds, xown, xmown, red, etab[t >> 6]);
+    const int gi = b - before, nod = a.E / kODRows, ngu = (a.F + 63) / 64;
+    if (gi < nod)
+      od_loop<TRACE>(a, gi, tag, tok, lds, xown, xmown, red);
+    else if (gi < nod + ngu)
+      gu_loop<TRACE>(a, gi - nod, ngu, tag, lds, red, etab[t >> 6]);
   }
 }
 

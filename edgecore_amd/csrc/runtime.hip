@@ -754,7 +754,7 @@ static bool step_shape_ok(const GPT2 *g, const DevModel *d) {
   const int H = g->n_head, KVH = g->n_kv_head, E = g->n_embd, F = d->F;
   return g->arch == ARCH_QWEN2 && g->precision == 0 && E == 896 && g->head_dim == 64 && KVH >= 1 && KVH <= 8 &&
          H % KVH == 0 && (H / KVH) * kStepSlices <= kStepBlocks / 8 && F % 16 == 0 && F <= 5120 &&
-         F <= 64 * kStepBlocks && g_prop.multiProcessorCount == kStepBlocks;
+         H * kStepSlices + E / 16 + (F + 63) / 64 <= kStepBlocks && g_prop.multiProcessorCount == kStepBlocks;
 }
 
 static int load_impl(GPT2 *g, const char *path, int batch_cap, int max_ctx) {

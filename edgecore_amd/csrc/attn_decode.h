@@ -337,7 +337,10 @@ __host__ __device__ constexpr inline int attn_sswz(int hs) { return hs <= 16 ? 0
 // a.scores[(m * H + h) * sc_ld + i] (position lo + i), written by the scores
 // pass with this body's arithmetic, and the cache already holds the token's k
 // and v (FUSED must be false).
-template <int HD, bool FUSED, int NS, bool SCORED = false, class Out>
+// PREK (the persistent step): the K rows of positions [lo, lo + min(n - 1,
+// KQ)) are already in the K tile (attn_prefetch_k, waited for by the caller
+// before its last barrier); the body loads and writes only the rest.
+template <int HD, bool FUSED, int NS, bool SCORED = false, bool PREK = false, class Out>
 __device__ __forceinline__ void attn_decode_block(const AttnArgs &a, int m, int h, int slice, const float *qrow,
                                                   const float *krow, const float *vrow, float *lds, Out &&out,
                                                   size_t coff = 0) {
@@ -449,7 +452,7 @@ __device__ __forceinline__ void attn_decode_block(const AttnArgs &a, int m, int 
     }
   } else {
   v4u kr[HD > 0 ? KU : 1][4];
-  if constexpr (HD > 0) {
+  if constexpr (HD > 0 && !PREK) {
 #pragma unroll
     for (int u = 0; u < KU; u++) {
       const int unit = t + NT * u, qd = unit / CPR, cd = unit - qd * CPR;
@@ -499,7 +502,7 @@ __device__ __forceinline__ void attn_decode_block(const AttnArgs &a, int m, int 
   }
   // K tile: row i, chunk c at 16-byte slot i*KP + c
   v4u *ktile = reinterpret_cast<v4u *>(prod);
-  if constexpr (HD > 0) {
+  if constexpr (HD > 0 && !PREK) {
 #pragma unroll
     for (int u = 0; u < KU; u++) {
       const int unit = t + NT * u, qd = unit / CPR, cd = unit - qd * CPR;
@@ -743,5 +746,38 @@ __device__ __forceinline__ void attn_decode_block(const AttnArgs &a, int m, int 
   if (t < hs) out(t, o);
 }
 
+// For attn_decode_block<HD, true, NS, false, true> (element slices, FUSED):
+// load the K rows of positions [lo, lo + min(n - 1, KQ)) of token m's KV
+// group (head h) straight from the cache into the K tile of lds, in the
+// tile's layout (row i at 16-byte slot i * KP, chunk c at + c), one row per
+// instruction (8 lanes of 16 bytes each).  Every thread of the block calls
+// it; the loads complete asynchronously (vmcnt): the caller waits for them
+// and then passes a barrier before the body reads the tile.
+template <int HD, int NS>
+__device__ __forceinline__ void attn_prefetch_k(const AttnArgs &a, int m, int h, float *lds, size_t coff = 0) {
+  static_assert(HD == 64 && NS > 1, "element slices of head_dim 64");
+  constexpr int NT = 512, KU = kAttnUnits / 2, CPR = HD / 8, KP = CPR + 1;
+  constexpr int KQMAX = NT * KU * 4 / CPR;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int pos = ld_uniform(a.pos + m), slot = ld_uniform(a.slot + m);
+  int lo = 0;
+  if (a.window > 0) {
+    lo = pos - a.window + 1;
+    if (lo < 0) lo = 0;
+  }
+  const int n = pos + 1 - lo;
+  const int KQ = min(KQMAX, (a.vtile / 4) * attn_pitch(HD, a.kv) / KP);
+  const int rows = min(n - 1, KQ);
+  const int kvh = h * a.KVH / a.H;
+  const uint16_t *K = a.kc + coff + (size_t)slot * a.C * a.kv + (size_t)kvh * HD + (size_t)lo * a.kv;
+  char *tile = reinterpret_cast<char *>(lds + 3 * HD + ((a.max_npos + 3) & ~3));
+  typedef __attribute__((address_space(1))) void gvoid;
+  typedef __attribute__((address_space(3))) void lvoid;
+  if (lane < CPR) {
+    for (int i = wave; i < rows; i += NT / 64)
+      __builtin_amdgcn_global_load_lds((gvoid *)(K + (size_t)i * a.kv + 8 * lane), (lvoid *)(tile + (size_t)i * KP * 16),
+                                       16, 0, 0);
+  }
+}
 
 }  // namespace ec

@@ -297,8 +297,8 @@ __device__ void attention_loop(const StepArgs &a, int head, int slice, unsigned 
   const int b = blockIdx.x;
   const int E = a.E, F = a.F, kv = 64 * a.KVH, kvh = head * a.KVH / a.H;
   const size_t S = (size_t)3 * E + F;
-  float *xs = lds;
-  int8_t *codes = reinterpret_cast<int8_t *>(lds + (E > F ? E : F));
+  float *xs = lds + a.norm_off;  // past the attention area
+  int8_t *codes = reinterpret_cast<int8_t *>(xs + E);
   v4i w[3][7];
   float ws[3], gam[2];
   int sink = 0;
@@ -318,6 +318,7 @@ __device__ void attention_loop(const StepArgs &a, int head, int slice, unsigned 
     for (int j = 0; j < 2; j++) gam[j] = gbl(W.ln1_g)[min(t + kStepThreads * j, E - 1)];
   };
   load_layer(0);
+  attn_prefetch_k<64, kStepSlices>(a.attn, 0, uniform_opaque(head), lds, 0);
   for (int l = 0; l < a.L; l++) {
     mark<TRACE>(a, b, l, 0);
     const int t = tid_opaque(), grp = t >> 3, sub = t & 7;
@@ -327,6 +328,9 @@ __device__ void attention_loop(const StepArgs &a, int head, int slice, unsigned 
     } else {
       gather<1>(a.xch + (size_t)(l - 1) * S, E, tag, xs, a.err);
     }
+    // this wave's K-tile rows have landed; the norm's barriers publish them
+    // to the block before the attention body reads the tile
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     mark<TRACE>(a, b, l, 1);
     const float sx = block_norm_quant(xs, E, gam, a.eps, codes, red);
     mark<TRACE>(a, b, l, 11);
@@ -343,20 +347,21 @@ __device__ void attention_loop(const StepArgs &a, int head, int slice, unsigned 
     const int hh = uniform_opaque(head), ss = uniform_opaque(slice);
     unsigned long long *att = a.xch + (size_t)l * S + 2 * E;
     const int o0 = hh * 64 + 16 * ss;
-    attn_decode_block<64, true, kStepSlices>(a.attn, 0, hh, ss, qkv_s, qkv_s + 64, qkv_s + 128, lds,
+    attn_decode_block<64, true, kStepSlices, false, true>(a.attn, 0, hh, ss, qkv_s, qkv_s + 64, qkv_s + 128, lds,
                                              [&](int i, float o) { put_word(att + o0 + i, o, tag); },
                                              a.kv_layer * l);
     __syncthreads();  // the body's LDS is reused by the next layer
     mark<TRACE>(a, b, l, 3);
     if (l + 1 < a.L) {
       load_layer(l + 1);
-      // K and V rows [0, pos) of the group in the next layer: one 4-byte
-      // load per 128-byte line (a K row and a V row are 128 bytes each)
+      // the next layer's K rows into the K tile (its first KQ positions)
+      attn_prefetch_k<64, kStepSlices>(a.attn, 0, hh, lds, a.kv_layer * (l + 1));
+      // V rows [0, pos) of the group in the next layer: one 4-byte load per
+      // 128-byte line (a V row is 128 bytes)
       const int pos = ld_uniform(a.attn.pos), slot = ld_uniform(a.attn.slot);
       const size_t base = a.kv_layer * (l + 1) + (size_t)slot * a.attn.C * kv + (size_t)kvh * 64;
-      const auto kc = gbl(reinterpret_cast<const int *>(a.attn.kc + base));
       const auto vc = gbl(reinterpret_cast<const int *>(a.attn.vc + base));
-      for (int p = t; p < pos; p += kStepThreads) sink ^= kc[(size_t)p * kv / 2] ^ vc[(size_t)p * kv / 2];
+      for (int p = t; p < pos; p += kStepThreads) sink ^= vc[(size_t)p * kv / 2];
     }
   }
   if (sink == 0x7fffffff && tag == 0) red[0] = (float)sink;  // keeps the touches (tag is never 0)

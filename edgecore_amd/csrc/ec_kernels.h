@@ -251,7 +251,13 @@ struct StepArgs {
   // the attention body's arguments for layer 0 (kc/vc, kc_w/vc_w at layer
   // 0, fused RoPE + append, M = 1); layer l adds l * kv_layer to the caches
   AttnArgs attn;
+  // attention blocks: their fp32 row and int8 codes start this many floats
+  // into the dynamic LDS, past the attention body's area (whose K tile is
+  // filled for the next layer while they normalize)
+  int norm_off;
 };
+// dynamic LDS of the attention blocks' row and codes (d_model E)
+constexpr inline size_t step_norm_bytes(int E) { return ((size_t)E * 5 + 15) & ~(size_t)15; }
 size_t decode_step_scratch_bytes(int E, int F);
 // cooperative: a cooperative launch (every block resident by contract);
 // otherwise a plain launch of the same kStepBlocks blocks, one per CU, which the

@@ -7,9 +7,12 @@ N(0, 0.02) from seed 0 (synthetic, bin/ecm_synth), a 256-token prompt of ids
 uniform in [0, 151936) from seed 1, greedy decoding.  One step is one decode
 token: the forward at M=1 plus the GPU argmax.  The steps run through
 ec_generate_greedy, which chains them on the device (each argmax id becomes
-the next step's token there; the K ids come back to the host at the end).
+the next step's token there; the K ids come back to the host at the end;
+runs of 16 steps inside one 512-position bucket are one HIP graph launch).
 The prompt is prefilled first (reported as prefill tok/s, untimed), then W
-warmup steps, then K timed steps bracketed by stream synchronisation.
+warmup steps, then the K steps once untimed (their graphs are captured on
+first use), then the same K steps timed, bracketed by stream
+synchronisation; both runs give the same ids.
 
 Two passes of the same K steps run, each after the same prefill and warmup.
 In the first, every kernel launch records its own dispatch start and stop on
@@ -468,6 +471,11 @@ def main() -> int:
         if W > 0:
             cur, pos = int(m.generate_greedy(cur, pos, 0, W)[-1]), pos + W
         L.ec_sync()
+        # the same K steps once, untimed: graph capture and instantiation of
+        # the steps' buckets happen here (the timed run rewrites the same
+        # cache rows with the same values)
+        first = [int(x) for x in m.generate_greedy(cur, pos, 0, K)]
+        L.ec_sync()
         if prof_filter is not None:
             L.ec_prof_start(prof_filter.encode())
         L.ec_sync()
@@ -475,6 +483,8 @@ def main() -> int:
         ids = [int(x) for x in m.generate_greedy(cur, pos, 0, K)]
         L.ec_sync()
         elapsed = time.perf_counter() - t0
+        if ids != first:
+            raise SystemExit("bench.py: the untimed and timed decode runs produced different tokens")
         kern = []
         if prof_filter is not None:
             buf = __import__("ctypes").create_string_buffer(1 << 16)

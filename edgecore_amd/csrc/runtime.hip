@@ -614,8 +614,10 @@ struct DevModel {
   int step_bucket = 0;  // the graph's attention LDS covers positions < step_bucket
   // chained greedy decode (ec_generate_greedy): steps whose token comes from
   // the previous step's argmax on the device; ids collected in d_gen
-  hipGraphExec_t chain_graph = nullptr;
-  int chain_bucket = 0;
+  // [0]: one step, [1]: kChainBurst steps in a row (one launch's overhead
+  // for all of them), each for one 512-position bucket
+  hipGraphExec_t chain_graph[2] = {nullptr, nullptr};
+  int chain_bucket[2] = {0, 0};
   bool chaining = false;  // set while a chained step is enqueued or captured
   int *d_gen = nullptr;
   int *h_amax = nullptr;  // pinned: the graphs' argmax outputs (batch_cap ids)
@@ -706,7 +708,8 @@ static void free_dev(DevModel *d) {
   if (d->h_amax) (void)hipHostFree(d->h_amax);
   if (d->h_step_io) (void)hipHostFree(d->h_step_io);
   if (d->step_graph) (void)hipGraphExecDestroy(d->step_graph);
-  if (d->chain_graph) (void)hipGraphExecDestroy(d->chain_graph);
+  for (hipGraphExec_t ge : d->chain_graph)
+    if (ge) (void)hipGraphExecDestroy(ge);
   for (auto &dg : d->dec_graphs) (void)hipGraphExecDestroy(dg.exec);
   d->dec_graphs.clear();
   delete d;
@@ -1451,10 +1454,11 @@ static int enqueue_forward(GPT2 *g, DevModel *d, int M, int lm_from, bool distin
     }
     d->last_lm_rows = rows;
   }
-  if (step && d->chaining && !advanced)
-    EC_HIP(step_advance(d->d_step_io, d->d_gen, s));
-  else if (step)
+  if (step && d->chaining) {  // nothing goes to the host: the next step reads its inputs on the device
+    if (!advanced) EC_HIP(step_advance(d->d_step_io, d->d_gen, s));
+  } else if (step) {
     EC_HIP(hipMemcpyAsync(d->h_step_io + 4, d->d_step_io + 4, 2 * sizeof(int), hipMemcpyDeviceToHost, s));
+  }
   else if (argmax && lm_from < M)
     EC_HIP(hipMemcpyAsync(argmax, d->d_amax, (size_t)(M - lm_from) * 4, hipMemcpyDeviceToHost, s));
   return 0;
@@ -1470,12 +1474,19 @@ static int step_timed_out(DevModel *d) {
   if (g_step_coop) return 0;
   g_step_coop = true;
   if (d->step_graph) (void)hipGraphExecDestroy(d->step_graph);
-  if (d->chain_graph) (void)hipGraphExecDestroy(d->chain_graph);
-  d->step_graph = d->chain_graph = nullptr;
-  d->step_bucket = d->chain_bucket = 0;
+  for (int i = 0; i < 2; i++) {
+    if (d->chain_graph[i]) (void)hipGraphExecDestroy(d->chain_graph[i]);
+    d->chain_graph[i] = nullptr;
+    d->chain_bucket[i] = 0;
+  }
+  d->step_graph = nullptr;
+  d->step_bucket = 0;
   fprintf(stderr, "edgecore: a decode step's blocks were not all resident; cooperative launches from now on\n");
   return 1;
 }
+
+// chained greedy steps per graph launch when they fit one bucket
+constexpr int kChainBurst = 16;
 
 // the host-side stand-in for a timed-out plain step (EDGECORE_STEP_TEST_FAIL=1)
 static bool step_test_fail() {
@@ -1783,44 +1794,50 @@ extern "C" int ec_generate_greedy(GPT2 *g, int token, int pos, int slot, int n, 
   io[3] = (int)(d->step_tag + 1u);
   io[4] = io[5] = io[6] = 0;
   EC_HIP(hipMemcpyAsync(d->d_step_io, io, 7 * sizeof(int), hipMemcpyHostToDevice, s));
-  for (int k = 0; k < n; k++) {
+  for (int k = 0; k < n;) {
     const int max_npos = pos + k + 1;
     int bucket = (max_npos + 511) / 512 * 512;
     if (bucket > d->eff_ctx) bucket = d->eff_ctx;
+    // kChainBurst steps in one graph when their positions stay in the bucket
+    const int len = (n - k >= kChainBurst && bucket - (pos + k) >= kChainBurst) ? kChainBurst : 1;
+    const int gi = len == 1 ? 0 : 1;
     bool graph = g_use_graphs && !d->step_nograph && step_vtile(bucket, g->n_embd) >= 4;
-    if (graph && (!d->chain_graph || d->chain_bucket != bucket)) {
-      if (d->chain_graph) {
-        EC_HIP(hipGraphExecDestroy(d->chain_graph));
-        d->chain_graph = nullptr;
+    if (graph && (!d->chain_graph[gi] || d->chain_bucket[gi] != bucket)) {
+      if (d->chain_graph[gi]) {
+        EC_HIP(hipGraphExecDestroy(d->chain_graph[gi]));
+        d->chain_graph[gi] = nullptr;
       }
       hipGraph_t gr = nullptr;
       hipError_t e = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
       int r = 0;
       if (e == hipSuccess) {
         d->chaining = true;
-        r = enqueue_forward(g, d, 1, 0, true, false, bucket, 0.0, nullptr, io + 5, nullptr, s, true);
+        for (int j = 0; j < len && r == 0; j++)
+          r = enqueue_forward(g, d, 1, 0, true, false, bucket, 0.0, nullptr, io + 5, nullptr, s, true);
         d->chaining = false;
         e = hipStreamEndCapture(s, &gr);
       }
-      if (e == hipSuccess && r == 0) e = hipGraphInstantiate(&d->chain_graph, gr, nullptr, nullptr, 0);
+      if (e == hipSuccess && r == 0) e = hipGraphInstantiate(&d->chain_graph[gi], gr, nullptr, nullptr, 0);
       if (gr) (void)hipGraphDestroy(gr);
       if (e != hipSuccess || r != 0) {
         (void)hipGetLastError();
         g_err[0] = 0;
-        d->chain_graph = nullptr;
+        d->chain_graph[gi] = nullptr;
         graph = false;
       } else {
-        d->chain_bucket = bucket;
+        d->chain_bucket[gi] = bucket;
       }
     }
     int r = 0;
     if (graph) {
-      const hipError_t e = hipGraphLaunch(d->chain_graph, s);
+      const hipError_t e = hipGraphLaunch(d->chain_graph[gi], s);
       if (e != hipSuccess) r = set_err(-3, "ec_generate_greedy: graph launch: %s", hipGetErrorString(e));
+      k += len;
     } else {
       d->chaining = true;
       r = enqueue_forward(g, d, 1, 0, true, false, max_npos, 0.0, nullptr, io + 5, nullptr, s, true);
       d->chaining = false;
+      k += 1;
     }
     if (r) return r;
   }

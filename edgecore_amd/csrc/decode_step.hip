@@ -194,6 +194,80 @@ __device__ float gather_quant(const unsigned long long *buf, int n, unsigned tag
 }
 
 
+// The FFN activation: plain fp32 words, kStepFfEmpty until written (each
+// word by one 4-byte store).  gather_quant_ff waits until words [0, n) of buf
+// (n % 4 == 0, buf 16-byte aligned) are all written -- thread t owns the
+// quads t + kStepThreads * j (j < WQ), one 16-byte device-coherent load each,
+// reissued only for the quads still incomplete -- then quantizes them as
+// gather_quant does.
+template <int WQ>
+__device__ float gather_quant_ff(const float *buf, int n, int8_t *codes, float *red, int *err) {
+  const int t = threadIdx.x;
+  __syncthreads();  // codes are still read by the previous phase
+  const uint64_t bp = (uint64_t)(uintptr_t)buf;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)bp), hi = __builtin_amdgcn_readfirstlane((uint32_t)(bp >> 32));
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)(uintptr_t)(((uint64_t)hi << 32) | lo), 0, __builtin_amdgcn_readfirstlane(n * 4), 0x00020000);
+  unsigned pending = 0;
+#pragma unroll
+  for (int j = 0; j < WQ; j++)
+    if (t + kStepThreads * j < (n >> 2)) pending |= 1u << j;
+  const unsigned own = pending;
+  v4u v[WQ];
+  float x[WQ][4];
+#pragma unroll
+  for (int j = 0; j < WQ; j++) x[j][0] = x[j][1] = x[j][2] = x[j][3] = 0.0f;
+  for (int it = 0; pending; it++) {
+#pragma unroll
+    for (int j = 0; j < WQ; j++)
+      if ((pending >> j) & 1u)
+        v[j] = __builtin_amdgcn_raw_buffer_load_b128(rs, (t + kStepThreads * j) * 16, 0, 16 /* sc1 */);
+#pragma unroll
+    for (int j = 0; j < WQ; j++) {
+      if (((pending >> j) & 1u) && v[j].x != kStepFfEmpty && v[j].y != kStepFfEmpty && v[j].z != kStepFfEmpty &&
+          v[j].w != kStepFfEmpty) {
+        x[j][0] = __uint_as_float(v[j].x);
+        x[j][1] = __uint_as_float(v[j].y);
+        x[j][2] = __uint_as_float(v[j].z);
+        x[j][3] = __uint_as_float(v[j].w);
+        pending &= ~(1u << j);
+      }
+    }
+    if (!pending) break;
+    if (it >= kSpin) {
+      atomicOr(err, 1);
+      break;
+    }
+    if ((it & 63) == 63 && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) break;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  float mx = 0.0f;
+#pragma unroll
+  for (int j = 0; j < WQ; j++)
+    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(x[j][0]), fabsf(x[j][1])), fmaxf(fabsf(x[j][2]), fabsf(x[j][3]))));
+  mx = block_max_1b<kNW>(mx, red);
+  const float sc = quant_scale(mx);
+  auto put = [&](auto q1) {
+#pragma unroll
+    for (int j = 0; j < WQ; j++) {
+      if (!((own >> j) & 1u)) continue;
+      uint32_t c = 0;
+#pragma unroll
+      for (int e = 0; e < 4; e++) c |= (uint32_t)(uint8_t)q1(x[j][e]) << (8 * e);
+      *reinterpret_cast<uint32_t *>(codes + 4 * (t + kStepThreads * j)) = c;
+    }
+  };
+  // one branch per block (sc is uniform), not a select per element
+  if (ec_quant_rcp_ok(sc)) {
+    const float rcp = 1.0f / sc;
+    put([&](float v) { return ec_quant1_rcp(v, sc, rcp); });
+  } else {
+    put([&](float v) { return quant1(v, sc); });
+  }
+  __syncthreads();
+  return sc;
+}
+
 // sum over the 8 lanes of each row group (exact int32)
 __device__ __forceinline__ int sum8(int v) {
   v = v + dpp_mov<0xB1>(v);   // quad_perm [1,0,3,2]
@@ -295,8 +369,8 @@ template <bool TRACE>
 __device__ void attention_loop(const StepArgs &a, int head, int slice, unsigned tag, int tok, float *lds,
                                float *qkv_s, float *red) {
   const int b = blockIdx.x;
-  const int E = a.E, F = a.F, kv = 64 * a.KVH, kvh = head * a.KVH / a.H;
-  const size_t S = (size_t)3 * E + F;
+  const int E = a.E, kv = 64 * a.KVH, kvh = head * a.KVH / a.H;
+  const size_t S = (size_t)3 * E;
   float *xs = lds + a.norm_off;  // past the attention area
   int8_t *codes = reinterpret_cast<int8_t *>(xs + E);
   v4i w[3][7];
@@ -376,13 +450,14 @@ __device__ void od_loop(const StepArgs &a, int gi, unsigned tag, int tok, float 
                         float *red) {
   const int b = blockIdx.x;
   const int E = a.E, F = a.F;
-  const size_t S = (size_t)3 * E + F;
+  const size_t S = (size_t)3 * E;
   int8_t *codes = reinterpret_cast<int8_t *>(lds + (E > F ? E : F));
   if ((int)threadIdx.x < kODRows) xown[threadIdx.x] = h2f(gbl(a.wte)[(size_t)tok * E + gi * kODRows + threadIdx.x]);
   for (int l = 0; l < a.L; l++) {
     const StepLayer &W = a.layers[l];
     mark<TRACE>(a, b, l, 0);
-    unsigned long long *X = a.xch + (size_t)l * S, *XM = X + E, *ATT = X + 2 * E, *FF = X + 3 * E;
+    unsigned long long *X = a.xch + (size_t)l * S, *XM = X + E, *ATT = X + 2 * E;
+    const float *FV = a.ffv + ((size_t)(tag & 1u) * a.L + l) * F;
     const int t = tid_opaque(), lane = t & 63, wave = t >> 6;
     const int grp = t >> 3, sub = t & 7;  // 64 row groups of 8 lanes (rows of E int8)
     const int r0 = uniform_opaque(gi) * kODRows;
@@ -424,8 +499,8 @@ __device__ void od_loop(const StepArgs &a, int gi, unsigned tag, int tok, float 
 
     // ---------------- D: down projection + residual ----------------
     {
-      const float sf =
-          gather_quant<(kFMax / 2 + kStepThreads - 1) / kStepThreads, TRACE>(FF, F, tag, codes, red, a.err, &a, l, 12);
+      const float sf = gather_quant_ff<(kFMax / 4 + kStepThreads - 1) / kStepThreads>(FV, F, codes, red, a.err);
+      mark<TRACE>(a, b, l, 12);
       mark<TRACE>(a, b, l, 8);
       int acc0 = 0, acc1 = 0;
 #pragma unroll
@@ -464,13 +539,14 @@ template <bool TRACE>
 __device__ void gu_loop(const StepArgs &a, int gi, int ng, unsigned tag, float *lds, float *red, uint64_t *etab) {
   const int b = blockIdx.x;
   const int E = a.E, F = a.F;
-  const size_t S = (size_t)3 * E + F;
+  const size_t S = (size_t)3 * E;
   float *xs = lds;
   int8_t *codes = reinterpret_cast<int8_t *>(lds + (E > F ? E : F));
   for (int l = 0; l < a.L; l++) {
     const StepLayer &W = a.layers[l];
     mark<TRACE>(a, b, l, 0);
-    unsigned long long *XM = a.xch + (size_t)l * S + E, *FF = a.xch + (size_t)l * S + 3 * E;
+    unsigned long long *XM = a.xch + (size_t)l * S + E;
+    float *FV = a.ffv + ((size_t)(tag & 1u) * a.L + l) * F;
     const int t = tid_opaque();
     const int grp = t >> 3, sub = t & 7;  // 64 row groups of 8 lanes (rows of E int8)
     const int g = uniform_opaque(gi);
@@ -505,11 +581,22 @@ __device__ void gu_loop(const StepArgs &a, int gi, int ng, unsigned tag, float *
     au = sum8(au);
     if (on_g && sub == 0) {
       const float gv = i8_epilogue(ag, sx, bsg, 0.0f), u = i8_epilogue(au, sx, bsu, 0.0f);
-      put_word(FF + ngt, silu(gv, etab) * u, tag);
+      __hip_atomic_store(reinterpret_cast<uint32_t *>(FV + ngt), __float_as_uint(silu(gv, etab) * u), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
     }
     if constexpr (TRACE) __syncthreads();  // the mark follows every wave's stores
     mark<TRACE>(a, b, l, 7);
   }
+}
+
+// A block with no role (ib of nb): fill the FFN half that the next step
+// (tag + 1) uses with kStepFfEmpty.  The previous step used it and has
+// ended; the next one starts after this launch ends.
+__device__ void ff_rearm(const StepArgs &a, int ib, int nb, unsigned tag) {
+  const size_t nq = (size_t)a.L * a.F / 4;
+  v4u *q = reinterpret_cast<v4u *>(a.ffv + (size_t)((tag + 1u) & 1u) * a.L * a.F);
+  const v4u e = {kStepFfEmpty, kStepFfEmpty, kStepFfEmpty, kStepFfEmpty};
+  for (size_t i = (size_t)ib * kStepThreads + threadIdx.x; i < nq; i += (size_t)nb * kStepThreads) q[i] = e;
 }
 
 template <bool TRACE>
@@ -542,6 +629,8 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepArgs a) {
       od_loop<TRACE>(a, gi, tag, tok, lds, xown, xmown, red);
     else if (gi < nod + ngu)
       gu_loop<TRACE>(a, gi - nod, ngu, tag, lds, red, etab[t >> 6]);
+    else
+      ff_rearm(a, gi - nod - ngu, kStepBlocks - a.KVH * na - nod - ngu, tag);
   }
 }
 

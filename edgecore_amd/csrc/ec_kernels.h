@@ -215,8 +215,9 @@ hipError_t attention_after_scores(const AttnArgs &a, hipStream_t st);
 // forward for one token in one co-resident launch of kStepBlocks blocks of
 // kStepThreads threads (d_model 896, head_dim 64, 4 attention blocks per
 // query head, up to 8 query heads per KV group, FFN <= 5120).  Blocks exchange
-// activations through tagged words (value, step tag) in `xch`: per layer
-// [x after the layer: E][x after o: E][attention output: E][FFN activation: F].
+// activations through tagged words (value, step tag) in `xch`, per layer
+// [x after the layer: E][x after o: E][attention output: E], and the FFN
+// activation through plain words in `ffv` (StepArgs).
 constexpr int kStepBlocks = 256, kStepThreads = 512, kStepSlices = 4;
 // phase timestamps per block and layer: 0 layer start, 1 x gathered (attention
 // blocks), 2 q/k/v rows done, 3 attention done, 4 attention output gathered,
@@ -255,7 +256,14 @@ struct StepArgs {
   // into the dynamic LDS, past the attention body's area (whose K tile is
   // filled for the next layer while they normalize)
   int norm_off;
+  // the FFN activation, [2][L][F] floats: step tag t writes and reads half
+  // t & 1 (plain values, kStepFfEmpty until written), and re-arms the other
+  // half for the next step
+  float *ffv;
 };
+// the FFN words' "not written" pattern: a signaling NaN, which arithmetic never
+// produces (its NaN results are quiet)
+constexpr uint32_t kStepFfEmpty = 0x7FA5A5A5u;
 // dynamic LDS of the attention blocks' row and codes (d_model E)
 constexpr inline size_t step_norm_bytes(int E) { return ((size_t)E * 5 + 15) & ~(size_t)15; }
 size_t decode_step_scratch_bytes(int E, int F);

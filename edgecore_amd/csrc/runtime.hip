@@ -638,6 +638,8 @@ struct DevModel {
   bool step_ok = false;
   StepLayer *d_layers = nullptr;  // device copy of the layers' pointers
   unsigned long long *xch = nullptr;  // tagged exchange words
+  float *ffv = nullptr;               // the step's FFN words, two halves of [L][F]
+  size_t ffv_words = 0;
   size_t xch_bytes = 0;
   // one-token step I/O, device and pinned host: [0] token, [1] position,
   // [2] slot, [3] tag (copied in, 16 bytes); [4] a wait timed out, [5] the
@@ -700,7 +702,7 @@ static void free_dev(DevModel *d) {
   if (!d) return;
   void *ps[] = {d->arena, d->rope, d->d_tok, d->d_pos, d->d_slot, d->d_amax, d->x, d->h, d->qkv,
                 d->att, d->ff, d->aq, d->as, d->ah, d->ahs, d->att_sc, d->logits, d->kc, d->vc, d->cand, d->tk_cand,
-                d->tk_nan, d->tk_vals, d->tk_idx, d->tk_status, d->d_layers, d->xch, d->d_step_io, d->d_trace,
+                d->tk_nan, d->tk_vals, d->tk_idx, d->tk_status, d->d_layers, d->xch, d->ffv, d->d_step_io, d->d_trace,
                 d->d_gen};
   for (void *p : ps)
     if (p) (void)hipFree(p);
@@ -749,6 +751,14 @@ static DevModel *dev_detach(const GPT2 *g) {
 // head on one XCD of 32 CUs), up to 8 KV groups, FFN <= 5120 in 16-byte rows,
 // on a device with 256 CUs and cooperative launch.  EDGECORE_STEP=0 turns it
 // off (the forward then runs a kernel per operation).
+// The persistent step's exchange state back to "nothing written": the tagged
+// words to tag 0, both FFN halves to kStepFfEmpty (not inside a capture).
+static hipError_t step_clear(DevModel *d, hipStream_t s) {
+  hipError_t e = hipMemsetAsync(d->xch, 0, d->xch_bytes, s);
+  if (e == hipSuccess) e = hipMemsetD32Async((hipDeviceptr_t)d->ffv, (int)kStepFfEmpty, d->ffv_words, s);
+  return e;
+}
+
 static bool step_shape_ok(const GPT2 *g, const DevModel *d) {
   const char *env = getenv("EDGECORE_STEP");
   if (env && !strcmp(env, "0")) return false;
@@ -757,7 +767,7 @@ static bool step_shape_ok(const GPT2 *g, const DevModel *d) {
   const int H = g->n_head, KVH = g->n_kv_head, E = g->n_embd, F = d->F;
   return g->arch == ARCH_QWEN2 && g->precision == 0 && E == 896 && g->head_dim == 64 && KVH >= 1 && KVH <= 8 &&
          H % KVH == 0 && (H / KVH) * kStepSlices <= kStepBlocks / 8 && F % 16 == 0 && F <= 5120 &&
-         H * kStepSlices + E / 16 + (F + 63) / 64 <= kStepBlocks && g_prop.multiProcessorCount == kStepBlocks;
+         H * kStepSlices + E / 16 + (F + 63) / 64 < kStepBlocks && g_prop.multiProcessorCount == kStepBlocks;
 }
 
 static int load_impl(GPT2 *g, const char *path, int batch_cap, int max_ctx) {
@@ -1042,9 +1052,12 @@ static int load_impl(GPT2 *g, const char *path, int batch_cap, int max_ctx) {
     }
     EC_HIP(hipMalloc(&d->d_layers, sl.size() * sizeof(StepLayer)));
     EC_HIP(hipMemcpy(d->d_layers, sl.data(), sl.size() * sizeof(StepLayer), hipMemcpyHostToDevice));
-    d->xch_bytes = (size_t)Lc * (3 * (size_t)E + F) * sizeof(unsigned long long);
+    d->xch_bytes = (size_t)Lc * 3 * (size_t)E * sizeof(unsigned long long);
     EC_HIP(hipMalloc(&d->xch, d->xch_bytes));
-    EC_HIP(hipMemset(d->xch, 0, d->xch_bytes));
+    d->ffv_words = (size_t)2 * Lc * F;
+    EC_HIP(hipMalloc(&d->ffv, d->ffv_words * sizeof(float)));
+    EC_HIP(step_clear(d, nullptr));
+    EC_HIP(hipDeviceSynchronize());
     EC_HIP(hipMalloc(&d->d_step_io, 8 * sizeof(int)));
     EC_HIP(hipMemset(d->d_step_io, 0, 8 * sizeof(int)));
     EC_HIP(hipHostMalloc((void **)&d->h_step_io, 8 * sizeof(int), hipHostMallocDefault));
@@ -1269,7 +1282,7 @@ static int enqueue_step(GPT2 *g, DevModel *d, int max_npos, hipStream_t s) {
   aa.half = d->half;
   StepArgs sa{d->d_layers, g->wte, g->n_layer, g->n_embd, g->n_head, g->n_kv_head, d->F, g->eps, d->kv_layer,
               io, reinterpret_cast<const unsigned *>(io + 3), d->xch, d->x, io + 4, d->d_trace, aa,
-              (int)(step_attn_area(max_npos, vtile) / sizeof(float))};
+              (int)(step_attn_area(max_npos, vtile) / sizeof(float)), d->ffv};
   const size_t lds = step_lds(g, d, max_npos, vtile);
   // decode_step is a cooperative launch (not through klaunch): its profiler
   // events are recorded on the stream around it
@@ -1471,6 +1484,8 @@ static int step_timed_out(DevModel *d) {
   int *io = d->h_step_io;
   io[4] = 0;
   if (hipMemset(d->d_step_io + 4, 0, sizeof(int)) != hipSuccess) return 0;
+  // the redo must not find FFN words of the abandoned launch
+  if (step_clear(d, nullptr) != hipSuccess || hipDeviceSynchronize() != hipSuccess) return 0;
   if (g_step_coop) return 0;
   g_step_coop = true;
   if (d->step_graph) (void)hipGraphExecDestroy(d->step_graph);
@@ -1561,7 +1576,7 @@ static int forward_impl(GPT2 *g, const int *tokens, const int *positions, const 
     io[1] = st[d->mmax];
     io[2] = st[2 * d->mmax];
     if (++d->step_tag == 0) {  // after 2^32 steps: clear the words of the old tags
-      EC_HIP(hipMemsetAsync(d->xch, 0, d->xch_bytes, s));
+      EC_HIP(step_clear(d, s));
       d->step_tag = 1;
     }
     io[3] = (int)d->step_tag;
@@ -1784,7 +1799,7 @@ extern "C" int ec_generate_greedy(GPT2 *g, int token, int pos, int slot, int n, 
   }
   hipStream_t s = g_stream;
   if (d->step_tag > 0xFFFFFFFFu - (unsigned)n - 1u) {  // the tags below must not wrap: clear the old ones
-    EC_HIP(hipMemsetAsync(d->xch, 0, d->xch_bytes, s));
+    EC_HIP(step_clear(d, s));
     d->step_tag = 0;
   }
   int *io = d->h_step_io;

@@ -6,9 +6,10 @@
 // 1-9 MB each; each launch starts with a cold weight stream and pays the
 // dispatch between kernels.  Here one launch runs all layers.  Blocks hand
 // their results to each other through tagged 64-bit words -- (float value,
-// step tag) written with one device-coherent store -- and a consumer issues
-// its phase's weight loads before it waits for the words of its input, so
-// the weight stream overlaps the wait instead of following it.
+// step tag) written with one device-coherent store; the FFN activation
+// through plain fp32 words in a half of a double buffer (ff_rearm) -- and a
+// consumer issues its phase's weight loads before it waits for the words of
+// its input, so the weight stream overlaps the wait instead of following it.
 //
 // Grid: kStepBlocks blocks of kStepThreads threads, one per CU (a plain
 // launch on an idle device, or a cooperative one: all blocks resident, so the

@@ -340,10 +340,16 @@ __host__ __device__ constexpr inline int attn_sswz(int hs) { return hs <= 16 ? 0
 // PREK (the persistent step): the K rows of positions [lo, lo + min(n - 1,
 // KQ)) are already in the K tile (attn_prefetch_k, waited for by the caller
 // before its last barrier); the body loads and writes only the rest.
-template <int HD, bool FUSED, int NS, bool SCORED = false, bool PREK = false, class Out>
+// mk(e) (optional) is called by every thread at phase boundaries, for a
+// caller's timestamps: 0 the scores start, 1 the softmax starts, 2 the
+// products and sums start.
+struct NoMark {
+  __device__ void operator()(int) const {}
+};
+template <int HD, bool FUSED, int NS, bool SCORED = false, bool PREK = false, class Out, class Mark = NoMark>
 __device__ __forceinline__ void attn_decode_block(const AttnArgs &a, int m, int h, int slice, const float *qrow,
                                                   const float *krow, const float *vrow, float *lds, Out &&out,
-                                                  size_t coff = 0) {
+                                                  size_t coff = 0, Mark mk = Mark{}) {
   static_assert(NS == 1 || (HD == 64 && (NS == 2 || NS == 4 || NS == 8)), "element slices: head_dim 64, 2 / 4 / 8");
   static_assert(!(SCORED && FUSED), "the scores pass appends the new k / v");
   // threads per block: 512 with element slices (one scored position per
@@ -534,6 +540,7 @@ __device__ __forceinline__ void attn_decode_block(const AttnArgs &a, int m, int 
   load_v(0);
   __syncthreads();
 
+  mk(0);
   // ---- 4. scores ----
   auto put = [&](int i, float s) {
     s = (float)((double)s * a.inv_hd);
@@ -595,6 +602,7 @@ __device__ __forceinline__ void attn_decode_block(const AttnArgs &a, int m, int 
       put(i, (FUSED && i == n - 1) ? dot_new_k<HD>(qs, kn, hd) : dot_k_row<HD>(qs, K + (size_t)i * a.kv, hd));
   }
   }  // !SCORED
+  mk(1);
   mx = block_max_1b<NT / 64>(mx, redf);
   // this thread's first two values stay in registers until the sum is known
   // (positions below 512); further ones go through LDS
@@ -623,6 +631,7 @@ __device__ __forceinline__ void attn_decode_block(const AttnArgs &a, int m, int 
   }
   for (int i = t + 2 * NT; i < n; i += NT) sc[i] = (float)((double)sc[i] * isum);
 
+  mk(2);
   // ---- 5. products p*v, and the sequential sums ----
   // element d of quad q sits in 16-byte slot q*P + (d ^ ((d >> 4) & sw)); with
   // P and sw from attn_pitch/attn_swz every 16 consecutive lanes of the

@@ -424,7 +424,7 @@ __device__ void attention_loop(const StepArgs &a, int head, int slice, unsigned 
     const int o0 = hh * 64 + 16 * ss;
     attn_decode_block<64, true, kStepSlices, false, true>(a.attn, 0, hh, ss, qkv_s, qkv_s + 64, qkv_s + 128, lds,
                                              [&](int i, float o) { put_word(att + o0 + i, o, tag); },
-                                             a.kv_layer * l);
+                                             a.kv_layer * l, [&](int e) { mark<TRACE>(a, b, l, 15 + e); });
     __syncthreads();  // the body's LDS is reused by the next layer
     mark<TRACE>(a, b, l, 3);
     if (l + 1 < a.L) {

@@ -223,9 +223,10 @@ constexpr int kStepBlocks = 256, kStepThreads = 512, kStepSlices = 4;
 // blocks), 2 q/k/v rows done, 3 attention done, 4 attention output gathered,
 // 5 o done, 6 x_mid gathered, 7 gate/up done, 8 FFN activation gathered,
 // 9 down done, 10 x_mid normalized and quantized, 11 x normalized and
-// quantized (attention blocks), 12 FFN activation received (before its
-// quantization), 13 attention output received (before its quantization)
-constexpr int kStepEvents = 14;
+// quantized (attention blocks), 12 FFN activation received and quantized,
+// 13 attention output received (before its quantization), 14 unused, 15-17
+// inside the attention body: scores start, softmax starts, products start
+constexpr int kStepEvents = 18;
 struct StepLayer {
   const float *ln1_g, *ln2_g;
   const int8_t *wqkv;  // [E + 2 kv][E]: q | k | v rows

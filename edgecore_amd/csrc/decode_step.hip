@@ -349,12 +349,20 @@ __device__ float block_norm_quant(const float *xs, int K, const float *g, double
   }
   mx = block_max_1b<kNW>(mx, red);
   const float sc = quant_scale(mx);
-  const bool fast = ec_quant_rcp_ok(sc);
-  const float rcp = 1.0f / sc;
+  // one branch per block (sc is uniform), not a select per element
+  if (ec_quant_rcp_ok(sc)) {
+    const float rcp = 1.0f / sc;
 #pragma unroll
-  for (int j = 0; j < 2; j++) {
-    const int i = t + kStepThreads * j;
-    if (i < K) codes[i] = fast ? ec_quant1_rcp(y[j], sc, rcp) : quant1(y[j], sc);
+    for (int j = 0; j < 2; j++) {
+      const int i = t + kStepThreads * j;
+      if (i < K) codes[i] = ec_quant1_rcp(y[j], sc, rcp);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const int i = t + kStepThreads * j;
+      if (i < K) codes[i] = quant1(y[j], sc);
+    }
   }
   __syncthreads();
   return sc;

@@ -445,6 +445,10 @@ __device__ __forceinline__ void attn_decode_block(const AttnArgs &a, int m, int 
       }
     }
   };
+  // PREK with the whole context in one product tile: the product threads read
+  // V from the V tile in LDS (attn_prefetch_v) instead of loading registers
+  const bool vpre = PREK && HD == 64 && NS > 1 && n <= T;
+  const v4u *vtl = reinterpret_cast<const v4u *>(reinterpret_cast<const char *>(prod) + step_vtile_off(T, a.kv));
   float mx = -FLT_MAX;
   if constexpr (SCORED) {
     // V of the first tile, then the scores into LDS and their maximum
@@ -537,7 +541,7 @@ __device__ __forceinline__ void attn_decode_block(const AttnArgs &a, int m, int 
   if (HD > 0 && n > KQ) load_k(KQ);
   // the product threads' V loads go out after the K rows are written, so no
   // wait before this point counts them; scores and softmax cover their latency
-  load_v(0);
+  if (!vpre) load_v(0);
   __syncthreads();
 
   mk(0);
@@ -700,6 +704,10 @@ __device__ __forceinline__ void attn_decode_block(const AttnArgs &a, int m, int 
             const int qd = stage_lo(s) + QPU * u + pt / CPRV, cd = pt % CPRV;
             v4u *vu = vr[min(s, NSTG - 1) * UPS + u];
             if (s < nst && 4 * qd < cnt && qd < stage_lo(s + 1)) {
+              if (vpre) {
+#pragma unroll
+                for (int e = 0; e < 4; e++) vu[e] = vtl[(e * (T / 4) + qd) * CPRV + cd];
+              }
               if (FUSED) {
                 // the token's own position takes the fp16-rounded new v (one lane)
                 const int en = n - 1 - t0 - 4 * qd;
@@ -786,6 +794,44 @@ __device__ __forceinline__ void attn_prefetch_k(const AttnArgs &a, int m, int h,
     for (int i = wave; i < rows; i += NT / 64)
       __builtin_amdgcn_global_load_lds((gvoid *)(K + (size_t)i * a.kv + 8 * lane), (lvoid *)(tile + (size_t)i * KP * 16),
                                        16, 0, 0);
+  }
+}
+
+// For the same body: chunk c (c < 2) of this block's element slice of the V
+// rows of positions [lo, lo + min(n - 1, T)) into the V tile (16-byte slot
+// ((e * T / 4 + q) * 2 + c) for position 4 q + e, past the K tile and the
+// products, step_vtile_off).  One instruction covers 32 quads of one e, each
+// lane one chunk; lanes past the positions load nothing.  As
+// attn_prefetch_k: every thread calls it, the caller waits and then passes a
+// barrier.
+template <int HD, int NS>
+__device__ __forceinline__ void attn_prefetch_v(const AttnArgs &a, int m, int h, int slice, float *lds,
+                                                size_t coff = 0) {
+  static_assert(HD == 64 && NS == 4, "element slices of 16 of head_dim 64");
+  constexpr int NT = 512, CPRV = HD / 8 / NS;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int pos = ld_uniform(a.pos + m), slot = ld_uniform(a.slot + m);
+  int lo = 0;
+  if (a.window > 0) {
+    lo = pos - a.window + 1;
+    if (lo < 0) lo = 0;
+  }
+  const int n = pos + 1 - lo, T = a.vtile, QM = T / 4;
+  if (n > T) return;  // the body then loads V into registers
+  const int rows = n - 1;
+  const int kvh = h * a.KVH / a.H;
+  const uint16_t *V = a.vc + coff + (size_t)slot * a.C * a.kv + (size_t)kvh * HD + (size_t)lo * a.kv;
+  char *vt = reinterpret_cast<char *>(lds + 3 * HD + ((a.max_npos + 3) & ~3)) + step_vtile_off(T, a.kv);
+  typedef __attribute__((address_space(1))) void gvoid;
+  typedef __attribute__((address_space(3))) void lvoid;
+  const int qd = lane / CPRV, cd = lane % CPRV;  // within an instruction's 32 quads
+  for (int e = 0; e < 4; e++) {
+    for (int q0 = 32 * wave; 4 * q0 + e < rows; q0 += 32 * (NT / 64)) {
+      const int p = 4 * (q0 + qd) + e;
+      if (p < rows)
+        __builtin_amdgcn_global_load_lds((gvoid *)(V + (size_t)p * a.kv + 8 * (CPRV * slice + cd)),
+                                         (lvoid *)(vt + (size_t)(e * QM + q0) * CPRV * 16), 16, 0, 0);
+    }
   }
 }
 

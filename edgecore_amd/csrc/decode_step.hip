@@ -384,7 +384,6 @@ __device__ void attention_loop(const StepArgs &a, int head, int slice, unsigned 
   int8_t *codes = reinterpret_cast<int8_t *>(xs + E);
   v4i w[3][7];
   float ws[3], gam[2];
-  int sink = 0;
   auto load_layer = [&](int l) {
     const StepLayer &W = a.layers[l];
     const int t = tid_opaque(), grp = t >> 3, sub = t & 7;
@@ -402,6 +401,7 @@ __device__ void attention_loop(const StepArgs &a, int head, int slice, unsigned 
   };
   load_layer(0);
   attn_prefetch_k<64, kStepSlices>(a.attn, 0, uniform_opaque(head), lds, 0);
+  attn_prefetch_v<64, kStepSlices>(a.attn, 0, uniform_opaque(head), uniform_opaque(slice), lds, 0);
   for (int l = 0; l < a.L; l++) {
     mark<TRACE>(a, b, l, 0);
     const int t = tid_opaque(), grp = t >> 3, sub = t & 7;
@@ -437,17 +437,12 @@ __device__ void attention_loop(const StepArgs &a, int head, int slice, unsigned 
     mark<TRACE>(a, b, l, 3);
     if (l + 1 < a.L) {
       load_layer(l + 1);
-      // the next layer's K rows into the K tile (its first KQ positions)
+      // the next layer's K rows into the K tile (its first KQ positions) and
+      // this slice's V rows into the V tile
       attn_prefetch_k<64, kStepSlices>(a.attn, 0, hh, lds, a.kv_layer * (l + 1));
-      // V rows [0, pos) of the group in the next layer: one 4-byte load per
-      // 128-byte line (a V row is 128 bytes)
-      const int pos = ld_uniform(a.attn.pos), slot = ld_uniform(a.attn.slot);
-      const size_t base = a.kv_layer * (l + 1) + (size_t)slot * a.attn.C * kv + (size_t)kvh * 64;
-      const auto vc = gbl(reinterpret_cast<const int *>(a.attn.vc + base));
-      for (int p = t; p < pos; p += kStepThreads) sink ^= vc[(size_t)p * kv / 2];
+      attn_prefetch_v<64, kStepSlices>(a.attn, 0, hh, ss, lds, a.kv_layer * (l + 1));
     }
   }
-  if (sink == 0x7fffffff && tag == 0) red[0] = (float)sink;  // keeps the touches (tag is never 0)
 }
 
 // The o / down blocks' loop (block gi): per layer the o rows [r0, r0 + kODRows)

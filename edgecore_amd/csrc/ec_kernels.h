@@ -298,6 +298,18 @@ __host__ __device__ constexpr inline int attn_swz(int hd, int kv) {
   (void)kv;
   return hd == 32 ? 1 : hd == 64 ? 3 : hd == 128 ? 7 : 0;
 }
+
+// The persistent step's attention body (head_dim 64, element slices of 16)
+// keeps the V rows of its slice for the first product tile of T positions
+// in LDS (attn_prefetch_v): 16-byte slot ((e * T / 4 + q) * 2 + c) holds
+// chunk c of position 4 q + e.  Its offset in bytes from the product area's
+// start: past the K tile's capacity (KQ rows of 144 bytes) and the slice
+// products' extent (T / 4 + 32 quads of 17 slots).
+__host__ __device__ constexpr inline size_t step_vtile_off(int T, int kv) {
+  const int kq = (T / 4) * attn_pitch(64, kv) / 9;
+  const size_t k = (size_t)(kq < 512 ? kq : 512) * 144, p = ((size_t)T / 4 + 32) * 17 * 16;
+  return ((k > p ? k : p) + 255) & ~(size_t)255;
+}
 // dynamic LDS of a launch: q, new k, new v, max_npos scores, the product tile
 size_t attention_lds_bytes(int max_npos, int hd, int vtile);
 // largest vtile the kernel accepts for this head_dim / KV row length

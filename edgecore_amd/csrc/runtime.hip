@@ -1218,9 +1218,20 @@ static int attn_vtile(int max_npos, int hd, int kv) {
 // LDS the persistent step reserves outside the dynamic area (its static arrays)
 constexpr size_t kStepStaticLds = 4096;
 
+// the attention area of the step's dynamic LDS (the attention kernel's
+// layout, with room for the prefetched V tile), rounded to 16 bytes; the
+// attention blocks' row and codes follow it
+static size_t step_attn_area(int max_npos, int vtile, int kv) {
+  const size_t a = attention_lds_bytes(max_npos, 64, vtile);
+  const size_t prod = (3 * 64 + (size_t)((max_npos + 3) & ~3)) * sizeof(float);
+  const size_t v = prod + step_vtile_off(vtile, kv) + (size_t)vtile * 32;
+  return ((a > v ? a : v) + 15) & ~(size_t)15;
+}
+
 // the attention product tile of the persistent step for max_npos positions
-// (attn_vtile with the step's static LDS set aside)
-static int step_vtile(int max_npos, int E) {
+// (attn_vtile with the step's static LDS and the attention blocks' row set
+// aside, and room for the V tile)
+static int step_vtile(int max_npos, int E, int kv) {
   const size_t budget = (size_t)g_max_lds - kStepStaticLds - step_norm_bytes(E);
   const size_t lds_fixed = attention_lds_bytes(max_npos, 64, 0);
   if (lds_fixed >= budget) return 0;
@@ -1228,17 +1239,12 @@ static int step_vtile(int max_npos, int E) {
   const size_t cap = (size_t)attention_max_vtile(64, 128);
   int vtile = (int)(room < cap ? room : cap) & ~3;
   if (vtile > ((max_npos + 3) & ~3)) vtile = (max_npos + 3) & ~3;
+  while (vtile >= 4 && step_attn_area(max_npos, vtile, kv) > budget) vtile -= 4;
   return vtile;
 }
 
-// the attention area of the step's dynamic LDS, rounded to 16 bytes; the
-// attention blocks' row and codes follow it
-static size_t step_attn_area(int max_npos, int vtile) {
-  return (attention_lds_bytes(max_npos, 64, vtile) + 15) & ~(size_t)15;
-}
-
 static size_t step_lds(const GPT2 *g, const DevModel *d, int max_npos, int vtile) {
-  const size_t a = step_attn_area(max_npos, vtile) + step_norm_bytes(g->n_embd),
+  const size_t a = step_attn_area(max_npos, vtile, g->n_kv_embd) + step_norm_bytes(g->n_embd),
                b = decode_step_scratch_bytes(g->n_embd, d->F);
   return a > b ? a : b;
 }
@@ -1255,7 +1261,7 @@ static double step_bytes(const GPT2 *g, const DevModel *d, int npos) {
 // The layers of a one-token forward as one persistent launch (decode_step.hip);
 // x after the last layer lands in d->x.
 static int enqueue_step(GPT2 *g, DevModel *d, int max_npos, hipStream_t s) {
-  const int vtile = step_vtile(max_npos, g->n_embd);
+  const int vtile = step_vtile(max_npos, g->n_embd, g->n_kv_embd);
   if (vtile < 4) return set_err(-1, "decode step: position %d does not fit the LDS", max_npos - 1);
   if (!d->chaining)  // a chained step's inputs were written by the previous step
     EC_HIP(hipMemcpyAsync(d->d_step_io, d->h_step_io, 4 * sizeof(int), hipMemcpyHostToDevice, s));
@@ -1282,7 +1288,7 @@ static int enqueue_step(GPT2 *g, DevModel *d, int max_npos, hipStream_t s) {
   aa.half = d->half;
   StepArgs sa{d->d_layers, g->wte, g->n_layer, g->n_embd, g->n_head, g->n_kv_head, d->F, g->eps, d->kv_layer,
               io, reinterpret_cast<const unsigned *>(io + 3), d->xch, d->x, io + 4, d->d_trace, aa,
-              (int)(step_attn_area(max_npos, vtile) / sizeof(float)), d->ffv};
+              (int)(step_attn_area(max_npos, vtile, g->n_kv_embd) / sizeof(float)), d->ffv};
   const size_t lds = step_lds(g, d, max_npos, vtile);
   // decode_step is a cooperative launch (not through klaunch): its profiler
   // events are recorded on the stream around it
@@ -1563,7 +1569,7 @@ static int forward_impl(GPT2 *g, const int *tokens, const int *positions, const 
   if (bucket > d->eff_ctx) bucket = d->eff_ctx;
   if (tk && !topk_ok(V, tk->top_k))
     return set_err(-1, "top_k=%d outside (0, %d) or above %d", tk->top_k, V, kTopkMax);
-  const bool step = M == 1 && lm_from == 0 && d->step_ok && step_vtile(max_npos, g->n_embd) >= 4;
+  const bool step = M == 1 && lm_from == 0 && d->step_ok && step_vtile(max_npos, g->n_embd, g->n_kv_embd) >= 4;
   if (step) {
     // one token through the persistent step: its inputs and the step's tag
     // into the pinned I/O block, then -- for a greedy step without logits --
@@ -1582,7 +1588,7 @@ static int forward_impl(GPT2 *g, const int *tokens, const int *positions, const 
     io[3] = (int)d->step_tag;
     io[4] = io[5] = 0;
     bool graph = argmax && !logits && !tk && !g_prof_on && g_use_graphs && !d->step_nograph &&
-                 step_vtile(bucket, g->n_embd) >= 4;
+                 step_vtile(bucket, g->n_embd, g->n_kv_embd) >= 4;
     if (graph && (!d->step_graph || d->step_bucket != bucket)) {
       if (d->step_graph) {
         EC_HIP(hipGraphExecDestroy(d->step_graph));
@@ -1787,7 +1793,7 @@ extern "C" int ec_generate_greedy(GPT2 *g, int token, int pos, int slot, int n, 
     return set_err(-1, "ec_generate_greedy: positions %d..%d outside [0, %d)", pos, pos + n - 1, d->eff_ctx);
   if (slot < 0) return set_err(-1, "ec_generate_greedy: negative slot %d", slot);
   if (slot >= g->batch_cap) slot = g->batch_cap - 1;  // as the forward (src/gpt2.c:512-513)
-  if (!d->step_ok || g_prof_on || step_vtile(pos + n, g->n_embd) < 4) {
+  if (!d->step_ok || g_prof_on || step_vtile(pos + n, g->n_embd, g->n_kv_embd) < 4) {
     int t = token;
     for (int k = 0; k < n; k++) {
       const int p = pos + k;
@@ -1816,7 +1822,7 @@ extern "C" int ec_generate_greedy(GPT2 *g, int token, int pos, int slot, int n, 
     // kChainBurst steps in one graph when their positions stay in the bucket
     const int len = (n - k >= kChainBurst && bucket - (pos + k) >= kChainBurst) ? kChainBurst : 1;
     const int gi = len == 1 ? 0 : 1;
-    bool graph = g_use_graphs && !d->step_nograph && step_vtile(bucket, g->n_embd) >= 4;
+    bool graph = g_use_graphs && !d->step_nograph && step_vtile(bucket, g->n_embd, g->n_kv_embd) >= 4;
     if (graph && (!d->chain_graph[gi] || d->chain_bucket[gi] != bucket)) {
       if (d->chain_graph[gi]) {
         EC_HIP(hipGraphExecDestroy(d->chain_graph[gi]));

@@ -346,10 +346,26 @@ __host__ __device__ constexpr inline int attn_sswz(int hs) { return hs <= 16 ? 0
 struct NoMark {
   __device__ void operator()(int) const {}
 };
+// The RoPE table entry that thread t's element uses (FUSED: rotated elements
+// their pair's index, the others entry 0; rot = the rotated half or 0).
+__device__ __forceinline__ int attn_rope_entry(int t, int hd, int rot) {
+  const int tt = min(t, hd - 1);
+  const bool rr = tt < 2 * rot;
+  const int i0 = rr ? (tt < rot ? tt : tt - rot) : tt;
+  return rr ? i0 : 0;
+}
+// Values a caller that runs the body for one token many times (the
+// persistent step, once per layer) keeps in LDS: the 2^(i/32) table of
+// ec_expf_tab, and thread t's (cos, sin) at the token's position, cs[t] =
+// a.cs[pos * half + attn_rope_entry(t, hd, rot)] for t < hd.
+struct AttnPre {
+  const uint64_t *etab;
+  const double2 *cs;
+};
 template <int HD, bool FUSED, int NS, bool SCORED = false, bool PREK = false, class Out, class Mark = NoMark>
 __device__ __forceinline__ void attn_decode_block(const AttnArgs &a, int m, int h, int slice, const float *qrow,
                                                   const float *krow, const float *vrow, float *lds, Out &&out,
-                                                  size_t coff = 0, Mark mk = Mark{}) {
+                                                  size_t coff = 0, Mark mk = Mark{}, const AttnPre *pre = nullptr) {
   static_assert(NS == 1 || (HD == 64 && (NS == 2 || NS == 4 || NS == 8)), "element slices: head_dim 64, 2 / 4 / 8");
   static_assert(!(SCORED && FUSED), "the scores pass appends the new k / v");
   // threads per block: 512 with element slices (one scored position per
@@ -364,7 +380,9 @@ __device__ __forceinline__ void attn_decode_block(const AttnArgs &a, int m, int 
   constexpr int CPRV = HD > 0 ? CPR / NS : 1;  // 16-byte V chunks per slice
   const int t = tid_opaque();
   const int pos = ld_uniform(a.pos + m), slot = ld_uniform(a.slot + m);
-  const uint64_t et = ec_exp2_32[t & 31];
+  uint64_t et = 0;
+  if (!pre) et = ec_exp2_32[t & 31];
+  const uint64_t *etp = pre ? pre->etab : etab;
   const int kvh = h * a.KVH / a.H;
   int lo = 0;
   if (a.window > 0) {
@@ -401,7 +419,7 @@ __device__ __forceinline__ void attn_decode_block(const AttnArgs &a, int m, int 
     ka = krow[i0];
     kb = krow[i1];
     vv = vrow[tt];
-    if (rot) c2 = a.cs[(size_t)pos * a.half + (rr ? i0 : 0)];
+    if (rot) c2 = pre ? pre->cs[tt] : a.cs[(size_t)pos * a.half + (rr ? i0 : 0)];
   }
 
   // ---- 2. K rows of the first KQ positions ----
@@ -452,7 +470,7 @@ __device__ __forceinline__ void attn_decode_block(const AttnArgs &a, int m, int 
   float mx = -FLT_MAX;
   if constexpr (SCORED) {
     // V of the first tile, then the scores into LDS and their maximum
-    if (t < 32) etab[t] = et;
+    if (!pre && t < 32) etab[t] = et;
     load_v(0);
     const float *src = a.scores + ((size_t)m * a.H + h) * a.sc_ld;
     for (int i = t; i < n; i += NT) {
@@ -476,7 +494,7 @@ __device__ __forceinline__ void attn_decode_block(const AttnArgs &a, int m, int 
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- 3. RoPE, fp16 rounding of the new k/v, cache append ----
-  if (t < 32) etab[t] = et;
+  if (!pre && t < 32) etab[t] = et;
   if (t < hd) {
     float qv = qa, kv_ = ka;
     if (rr) {
@@ -617,12 +635,12 @@ __device__ __forceinline__ void attn_decode_block(const AttnArgs &a, int m, int 
     const int i = t + NT * k;
     ev[k] = 0.0f;
     if (i < n) {
-      ev[k] = ec_expf_tab(sc[i] - mx, etab);
+      ev[k] = ec_expf_tab(sc[i] - mx, etp);
       sum += (double)ev[k];
     }
   }
   for (int i = t + 2 * NT; i < n; i += NT) {
-    const float e = ec_expf_tab(sc[i] - mx, etab);
+    const float e = ec_expf_tab(sc[i] - mx, etp);
     sc[i] = e;
     sum += (double)e;
   }

@@ -376,7 +376,7 @@ __device__ float block_norm_quant(const float *xs, int K, const float *g, double
 // so that they come from L2 when it runs.
 template <bool TRACE>
 __device__ void attention_loop(const StepArgs &a, int head, int slice, unsigned tag, int tok, float *lds,
-                               float *qkv_s, float *red) {
+                               float *qkv_s, float *red, const uint64_t *etab) {
   const int b = blockIdx.x;
   const int E = a.E, kv = 64 * a.KVH, kvh = head * a.KVH / a.H;
   const size_t S = (size_t)3 * E;
@@ -402,6 +402,17 @@ __device__ void attention_loop(const StepArgs &a, int head, int slice, unsigned 
   load_layer(0);
   attn_prefetch_k<64, kStepSlices>(a.attn, 0, uniform_opaque(head), lds, 0);
   attn_prefetch_v<64, kStepSlices>(a.attn, 0, uniform_opaque(head), uniform_opaque(slice), lds, 0);
+  // the token's RoPE (cos, sin) per element, the same in every layer, kept in
+  // LDS (the norm's barriers publish it before the first use); the exp
+  // table is the block's copy of the SiLU table
+  __shared__ double2 cs_s[64];
+  {
+    const int t = threadIdx.x, rot = a.attn.cs ? a.attn.half : 0;
+    if (t < 64)
+      cs_s[t] = rot ? a.attn.cs[(size_t)ld_uniform(a.attn.pos) * a.attn.half + attn_rope_entry(t, 64, rot)]
+                    : make_double2(1.0, 0.0);
+  }
+  const AttnPre pre{etab, cs_s};
   for (int l = 0; l < a.L; l++) {
     mark<TRACE>(a, b, l, 0);
     const int t = tid_opaque(), grp = t >> 3, sub = t & 7;
@@ -432,7 +443,7 @@ __device__ void attention_loop(const StepArgs &a, int head, int slice, unsigned 
     const int o0 = hh * 64 + 16 * ss;
     attn_decode_block<64, true, kStepSlices, false, true>(a.attn, 0, hh, ss, qkv_s, qkv_s + 64, qkv_s + 128, lds,
                                              [&](int i, float o) { put_word(att + o0 + i, o, tag); },
-                                             a.kv_layer * l, [&](int e) { mark<TRACE>(a, b, l, 15 + e); });
+                                             a.kv_layer * l, [&](int e) { mark<TRACE>(a, b, l, 15 + e); }, &pre);
     __syncthreads();  // the body's LDS is reused by the next layer
     mark<TRACE>(a, b, l, 3);
     if (l + 1 < a.L) {
@@ -624,7 +635,7 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepArgs a) {
   const int rpg = a.H / a.KVH, na = rpg * kStepSlices;
   const int xcd = b & 7, jx = b >> 3;
   if (xcd < a.KVH && jx < na) {
-    attention_loop<TRACE>(a, xcd * rpg + jx / kStepSlices, jx % kStepSlices, tag, tok, lds, qkv_s, red);
+    attention_loop<TRACE>(a, xcd * rpg + jx / kStepSlices, jx % kStepSlices, tag, tok, lds, qkv_s, red, etab[0]);
   } else {
     int before = 0;  // attention blocks with a lower index
     for (int x = 0; x < a.KVH; x++) before += b > x ? min(na, (b - x + 7) / 8) : 0;

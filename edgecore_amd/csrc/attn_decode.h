@@ -626,32 +626,18 @@ __device__ __forceinline__ void attn_decode_block(const AttnArgs &a, int m, int 
   }  // !SCORED
   mk(1);
   mx = block_max_1b<NT / 64>(mx, redf);
-  // this thread's first two values stay in registers until the sum is known
-  // (positions below 512); further ones go through LDS
+  // e = expf(s - max) replaces each score in LDS; the sum's barrier publishes
+  // them, and the threads that form the products turn them into the
+  // probabilities p = (float)(e * (1 / sum)) as they read them (no separate
+  // normalization pass and barrier)
   double sum = 0.0;
-  float ev[2];
-#pragma unroll
-  for (int k = 0; k < 2; k++) {
-    const int i = t + NT * k;
-    ev[k] = 0.0f;
-    if (i < n) {
-      ev[k] = ec_expf_tab(sc[i] - mx, etp);
-      sum += (double)ev[k];
-    }
-  }
-  for (int i = t + 2 * NT; i < n; i += NT) {
+  for (int i = t; i < n; i += NT) {
     const float e = ec_expf_tab(sc[i] - mx, etp);
     sc[i] = e;
     sum += (double)e;
   }
   sum = block_sum_1b<NT / 64>(sum, redd);
   const double isum = 1.0 / sum;
-#pragma unroll
-  for (int k = 0; k < 2; k++) {
-    const int i = t + NT * k;
-    if (i < n) sc[i] = (float)((double)ev[k] * isum);
-  }
-  for (int i = t + 2 * NT; i < n; i += NT) sc[i] = (float)((double)sc[i] * isum);
 
   mk(2);
   // ---- 5. products p*v, and the sequential sums ----
@@ -704,7 +690,7 @@ __device__ __forceinline__ void attn_decode_block(const AttnArgs &a, int m, int 
   for (int t0 = 0; t0 < n; t0 += T) {
     const int cnt = min(T, n - t0);
     const int nq = cnt >> 2;  // complete quads
-    __syncthreads();  // probabilities written / previous tile's sums done
+    if (t0 > 0) __syncthreads();  // the previous tile's sums are done (the first tile: the sum's barrier)
     if constexpr (HD > 0) {
       // Stage s: the product threads form the products of their UPS units of
       // stage s (quads [stage_lo(s), stage_lo(s+1))) while the summing lanes
@@ -741,8 +727,9 @@ __device__ __forceinline__ void attn_decode_block(const AttnArgs &a, int m, int 
                     if (e == en) vu[e] = nv;
                 }
               }
-              const float4 pq = *reinterpret_cast<const float4 *>(sc + t0 + 4 * qd);
-              const float pe[4] = {pq.x, pq.y, pq.z, pq.w};
+              const float4 eq = *reinterpret_cast<const float4 *>(sc + t0 + 4 * qd);
+              const float pe[4] = {(float)((double)eq.x * isum), (float)((double)eq.y * isum),
+                                   (float)((double)eq.z * isum), (float)((double)eq.w * isum)};
               float pr[8][4];
 #pragma unroll
               for (int e = 0; e < 4; e++) {
@@ -769,7 +756,8 @@ __device__ __forceinline__ void attn_decode_block(const AttnArgs &a, int m, int 
       for (int e = t; e < cnt * hd; e += NT) {
         const int i = e / hd, d = e - i * hd;
         const float v = (FUSED && t0 + i == n - 1) ? vn[d] : h2f(V[(size_t)(t0 + i) * a.kv + d]);
-        prod[((size_t)(i >> 2) * P + (d ^ ((d >> 4) & sw))) * 4 + (i & 3)] = sc[t0 + i] * v;
+        const float p = (float)((double)sc[t0 + i] * isum);
+        prod[((size_t)(i >> 2) * P + (d ^ ((d >> 4) & sw))) * 4 + (i & 3)] = p * v;
       }
       __syncthreads();
       if (t < hd) {

@@ -512,8 +512,23 @@ __global__ __launch_bounds__(256) void split_kernel(const float *x, int ldx, int
 // are summed through LDS in wave order (exact for int32) and the block
 // applies the epilogue: for int8 the same int32 dots and epilogue code as
 // gemm_mfma_kernel, so the same floats; for 16-bit weights the same class of
-// fp32 sums.  No workspace, no atomics.
+// fp32 sums.
+//
+// Split K (int8 only): when the column tiles alone leave most CUs idle
+// (down, o and q|k|v at batch 16), gridDim.y blocks share a column group,
+// each taking a contiguous range of K steps.  Each writes its int32 tile
+// to sk_part, and the last of them to arrive (a counter per column group,
+// reset by that block, so every launch finds it at zero) adds the gridDim.y
+// tiles and applies the epilogue.  int32 sums are exact in any order, so the
+// floats are the same as with one block per column group.  The workspace is
+// one per device and the launches that use it must not overlap (the forward
+// issues its linears on one stream).
 namespace {
+
+constexpr int kSkMaxGroups = 256;              // column groups of a split launch
+constexpr int kSkPartInts = 256 * 1024;        // int32 partial tiles of a split launch
+__device__ int sk_part[kSkPartInts];
+__device__ unsigned sk_cnt[kSkMaxGroups];
 
 template <int OP, int TI, int NJ, int EPI>
 __global__ __launch_bounds__(1024) void gemm_skinny_kernel(GemvArgs a) {
@@ -562,14 +577,17 @@ __global__ __launch_bounds__(1024) void gemm_skinny_kernel(GemvArgs a) {
 #pragma unroll
     for (int j = 0; j < NB; j++) acc[i][j] = Acc{0, 0, 0, 0};
 
-  // this wave's steps: wave, wave + nw, ... < ksteps, U at a time; bytes
-  // past the row read a clamped address and the A fragments are zeroed
-  for (int sb = wave; sb < ksteps; sb += nw * U) {
+  // this block's K steps [ks0, ks1) (all of them unless K is split)
+  const int kper = (ksteps + gridDim.y - 1) / gridDim.y;
+  const int ks0 = min(ksteps, kper * (int)blockIdx.y), ks1 = min(ksteps, ks0 + kper);
+  // this wave's steps: ks0 + wave, + nw, ... < ks1, U at a time; bytes past
+  // the row read a clamped address and the A fragments are zeroed
+  for (int sb = ks0 + wave; sb < ks1; sb += nw * U) {
     v4i fa[U][TI][NP], fb[U][NB];
 #pragma unroll
     for (int u = 0; u < U; u++) {
       const int st = sb + nw * u;  // uniform over the wave
-      if (st < ksteps) {
+      if (st < ks1) {
         const int kc = min(64 * st + 16 * lq, KB - 16);
 #pragma unroll
         for (int i = 0; i < TI; i++)
@@ -582,7 +600,7 @@ __global__ __launch_bounds__(1024) void gemm_skinny_kernel(GemvArgs a) {
 #pragma unroll
     for (int u = 0; u < U; u++) {
       const int st = sb + nw * u;
-      if (st < ksteps) {
+      if (st < ks1) {
         const bool in = 64 * st + 16 * lq < KB;
 #pragma unroll
         for (int i = 0; i < TI; i++)
@@ -606,20 +624,58 @@ __global__ __launch_bounds__(1024) void gemm_skinny_kernel(GemvArgs a) {
 #pragma unroll
     for (int j = 0; j < NB; j++) part[wave][i][j][lane] = acc[i][j];
   __syncthreads();
-  if (t >= 256 * TI * NO) return;
+  const bool outt = t < 256 * TI * NO;  // an output thread
   const int jo = t / (256 * TI), i = (t >> 8) % TI, r = (t >> 6) & 3;
   const int m = 16 * i + 4 * lq + r, n = n0 + 16 * jo + lr;
-  if (m >= M || n >= N) return;
   using Sum = std::conditional_t<I8, int, float>;
   constexpr int NS = SWI ? 2 : 1;
   Sum sum[NS];
 #pragma unroll
   for (int k = 0; k < NS; k++) {
     const int j = SWI ? k : jo;
-    Sum v = part[0][i][j][lane][r];
-    for (int w = 1; w < nw; w++) v = v + part[w][i][j][lane][r];
+    Sum v = 0;
+    if (outt) {
+      v = part[0][i][j][lane][r];
+      for (int w = 1; w < nw; w++) v = v + part[w][i][j][lane][r];
+    }
     sum[k] = v;
   }
+  if constexpr (I8) {
+    if (gridDim.y > 1) {
+      // split K: publish this block's tile; the group's last block adds them
+      constexpr int TS = 256 * TI * NO * NS;  // ints per tile
+      int *wp = sk_part + (size_t)blockIdx.x * gridDim.y * TS;
+      // Device-coherent stores and loads (they bypass the XCD's L2) and a
+      // wait for the stores' completion before the counter, instead of
+      // fences: a device-scope fence writes back the whole L2 (about 50 us
+      // per launch measured)
+      if (outt) {
+#pragma unroll
+        for (int k = 0; k < NS; k++)
+          __hip_atomic_store(wp + (size_t)blockIdx.y * TS + 256 * TI * NO * k + t, sum[k], __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+      }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __shared__ int s_last;
+      __syncthreads();
+      if (t == 0)
+        s_last = __hip_atomic_fetch_add(&sk_cnt[blockIdx.x], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                 gridDim.y - 1;
+      __syncthreads();
+      if (!s_last) return;
+      if (outt) {
+#pragma unroll
+        for (int k = 0; k < NS; k++) {
+          int v = 0;
+          for (int y = 0; y < (int)gridDim.y; y++) v += __hip_atomic_load(wp + (size_t)y * TS + 256 * TI * NO * k + t,
+                                                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          sum[k] = v;
+        }
+      }
+      if (t == 0) __hip_atomic_store(&sk_cnt[blockIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  if (!outt || m >= M || n >= N) return;
 
   // epilogue (the same code as gemm_mfma_kernel's)
   const float as = a.as[m];
@@ -650,24 +706,41 @@ __global__ __launch_bounds__(1024) void gemm_skinny_kernel(GemvArgs a) {
 }
 
 template <int OP, int TI, int NJ, int EPI>
-hipError_t launch_skinny_nj(const GemvArgs &a, int wpb, hipStream_t s) {
+hipError_t launch_skinny_nj(const GemvArgs &a, int wpb, int ksplit, hipStream_t s) {
   const int ksteps = (a.K * MfmaOp<OP>::EB + 63) / 64;
   constexpr int NO = EPI == EPI_SWIGLU ? 1 : NJ;
+  const int groups = (a.N + 16 * NJ - 1) / (16 * NJ);
+  if (ksplit < 1 || OP != OP_I8 || groups > kSkMaxGroups ||
+      (size_t)groups * ksplit * 256 * TI * NO * (EPI == EPI_SWIGLU ? 2 : 1) > (size_t)kSkPartInts)
+    ksplit = 1;
+  ksplit = min(ksplit, ksteps);
+  const int kper = (ksteps + ksplit - 1) / ksplit;
   // waves per block: two or more K steps each, 4 to 16 waves, and at least
   // 4 TI NO (the epilogue takes one thread per output of 16 TI rows x 16 NO)
-  if (wpb <= 0) wpb = min(16, max(4, ksteps / 2));
+  if (wpb <= 0) wpb = min(16, max(4, kper / 2));
   wpb = max(min(wpb, 16), 4 * TI * NO);
-  klaunch((gemm_skinny_kernel<OP, TI, NJ, EPI>), dim3((a.N + 16 * NJ - 1) / (16 * NJ)), dim3(64 * wpb), 0, s, a);
+  klaunch((gemm_skinny_kernel<OP, TI, NJ, EPI>), dim3(groups, ksplit), dim3(64 * wpb), 0, s, a);
   return hipGetLastError();
 }
 
-// four column tiles per block for wide outputs (at least 1024 of them), else one
+// four column tiles per block for wide outputs (at least 1024 of them), else
+// one.  int8 outputs of a long K (64 or more K steps: down at batch 16)
+// whose column groups fill less than about 3/4 of the CUs split K over up to
+// 8 blocks per group (four column tiles each, so that a block's activation
+// fragments serve 64 columns).  The split's publish-and-add round trip costs
+// ~3 us, more than it saves for K = 1536 (o and q|k|v at batch 16: 4.7 ->
+// 7.2-7.7 us measured); down (K = 8960) goes from 12.6 to 10.2 us.
 template <int OP, int TI, int EPI>
 hipError_t launch_skinny(const GemvArgs &a, int wpb, hipStream_t s) {
   if constexpr (EPI != EPI_SWIGLU && TI == 1) {
-    if (a.N >= 16 * 1024) return launch_skinny_nj<OP, TI, 4, EPI>(a, wpb, s);
+    if (a.N >= 16 * 1024) return launch_skinny_nj<OP, TI, 4, EPI>(a, wpb, 1, s);
+    if (OP == OP_I8 && (a.N + 15) / 16 < 192 && (a.K + 63) / 64 >= 64) {
+      const int ksteps = (a.K + 63) / 64, groups = (a.N + 63) / 64;
+      const int ks = min(8, min(256 / groups, ksteps / 4));
+      if (ks > 1) return launch_skinny_nj<OP, TI, 4, EPI>(a, wpb, ks, s);
+    }
   }
-  return launch_skinny_nj<OP, TI, 1, EPI>(a, wpb, s);
+  return launch_skinny_nj<OP, TI, 1, EPI>(a, wpb, 1, s);
 }
 
 template <int OP, int TI>

@@ -308,10 +308,15 @@ def test_gemm_fp16_matrix_core_row_scale_range(scale):
 # ------------------------------------------------------------------ skinny int8 GEMM (M <= 32)
 # bm=16 forces the batched-decode kernel: one block per 16 output columns,
 # MFMA fragments straight from global memory, K split over up to 16 waves
-# whose exact int32 partial tiles are summed through LDS.  Shapes give few
-# and many K steps per wave, row / column / K tails and both row fragments.
+# whose exact int32 partial tiles are summed through LDS.  Up to 16 rows with
+# K >= 4096 and fewer than 192 column tiles also split K over several blocks
+# per 64 columns (the last block to finish adds their int32 tiles):
+# (16, 8960, 1536), (16, 4864, 896), (1, 4864, 70), (9, 4112, 200) and
+# (16, 5008, 2900).  Shapes give few and many K steps per wave, row / column /
+# K tails and both row fragments.
 SKINNY_SHAPES = [(16, 8960, 1536), (16, 1536, 2048), (16, 4864, 896), (32, 8960, 300), (20, 1040, 200),
-                 (17, 16, 129), (1, 4864, 70), (25, 2048, 8960), (16, 896, 17000)]  # last: 4 tiles per block
+                 (17, 16, 129), (1, 4864, 70), (25, 2048, 8960), (16, 896, 17000),  # 4 tiles per block
+                 (9, 4112, 200), (16, 5008, 2900)]
 
 
 @pytest.mark.parametrize("M,K,N", SKINNY_SHAPES)

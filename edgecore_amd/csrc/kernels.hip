@@ -161,6 +161,93 @@ __global__ __launch_bounds__(256) void norm_kernel(const float *x, int E, const 
   }
 }
 
+// The same arithmetic per element for rows of E % 4 == 0 (16-byte aligned
+// rows, gamma and beta): each thread loads its NV float4 of x, gamma and beta
+// at the start and keeps them in registers (no LDS row, no dependent gamma
+// load after the reductions), and each reduction takes one barrier.  The
+// double sums run in another order than norm_kernel's (per thread over its
+// float4s, then the block tree), which can move only their last bits.
+template <bool LN, bool QUANT, int NV>
+__global__ __launch_bounds__(256) void norm_vec_kernel(const float *x, int E, const float *gamma,
+                                                       const float *beta, double eps, float *h, int ldh,
+                                                       int8_t *q, int ldq, float *qs) {
+  __shared__ double redd[8];
+  __shared__ float redf[4];
+  const int m = blockIdx.x, t = threadIdx.x, E4 = E / 4;
+  const float4 *xr = reinterpret_cast<const float4 *>(x + (size_t)m * E);
+  const float4 *g4 = reinterpret_cast<const float4 *>(gamma);
+  const float4 *b4 = reinterpret_cast<const float4 *>(beta);
+  float4 v[NV], g[NV], b[NV];
+#pragma unroll
+  for (int j = 0; j < NV; j++) {
+    const int i = t + 256 * j;
+    v[j] = g[j] = b[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (i < E4) {
+      v[j] = xr[i];
+      g[j] = g4[i];
+      if constexpr (LN) b[j] = b4[i];
+    }
+  }
+  double acc = 0.0;
+#pragma unroll
+  for (int j = 0; j < NV; j++) {
+    const double d0 = v[j].x, d1 = v[j].y, d2 = v[j].z, d3 = v[j].w;
+    acc += LN ? ((d0 + d1) + d2) + d3 : ((d0 * d0 + d1 * d1) + d2 * d2) + d3 * d3;
+  }
+  const double tot = block_sum256_1b(acc, redd);
+  double mean = 0.0, rstd;
+  if constexpr (LN) {
+    mean = tot / E;
+    double a2 = 0.0;
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+      if (t + 256 * j < E4) {
+        const double d0 = (double)v[j].x - mean, d1 = (double)v[j].y - mean, d2 = (double)v[j].z - mean,
+                     d3 = (double)v[j].w - mean;
+        a2 += ((d0 * d0 + d1 * d1) + d2 * d2) + d3 * d3;
+      }
+    }
+    rstd = 1.0 / sqrt(block_sum256_1b(a2, redd + 4) / E + eps);
+  } else {
+    rstd = 1.0 / sqrt(tot / E + eps);
+  }
+  auto nrm = [&](float xv, float gv, float bv) {
+    float r = LN ? (float)(((double)xv - mean) * rstd) : (float)((double)xv * rstd);
+    r = r * gv;
+    if constexpr (LN) r = r + bv;
+    return r;
+  };
+  float mx = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NV; j++) {
+    v[j] = make_float4(nrm(v[j].x, g[j].x, b[j].x), nrm(v[j].y, g[j].y, b[j].y), nrm(v[j].z, g[j].z, b[j].z),
+                       nrm(v[j].w, g[j].w, b[j].w));
+    if (t + 256 * j < E4) {
+      if constexpr (QUANT) {
+        mx = fmaxf(mx, fabsf(v[j].x));
+        mx = fmaxf(mx, fabsf(v[j].y));
+        mx = fmaxf(mx, fabsf(v[j].z));
+        mx = fmaxf(mx, fabsf(v[j].w));
+      } else {
+        reinterpret_cast<float4 *>(h + (size_t)m * ldh)[t + 256 * j] = v[j];
+      }
+    }
+  }
+  if constexpr (QUANT) {
+    mx = block_max256_1b(mx, redf);
+    const float sc = quant_scale(mx);
+    if (t == 0) qs[m] = sc;
+    uint32_t *qr = reinterpret_cast<uint32_t *>(q + (size_t)m * ldq);
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+      const int i = t + 256 * j;
+      if (i < E4)
+        qr[i] = (uint32_t)(uint8_t)quant1(v[j].x, sc) | ((uint32_t)(uint8_t)quant1(v[j].y, sc) << 8) |
+                ((uint32_t)(uint8_t)quant1(v[j].z, sc) << 16) | ((uint32_t)(uint8_t)quant1(v[j].w, sc) << 24);
+    }
+  }
+}
+
 template <bool BF16>
 __global__ __launch_bounds__(256) void embed_kernel(const uint16_t *wte, const uint16_t *wpe,
                                                     const int *tok, const int *pos, int E,
@@ -483,9 +570,31 @@ hipError_t quant_rows(const float *in, int ldi, int M, int K, int8_t *q, int ldq
   return hipGetLastError();
 }
 
+template <bool LN, bool QUANT>
+static void launch_norm_vec(int nv, const float *x, int M, int E, const float *gamma, const float *beta, double eps,
+                            float *h, int ldh, int8_t *q, int ldq, float *qs, hipStream_t st) {
+  if (nv <= 1) klaunch((norm_vec_kernel<LN, QUANT, 1>), dim3(M), dim3(256), 0, st, x, E, gamma, beta, eps, h, ldh, q, ldq, qs);
+  else if (nv <= 2) klaunch((norm_vec_kernel<LN, QUANT, 2>), dim3(M), dim3(256), 0, st, x, E, gamma, beta, eps, h, ldh, q, ldq, qs);
+  else klaunch((norm_vec_kernel<LN, QUANT, 4>), dim3(M), dim3(256), 0, st, x, E, gamma, beta, eps, h, ldh, q, ldq, qs);
+}
+
 hipError_t norm_rows(const float *x, int M, int E, const float *gamma, const float *beta,
                      double eps, float *h, int ldh, int8_t *q, int ldq, float *qs,
                      hipStream_t st) {
+  const bool vec = E % 4 == 0 && E <= 256 * 4 * 4 && ((uintptr_t)x & 15u) == 0 && ((uintptr_t)gamma & 15u) == 0 &&
+                   (!beta || ((uintptr_t)beta & 15u) == 0) &&
+                   (q ? (ldq % 4 == 0 && ((uintptr_t)q & 3u) == 0) : (ldh % 4 == 0 && ((uintptr_t)h & 15u) == 0));
+  if (vec) {
+    const int nv = (E / 4 + 255) / 256;
+    if (beta) {
+      if (q) launch_norm_vec<true, true>(nv, x, M, E, gamma, beta, eps, h, ldh, q, ldq, qs, st);
+      else launch_norm_vec<true, false>(nv, x, M, E, gamma, beta, eps, h, ldh, q, ldq, qs, st);
+    } else {
+      if (q) launch_norm_vec<false, true>(nv, x, M, E, gamma, beta, eps, h, ldh, q, ldq, qs, st);
+      else launch_norm_vec<false, false>(nv, x, M, E, gamma, beta, eps, h, ldh, q, ldq, qs, st);
+    }
+    return hipGetLastError();
+  }
   const size_t lds = (size_t)E * sizeof(float);
   if (beta) {
     if (q) klaunch((norm_kernel<true, true>), dim3(M), dim3(256), lds, st, x, E, gamma, beta, eps, h, ldh, q, ldq, qs);

@@ -97,7 +97,7 @@ __global__ __launch_bounds__(256) void quant_vec_kernel(const float *in, int ldi
       mx = fmaxf(mx, fabsf(v[j].w));
     }
   }
-  mx = block_max256(mx, red);
+  mx = block_max256_1b(mx, red);
   const float sc = quant_scale(mx);
   if (t == 0) s[m] = sc;
   uint32_t *qr = reinterpret_cast<uint32_t *>(q + (size_t)m * ldq);

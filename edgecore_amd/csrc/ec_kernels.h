@@ -86,8 +86,10 @@ hipError_t gemm_i8(const GemvArgs &a, int epi, hipStream_t s);
 hipError_t gemm_i8_tile(const GemvArgs &a, int epi, int bm, hipStream_t s);
 // skinny int8 matrix-core GEMM for M <= 32 rows (batched decode): one block
 // of wpb waves (0: the library's choice, at most 16) per 16 output columns,
-// K split over the waves and summed exactly through LDS.  Same floats as
-// gemm_i8.
+// K split over the waves and summed exactly through LDS; for M <= 16, K >=
+// 4096 and few column tiles, K is also split over up to 8 blocks per 64
+// columns whose int32 tiles meet in a per-device workspace (launches that
+// use it must not overlap on one device).  Same floats as gemm_i8.
 hipError_t gemm_i8_skinny(const GemvArgs &a, int epi, int wpb, hipStream_t s);
 // 16-bit-weight matrix-core GEMM (gemm_mfma.hip) for M >= kGemmMinM: fp32 A
 // rows (lda), fp16 or bf16 weights, every epilogue but argmax candidates,

@@ -104,6 +104,8 @@ _SIG = {
     "ecm_parse": (_I, [_P, C.c_size_t, _P, _I, _P]),
     "ec_last_error": (C.c_char_p, []),
     "ec_init": (_I, []),
+    "ec_release": (_I, []),
+    "ec_alloc_count": (C.c_long, []),
     "ec_device_info": (_I, [C.c_char_p, _I]),
     "ec_stream": (_P, []),
     "ec_sync": (_I, []),

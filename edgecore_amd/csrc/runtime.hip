@@ -43,7 +43,7 @@ static hipStream_t g_stream = nullptr;
 static hipStream_t g_side = nullptr;
 static hipEvent_t g_touch_ev[4] = {};
 static unsigned g_touch_i = 0;
-static unsigned *g_touch_sink = nullptr;
+static unsigned *g_touch_sink = nullptr;  // this GPU's copy of touch_sink (below)
 static bool g_touch = true;
 // the persistent decode step: a plain launch of one block per CU (no
 // cooperative-launch barriers: ~30 us less per step) until a step reports a
@@ -91,9 +91,33 @@ constexpr size_t kNoAllocScratch = (size_t)4 << 20;
 constexpr int kMaxDevices = 64;
 static __device__ __align__(256) unsigned char scratch[kNoAllocScratch];
 static void *g_scratch_dev[kMaxDevices] = {};
+// The weight-touch kernel's sink word (it stores a value no load can be
+// proven dead against), also a file-scope device array: the library's set-up
+// allocates nothing, so a first call into ec_topk_dev_noalloc allocates
+// nothing either.
+static __device__ __align__(256) unsigned touch_sink[64];
 
-extern "C" int ec_init(void) {
-  if (g_inited) return 0;
+// Every device and pinned-host allocation of the library goes through these
+// helpers, which count them (ec_alloc_count).
+static long g_allocs = 0;
+template <class T>
+static hipError_t dev_malloc(T **p, size_t bytes) {
+  __atomic_add_fetch(&g_allocs, 1, __ATOMIC_RELAXED);
+  return hipMalloc((void **)p, bytes);
+}
+template <class T>
+static hipError_t host_malloc(T **p, size_t bytes, unsigned flags) {
+  __atomic_add_fetch(&g_allocs, 1, __ATOMIC_RELAXED);
+  return hipHostMalloc((void **)p, bytes, flags);
+}
+extern "C" long ec_alloc_count(void) { return __atomic_load_n(&g_allocs, __ATOMIC_RELAXED); }
+
+// Device selection, properties, settings and the device arrays' addresses:
+// everything the library's set-up does that neither allocates nor creates a
+// stream or an event (ec_topk_dev_noalloc needs no more).
+static int g_dev_inited = 0;
+static int init_device(void) {
+  if (g_dev_inited) return 0;
   const char *d = getenv("EDGECORE_DEVICE");
   g_device = d ? atoi(d) : 0;
   int n = 0;
@@ -107,10 +131,6 @@ extern "C" int ec_init(void) {
   if (hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, g_device) == hipSuccess &&
       lds > 0)
     g_max_lds = lds;
-  EC_HIP(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
-  EC_HIP(hipStreamCreateWithFlags(&g_side, hipStreamNonBlocking));
-  for (hipEvent_t &ev : g_touch_ev) EC_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
-  EC_HIP(hipMalloc(&g_touch_sink, 256));
   const char *tch = getenv("EDGECORE_TOUCH");
   g_touch = !(tch && !strcmp(tch, "0"));
   const char *sc = getenv("EDGECORE_STEP_COOP");
@@ -130,6 +150,18 @@ extern "C" int ec_init(void) {
     if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) == hipSuccess) g_scratch_dev[g_device] = p;
     else (void)hipGetLastError();  // ec_topk_dev_noalloc reports it
   }
+  EC_HIP(hipGetSymbolAddress((void **)&g_touch_sink, HIP_SYMBOL(touch_sink)));
+  g_dev_inited = 1;
+  return 0;
+}
+
+extern "C" int ec_init(void) {
+  if (g_inited) return 0;
+  const int r = init_device();
+  if (r) return r;
+  EC_HIP(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
+  EC_HIP(hipStreamCreateWithFlags(&g_side, hipStreamNonBlocking));
+  for (hipEvent_t &ev : g_touch_ev) EC_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
   g_inited = 1;
   return 0;
 }
@@ -164,7 +196,7 @@ extern "C" int ec_device_info(char *buf, int len) {
 extern "C" void *ec_dev_alloc(size_t bytes) {
   if (ec_init()) return nullptr;
   void *p = nullptr;
-  if (hipMalloc(&p, bytes ? bytes : 1) != hipSuccess) {
+  if (dev_malloc(&p, bytes ? bytes : 1) != hipSuccess) {
     set_err(-3, "hipMalloc(%zu) failed", bytes);
     return nullptr;
   }
@@ -399,7 +431,7 @@ static int w16_workspace(int M, int ldp) {
     if (g_w16_parts) EC_HIP(hipFree(g_w16_parts));
     g_w16_parts = nullptr;
     g_w16_halves = 0;
-    EC_HIP(hipMalloc(&g_w16_parts, halves * sizeof(uint16_t)));
+    EC_HIP(dev_malloc(&g_w16_parts, halves * sizeof(uint16_t)));
     g_w16_halves = halves;
   }
   if ((size_t)M > g_w16_rows) {
@@ -407,7 +439,7 @@ static int w16_workspace(int M, int ldp) {
     if (g_w16_rs) EC_HIP(hipFree(g_w16_rs));
     g_w16_rs = nullptr;
     g_w16_rows = 0;
-    EC_HIP(hipMalloc(&g_w16_rs, (size_t)M * sizeof(float)));
+    EC_HIP(dev_malloc(&g_w16_rs, (size_t)M * sizeof(float)));
     g_w16_rows = M;
   }
   return 0;
@@ -494,7 +526,7 @@ static int stage(int i, size_t bytes, void **out) {
     if (g_st[i].p) EC_HIP(hipFree(g_st[i].p));
     g_st[i].p = nullptr;
     g_st[i].n = 0;
-    EC_HIP(hipMalloc(&g_st[i].p, bytes));
+    EC_HIP(dev_malloc(&g_st[i].p, bytes));
     g_st[i].n = bytes;
   }
   *out = g_st[i].p;
@@ -912,7 +944,7 @@ static int load_impl(GPT2 *g, const char *path, int batch_cap, int max_ctx) {
 
   // upload the arena
   d->arena_bytes = (ld.cursor + 255) & ~(size_t)255;
-  EC_HIP(hipMalloc(&d->arena, d->arena_bytes));
+  EC_HIP(dev_malloc(&d->arena, d->arena_bytes));
   for (const Place &p : ld.places)
     EC_HIP(hipMemcpy(d->arena + p.off, ld.base + p.t->offset, p.t->bytes, hipMemcpyHostToDevice));
   char *A = d->arena;
@@ -987,15 +1019,15 @@ static int load_impl(GPT2 *g, const char *path, int batch_cap, int max_ctx) {
         const double f = (double)p * invf[i];
         tab[(size_t)p * half + i] = make_double2(cos(f) * scale, sin(f) * scale);
       }
-    EC_HIP(hipMalloc(&d->rope, tab.size() * sizeof(double2)));
+    EC_HIP(dev_malloc(&d->rope, tab.size() * sizeof(double2)));
     EC_HIP(hipMemcpy(d->rope, tab.data(), tab.size() * sizeof(double2), hipMemcpyHostToDevice));
   }
 
   // KV cache [L][B][eff_ctx][kv] fp16, zeroed
   d->kv_layer = (size_t)g->batch_cap * eff * kv;
   const size_t kvb = d->kv_layer * Lc * sizeof(uint16_t);
-  EC_HIP(hipMalloc(&d->kc, kvb));
-  EC_HIP(hipMalloc(&d->vc, kvb));
+  EC_HIP(dev_malloc(&d->kc, kvb));
+  EC_HIP(dev_malloc(&d->vc, kvb));
   EC_HIP(hipMemset(d->kc, 0, kvb));
   EC_HIP(hipMemset(d->vc, 0, kvb));
   g->k_cache = d->kc;
@@ -1009,39 +1041,39 @@ static int load_impl(GPT2 *g, const char *path, int batch_cap, int max_ctx) {
   d->aq_ld = (qmax + 15) & ~15;
   d->lm_rows = mmax < 64 ? mmax : 64;
   if (d->lm_rows < g->batch_cap) d->lm_rows = g->batch_cap;
-  EC_HIP(hipMalloc(&d->x, (size_t)mmax * E * 4));
-  EC_HIP(hipMalloc(&d->h, (size_t)mmax * E * 4));
-  EC_HIP(hipMalloc(&d->qkv, (size_t)mmax * d->qkv_ld * 4));
-  EC_HIP(hipMalloc(&d->att, (size_t)mmax * E * 4));
-  EC_HIP(hipMalloc(&d->ff, (size_t)mmax * F * 4));
-  EC_HIP(hipMalloc(&d->aq, (size_t)mmax * d->aq_ld));
-  EC_HIP(hipMalloc(&d->as, (size_t)mmax * 4));
+  EC_HIP(dev_malloc(&d->x, (size_t)mmax * E * 4));
+  EC_HIP(dev_malloc(&d->h, (size_t)mmax * E * 4));
+  EC_HIP(dev_malloc(&d->qkv, (size_t)mmax * d->qkv_ld * 4));
+  EC_HIP(dev_malloc(&d->att, (size_t)mmax * E * 4));
+  EC_HIP(dev_malloc(&d->ff, (size_t)mmax * F * 4));
+  EC_HIP(dev_malloc(&d->aq, (size_t)mmax * d->aq_ld));
+  EC_HIP(dev_malloc(&d->as, (size_t)mmax * 4));
   {
     // 16-bit linears: every row of every layer; int8 models: the LM head's rows
     const bool w16 = g->precision != 0;
     d->ah_rows = w16 ? mmax : d->lm_rows;
     d->ah_ld = ((w16 ? qmax : E) + 7) & ~7;
-    EC_HIP(hipMalloc(&d->ah, (size_t)d->ah_rows * 3 * d->ah_ld * sizeof(uint16_t)));
-    EC_HIP(hipMalloc(&d->ahs, (size_t)d->ah_rows * 4));
+    EC_HIP(dev_malloc(&d->ah, (size_t)d->ah_rows * 3 * d->ah_ld * sizeof(uint16_t)));
+    EC_HIP(dev_malloc(&d->ahs, (size_t)d->ah_rows * 4));
   }
-  EC_HIP(hipMalloc(&d->att_sc, (size_t)g->batch_cap * g->n_head * eff * sizeof(float)));
-  EC_HIP(hipMalloc(&d->logits, (size_t)d->lm_rows * V * 4));
-  EC_HIP(hipMalloc(&d->d_tok, (size_t)mmax * 4));
-  EC_HIP(hipMalloc(&d->d_pos, (size_t)mmax * 4));
-  EC_HIP(hipMalloc(&d->d_slot, (size_t)mmax * 4));
-  EC_HIP(hipMalloc(&d->d_amax, (size_t)mmax * 4));
-  EC_HIP(hipHostMalloc((void **)&d->h_stage, ((size_t)mmax * 3 + 1) * 4, hipHostMallocDefault));
-  EC_HIP(hipHostMalloc((void **)&d->h_amax, (size_t)(g->batch_cap > 4 ? g->batch_cap : 4) * sizeof(int),
+  EC_HIP(dev_malloc(&d->att_sc, (size_t)g->batch_cap * g->n_head * eff * sizeof(float)));
+  EC_HIP(dev_malloc(&d->logits, (size_t)d->lm_rows * V * 4));
+  EC_HIP(dev_malloc(&d->d_tok, (size_t)mmax * 4));
+  EC_HIP(dev_malloc(&d->d_pos, (size_t)mmax * 4));
+  EC_HIP(dev_malloc(&d->d_slot, (size_t)mmax * 4));
+  EC_HIP(dev_malloc(&d->d_amax, (size_t)mmax * 4));
+  EC_HIP(host_malloc((void **)&d->h_stage, ((size_t)mmax * 3 + 1) * 4, hipHostMallocDefault));
+  EC_HIP(host_malloc((void **)&d->h_amax, (size_t)(g->batch_cap > 4 ? g->batch_cap : 4) * sizeof(int),
                        hipHostMallocDefault));
   d->ncand = gemv_max_blocks();
-  EC_HIP(hipMalloc(&d->cand, (size_t)d->lm_rows * d->ncand * sizeof(unsigned long long)));
+  EC_HIP(dev_malloc(&d->cand, (size_t)d->lm_rows * d->ncand * sizeof(unsigned long long)));
   {
     const size_t nb = (size_t)topk_chunks(V), n = kTopkMax + 1;
-    EC_HIP(hipMalloc(&d->tk_cand, (size_t)d->lm_rows * nb * n * sizeof(unsigned long long)));
-    EC_HIP(hipMalloc(&d->tk_nan, (size_t)d->lm_rows * nb));
-    EC_HIP(hipMalloc(&d->tk_vals, (size_t)d->lm_rows * n * sizeof(float)));
-    EC_HIP(hipMalloc(&d->tk_idx, (size_t)d->lm_rows * n * sizeof(int)));
-    EC_HIP(hipMalloc(&d->tk_status, (size_t)d->lm_rows * sizeof(int)));
+    EC_HIP(dev_malloc(&d->tk_cand, (size_t)d->lm_rows * nb * n * sizeof(unsigned long long)));
+    EC_HIP(dev_malloc(&d->tk_nan, (size_t)d->lm_rows * nb));
+    EC_HIP(dev_malloc(&d->tk_vals, (size_t)d->lm_rows * n * sizeof(float)));
+    EC_HIP(dev_malloc(&d->tk_idx, (size_t)d->lm_rows * n * sizeof(int)));
+    EC_HIP(dev_malloc(&d->tk_status, (size_t)d->lm_rows * sizeof(int)));
   }
   if (step_shape_ok(g, d)) {
     std::vector<StepLayer> sl(Lc);
@@ -1050,23 +1082,23 @@ static int load_impl(GPT2 *g, const char *path, int batch_cap, int max_ctx) {
       sl[l] = StepLayer{W.ln1_g, W.ln2_g, (const int8_t *)W.wqkv, W.sqkv, (const int8_t *)W.wo, W.so,
                         (const int8_t *)W.wg, (const int8_t *)W.wu, W.sg, W.su, (const int8_t *)W.wd, W.sd};
     }
-    EC_HIP(hipMalloc(&d->d_layers, sl.size() * sizeof(StepLayer)));
+    EC_HIP(dev_malloc(&d->d_layers, sl.size() * sizeof(StepLayer)));
     EC_HIP(hipMemcpy(d->d_layers, sl.data(), sl.size() * sizeof(StepLayer), hipMemcpyHostToDevice));
     d->xch_bytes = (size_t)Lc * 3 * (size_t)E * sizeof(unsigned long long);
-    EC_HIP(hipMalloc(&d->xch, d->xch_bytes));
+    EC_HIP(dev_malloc(&d->xch, d->xch_bytes));
     d->ffv_words = (size_t)2 * Lc * F;
-    EC_HIP(hipMalloc(&d->ffv, d->ffv_words * sizeof(float)));
+    EC_HIP(dev_malloc(&d->ffv, d->ffv_words * sizeof(float)));
     EC_HIP(step_clear(d, nullptr));
     EC_HIP(hipDeviceSynchronize());
-    EC_HIP(hipMalloc(&d->d_step_io, 8 * sizeof(int)));
+    EC_HIP(dev_malloc(&d->d_step_io, 8 * sizeof(int)));
     EC_HIP(hipMemset(d->d_step_io, 0, 8 * sizeof(int)));
-    EC_HIP(hipHostMalloc((void **)&d->h_step_io, 8 * sizeof(int), hipHostMallocDefault));
+    EC_HIP(host_malloc((void **)&d->h_step_io, 8 * sizeof(int), hipHostMallocDefault));
     memset(d->h_step_io, 0, 8 * sizeof(int));
-    EC_HIP(hipMalloc(&d->d_gen, (size_t)d->eff_ctx * sizeof(int)));
+    EC_HIP(dev_malloc(&d->d_gen, (size_t)d->eff_ctx * sizeof(int)));
     const char *tr = getenv("EDGECORE_STEP_TRACE");
     if (tr && !strcmp(tr, "1")) {
       const size_t tb = (size_t)kStepBlocks * Lc * kStepEvents * sizeof(unsigned long long);
-      EC_HIP(hipMalloc(&d->d_trace, tb));
+      EC_HIP(dev_malloc(&d->d_trace, tb));
       EC_HIP(hipMemset(d->d_trace, 0, tb));
     }
     d->step_ok = true;
@@ -1720,11 +1752,11 @@ extern "C" int ec_topk_dev(const float *logits, int rows, int vocab, int ld, int
   unsigned char *nanf = nullptr;
   float *dv = nullptr;
   int *di = nullptr, *ds = nullptr;
-  hipError_t e = hipMalloc(&cand, (size_t)rows * nb * n * sizeof(unsigned long long));
-  if (e == hipSuccess) e = hipMalloc(&nanf, (size_t)rows * nb);
-  if (e == hipSuccess) e = hipMalloc(&dv, (size_t)rows * n * 4);
-  if (e == hipSuccess) e = hipMalloc(&di, (size_t)rows * n * 4);
-  if (e == hipSuccess) e = hipMalloc(&ds, (size_t)rows * 4);
+  hipError_t e = dev_malloc(&cand, (size_t)rows * nb * n * sizeof(unsigned long long));
+  if (e == hipSuccess) e = dev_malloc(&nanf, (size_t)rows * nb);
+  if (e == hipSuccess) e = dev_malloc(&dv, (size_t)rows * n * 4);
+  if (e == hipSuccess) e = dev_malloc(&di, (size_t)rows * n * 4);
+  if (e == hipSuccess) e = dev_malloc(&ds, (size_t)rows * 4);
   if (e == hipSuccess) e = topk_select(logits, rows, vocab, ld, top_k, cand, nanf, g_stream);
   if (e == hipSuccess) e = topk_merge(cand, nanf, rows, vocab, top_k, dv, di, ds, g_stream);
   if (e == hipSuccess) e = hipMemcpyAsync(vals, dv, (size_t)rows * n * 4, hipMemcpyDeviceToHost, g_stream);
@@ -1745,7 +1777,13 @@ extern "C" int ec_topk_dev(const float *logits, int rows, int vocab, int ld, int
 // array and race.
 extern "C" int ec_topk_dev_noalloc(const float *logits, int rows, int vocab, int ld, int top_k, float *vals,
                                    int *idx, int *status) {
-  EC_INIT();
+  // the device set-up only: no allocation, stream or event; the library's
+  // stream once some other call has created it, else the null stream
+  {
+    const int r0 = init_device();
+    if (r0) return r0;
+  }
+  hipStream_t s = g_inited ? g_stream : nullptr;
   if (rows < 0 || ld < vocab) return set_err(-1, "ec_topk_dev_noalloc: rows=%d ld=%d vocab=%d", rows, ld, vocab);
   if (rows == 0) return 0;
   if (!topk_ok(vocab, top_k))
@@ -1765,12 +1803,12 @@ extern "C" int ec_topk_dev_noalloc(const float *logits, int rows, int vocab, int
   unsigned char *nanf = (unsigned char *)(base + o_nan);
   float *dv = (float *)(base + o_v);
   int *di = (int *)(base + o_i), *ds = (int *)(base + o_s);
-  hipError_t e = topk_select(logits, rows, vocab, ld, top_k, cand, nanf, g_stream);
-  if (e == hipSuccess) e = topk_merge(cand, nanf, rows, vocab, top_k, dv, di, ds, g_stream);
-  if (e == hipSuccess) e = hipMemcpyAsync(vals, dv, (size_t)rows * n * 4, hipMemcpyDeviceToHost, g_stream);
-  if (e == hipSuccess) e = hipMemcpyAsync(idx, di, (size_t)rows * n * 4, hipMemcpyDeviceToHost, g_stream);
-  if (e == hipSuccess) e = hipMemcpyAsync(status, ds, (size_t)rows * 4, hipMemcpyDeviceToHost, g_stream);
-  if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
+  hipError_t e = topk_select(logits, rows, vocab, ld, top_k, cand, nanf, s);
+  if (e == hipSuccess) e = topk_merge(cand, nanf, rows, vocab, top_k, dv, di, ds, s);
+  if (e == hipSuccess) e = hipMemcpyAsync(vals, dv, (size_t)rows * n * 4, hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipMemcpyAsync(idx, di, (size_t)rows * n * 4, hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipMemcpyAsync(status, ds, (size_t)rows * 4, hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
   if (e != hipSuccess) return set_err(-3, "ec_topk_dev_noalloc: %s", hipGetErrorString(e));
   return 0;
 }
@@ -1814,6 +1852,17 @@ extern "C" int ec_generate_greedy(GPT2 *g, int token, int pos, int slot, int n, 
   io[2] = slot;
   io[3] = (int)(d->step_tag + 1u);
   io[4] = io[5] = io[6] = 0;
+  // An error after the first step was enqueued leaves steps with the tags
+  // step_tag + 1.. possibly run (wholly or in part): their words carry tags
+  // that the next call would use again.  Wait for what was enqueued, clear
+  // every exchange word and FFN half, and start the tags over.
+  auto abandon = [&](int r) {
+    (void)hipStreamSynchronize(s);
+    if (step_clear(d, s) == hipSuccess) (void)hipStreamSynchronize(s);
+    (void)hipGetLastError();
+    d->step_tag = 0;
+    return r;
+  };
   EC_HIP(hipMemcpyAsync(d->d_step_io, io, 7 * sizeof(int), hipMemcpyHostToDevice, s));
   for (int k = 0; k < n;) {
     const int max_npos = pos + k + 1;
@@ -1825,8 +1874,10 @@ extern "C" int ec_generate_greedy(GPT2 *g, int token, int pos, int slot, int n, 
     bool graph = g_use_graphs && !d->step_nograph && step_vtile(bucket, g->n_embd, g->n_kv_embd) >= 4;
     if (graph && (!d->chain_graph[gi] || d->chain_bucket[gi] != bucket)) {
       if (d->chain_graph[gi]) {
-        EC_HIP(hipGraphExecDestroy(d->chain_graph[gi]));
+        const hipError_t ed = hipGraphExecDestroy(d->chain_graph[gi]);
         d->chain_graph[gi] = nullptr;
+        if (ed != hipSuccess)
+          return abandon(set_err(-3, "ec_generate_greedy: hipGraphExecDestroy: %s", hipGetErrorString(ed)));
       }
       hipGraph_t gr = nullptr;
       hipError_t e = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
@@ -1860,12 +1911,13 @@ extern "C" int ec_generate_greedy(GPT2 *g, int token, int pos, int slot, int n, 
       d->chaining = false;
       k += 1;
     }
-    if (r) return r;
+    if (r) return abandon(r);
   }
   d->step_tag += (unsigned)n;
-  EC_HIP(hipMemcpyAsync(io + 4, d->d_step_io + 4, sizeof(int), hipMemcpyDeviceToHost, s));
-  EC_HIP(hipMemcpyAsync(out, d->d_gen, (size_t)n * sizeof(int), hipMemcpyDeviceToHost, s));
-  EC_HIP(hipStreamSynchronize(s));
+  hipError_t e = hipMemcpyAsync(io + 4, d->d_step_io + 4, sizeof(int), hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipMemcpyAsync(out, d->d_gen, (size_t)n * sizeof(int), hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return abandon(set_err(-3, "ec_generate_greedy: %s", hipGetErrorString(e)));
   if (io[4] || step_test_fail()) {
     if (step_timed_out(d)) return ec_generate_greedy(g, token, pos, slot, n, out);
     return set_err(-3, "ec_generate_greedy: a block's wait for another's results timed out (ids discarded)");
@@ -1896,8 +1948,8 @@ extern "C" int ec_attention_dev(const float *q, int ldq, const uint16_t *kc, con
   if (vtile < 4) return set_err(-1, "ec_attention_dev: position %d needs more LDS than the device has", max_npos - 1);
   int *dps = nullptr;
   float *dsc = nullptr;
-  hipError_t e = hipMalloc(&dps, (size_t)2 * M * sizeof(int));
-  if (e == hipSuccess && path == 2) e = hipMalloc(&dsc, (size_t)M * H * C * sizeof(float));
+  hipError_t e = dev_malloc(&dps, (size_t)2 * M * sizeof(int));
+  if (e == hipSuccess && path == 2) e = dev_malloc(&dsc, (size_t)M * H * C * sizeof(float));
   if (e == hipSuccess) e = hipMemcpyAsync(dps, pos, (size_t)M * sizeof(int), hipMemcpyHostToDevice, g_stream);
   if (e == hipSuccess) e = hipMemcpyAsync(dps + M, slot, (size_t)M * sizeof(int), hipMemcpyHostToDevice, g_stream);
   AttnArgs aa{q, ldq, kc, vc, out, ldo, dps, dps + M, H, KVH, hd, kv, C, window, 1.0 / sqrt((double)hd), M, max_npos,
@@ -1937,4 +1989,42 @@ extern "C" void qwen2_forward(GPT2 *g, const int *tokens, const int *positions, 
     exit(1);
   }
   gpt2_forward(g, tokens, positions, seqs, M, logits);
+}
+
+// Releases what the library holds outside models: its two streams and their
+// events, the timing events, and the staging and part buffers of the
+// host-pointer GEMM entry points.  Every model must have been freed
+// (gpt2_free) first.  A later call sets the library up again.  The driver
+// calls it before it exits, so that nothing of the library's is left for the
+// HIP runtime's own teardown.
+extern "C" int ec_release(void) {
+  if (!g_inited) return 0;
+  {
+    std::lock_guard<std::mutex> lk(g_models_mu);
+    if (!g_models.empty()) return set_err(-1, "ec_release: %zu models still loaded", g_models.size());
+  }
+  EC_HIP(hipStreamSynchronize(g_stream));
+  EC_HIP(hipStreamSynchronize(g_side));
+  prof_release_events();
+  g_prof.clear();
+  g_prof_agg.clear();
+  g_prof_on = false;
+  for (Staging &st : g_st) {
+    if (st.p) EC_HIP(hipFree(st.p));
+    st = Staging{};
+  }
+  if (g_w16_parts) EC_HIP(hipFree(g_w16_parts));
+  if (g_w16_rs) EC_HIP(hipFree(g_w16_rs));
+  g_w16_parts = nullptr;
+  g_w16_rs = nullptr;
+  g_w16_halves = g_w16_rows = 0;
+  for (hipEvent_t &ev : g_touch_ev) {
+    if (ev) EC_HIP(hipEventDestroy(ev));
+    ev = nullptr;
+  }
+  EC_HIP(hipStreamDestroy(g_side));
+  EC_HIP(hipStreamDestroy(g_stream));
+  g_side = g_stream = nullptr;
+  g_inited = 0;
+  return 0;
 }

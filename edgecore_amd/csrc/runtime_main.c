@@ -745,6 +745,7 @@ int main(int argc, char **argv)
         fprintf(stderr, "model file uses %s weights, but --precision %s was requested\n", dtype_name(g.precision),
                 c.precision);
         gpt2_free(&g);
+        ec_release();
         return 2;
     }
     c.precision = dtype_name(g.precision);
@@ -757,5 +758,8 @@ int main(int argc, char **argv)
         rc = 2;
     }
     gpt2_free(&g);
+    /* the library's streams, events and buffers go before the process exits,
+       not in the HIP runtime's own teardown */
+    if (ec_release() != 0) fprintf(stderr, "edgecore: release: %s\n", ec_last_error());
     return rc;
 }

@@ -360,7 +360,9 @@ int ec_topk_dev(const float *logits, int rows, int vocab, int ld, int top_k, flo
  * harnesses that forbid hipMalloc).  Its scratch is a 4 MiB device array of
  * the library, one per GPU for the life of the process; a call needing more
  * (about 40 KB per row at vocab 151936 and top_k 128) fails with a message.
- * Calls overlapping on one GPU share that array and race. */
+ * Calls overlapping on one GPU share that array and race.  A first call into
+ * the library may be this one: it then sets up only the device (no stream,
+ * event or allocation) and runs on the null stream. */
 int ec_topk_dev_noalloc(const float *logits, int rows, int vocab, int ld, int top_k, float *vals, int *idx,
                         int *status);
 
@@ -398,8 +400,20 @@ size_t ec_gpt2_sizeof(void);
 /* Error message of the last failing call on this thread ("" if none). */
 const char *ec_last_error(void);
 
-/* Opens the GPU on first use; 0 ok.  Every other entry point calls it. */
+/* Opens the GPU on first use; 0 ok.  Every other entry point calls it
+ * (ec_topk_dev_noalloc only its part that creates and allocates nothing). */
 int ec_init(void);
+
+/* Releases the library's streams, events and host-ABI staging buffers once
+ * every model is freed; 0 ok, <0 while a model is still loaded.  The next
+ * call sets the library up again.  No reference counterpart: the driver calls
+ * it before it exits, so that nothing is left to the HIP runtime's teardown. */
+int ec_release(void);
+
+/* Device and pinned-host allocations the library has made so far (every one
+ * goes through one counting helper); for tests of the no-allocation entry
+ * point. */
+long ec_alloc_count(void);
 
 /* One-line JSON description of the GPU: name, gcnArchName, CUs, HBM bytes. */
 int ec_device_info(char *buf, int len);

@@ -82,3 +82,60 @@ def test_qwen25_15b_shape_long_prefill(c5_model):
             assert list(am) == [int(r.argmax()) for r in want]
             cur, pos = [int(x) for x in am], [p + 1 for p in pos]
         om.close()
+
+
+def test_qwen25_15b_shape_c5_workload(c5_model):
+    """The C5 decode workload at 2 layers: 16 slots, each prefilled with a
+    1024-token prompt (ids from seeds 1-16, as the benchmark's batched leg
+    draws them), then 32 greedy steps at M=16 from position 1024 -- the
+    two-pass head_dim-128 attention (scores pass over the 16 slots' scores
+    workspace, then softmax and sums) and the M=16 decode graph of the
+    1024-1535 position bucket.  First the steps as the benchmark runs them
+    (argmax only: the captured graph), ids against the oracle; then the same
+    steps again from a fresh prefill with logits (direct launches), every
+    step within max-abs 2e-2 of the oracle."""
+    n, steps = 1024, 32
+    ctx = n + steps + 8
+    prompts = [prompt_ids(n, V, seed=b + 1) for b in range(B)]
+    with ec.Model(c5_model, B, ctx) as m:
+        om = oracle.OracleModel(c5_model, B, ctx)
+        om.kv_reset()
+        first = []
+        for b, p in enumerate(prompts):
+            want = om.forward(p, np.arange(n), np.full(n, b, np.int32), lm_from=n - 1)
+            first.append(int(want[0].argmax()))
+        ocur, opos, oids, ologits = list(first), [n] * B, [], []
+        for _ in range(steps):
+            want = om.forward(ocur, opos, None)
+            ocur = [int(r.argmax()) for r in want]
+            oids.append(ocur)
+            ologits.append(want)
+            opos = [p + 1 for p in opos]
+        om.close()
+
+        def prefill():
+            m.kv_reset()
+            out = []
+            for b, p in enumerate(prompts):
+                _, am = m.forward(p, np.arange(n), np.full(n, b, np.int32), lm_from=n - 1, want_logits=False,
+                                  want_argmax=True)
+                out.append(int(am[0]))
+            return out
+
+        assert prefill() == first
+        cur, pos = list(first), [n] * B
+        for s in range(steps):
+            _, am = m.forward(cur, pos, None, want_logits=False, want_argmax=True)
+            cur, pos = [int(x) for x in am], [p + 1 for p in pos]
+            assert cur == oids[s], s
+
+        assert prefill() == first
+        cur, pos, worst = list(first), [n] * B, 0.0
+        for s in range(steps):
+            got, am = m.forward(cur, pos, None, want_logits=True, want_argmax=True)
+            err = float(np.abs(got - ologits[s]).max())
+            worst = max(worst, err)
+            assert err <= 2e-2, (s, err)
+            cur, pos = [int(x) for x in am], [p + 1 for p in pos]
+            assert cur == oids[s], s
+    print(f"C5 workload (16 x 1024 + 32 steps at M=16, 2 layers): max-abs logits diff {worst:.3e}")

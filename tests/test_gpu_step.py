@@ -190,3 +190,48 @@ def test_step_launch_modes_and_timeout_switch(step_model):
         ids, err = _child_ids(step_model, mode, {"EDGECORE_STEP_TEST_FAIL": "1"})
         assert ids == plain, mode
         assert "cooperative launches from now on" in err, (mode, err[-500:])
+
+
+def _step_vs_kernel_per_op_and_oracle(path, prompt, steps):
+    lg_s, ids_s, fam_s = _decode(path, prompt, steps, True)
+    lg_k, ids_k, fam_k = _decode(path, prompt, steps, False)
+    assert "decode_step" in fam_s and "gemv_qkv" not in fam_s, sorted(fam_s)
+    assert "decode_step" not in fam_k, sorted(fam_k)
+    assert ids_s == ids_k
+    assert np.array_equal(lg_s.view(np.uint32), lg_k.view(np.uint32)), float(np.abs(lg_s - lg_k).max())
+    om = oracle.OracleModel(path, 1, len(prompt) + steps + 8)
+    oids, olg = om.generate(prompt, steps, want_logits=True)
+    om.close()
+    assert ids_s == [int(x) for x in oids[len(prompt):]]
+    err = float(np.abs(lg_s - olg).max())
+    assert err <= 2e-2, err
+    return err
+
+
+def test_step_long_context_crosses_2048(step_model):
+    """A 2040-token prompt, then 16 steps at positions 2040-2055: the K rows
+    of the first tile come from the prefetch, the later K tiles (positions
+    512 and on, including the tile loop past the second tile) are loaded by
+    the attention body, and V no longer fits the step's V tile (the product
+    threads load it themselves); the decode crosses the 2048-position
+    bucket boundary."""
+    err = _step_vs_kernel_per_op_and_oracle(step_model, prompt_ids(2040, V, seed=13), 16)
+    print(f"step at positions 2040-2055: max-abs logits diff to the oracle {err:.3e}")
+
+
+@pytest.fixture(scope="module")
+def window_model(model_dir):
+    path = model_dir / "qwen2-0.5b-3l-w700-int8.ecm"
+    if not path.exists():
+        ec.synth(path, name="qwen2-0.5b-3l-w700", arch="qwen2", layers=3, embd=896, heads=14, kv_heads=2,
+                 ffn=4864, ctx=32768, vocab=V, precision="int8", tie=1, sliding_window=700)
+    return path
+
+
+def test_step_sliding_window(window_model):
+    """The Qwen2-0.5B per-layer shapes with a 700-position sliding window
+    (src/gpt2.c:753-754): a 1000-token prompt, then 16 steps, so every step
+    attends to positions [pos - 699, pos] -- the window branch (lo > 0) of
+    the K and V prefetch, with more rows than the first K tile holds."""
+    err = _step_vs_kernel_per_op_and_oracle(window_model, prompt_ids(1000, V, seed=17), 16)
+    print(f"windowed step: max-abs logits diff to the oracle {err:.3e}")

@@ -423,6 +423,9 @@ def main() -> int:
     ap.add_argument("--no-prefill", action="store_true", help="skip the 4 x 2048-token prefill leg")
     ap.add_argument("--no-gpt2", action="store_true", help="skip the GPT-2 small fp16 leg")
     ap.add_argument("--no-m16", action="store_true", help="skip the Qwen2.5-1.5B M=16 batched-decode leg")
+    ap.add_argument("--only", choices=("c4", "c2", "c5"),
+                    help="run only this leg beside nothing else (4 x 2048 prefill + M=4 decode, GPT-2 small fp16, "
+                         "Qwen2.5-1.5B M=16) and print its JSON: a profiling entry")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="also run the plain copy kernel (ec_device_math op 6) 8 times on this many "
                          "bytes: the reference for HBM traffic counters and achievable bandwidth")
@@ -454,6 +457,12 @@ def main() -> int:
         dst.close()
 
     model, prompt_file = ensure_inputs(Path(args.cache))
+    if args.only:
+        legs = {"c4": lambda: prefill_c4(ec, np, model, Path(args.cache)),
+                "c2": lambda: leg_gpt2_small_fp16(ec, np, Path(args.cache)),
+                "c5": lambda: leg_qwen25_15b_int8_m16(ec, np, Path(args.cache))}
+        print(json.dumps({"leg": args.only, **legs[args.only]()}))
+        return 0
     prompt = ec.read_ids(prompt_file)
     K, W = args.steps, args.warmup
     max_ctx = PROMPT + W + K + 8

@@ -93,6 +93,7 @@ _SIG = {
     "gpt2_forward_topk": (_I, [_P, _P, _P, _P, _I, _I, _I, _P, _P, _P]),
     "ec_topk_max": (_I, []),
     "ec_generate_greedy": (_I, [_P, _I, _I, _I, _I, _P]),
+    "ec_generate_greedy_timed": (_I, [_P, _I, _I, _I, _I, _P, _P]),
     "ec_last_logits": (_I, [_P, _I, _P]),
     "ec_topk_dev": (_I, [_P, _I, _I, _I, _I, _P, _P, _P]),
     "ec_topk_dev_noalloc": (_I, [_P, _I, _I, _I, _I, _P, _P, _P]),
@@ -368,6 +369,14 @@ class Model:
         _check(lib().ec_generate_greedy(C.byref(self.g), int(token), int(pos), int(slot), int(n), _ptr(out)),
                "ec_generate_greedy")
         return out
+
+    def generate_greedy_timed(self, token: int, pos: int, slot: int, n: int):
+        """ec_generate_greedy_timed: (ids, per-step ms) of n greedy steps."""
+        out = np.empty(n, np.int32)
+        ms = np.empty(n, np.float64)
+        _check(lib().ec_generate_greedy_timed(C.byref(self.g), int(token), int(pos), int(slot), int(n), _ptr(out),
+                                              _ptr(ms)), "ec_generate_greedy_timed")
+        return out, ms
 
     def last_logits(self, row: int) -> np.ndarray:
         out = np.empty(self.vocab, np.float32)

@@ -170,8 +170,10 @@ struct TouchArgs {
 hipError_t touch_ranges(const TouchArgs &a, int blocks, hipStream_t st);
 // chained greedy decode: io[0..6] = token, position, slot, tag, error, argmax
 // id, ids written; moves the argmax id into the next step's inputs and
-// appends it to out[io[6]]
-hipError_t step_advance(int *io, int *out, hipStream_t st);
+// appends it to out[io[6]]; with stamps, the 100 MHz clock at that moment
+// into stamps[io[6] + 1] (chain_stamp writes stamps[0] before the first step)
+hipError_t step_advance(int *io, int *out, hipStream_t st, unsigned long long *stamps = nullptr);
+hipError_t chain_stamp(unsigned long long *t, hipStream_t st);
 
 // causal attention over the fp16 cache for every (head, token), in the
 // reference's arithmetic order (see kernels.hip).  With `cs`/`fuse_kv` set it
@@ -327,10 +329,11 @@ hipError_t argmax_rows_chunked(const float *logits, int rows, int V, unsigned lo
 hipError_t argmax_chunks(const float *logits, int rows, int V, unsigned long long *cand, int cap, int *nc,
                          hipStream_t st);
 // final reduction of the LM head's per-block argmax candidates; with
-// chain_io (one row), also step_advance's work on chain_io / chain_out
+// chain_io (one row), also step_advance's work on chain_io / chain_out /
+// chain_t
 hipError_t argmax_finalize(const unsigned long long *cand, int ncand, const float *logits,
                            int ldl, int rows, int *out, hipStream_t st, int *chain_io = nullptr,
-                           int *chain_out = nullptr);
+                           int *chain_out = nullptr, unsigned long long *chain_t = nullptr);
 
 // top_k + 1 largest logits per row for sampling (topk.hip).  topk_select sorts
 // chunks of 4096 logits into cand [rows][topk_chunks(V)][top_k + 1] keys and

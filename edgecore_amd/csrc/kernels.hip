@@ -395,7 +395,8 @@ __global__ __launch_bounds__(256) void argmax_chunk_kernel(const float *L, int V
 // non-NaN logit -> 0, like the reference's strict '>' scan from index 0
 __global__ __launch_bounds__(256) void argmax_finalize_kernel(const unsigned long long *cand, int ncand,
                                                               const float *logits, int ldl, int *out,
-                                                              int *chain_io, int *chain_out) {
+                                                              int *chain_io, int *chain_out,
+                                                              unsigned long long *chain_t) {
   __shared__ unsigned long long red[4];
   const int r = blockIdx.x;
   unsigned long long b = 0ull;
@@ -412,6 +413,7 @@ __global__ __launch_bounds__(256) void argmax_finalize_kernel(const unsigned lon
     const int id = (l0 != l0 || b == 0ull) ? 0 : (int)(0xFFFFFFFFu - (uint32_t)(b & 0xFFFFFFFFull));
     out[r] = id;
     if (chain_io) {  // a chained greedy step (one row): step_advance_kernel's work
+      if (chain_t) chain_t[chain_io[6] + 1] = __builtin_amdgcn_s_memrealtime();
       chain_out[chain_io[6]] = id;
       chain_io[6] = chain_io[6] + 1;
       chain_io[0] = id;
@@ -649,8 +651,9 @@ hipError_t touch_ranges(const TouchArgs &a, int blocks, hipStream_t st) {
 // After a chained greedy decode step (io: token, position, slot, tag, error,
 // argmax id, ids written): the argmax id becomes the next step's token at the
 // next position under the next tag, and is appended to out.
-__global__ void step_advance_kernel(int *io, int *out) {
+__global__ void step_advance_kernel(int *io, int *out, unsigned long long *stamps) {
   const int t = io[5];
+  if (stamps) stamps[io[6] + 1] = __builtin_amdgcn_s_memrealtime();
   out[io[6]] = t;
   io[6] = io[6] + 1;
   io[0] = t;
@@ -658,8 +661,16 @@ __global__ void step_advance_kernel(int *io, int *out) {
   io[3] = (int)((unsigned)io[3] + 1u);
 }
 
-hipError_t step_advance(int *io, int *out, hipStream_t st) {
-  klaunch(step_advance_kernel, dim3(1), dim3(1), 0, st, io, out);
+// the constant 100 MHz clock into t[0]: the start of a run of chained steps
+__global__ void chain_stamp_kernel(unsigned long long *t) { t[0] = __builtin_amdgcn_s_memrealtime(); }
+
+hipError_t chain_stamp(unsigned long long *t, hipStream_t st) {
+  klaunch(chain_stamp_kernel, dim3(1), dim3(1), 0, st, t);
+  return hipGetLastError();
+}
+
+hipError_t step_advance(int *io, int *out, hipStream_t st, unsigned long long *stamps) {
+  klaunch(step_advance_kernel, dim3(1), dim3(1), 0, st, io, out, stamps);
   return hipGetLastError();
 }
 
@@ -865,9 +876,11 @@ hipError_t attention_after_scores(const AttnArgs &a, hipStream_t st) {
 }
 
 hipError_t argmax_finalize(const unsigned long long *cand, int ncand, const float *logits, int ldl, int rows,
-                           int *out, hipStream_t st, int *chain_io, int *chain_out) {
+                           int *out, hipStream_t st, int *chain_io, int *chain_out,
+                           unsigned long long *chain_t) {
   if (chain_io && (rows != 1 || !chain_out)) return hipErrorInvalidValue;
-  klaunch(argmax_finalize_kernel, dim3(rows), dim3(256), 0, st, cand, ncand, logits, ldl, out, chain_io, chain_out);
+  klaunch(argmax_finalize_kernel, dim3(rows), dim3(256), 0, st, cand, ncand, logits, ldl, out, chain_io, chain_out,
+          chain_io ? chain_t : nullptr);
   return hipGetLastError();
 }
 

@@ -652,6 +652,9 @@ struct DevModel {
   int chain_bucket[2] = {0, 0};
   bool chaining = false;  // set while a chained step is enqueued or captured
   int *d_gen = nullptr;
+  // the 100 MHz clock before the first chained step ([0]) and at the end of
+  // each (argmax) step k ([k + 1]), [eff_ctx + 1]
+  unsigned long long *d_gen_t = nullptr;
   int *h_amax = nullptr;  // pinned: the graphs' argmax outputs (batch_cap ids)
   // greedy decode steps of M tokens in distinct slots (kernel-per-op path),
   // one HIP graph per (M, 512-position bucket), oldest replaced first
@@ -735,7 +738,7 @@ static void free_dev(DevModel *d) {
   void *ps[] = {d->arena, d->rope, d->d_tok, d->d_pos, d->d_slot, d->d_amax, d->x, d->h, d->qkv,
                 d->att, d->ff, d->aq, d->as, d->ah, d->ahs, d->att_sc, d->logits, d->kc, d->vc, d->cand, d->tk_cand,
                 d->tk_nan, d->tk_vals, d->tk_idx, d->tk_status, d->d_layers, d->xch, d->ffv, d->d_step_io, d->d_trace,
-                d->d_gen};
+                d->d_gen, d->d_gen_t};
   for (void *p : ps)
     if (p) (void)hipFree(p);
   if (d->h_stage) (void)hipHostFree(d->h_stage);
@@ -1095,6 +1098,7 @@ static int load_impl(GPT2 *g, const char *path, int batch_cap, int max_ctx) {
     EC_HIP(host_malloc((void **)&d->h_step_io, 8 * sizeof(int), hipHostMallocDefault));
     memset(d->h_step_io, 0, 8 * sizeof(int));
     EC_HIP(dev_malloc(&d->d_gen, (size_t)d->eff_ctx * sizeof(int)));
+    EC_HIP(dev_malloc(&d->d_gen_t, (size_t)(d->eff_ctx + 1) * sizeof(unsigned long long)));
     const char *tr = getenv("EDGECORE_STEP_TRACE");
     if (tr && !strcmp(tr, "1")) {
       const size_t tb = (size_t)kStepBlocks * Lc * kStepEvents * sizeof(unsigned long long);
@@ -1481,7 +1485,7 @@ static int enqueue_forward(GPT2 *g, DevModel *d, int M, int lm_from, bool distin
         EC_LAUNCH("argmax", 8.0 * rows * gemv_grid_x(a, lwt, EPI_STORE),
                   argmax_finalize(d->cand, gemv_grid_x(a, lwt, EPI_STORE), d->logits, V, rows,
                                   amax_dev + (r0 - lm_from), s, adv ? d->d_step_io : nullptr,
-                                  adv ? d->d_gen : nullptr));
+                                  adv ? d->d_gen : nullptr, adv ? d->d_gen_t : nullptr));
         if (adv) advanced = true;
       } else {
         int nc = 0;
@@ -1506,7 +1510,7 @@ static int enqueue_forward(GPT2 *g, DevModel *d, int M, int lm_from, bool distin
     d->last_lm_rows = rows;
   }
   if (step && d->chaining) {  // nothing goes to the host: the next step reads its inputs on the device
-    if (!advanced) EC_HIP(step_advance(d->d_step_io, d->d_gen, s));
+    if (!advanced) EC_HIP(step_advance(d->d_step_io, d->d_gen, s, d->d_gen_t));
   } else if (step) {
     EC_HIP(hipMemcpyAsync(d->h_step_io + 4, d->d_step_io + 4, 2 * sizeof(int), hipMemcpyDeviceToHost, s));
   }
@@ -1821,7 +1825,7 @@ extern "C" int ec_topk_dev_noalloc(const float *logits, int rows, int vocab, int
 // n steps back to back and reads the ids once; one HIP graph per 512-position
 // bucket.  Otherwise (no persistent step for this model, or the profiler on)
 // one forward per token.
-extern "C" int ec_generate_greedy(GPT2 *g, int token, int pos, int slot, int n, int *out) {
+extern "C" int ec_generate_greedy_timed(GPT2 *g, int token, int pos, int slot, int n, int *out, double *step_ms) {
   EC_INIT();
   DevModel *d = dev_of(g);
   if (!d) return set_err(-1, "model not loaded");
@@ -1835,8 +1839,10 @@ extern "C" int ec_generate_greedy(GPT2 *g, int token, int pos, int slot, int n, 
     int t = token;
     for (int k = 0; k < n; k++) {
       const int p = pos + k;
+      const double t0 = now_sec();
       const int r = forward_impl(g, &t, &p, &slot, 1, 0, nullptr, &out[k]);
       if (r) return r;
+      if (step_ms) step_ms[k] = (now_sec() - t0) * 1e3;
       t = out[k];
     }
     return 0;
@@ -1864,6 +1870,7 @@ extern "C" int ec_generate_greedy(GPT2 *g, int token, int pos, int slot, int n, 
     return r;
   };
   EC_HIP(hipMemcpyAsync(d->d_step_io, io, 7 * sizeof(int), hipMemcpyHostToDevice, s));
+  if (step_ms) EC_HIP(chain_stamp(d->d_gen_t, s));
   for (int k = 0; k < n;) {
     const int max_npos = pos + k + 1;
     int bucket = (max_npos + 511) / 512 * 512;
@@ -1916,13 +1923,23 @@ extern "C" int ec_generate_greedy(GPT2 *g, int token, int pos, int slot, int n, 
   d->step_tag += (unsigned)n;
   hipError_t e = hipMemcpyAsync(io + 4, d->d_step_io + 4, sizeof(int), hipMemcpyDeviceToHost, s);
   if (e == hipSuccess) e = hipMemcpyAsync(out, d->d_gen, (size_t)n * sizeof(int), hipMemcpyDeviceToHost, s);
+  std::vector<unsigned long long> stamps(step_ms ? (size_t)n + 1 : 0);
+  if (step_ms && e == hipSuccess)
+    e = hipMemcpyAsync(stamps.data(), d->d_gen_t, (size_t)(n + 1) * sizeof(unsigned long long),
+                       hipMemcpyDeviceToHost, s);
   if (e == hipSuccess) e = hipStreamSynchronize(s);
   if (e != hipSuccess) return abandon(set_err(-3, "ec_generate_greedy: %s", hipGetErrorString(e)));
+  // s_memrealtime counts a constant 100 MHz clock: 1e5 ticks per ms
+  for (int k = 0; step_ms && k < n; k++) step_ms[k] = (double)(stamps[k + 1] - stamps[k]) * 1e-5;
   if (io[4] || step_test_fail()) {
-    if (step_timed_out(d)) return ec_generate_greedy(g, token, pos, slot, n, out);
+    if (step_timed_out(d)) return ec_generate_greedy_timed(g, token, pos, slot, n, out, step_ms);
     return set_err(-3, "ec_generate_greedy: a block's wait for another's results timed out (ids discarded)");
   }
   return 0;
+}
+
+extern "C" int ec_generate_greedy(GPT2 *g, int token, int pos, int slot, int n, int *out) {
+  return ec_generate_greedy_timed(g, token, pos, slot, n, out, nullptr);
 }
 
 extern "C" int ec_attention_dev(const float *q, int ldq, const uint16_t *kc, const uint16_t *vc, int nslots, int C,

@@ -22,7 +22,11 @@
  * Decoder object that owns the per-step buffers.  Differences in behaviour,
  * all additive or result-preserving: the KV cache is cleared on the device
  * (gpt2_kv_reset); greedy steps take the argmax on the GPU and copy back one
- * id per row; the prompt's forward computes the LM head of its last row only;
+ * id per row; at batch 1 the greedy steps are chained on the GPU
+ * (ec_generate_greedy_timed: each id becomes the next step's token there) and
+ * each step's time is read from the GPU's clock, the ids coming back once
+ * (key step_timing: "gpu-clock", else "host");
+ * the prompt's forward computes the LM head of its last row only;
  * a prompt plus n-tokens beyond the context is refused (exit 2) instead of
  * writing past the cache; the JSON ends with extra keys (backend, device,
  * token_ids, tokens_per_sec_aggregate, decode_bytes_per_step, decode_gbps).
@@ -437,6 +441,7 @@ typedef struct {
     double *step_ms;
     int *ids; /* prompt followed by the generated tokens of row 0 */
     int n_ids;
+    int gpu_timed; /* steps timed by the GPU's clock (chained greedy steps) */
 } Run;
 
 static void run_once(GPT2 *g, const Config *c, const int *prompt, int n, float temp, Run *r)
@@ -447,8 +452,19 @@ static void run_once(GPT2 *g, const Config *c, const int *prompt, int n, float t
     r->ids = malloc((size_t)(n + c->n_tokens) * sizeof(int));
     memcpy(r->ids, prompt, (size_t)n * sizeof(int));
     r->n_ids = n;
+    r->gpu_timed = 0;
     r->ttft_ms = decoder_prefill(&d, prompt, n);
-    for (int s = 0; s < c->n_tokens; s++) r->step_ms[s] = decoder_step(&d, &r->ids[r->n_ids++]);
+    if (c->batch == 1 && temp <= 0.0f && c->n_tokens > 0) {
+        /* greedy at batch 1: the steps chained on the GPU (each id becomes the
+         * next step's token there, the ids come back once), timed per step
+         * by the GPU's clock */
+        if (ec_generate_greedy_timed(g, d.cur[0], d.pos[0], 0, c->n_tokens, r->ids + r->n_ids, r->step_ms))
+            fail_forward();
+        r->n_ids += c->n_tokens;
+        r->gpu_timed = 1;
+    } else {
+        for (int s = 0; s < c->n_tokens; s++) r->step_ms[s] = decoder_step(&d, &r->ids[r->n_ids++]);
+    }
     decoder_free(&d);
 }
 
@@ -567,6 +583,7 @@ static int mode_generate(GPT2 *g, const Config *c, const CpuPin *pin)
     if (text) jstr(&j, "text", text);
     jstr(&j, "backend", "hip-gfx950");
     jraw(&j, "device", dev);
+    jstr(&j, "step_timing", r.gpu_timed ? "gpu-clock" : "host");
     jints(&j, "token_ids", r.ids + n, r.n_ids - n);
     jclose(&j);
     if (f != stdout) fclose(f);
@@ -655,10 +672,11 @@ static int mode_bench(GPT2 *g, const Config *c, const CpuPin *pin)
     double *tok_ms = malloc((size_t)(per_token > 0 ? per_token : 1) * sizeof(double));
     double *ttft = malloc((size_t)iters * sizeof(double));
     double step_total = 0.0;
-    int k = 0;
+    int k = 0, gpu_timed = 0;
     for (int it = 0; it < iters; it++) {
         run_once(g, c, prompt, n, 0.0f, &r);
         ttft[it] = r.ttft_ms;
+        gpu_timed = r.gpu_timed;
         for (int s = 0; s < nt; s++) {
             step_total += r.step_ms[s];
             for (int b = 0; b < B; b++) tok_ms[k++] = r.step_ms[s];
@@ -698,6 +716,7 @@ static int mode_bench(GPT2 *g, const Config *c, const CpuPin *pin)
     jms(&j, "peak_rss_gb", peak_rss_gb());
     jstr(&j, "backend", "hip-gfx950");
     jraw(&j, "device", dev);
+    jstr(&j, "step_timing", gpu_timed ? "gpu-clock" : "host");
     jms(&j, "tokens_per_sec_aggregate", step_total > 0 ? (double)B * nt * iters / (step_total / 1000.0) : 0.0);
     jint(&j, "decode_bytes_per_step", (long long)bytes);
     jkey(&j, "decode_gbps");

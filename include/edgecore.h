@@ -346,6 +346,17 @@ int ec_topk_max(void);
  * pos..pos+n-1 must lie in the allocated context.  0 or <0. */
 int ec_generate_greedy(GPT2 *g, int token, int pos, int slot, int n, int *out);
 
+/* ec_generate_greedy that also reports each step's time in ms (step_ms [n],
+ * nullable).  Chained steps take the times from the device: the GPU's
+ * constant 100 MHz clock (s_memrealtime) is read by a one-thread kernel just
+ * before the first step and by each step's argmax as it writes the id, and
+ * step k's time is the difference of stamps k + 1 and k (step 0 includes the
+ * launch of the first graph).  Steps run one forward at a time (no
+ * persistent step for this model) are timed on the host around each forward.
+ * No reference counterpart: the reference driver times each forward with the
+ * host clock (src/runtime_main.c:337-342). */
+int ec_generate_greedy_timed(GPT2 *g, int token, int pos, int slot, int n, int *out, double *step_ms);
+
 /* Row `row` (counted from lm_from, < the LM-head chunk of the last forward,
  * which holds at least batch_cap rows) of the last forward's logits, into out
  * [vocab] (host).  0 or <0. */

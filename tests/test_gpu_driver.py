@@ -99,3 +99,35 @@ def test_exit_codes(make_model, tmp_path):
     # prompt + n-tokens beyond the context is refused instead of overrunning the cache
     assert run("--model", path, "--mode", "generate", "--prompt", "hello world", "--n-tokens", 60,
                "--no-print", check=False).returncode == 2
+
+
+@pytest.fixture(scope="module")
+def step_model(model_dir):
+    """Qwen2-0.5B per-layer shapes at 3 layers: its one-token greedy steps run
+    through the persistent decode step"""
+    path = model_dir / "qwen2-0.5b-3l-int8.ecm"
+    if not path.exists():
+        ec.synth(path, name="qwen2-0.5b-3l", arch="qwen2", layers=3, embd=896, heads=14, kv_heads=2, ffn=4864,
+                 ctx=32768, vocab=151936, precision="int8", tie=1)
+    return path
+
+
+def test_greedy_batch1_chained_with_gpu_clock(step_model, tmp_path):
+    """At batch 1 with greedy decoding the driver chains the steps on the GPU
+    (ec_generate_greedy_timed) and times them with the GPU's clock: the same
+    ids as the oracle's greedy loop, in generate and in bench mode."""
+    from tests.conftest import prompt_ids
+    prompt = prompt_ids(200, 151936, seed=3)
+    (tmp_path / "p.txt").write_text(" ".join(map(str, prompt)))
+    d = json.loads(run("--model", step_model, "--mode", "generate", "--tokens-file", tmp_path / "p.txt",
+                       "--n-tokens", 24, "--max-ctx", 240, "--no-print").stdout)
+    assert d["step_timing"] == "gpu-clock"
+    om = oracle.OracleModel(step_model, 1, 240)
+    ids, _ = om.generate(prompt, 24)
+    om.close()
+    assert d["token_ids"] == [int(x) for x in ids[200:]]
+    assert 0 < d["p50_ms"] <= d["p95_ms"] and d["tokens_per_sec"] > 0
+    b = json.loads(run("--model", step_model, "--mode", "bench", "--tokens-file", tmp_path / "p.txt",
+                       "--n-tokens", 24, "--warmup", 1, "--iters", 2, "--max-ctx", 240).stdout)
+    assert b["step_timing"] == "gpu-clock" and b["n_generated_tokens"] == 24
+    assert 0 < b["p50_ms"] <= b["p95_ms"] <= b["p99_ms"] and b["tokens_per_sec"] > 0

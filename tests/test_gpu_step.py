@@ -235,3 +235,28 @@ def test_step_sliding_window(window_model):
     the K and V prefetch, with more rows than the first K tile holds."""
     err = _step_vs_kernel_per_op_and_oracle(window_model, prompt_ids(1000, V, seed=17), 16)
     print(f"windowed step: max-abs logits diff to the oracle {err:.3e}")
+
+
+def test_generate_greedy_timed(step_model):
+    """ec_generate_greedy_timed: the ids of ec_generate_greedy, and per-step
+    times from the GPU clock that are positive and add up to no more than the
+    host's wall time around the call (and to most of it)."""
+    import time
+
+    prompt = prompt_ids(300, V, seed=21)
+    n = len(prompt)
+    with _load(step_model, n + 48, True) as m:
+        m.kv_reset()
+        m.forward(prompt, np.arange(n), np.zeros(n, np.int32), lm_from=n, want_logits=False)
+        want = m.generate_greedy(int(prompt[-1]), n, 0, 40)
+        m.kv_reset()
+        m.forward(prompt, np.arange(n), np.zeros(n, np.int32), lm_from=n, want_logits=False)
+        ec.lib().ec_sync()
+        t0 = time.perf_counter()
+        ids, ms = m.generate_greedy_timed(int(prompt[-1]), n, 0, 40)
+        wall = (time.perf_counter() - t0) * 1e3
+    assert [int(x) for x in ids] == [int(x) for x in want]
+    assert (ms > 0).all(), ms
+    assert ms.sum() <= wall, (ms.sum(), wall)
+    assert ms.sum() >= 0.5 * wall, (ms.sum(), wall)
+    assert float(np.median(ms)) < 5.0, ms

@@ -369,8 +369,14 @@ __device__ __forceinline__ void attn_decode_block(const AttnArgs &a, int m, int 
   static_assert(NS == 1 || (HD == 64 && (NS == 2 || NS == 4 || NS == 8)), "element slices: head_dim 64, 2 / 4 / 8");
   static_assert(!(SCORED && FUSED), "the scores pass appends the new k / v");
   // threads per block: 512 with element slices (one scored position per
-  // thread up to 512 positions), else 256
-  constexpr int NT = NS > 1 ? 512 : 256;
+  // thread up to 512 positions) and for the scored head_dim 128 body (six
+  // product waves beside the two summing waves), else 256
+  constexpr int NT = attn_threads(HD, NS, SCORED);
+  // threads over which the softmax's double sum is partitioned (thread t:
+  // positions t, t + SP, ...; then the fixed tree over SP / 64 waves): the
+  // scored head_dim 128 body keeps the one-pass body's 256, so both give the
+  // same sum bit for bit
+  constexpr int SP = (SCORED && HD == 128) ? 256 : NT;
   constexpr int KU = NT == 512 ? kAttnUnits / 2 : kAttnUnits;  // K units per thread
   __shared__ float redf[NT / 64];
   __shared__ double redd[NT / 64];
@@ -631,12 +637,20 @@ __device__ __forceinline__ void attn_decode_block(const AttnArgs &a, int m, int 
   // probabilities p = (float)(e * (1 / sum)) as they read them (no separate
   // normalization pass and barrier)
   double sum = 0.0;
-  for (int i = t; i < n; i += NT) {
-    const float e = ec_expf_tab(sc[i] - mx, etp);
-    sc[i] = e;
-    sum += (double)e;
+  if constexpr (SP == NT) {
+    for (int i = t; i < n; i += NT) {
+      const float e = ec_expf_tab(sc[i] - mx, etp);
+      sc[i] = e;
+      sum += (double)e;
+    }
+  } else {
+    for (int i = t; i < n; i += NT) sc[i] = ec_expf_tab(sc[i] - mx, etp);
+    __syncthreads();
+    if (t < SP)
+      for (int i = t; i < n; i += SP) sum += (double)sc[i];
   }
-  sum = block_sum_1b<NT / 64>(sum, redd);
+  // (threads t >= SP hold 0 and write slots the SP / 64-wave tree never reads)
+  sum = block_sum_1b<SP / 64>(sum, redd);
   const double isum = 1.0 / sum;
 
   mk(2);

@@ -285,6 +285,11 @@ bool attention_prefill_ok(const AttnArgs &a, int max_lds);
 hipError_t attention_prefill(const AttnArgs &a, int max_lds, hipStream_t st);
 // V units (4 positions x 8 elements) per thread held in registers
 constexpr int kAttnUnits = 4;
+// threads per block of the decode attention body: 512 with element slices
+// and for the scored head_dim 128 body, else 256
+__host__ __device__ constexpr inline int attn_threads(int hd, int ns, bool scored) {
+  return (ns > 1 || (scored && hd == 128)) ? 512 : 256;
+}
 // head_dim with the 16-byte-load kernel (else the generic one)
 __host__ __device__ inline bool attn_vec(int hd, int kv) {
   return (kv & 7) == 0 && (hd == 32 || hd == 64 || hd == 128);

@@ -301,7 +301,7 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(KvArgs a) {
 // running attn_decode_block (attn_decode.h) on the token's q row and new k/v
 // rows in global memory.
 template <int HD, bool FUSED, int NS, bool SCORED = false>
-__global__ __launch_bounds__(NS > 1 ? 512 : 256) void attn_kernel(AttnArgs a) {
+__global__ __launch_bounds__(attn_threads(HD, NS, SCORED)) void attn_kernel(AttnArgs a) {
   extern __shared__ __attribute__((aligned(16))) float lds[];
   const int m = blockIdx.y;
   int h = blockIdx.x, slice = 0;
@@ -826,12 +826,17 @@ static void launch_attn_scored(AttnArgs a, hipStream_t st) {
   const int r = a.H / a.KVH;
   a.xcd_r = (a.KVH <= 8 && a.H % a.KVH == 0 && r > 1) ? r : 0;
   a.fuse_kv = 0;
-  // one block per query head: element slices of head_dim 128 (2 or 4 blocks
-  // per head, measured at 1290 positions) took 29 and 43 us per layer
-  // against 24 us, their extra blocks running in more rounds
+  // one block per query head of 512 threads (two summing waves, six
+  // product waves): 18.9 us per layer at C5's 1024-1290 positions against
+  // 24.9 us with 256 threads (two product waves).  Element slices of head_dim
+  // 128 (2 or 4 blocks per head) took 29 and 43 us against 24 us, their extra
+  // blocks running in more rounds; one block per (token, KV group, 16
+  // elements) for all six heads of a group, V read once per group, took 25
+  // us: each block recomputes the six heads' softmax (six times the
+  // exponentials of a per-head block)
   constexpr int NS = 1;
   const dim3 grid((a.xcd_r ? 8 * r : a.H) * NS, a.M);
-  klaunch((attn_kernel<HD, false, NS, true>), grid, dim3(NS > 1 ? 512 : 256),
+  klaunch((attn_kernel<HD, false, NS, true>), grid, dim3(attn_threads(HD, NS, true)),
           attention_lds_bytes(a.max_npos, HD, a.vtile), st, a);
 }
 

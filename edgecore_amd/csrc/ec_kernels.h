@@ -60,6 +60,16 @@ struct GemvArgs {
   int ldo;
   int M, K, N;
   unsigned long long *cand;  // EPI_STORE: [M][gridDim.x] argmax candidate keys, or null
+  // skinny int8 GEMM with the activation quantization fused (gemm_i8_skinny_q):
+  // A is fp32 [M][lda] and row m's maximum |A| is the largest of the partial
+  // maxima pmax[m * np + j], j < np (each >= 0, NaN counted as 0)
+  const float *pmax;
+  int np;
+  // skinny GEMM: when set, each column group's block also writes, per output
+  // row m, the largest |v| (NaN as 0) of its outputs to pmax_out[m * np_out +
+  // group] (np_out >= the number of column groups)
+  float *pmax_out;
+  int np_out;
 };
 
 // Weight types
@@ -91,6 +101,12 @@ hipError_t gemm_i8_tile(const GemvArgs &a, int epi, int bm, hipStream_t s);
 // columns whose int32 tiles meet in a per-device workspace (launches that
 // use it must not overlap on one device).  Same floats as gemm_i8.
 hipError_t gemm_i8_skinny(const GemvArgs &a, int epi, int wpb, hipStream_t s);
+// the skinny int8 GEMM on fp32 A rows, quantized as their fragments are read
+// (src/gpt2.c:446-461: the row scale from the row's maximum |a|, given as
+// partial maxima a.pmax / a.np, and the same codes as quant_rows); _ok: K a
+// multiple of 16, 16-byte aligned rows, pmax set
+bool gemm_i8_skinny_q_ok(const GemvArgs &a, int epi);
+hipError_t gemm_i8_skinny_q(const GemvArgs &a, int epi, hipStream_t s);
 // 16-bit-weight matrix-core GEMM (gemm_mfma.hip) for M >= kGemmMinM: fp32 A
 // rows (lda), fp16 or bf16 weights, every epilogue but argmax candidates,
 // no weight scales.  It first splits the rows into w16_parts(wt) 16-bit parts
@@ -205,6 +221,12 @@ struct AttnArgs {
   // softmax / sums pass; null to score inside the attention blocks
   float *scores;
   int sc_ld;
+  // decode launches (attn_kernel): when set, each block also writes the
+  // largest |out| (NaN as 0) of its outputs to pmax[m * np + 4 h + slice]
+  // (np >= 4 H), the partial row maxima of the o projection's fused
+  // quantization
+  float *pmax;
+  int np;
 };
 // positions from which attention() splits a decode launch into the scores
 // pass and the softmax / sums pass (when a.scores is set)

@@ -530,7 +530,11 @@ constexpr int kSkPartInts = 256 * 1024;        // int32 partial tiles of a split
 __device__ int sk_part[kSkPartInts];
 __device__ unsigned sk_cnt[kSkMaxGroups];
 
-template <int OP, int TI, int NJ, int EPI>
+// QA (int8 only): A holds fp32 rows, quantized as their fragments are read
+// with the row scale quant_scale(max |a|) of the row maximum given as partial
+// maxima (a.pmax, a.np); the codes are quant_rows' (the same scale and the
+// same per-element code), so the floats equal the unfused GEMM's.
+template <int OP, int TI, int NJ, int EPI, bool QA = false>
 __global__ __launch_bounds__(1024) void gemm_skinny_kernel(GemvArgs a) {
   using Op = MfmaOp<OP>;
   using Acc = typename Op::Acc;
@@ -540,11 +544,13 @@ __global__ __launch_bounds__(1024) void gemm_skinny_kernel(GemvArgs a) {
   constexpr bool RES = EPI == EPI_RESID || EPI == EPI_BIAS_RESID;
   constexpr bool GELU = EPI == EPI_GELU || EPI == EPI_BIAS_GELU;
   static_assert(!SWI || NJ == 1, "SwiGLU blocks take one tile of gate and up rows");
+  static_assert(!QA || I8, "fused quantization of int8 activations");
   constexpr int NB = SWI ? 2 : NJ;  // B tiles: NJ tiles of 16 rows, or 16 gate + 16 up rows
-  constexpr int FR = TI * NP + NB;  // 16-byte fragments per lane and step
+  constexpr int FR = TI * NP * (QA ? 4 : 1) + NB;  // 16-byte loads per lane and step
   constexpr int U = FR <= 3 ? 8 : FR <= 5 ? 4 : 2;  // K steps per wave in flight (within 128 VGPRs)
   __shared__ Acc part[16][TI][NB][64];  // [wave][i][j][lane]
   __shared__ uint64_t etab[SWI ? 32 : 1];
+  __shared__ float s_sc[QA ? 32 : 1];  // QA: the rows' scales
 
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, nw = blockDim.x >> 6;
   const int lr = lane & 15, lq = lane >> 4;
@@ -559,12 +565,51 @@ __global__ __launch_bounds__(1024) void gemm_skinny_kernel(GemvArgs a) {
 
   // fragment sources: part p of A row 16 i + lr (clamped), B row n0 + lr of W (and W2)
   const int8_t *arow[TI][NP];
+  const float *arowf[TI];  // QA: the fp32 row
   const int8_t *brow[NB];
 #pragma unroll
-  for (int i = 0; i < TI; i++)
+  for (int i = 0; i < TI; i++) {
 #pragma unroll
     for (int p = 0; p < NP; p++)
       arow[i][p] = (const int8_t *)a.A + ((size_t)min(16 * i + lr, M - 1) * NP + p) * ldab;
+    arowf[i] = (const float *)a.A + (size_t)min(16 * i + lr, M - 1) * a.lda;
+  }
+  // QA: each row's scale from its partial maxima (one wave per row), then
+  // this lane's rows' scale and reciprocal
+  float qs[TI], qr[TI];
+  bool qok[TI];
+  if constexpr (QA) {
+    // each wave's partial maxima loads of all its rows issued together
+    // (kQaLoads per lane and row; np <= 64 kQaLoads)
+    constexpr int kQaLoads = 10;
+    for (int m0 = wave; m0 < M; m0 += 2 * nw) {
+      float pv[2][kQaLoads];
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        const int m = min(m0 + nw * h, M - 1);
+#pragma unroll
+        for (int k = 0; k < kQaLoads; k++) {
+          const int j = lane + 64 * k;
+          pv[h][k] = j < a.np ? a.pmax[(size_t)m * a.np + j] : 0.0f;
+        }
+      }
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        float mx = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kQaLoads; k++) mx = fmaxf(mx, pv[h][k]);
+        mx = wave_max_dpp(mx);
+        if (lane == 0 && m0 + nw * h < M) s_sc[m0 + nw * h] = quant_scale(mx);
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < TI; i++) {
+      qs[i] = s_sc[min(16 * i + lr, M - 1)];
+      qok[i] = ec_quant_rcp_ok(qs[i]);
+      qr[i] = qok[i] ? 1.0f / qs[i] : 1.0f;
+    }
+  }
 #pragma unroll
   for (int j = 0; j < NB; j++) {
     if constexpr (SWI) brow[j] = (const int8_t *)(j ? a.W2 : a.W) + (size_t)min(n0 + lr, N - 1) * KB;
@@ -584,15 +629,22 @@ __global__ __launch_bounds__(1024) void gemm_skinny_kernel(GemvArgs a) {
   // the row read a clamped address and the A fragments are zeroed
   for (int sb = ks0 + wave; sb < ks1; sb += nw * U) {
     v4i fa[U][TI][NP], fb[U][NB];
+    float4 ff[QA ? U : 1][QA ? TI : 1][4];  // QA: the 16 floats of each A fragment
 #pragma unroll
     for (int u = 0; u < U; u++) {
       const int st = sb + nw * u;  // uniform over the wave
       if (st < ks1) {
         const int kc = min(64 * st + 16 * lq, KB - 16);
 #pragma unroll
-        for (int i = 0; i < TI; i++)
+        for (int i = 0; i < TI; i++) {
+          if constexpr (QA) {
 #pragma unroll
-          for (int p = 0; p < NP; p++) fa[u][i][p] = *reinterpret_cast<const v4i *>(arow[i][p] + kc);
+            for (int c = 0; c < 4; c++) ff[u][i][c] = *reinterpret_cast<const float4 *>(arowf[i] + kc + 4 * c);
+          } else {
+#pragma unroll
+            for (int p = 0; p < NP; p++) fa[u][i][p] = *reinterpret_cast<const v4i *>(arow[i][p] + kc);
+          }
+        }
 #pragma unroll
         for (int j = 0; j < NB; j++) fb[u][j] = *reinterpret_cast<const v4i *>(brow[j] + kc);
       }
@@ -602,6 +654,28 @@ __global__ __launch_bounds__(1024) void gemm_skinny_kernel(GemvArgs a) {
       const int st = sb + nw * u;
       if (st < ks1) {
         const bool in = 64 * st + 16 * lq < KB;
+        if constexpr (QA) {
+          // the codes of the fragment's 16 elements, packed four per word
+#pragma unroll
+          for (int i = 0; i < TI; i++) {
+            auto pack = [&](auto q1) {
+              int w4[4];
+#pragma unroll
+              for (int c = 0; c < 4; c++) {
+                const float e4[4] = {ff[u][i][c].x, ff[u][i][c].y, ff[u][i][c].z, ff[u][i][c].w};
+                uint32_t wd = 0;
+#pragma unroll
+                for (int k = 0; k < 4; k++) wd |= (uint32_t)(uint8_t)q1(e4[k]) << (8 * k);
+                w4[c] = (int)wd;
+              }
+              fa[u][i][0] = v4i{w4[0], w4[1], w4[2], w4[3]};
+            };
+            // the division-free form for every scale but extreme ones (a
+            // branch the lanes of ordinary rows all skip)
+            if (qok[i]) pack([&](float e) { return ec_quant1_rcp(e, qs[i], qr[i]); });
+            else pack([&](float e) { return quant1(e, qs[i]); });
+          }
+        }
 #pragma unroll
         for (int i = 0; i < TI; i++)
 #pragma unroll
@@ -675,11 +749,14 @@ __global__ __launch_bounds__(1024) void gemm_skinny_kernel(GemvArgs a) {
       if (t == 0) __hip_atomic_store(&sk_cnt[blockIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
-  if (!outt || m >= M || n >= N) return;
+  if (!outt) return;
+  const bool valid = m < M && n < N;
+  if (!valid && !a.pmax_out) return;
 
   // epilogue (the same code as gemm_mfma_kernel's)
-  const float as = a.as[m];
-  float v;
+  const float as = QA ? s_sc[min(m, M - 1)] : a.as[min(m, M - 1)];
+  float v = 0.0f;
+  if (valid) {
   if constexpr (I8) {
     const float bs = a.ws ? a.ws[n] : 1.0f;
     if constexpr (SWI) {
@@ -703,9 +780,31 @@ __global__ __launch_bounds__(1024) void gemm_skinny_kernel(GemvArgs a) {
     if constexpr (GELU) v = gelu_new(v);
   }
   a.out[(size_t)m * a.ldo + n] = v;
+  }
+  if (a.pmax_out) {
+    // the largest |v| of row m over this block's 16 NO columns: the 16 lanes
+    // of a DPP row hold one row's columns (NaN and absent outputs count 0)
+    float pv = valid ? fmaxf(0.0f, fabsf(v)) : 0.0f;
+    pv = fmaxf(pv, dpp_mov<0xB1>(pv));
+    pv = fmaxf(pv, dpp_mov<0x4E>(pv));
+    pv = fmaxf(pv, dpp_mov<0x141>(pv));
+    pv = fmaxf(pv, dpp_mov<0x140>(pv));
+    if constexpr (NO > 1) {
+      __shared__ float s_pm[4][32];  // [tile jo][row]
+      if (lr == 0 && m < M) s_pm[jo][m] = pv;
+      __syncthreads();
+      if (jo == 0 && lr == 0 && m < M) {
+        float b = s_pm[0][m];
+        for (int q = 1; q < NO; q++) b = fmaxf(b, s_pm[q][m]);
+        a.pmax_out[(size_t)m * a.np_out + blockIdx.x] = b;
+      }
+    } else {
+      if (lr == 0 && m < M) a.pmax_out[(size_t)m * a.np_out + blockIdx.x] = pv;
+    }
+  }
 }
 
-template <int OP, int TI, int NJ, int EPI>
+template <int OP, int TI, int NJ, int EPI, bool QA = false>
 hipError_t launch_skinny_nj(const GemvArgs &a, int wpb, int ksplit, hipStream_t s) {
   const int ksteps = (a.K * MfmaOp<OP>::EB + 63) / 64;
   constexpr int NO = EPI == EPI_SWIGLU ? 1 : NJ;
@@ -719,7 +818,8 @@ hipError_t launch_skinny_nj(const GemvArgs &a, int wpb, int ksplit, hipStream_t 
   // 4 TI NO (the epilogue takes one thread per output of 16 TI rows x 16 NO)
   if (wpb <= 0) wpb = min(16, max(4, kper / 2));
   wpb = max(min(wpb, 16), 4 * TI * NO);
-  klaunch((gemm_skinny_kernel<OP, TI, NJ, EPI>), dim3(groups, ksplit), dim3(64 * wpb), 0, s, a);
+  if (a.pmax_out && groups > a.np_out) return hipErrorInvalidValue;
+  klaunch((gemm_skinny_kernel<OP, TI, NJ, EPI, QA>), dim3(groups, ksplit), dim3(64 * wpb), 0, s, a);
   return hipGetLastError();
 }
 
@@ -730,17 +830,17 @@ hipError_t launch_skinny_nj(const GemvArgs &a, int wpb, int ksplit, hipStream_t 
 // fragments serve 64 columns).  The split's publish-and-add round trip costs
 // ~3 us, more than it saves for K = 1536 (o and q|k|v at batch 16: 4.7 ->
 // 7.2-7.7 us measured); down (K = 8960) goes from 12.6 to 10.2 us.
-template <int OP, int TI, int EPI>
+template <int OP, int TI, int EPI, bool QA = false>
 hipError_t launch_skinny(const GemvArgs &a, int wpb, hipStream_t s) {
   if constexpr (EPI != EPI_SWIGLU && TI == 1) {
-    if (a.N >= 16 * 1024) return launch_skinny_nj<OP, TI, 4, EPI>(a, wpb, 1, s);
+    if (a.N >= 16 * 1024) return launch_skinny_nj<OP, TI, 4, EPI, QA>(a, wpb, 1, s);
     if (OP == OP_I8 && (a.N + 15) / 16 < 192 && (a.K + 63) / 64 >= 64) {
       const int ksteps = (a.K + 63) / 64, groups = (a.N + 63) / 64;
       const int ks = min(8, min(256 / groups, ksteps / 4));
-      if (ks > 1) return launch_skinny_nj<OP, TI, 4, EPI>(a, wpb, ks, s);
+      if (ks > 1) return launch_skinny_nj<OP, TI, 4, EPI, QA>(a, wpb, ks, s);
     }
   }
-  return launch_skinny_nj<OP, TI, 1, EPI>(a, wpb, 1, s);
+  return launch_skinny_nj<OP, TI, 1, EPI, QA>(a, wpb, 1, s);
 }
 
 template <int OP, int TI>
@@ -832,6 +932,16 @@ hipError_t gemm_w16(const GemvArgs &a, int wt, int epi, uint16_t *parts, int ldp
 hipError_t gemm_i8_skinny(const GemvArgs &a, int epi, int wpb, hipStream_t s) {
   if (!gemm_i8_ok(a, epi) || a.M > 32 || wpb < 0 || wpb > 16) return hipErrorInvalidValue;
   return launch_skinny_op<OP_I8>(a, epi, wpb, s);
+}
+
+bool gemm_i8_skinny_q_ok(const GemvArgs &a, int epi) {
+  return epi == EPI_RESID && a.M >= 1 && a.M <= 32 && a.N >= 1 && a.K >= 16 && a.K % 16 == 0 && a.lda % 4 == 0 &&
+         aligned16(a.A) && aligned16(a.W) && a.pmax && a.np >= 1 && a.np <= 640 && !a.cand;
+}
+
+hipError_t gemm_i8_skinny_q(const GemvArgs &a, int epi, hipStream_t s) {
+  if (!gemm_i8_skinny_q_ok(a, epi)) return hipErrorInvalidValue;
+  return a.M <= 16 ? launch_skinny<OP_I8, 1, EPI_RESID, true>(a, 0, s) : launch_skinny<OP_I8, 2, EPI_RESID, true>(a, 0, s);
 }
 
 }  // namespace ec

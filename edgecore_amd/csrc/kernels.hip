@@ -324,8 +324,17 @@ __global__ __launch_bounds__(attn_threads(HD, NS, SCORED)) void attn_kernel(Attn
   const float *krow = a.k + (size_t)m * a.ldk + (size_t)kvh * hd;
   const float *vrow = a.v + (size_t)m * a.ldk + (size_t)kvh * hd;
   float *orow = a.out + (size_t)m * a.ldo + (size_t)h * hd + (size_t)(hd / NS) * slice;
-  attn_decode_block<HD, FUSED, NS, SCORED>(a, m, h, slice, qrow, krow, vrow, lds,
-                                            [&](int i, float o) { orow[i] = o; });
+  float oabs = 0.0f;  // the largest |output| of this thread (NaN as 0)
+  attn_decode_block<HD, FUSED, NS, SCORED>(a, m, h, slice, qrow, krow, vrow, lds, [&](int i, float o) {
+    orow[i] = o;
+    oabs = fmaxf(oabs, fabsf(o));
+  });
+  if (a.pmax) {  // uniform
+    constexpr int NT = attn_threads(HD, NS, SCORED);
+    __shared__ float red[NT / 64];
+    const float mx = block_max_1b<NT / 64>(oabs, red);
+    if (threadIdx.x == 0) a.pmax[(size_t)m * a.np + 4 * h + slice] = mx;
+  }
 }
 
 // ---------------------------------------------------------------------------

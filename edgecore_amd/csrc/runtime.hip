@@ -636,6 +636,15 @@ struct DevModel {
   float *ahs = nullptr;
   float *logits = nullptr;
   float *att_sc = nullptr;  // decode attention scores [batch_cap][H][eff_ctx] (long contexts)
+  // Batched decode (16-32 tokens) with the activation quantization of the o
+  // and down projections inside their skinny GEMMs (EDGECORE_FUSEQ=0 at load
+  // turns it off): partial row maxima of the attention output [32][4 H] and
+  // of the FFN activation [32][ceil(F / 16)], written by the attention and
+  // gate/up (fc) launches
+  bool fuse_quant = false;
+  bool ff_pmax = false;  // the last gate/up (fc) launch wrote pmax_ff
+  float *pmax_att = nullptr, *pmax_ff = nullptr;
+  int np_att = 0, np_ff = 0;
   uint16_t *kc = nullptr, *vc = nullptr;
   size_t kv_layer = 0;  // elements per layer of one cache
   const uint16_t *lm = nullptr;
@@ -738,7 +747,7 @@ static void free_dev(DevModel *d) {
   void *ps[] = {d->arena, d->rope, d->d_tok, d->d_pos, d->d_slot, d->d_amax, d->x, d->h, d->qkv,
                 d->att, d->ff, d->aq, d->as, d->ah, d->ahs, d->att_sc, d->logits, d->kc, d->vc, d->cand, d->tk_cand,
                 d->tk_nan, d->tk_vals, d->tk_idx, d->tk_status, d->d_layers, d->xch, d->ffv, d->d_step_io, d->d_trace,
-                d->d_gen, d->d_gen_t};
+                d->d_gen, d->d_gen_t, d->pmax_att, d->pmax_ff};
   for (void *p : ps)
     if (p) (void)hipFree(p);
   if (d->h_stage) (void)hipHostFree(d->h_stage);
@@ -1060,6 +1069,17 @@ static int load_impl(GPT2 *g, const char *path, int batch_cap, int max_ctx) {
     EC_HIP(dev_malloc(&d->ahs, (size_t)d->ah_rows * 4));
   }
   EC_HIP(dev_malloc(&d->att_sc, (size_t)g->batch_cap * g->n_head * eff * sizeof(float)));
+  {
+    const char *fq = getenv("EDGECORE_FUSEQ");
+    d->fuse_quant = g->precision == 0 && !(fq && !strcmp(fq, "0"));
+    d->np_att = 4 * g->n_head;
+    d->np_ff = (F + 15) / 16;
+    // partials a launch never writes stay 0, which no row maximum goes below
+    EC_HIP(dev_malloc(&d->pmax_att, (size_t)32 * d->np_att * sizeof(float)));
+    EC_HIP(dev_malloc(&d->pmax_ff, (size_t)32 * d->np_ff * sizeof(float)));
+    EC_HIP(hipMemset(d->pmax_att, 0, (size_t)32 * d->np_att * sizeof(float)));
+    EC_HIP(hipMemset(d->pmax_ff, 0, (size_t)32 * d->np_ff * sizeof(float)));
+  }
   EC_HIP(dev_malloc(&d->logits, (size_t)d->lm_rows * V * 4));
   EC_HIP(dev_malloc(&d->d_tok, (size_t)mmax * 4));
   EC_HIP(dev_malloc(&d->d_pos, (size_t)mmax * 4));
@@ -1169,6 +1189,12 @@ static const char *gemm_family(const char *fam) {
 static int linear(GPT2 *g, DevModel *d, const char *fam, GemvArgs a, int wt, int epi, int pro, hipStream_t s) {
   const double bytes = gemv_bytes(wt, pro, epi, a.M, a.K, a.N, a.ws != nullptr, a.bias != nullptr);
   if (wt == WT_I8 && g_use_mfma && a.M >= kGemmMinM) {
+    // batched decode: the quantization inside the skinny GEMM, from the
+    // producer's partial row maxima
+    if (pro == PRO_QUANT && a.pmax && (a.pmax != d->pmax_ff || d->ff_pmax) && gemm_i8_skinny_q_ok(a, epi)) {
+      EC_LAUNCH(gemm_family(fam), bytes, gemm_i8_skinny_q(a, epi, s));
+      return 0;
+    }
     // many rows: the norm / quantization as its own pass into int8 rows, then
     // the matrix-core GEMM
     GemvArgs q = a;
@@ -1185,10 +1211,13 @@ static int linear(GPT2 *g, DevModel *d, const char *fam, GemvArgs a, int wt, int
         EC_LAUNCH("norm_quant", 5.0 * a.M * a.K,
                   norm_rows(A, a.M, a.K, a.gamma, a.beta, g->eps, nullptr, 0, d->aq, d->aq_ld, d->as, s));
       }
-      if (a.M <= 32)
+      if (a.M <= 32) {
         EC_LAUNCH(gemm_family(fam), bytes, gemm_i8_skinny(q, epi, 0, s));
-      else
+        if (a.pmax_out == d->pmax_ff) d->ff_pmax = a.pmax_out != nullptr;
+      } else {
         EC_LAUNCH(gemm_family(fam), bytes, gemm_i8(q, epi, s));
+        if (a.pmax_out == d->pmax_ff) d->ff_pmax = false;
+      }
       return 0;
     }
   }
@@ -1208,6 +1237,7 @@ static int linear(GPT2 *g, DevModel *d, const char *fam, GemvArgs a, int wt, int
     EC_LAUNCH(gemm_family(fam), bytes, gemm_w16_parts(q, wt, epi, 0, d->ah, d->ah_ld, d->ahs, s));
     return 0;
   }
+  if (a.pmax_out == d->pmax_ff) d->ff_pmax = false;  // the paths below leave the partial maxima unwritten
   if (gemv_vector_ok(a, wt, pro)) {
     EC_LAUNCH(fam, bytes, gemv(a, wt, epi, pro, s));
     return 0;
@@ -1370,6 +1400,8 @@ static int enqueue_forward(GPT2 *g, DevModel *d, int M, int lm_from, bool distin
 
   const int F = d->F, ldq = d->qkv_ld;
   const int nqkv = qwen ? E + 2 * kv : 3 * E;
+  // batched decode of 16-32 tokens: o and down quantize inside their GEMMs
+  const bool fq = d->fuse_quant && i8 && g_use_mfma && !run && M >= kGemmMinM && M <= 32;
   bool touched = false;
   for (int l = 0; l < (step ? 0 : g->n_layer); l++) {
     const LayerDev &W = d->L[l];
@@ -1393,6 +1425,10 @@ static int enqueue_forward(GPT2 *g, DevModel *d, int M, int lm_from, bool distin
     if (!run && M <= g->batch_cap) {  // long decode contexts: scores pass, then softmax / sums
       aa.scores = d->att_sc;
       aa.sc_ld = d->eff_ctx;
+    }
+    if (fq) {
+      aa.pmax = d->pmax_att;
+      aa.np = d->np_att;
     }
     hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
     if (g_touch && run && M >= kTouchMinRows && hipStreamIsCapturing(s, &cap) == hipSuccess &&
@@ -1436,6 +1472,10 @@ static int enqueue_forward(GPT2 *g, DevModel *d, int M, int lm_from, bool distin
     {
       GemvArgs a{d->att, E, nullptr, nullptr, nullptr, 0.0, W.wo, nullptr, W.so, nullptr, W.bo, d->x, E, M, E, E,
                  nullptr};
+      if (fq) {
+        a.pmax = d->pmax_att;
+        a.np = d->np_att;
+      }
       const int epi = i8 ? EPI_RESID : (W.bo ? EPI_BIAS_RESID : EPI_RESID);
       if ((r = linear(g, d, "gemv_o", a, wt, epi, i8 ? PRO_QUANT : PRO_F32, s))) return r;
     }
@@ -1443,16 +1483,28 @@ static int enqueue_forward(GPT2 *g, DevModel *d, int M, int lm_from, bool distin
     if (qwen) {
       GemvArgs a{d->x, E, nullptr, W.ln2_g, nullptr, g->eps, W.wg, W.wu, W.sg, W.su, nullptr, d->ff, F, M, E, F,
                  nullptr};
+      if (fq) {
+        a.pmax_out = d->pmax_ff;
+        a.np_out = d->np_ff;
+      }
       if ((r = linear(g, d, "gemv_gateup", a, wt, EPI_SWIGLU, PRO_RMS, s))) return r;
     } else {
       GemvArgs a{d->x, E, nullptr, W.ln2_g, W.ln2_b, g->eps, W.wfc, nullptr, W.sfc, nullptr, W.bfc, d->ff, F, M,
                  E, F, nullptr};
+      if (fq) {
+        a.pmax_out = d->pmax_ff;
+        a.np_out = d->np_ff;
+      }
       if ((r = linear(g, d, "gemv_fc", a, wt, i8 ? EPI_GELU : EPI_BIAS_GELU, PRO_LN, s))) return r;
     }
     // MLP down + residual
     {
       GemvArgs a{d->ff, F, nullptr, nullptr, nullptr, 0.0, W.wd, nullptr, W.sd, nullptr, W.bd, d->x, E, M, F, E,
                  nullptr};
+      if (fq) {
+        a.pmax = d->pmax_ff;
+        a.np = d->np_ff;
+      }
       const int epi = i8 ? EPI_RESID : (W.bd ? EPI_BIAS_RESID : EPI_RESID);
       if ((r = linear(g, d, "gemv_down", a, wt, epi, i8 ? PRO_QUANT : PRO_F32, s))) return r;
     }

@@ -7,6 +7,8 @@ token per slot (the M=16 matrix-core GEMM, the head_dim-128 attention
 kernels).  Every step's logits must be within max-abs 2e-2 of the oracle's and
 the greedy tokens identical.  The layer count is cut so that the CPU oracle
 finishes in seconds; every per-layer shape is the real one."""
+import os
+
 import numpy as np
 import pytest
 
@@ -139,3 +141,49 @@ def test_qwen25_15b_shape_c5_workload(c5_model):
             cur, pos = [int(x) for x in am], [p + 1 for p in pos]
             assert cur == oids[s], s
     print(f"C5 workload (16 x 1024 + 32 steps at M=16, 2 layers): max-abs logits diff {worst:.3e}")
+
+
+def _decode_m16(path, fuse: bool, prompt: int, steps: int, vocab: int):
+    """16 slots prefilled with `prompt`-token prompts, then `steps` greedy
+    steps at M=16 with logits; the model loaded with the o / down
+    quantization inside the skinny GEMMs (fuse) or as its own pass."""
+    old = os.environ.get("EDGECORE_FUSEQ")
+    os.environ["EDGECORE_FUSEQ"] = "1" if fuse else "0"
+    try:
+        with ec.Model(path, B, prompt + steps + 8) as m:
+            m.kv_reset()
+            prompts = [prompt_ids(prompt, vocab, seed=60 + b) for b in range(B)]
+            for b, p in enumerate(prompts):
+                m.forward(p, np.arange(prompt), np.full(prompt, b, np.int32), lm_from=prompt, want_logits=False)
+            cur, pos, out = [int(p[-1]) for p in prompts], [prompt] * B, []
+            for _ in range(steps):
+                got, am = m.forward(cur, pos, None, want_logits=True, want_argmax=True)
+                out.append(got)
+                cur, pos = [int(x) for x in am], [p + 1 for p in pos]
+            return np.stack(out)
+    finally:
+        if old is None:
+            del os.environ["EDGECORE_FUSEQ"]
+        else:
+            os.environ["EDGECORE_FUSEQ"] = old
+
+
+@pytest.mark.parametrize("prompt", [40, 600])
+def test_fused_quantization_equals_separate_pass(c5_model, prompt):
+    """Batched decode at M=16 with the o and down projections quantizing
+    their fp32 inputs inside the skinny GEMM (row maxima from the attention's
+    and the gate/up epilogue's partial maxima) against the separate
+    quantization pass: the same logits bit for bit, after short prompts (the
+    one-pass attention) and past 512 positions (the scores pass)."""
+    a = _decode_m16(c5_model, True, prompt, 6, V)
+    b = _decode_m16(c5_model, False, prompt, 6, V)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_fused_quantization_gpt2_int8(make_model):
+    """The same on the tiny int8 GPT-2 (fc with the GELU epilogue writes the
+    partial maxima the down projection quantizes with; head_dim 32 attention)."""
+    path = make_model("tiny-gpt2-int8")
+    a = _decode_m16(path, True, 20, 6, 50257)
+    b = _decode_m16(path, False, 20, 6, 50257)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))

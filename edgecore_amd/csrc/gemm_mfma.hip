@@ -85,15 +85,16 @@ struct MfmaOp<OP_BF16> {
   }
 };
 
-// two stage buffers; the direct-to-LDS form (DL) has unpadded rows
-template <int OP, int BM, bool DL>
+// NB stage buffers (2, or up to 4 in the direct-to-LDS form); the
+// direct-to-LDS form (DL) has unpadded rows
+template <int OP, int BM, bool DL, int NB = 2>
 constexpr size_t gemm_lds_bytes() {
-  return (size_t)2 * (MfmaOp<OP>::NP * BM + kBN) * (DL ? kBK : kPitch);
+  return (size_t)NB * (MfmaOp<OP>::NP * BM + kBN) * (DL ? kBK : kPitch);
 }
 
 // A: [M * NP][lda] elements (row m's part p at row m * NP + p), as: per-row
 // scale (int8 quantization scale, or the split's 2^e; 1 for bf16)
-template <int OP, int BM, int EPI, bool DL>
+template <int OP, int BM, int EPI, bool DL, int NB = 2>
 __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemvArgs a) {
   using Op = MfmaOp<OP>;
   using Acc = typename Op::Acc;
@@ -309,16 +310,23 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemvArgs a) {
         __builtin_amdgcn_global_load_lds((gvoid *)(src[u] + k0), (lvoid *)(base + u * 8 * kBK), 16, 0, 0);
     };
     const int sw = lr & 7;  // fragment rows are 16-aligned: row & 7 == lr & 7
-    // stage s is waited for (each wave its own loads, then the barrier)
-    // before stage s+1 is loaded into the other buffer, whose reads of stage
-    // s-1 completed before their multiplies used them.  The barrier is bare:
-    // __syncthreads() adds a fence whose waits come out no better.
-    dload(0, 0);
+    // NB stage buffers, NB - 1 stages in flight: stage s is waited for (each
+    // wave its own loads -- the loads complete in order, so the NB - 2 later
+    // stages' UPW instructions each may stay outstanding -- then the
+    // barrier) before stage s + NB - 1 is loaded into the buffer that stage
+    // s - 1 used, whose reads completed before the barrier.  The barrier is
+    // bare: __syncthreads() adds a fence whose waits come out no better.
+    // (Few tiles per CU wait on each stage's load latency: the C2 prefill
+    // linears with NB 2 took ~1 us per stage.)
+#pragma unroll
+    for (int p = 0; p < NB - 1; p++)
+      if (p < ns) dload(p * kBK, p);
     for (int s = 0; s < ns; s++) {
-      __builtin_amdgcn_s_waitcnt(0);
+      if (NB > 2 && s + NB - 2 < ns) asm volatile("s_waitcnt vmcnt(%0)" ::"i"((NB - 2) * UPW) : "memory");
+      else __builtin_amdgcn_s_waitcnt(0);
       asm volatile("s_barrier" ::: "memory");
-      if (s + 1 < ns) dload((s + 1) * kBK, (s + 1) & 1);
-      const int buf = s & 1;
+      if (s + NB - 1 < ns) dload((s + NB - 1) * kBK, (s + NB - 1) % NB);
+      const int buf = s % NB;
       const int8_t *ta = lds + (size_t)buf * RT * kBK + (size_t)(wm * WM + lr) * kBK;
       const int8_t *tb = lds + (size_t)buf * RT * kBK + (size_t)(NP * BM + lr) * kBK;
 #pragma unroll
@@ -411,7 +419,21 @@ hipError_t launch_bm(const GemvArgs &a, hipStream_t s) {
   const int T = ((a.N + NOUT - 1) / NOUT) * ((a.M + BM - 1) / BM);
   const dim3 grid(8 * ((T + 7) / 8));
   const bool dl = EC_GEMM_DL && (a.K * MfmaOp<OP>::EB) % kBK == 0 && (a.lda * MfmaOp<OP>::EB) % kBK == 0;
-  if (dl) klaunch((gemm_mfma_kernel<OP, BM, EPI, true>), grid, dim3(256), gemm_lds_bytes<OP, BM, true>(), s, a);
+  // grids of at most two tiles per CU: the most stage buffers (up to 4) with
+  // which the tiles a CU holds at once still fit its LDS, so that 2-3
+  // stages' loads are in flight.  C2's 128-token linears (24-96 tiles):
+  // down 40.3 -> 23.6 us, q|k|v and o 11.9 -> 8.4 us; C4's down (448
+  // tiles) 23.6 -> 21.7 us.
+  const int bpc = T <= 256 ? 1 : 2;
+  const size_t budget = (size_t)(158 * 1024) / bpc;
+  constexpr size_t l4 = gemm_lds_bytes<OP, BM, true, 4>(), l3 = gemm_lds_bytes<OP, BM, true, 3>();
+  if (dl && T <= 512 && l4 <= budget)
+    klaunch((gemm_mfma_kernel<OP, BM, EPI, true, l4 <= 158 * 1024 ? 4 : 2>), grid, dim3(256),
+            gemm_lds_bytes<OP, BM, true, l4 <= 158 * 1024 ? 4 : 2>(), s, a);
+  else if (dl && T <= 512 && l3 <= budget)
+    klaunch((gemm_mfma_kernel<OP, BM, EPI, true, l3 <= 158 * 1024 ? 3 : 2>), grid, dim3(256),
+            gemm_lds_bytes<OP, BM, true, l3 <= 158 * 1024 ? 3 : 2>(), s, a);
+  else if (dl) klaunch((gemm_mfma_kernel<OP, BM, EPI, true>), grid, dim3(256), gemm_lds_bytes<OP, BM, true>(), s, a);
   else klaunch((gemm_mfma_kernel<OP, BM, EPI, false>), grid, dim3(256), gemm_lds_bytes<OP, BM, false>(), s, a);
   return hipGetLastError();
 }

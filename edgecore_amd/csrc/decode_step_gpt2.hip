@@ -1,0 +1,387 @@
+// Persistent decode step of the fp16 GPT-2 forward for one token (M = 1):
+// every layer of src/gpt2.c:470-574 (GPT-2 small: d_model 768, 12 heads of
+// head_dim 64, GELU FFN 3072, LayerNorm, biases) in one co-resident grid, for
+// the decode loop (src/runtime_main.c:335-352).
+//
+// The same scheme as the int8 Qwen2 step (decode_step.hip): blocks hand
+// results to each other through tagged words (step_common.h), and each block
+// issues its phase's weight loads before it waits for the words of its input.
+// 256 blocks of 512 threads, one per CU; block b runs on XCD b % 8.  Per layer:
+//
+//   Q  (48 q|k|v blocks, 48 of the 3 E rows each) -- wait for x; LayerNorm
+//      (ln_1); 48 rows of fp16 weights against the normalized row (fp32
+//      products and sums); + bias; publish.
+//   A  (48 attention blocks: head h, element slice s; the 4 slices of a head
+//      on one XCD) -- wait for the head's 64 q, 64 k and 64 v words; the
+//      decode attention body (attn_decode.h: fp16 KV append, scores,
+//      softmax, p*v sums, no RoPE); publish the slice of the output.
+//   O  (48 o / down blocks, 16 rows each) -- wait for the attention output;
+//      o rows + bias; x_mid = x + (o + bias); publish.
+//   F  (48 fc blocks, 64 rows each) -- wait for x_mid; LayerNorm (ln_2); fc
+//      rows + bias; gelu_new; publish.
+//   D  (the o / down blocks, the same rows as O) -- wait for the GELU
+//      outputs; down rows + bias; x = x_mid + (d + bias); publish.
+//
+// Arithmetic: LayerNorm's mean and variance in double (a fixed tree over
+// the block) and the reference's float normalization; GELU is gelu_new
+// (ec_device.h); the fp16 dots are fp32 fused multiply-adds in a fixed order
+// (the reference's AVX2 order is eight interleaved FMA chains: the fp16 path
+// is compared within a tolerance, not bit for bit).  The bias is added to the
+// finished dot, then the residual, as src/gpt2.c:425-429 and 561-572 do.
+//
+// Waits are bounded as in decode_step.hip: past kSpin polls a block sets *err
+// and goes on; the step then ends with invalid results and the host reports
+// the error.
+#include "attn_decode.h"
+#include "ec_device.h"
+#include "ec_kernels.h"
+#include "step_common.h"
+
+namespace ec {
+
+namespace {
+
+constexpr int E = kStep16E, F = kStep16F, HD = 64;
+constexpr int NW = kStepThreads / 64;  // waves per block
+constexpr int kQRows = 48;             // q|k|v rows per Q block: 3 E / 48 = 48 blocks
+constexpr int kFRows = 64;             // fc rows per F block: F / 64 = 48 blocks
+constexpr int kODRows = 16;            // o / down rows per O/D block: E / 16 = 48 blocks
+constexpr int kNQ = 3 * E / kQRows, kNOD = E / kODRows, kNF = F / kFRows;
+constexpr int kHeads = E / HD;
+constexpr int kNA = 4 * kHeads;  // attention blocks (4 slices per head)
+static_assert(kNA + kNQ + kNOD + kNF <= kStepBlocks, "roles");
+static_assert(kHeads <= 16, "heads 0-7 take j 0-3 of XCD h, heads 8-15 j 4-7 of XCD h - 8");
+
+// exchange words per layer: X [E] | XM [E] | ATT [E] | QKV [3 E] | FF [F]
+constexpr size_t kOffXM = E, kOffATT = 2 * E, kOffQKV = 3 * E, kOffFF = 6 * E;
+
+// the 8 fp16 of a 16-byte chunk times the 8 floats at h (LDS), fused into acc
+__device__ __forceinline__ float fma8(float acc, v4u w, const float *h) {
+  const float4 h0 = *reinterpret_cast<const float4 *>(h), h1 = *reinterpret_cast<const float4 *>(h + 4);
+  const float a[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+  const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    acc = __builtin_fmaf(a[2 * k], h2f((uint16_t)(ww[k] & 0xffffu)), acc);
+    acc = __builtin_fmaf(a[2 * k + 1], h2f((uint16_t)(ww[k] >> 16)), acc);
+  }
+  return acc;
+}
+
+// sums over the 16 lanes of each DPP row (fixed tree; every lane of the row gets it)
+__device__ __forceinline__ float sum16(float v) {
+  v = v + dpp_mov<0xB1>(v);   // quad_perm [1,0,3,2]
+  v = v + dpp_mov<0x4E>(v);   // quad_perm [2,3,0,1]
+  v = v + dpp_mov<0x141>(v);  // row_half_mirror
+  v = v + dpp_mov<0x140>(v);  // row_mirror
+  return v;
+}
+
+// LayerNorm of xs[E] into hs[E] (both LDS; src/gpt2.c:398-414): the mean and
+// the variance in double, each a block sum in a fixed tree (thread t holds
+// elements t and t + 512); hs = (float)((x - mean) * rstd) * gamma + beta.
+// g / b: gamma and beta of the thread's elements.  Ends with a barrier.
+__device__ void layer_norm(const float *xs, const float (&g)[2], const float (&b)[2], double eps, float *hs,
+                           double *redd) {
+  const int t = threadIdx.x;
+  const bool two = t + kStepThreads < E;
+  const float x0 = xs[t], x1 = two ? xs[t + kStepThreads] : 0.0f;
+  double s = (double)x0 + (two ? (double)x1 : 0.0);
+  s = block_sum_1b<NW>(s, redd);
+  const double mean = s / E;
+  const double d0 = (double)x0 - mean, d1 = two ? (double)x1 - mean : 0.0;
+  double v = d0 * d0 + d1 * d1;
+  v = block_sum_1b<NW>(v, redd + NW);
+  const double rstd = 1.0 / sqrt(v / E + eps);
+  hs[t] = (float)(d0 * rstd) * g[0] + b[0];
+  if (two) hs[t + kStepThreads] = (float)(d1 * rstd) * g[1] + b[1];
+  __syncthreads();
+}
+
+// x of the token at layer 0: fp32(wte[tok]) + fp32(wpe[pos]) (src/gpt2.c:489-499)
+__device__ __forceinline__ float embed_x(const Step16Args &a, int tok, int pos, int i) {
+  return h2f(gbl(a.wte)[(size_t)tok * E + i]) + h2f(gbl(a.wpe)[(size_t)pos * E + i]);
+}
+
+// Q blocks (block gi): rows [48 gi, 48 gi + 48) of q|k|v.  Wave w takes rows
+// 6 w + 2 i + (lane >= 32), i < 3; a lane takes 16-byte chunks (lane & 31) +
+// 32 c, c < 3, of those rows, so that it reads each chunk of the normalized
+// row once for its three rows.
+__device__ void q_loop(const Step16Args &a, int gi, unsigned tag, int tok, float *lds, double *redd) {
+  float *xs = lds, *hs = lds + E;
+  const int t = tid_opaque(), lane = t & 63, wave = t >> 6, half = lane >> 5, ln = lane & 31;
+  const int pos = ld_uniform(a.attn.pos);
+  for (int l = 0; l < a.L; l++) {
+    const Step16Layer &W = a.layers[l];
+    const unsigned long long *X = a.xch + (size_t)(l - 1) * kStep16Words;
+    unsigned long long *QKV = a.xch + (size_t)l * kStep16Words + kOffQKV;
+    // rows n0 + 2 i (lanes 0-31) and n0 + 2 i + 1 (lanes 32-63)
+    const int n0 = kQRows * uniform_opaque(gi) + 6 * wave;
+    v4u w[3][3];
+#pragma unroll
+    for (int i = 0; i < 3; i++) {
+      const auto src = gbl16(W.wqkv + (size_t)(n0 + 2 * i + half) * E);
+#pragma unroll
+      for (int c = 0; c < 3; c++) w[i][c] = __builtin_bit_cast(v4u, __builtin_nontemporal_load(src + ln + 32 * c));
+    }
+    float bias[6];
+#pragma unroll
+    for (int i = 0; i < 6; i++) bias[i] = gbl(W.bqkv)[n0 + i];
+    float g[2], b[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const int i = min(t + kStepThreads * j, E - 1);
+      g[j] = gbl(W.ln1_g)[i];
+      b[j] = gbl(W.ln1_b)[i];
+    }
+    if (l == 0) {
+      for (int i = t; i < E; i += kStepThreads) xs[i] = embed_x(a, tok, pos, i);
+      __syncthreads();
+    } else {
+      gather<1>(X, E, tag, xs, a.err);
+    }
+    layer_norm(xs, g, b, a.eps, hs, redd);
+    float acc[3] = {0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int c = 0; c < 3; c++) {
+      const float *h = hs + 8 * (ln + 32 * c);
+#pragma unroll
+      for (int i = 0; i < 3; i++) acc[i] = fma8(acc[i], w[i][c], h);
+    }
+#pragma unroll
+    for (int i = 0; i < 3; i++) {
+      const float s = sum16(acc[i]);
+      // the rows of lanes 0-31 and 32-63: the two DPP rows of each half
+      const float r0 = readlane(s, 0) + readlane(s, 16), r1 = readlane(s, 32) + readlane(s, 48);
+      if (lane == 0) {
+        put_word(QKV + n0 + 2 * i, r0 + bias[2 * i], tag);
+        put_word(QKV + n0 + 2 * i + 1, r1 + bias[2 * i + 1], tag);
+      }
+    }
+  }
+}
+
+// F blocks (block gi): fc rows [64 gi, 64 gi + 64), as the Q blocks' rows
+// (wave w: rows 8 w + 2 i + (lane >= 32), i < 4).
+__device__ void f_loop(const Step16Args &a, int gi, unsigned tag, float *lds, double *redd) {
+  float *xs = lds, *hs = lds + E;
+  const int t = tid_opaque(), lane = t & 63, wave = t >> 6, half = lane >> 5, ln = lane & 31;
+  for (int l = 0; l < a.L; l++) {
+    const Step16Layer &W = a.layers[l];
+    const unsigned long long *XM = a.xch + (size_t)l * kStep16Words + kOffXM;
+    unsigned long long *FF = a.xch + (size_t)l * kStep16Words + kOffFF;
+    const int n0 = kFRows * uniform_opaque(gi) + 8 * wave;
+    v4u w[4][3];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const auto src = gbl16(W.wfc + (size_t)(n0 + 2 * i + half) * E);
+#pragma unroll
+      for (int c = 0; c < 3; c++) w[i][c] = __builtin_bit_cast(v4u, __builtin_nontemporal_load(src + ln + 32 * c));
+    }
+    float bias[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) bias[i] = gbl(W.bfc)[n0 + i];
+    float g[2], b[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const int i = min(t + kStepThreads * j, E - 1);
+      g[j] = gbl(W.ln2_g)[i];
+      b[j] = gbl(W.ln2_b)[i];
+    }
+    gather<1>(XM, E, tag, xs, a.err);
+    layer_norm(xs, g, b, a.eps, hs, redd);
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int c = 0; c < 3; c++) {
+      const float *h = hs + 8 * (ln + 32 * c);
+#pragma unroll
+      for (int i = 0; i < 4; i++) acc[i] = fma8(acc[i], w[i][c], h);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const float s = sum16(acc[i]);
+      const float r0 = readlane(s, 0) + readlane(s, 16), r1 = readlane(s, 32) + readlane(s, 48);
+      if (lane == 0) {
+        put_word(FF + n0 + 2 * i, gelu_new(r0 + bias[2 * i]), tag);
+        put_word(FF + n0 + 2 * i + 1, gelu_new(r1 + bias[2 * i + 1]), tag);
+      }
+    }
+  }
+}
+
+// O/D blocks (block gi): rows [16 gi, 16 gi + 16) of o and of down; wave w
+// takes rows 2 w and 2 w + 1.  o: lanes 0-31 row 2 w, 32-63 row 2 w + 1, 3
+// chunks each; down (K = F): every lane both rows, 6 chunks, each GELU
+// chunk read once for the two rows.
+__device__ void od_loop(const Step16Args &a, int gi, unsigned tag, int tok, float *lds, float *xown, float *xmown) {
+  float *vs = lds;  // the attention output [E], then the GELU outputs [F]
+  const int t = tid_opaque(), lane = t & 63, wave = t >> 6, half = lane >> 5, ln = lane & 31;
+  const int pos = ld_uniform(a.attn.pos);
+  const int r0 = kODRows * uniform_opaque(gi);
+  if (t < kODRows) xown[t] = embed_x(a, tok, pos, r0 + t);
+  for (int l = 0; l < a.L; l++) {
+    const Step16Layer &W = a.layers[l];
+    unsigned long long *Xo = a.xch + (size_t)l * kStep16Words, *XM = Xo + kOffXM;
+    const unsigned long long *ATT = Xo + kOffATT, *FFw = Xo + kOffFF;
+    const int no = r0 + 2 * wave + half;
+    v4u wo[3], wd[2][6];
+    {
+      const auto so = gbl16(W.wo + (size_t)no * E);
+#pragma unroll
+      for (int c = 0; c < 3; c++) wo[c] = __builtin_bit_cast(v4u, __builtin_nontemporal_load(so + ln + 32 * c));
+#pragma unroll
+      for (int r = 0; r < 2; r++) {
+        const auto sd = gbl16(W.wd + (size_t)(r0 + 2 * wave + r) * F);
+#pragma unroll
+        for (int c = 0; c < 6; c++) wd[r][c] = __builtin_bit_cast(v4u, __builtin_nontemporal_load(sd + lane + 64 * c));
+      }
+    }
+    const float bo0 = gbl(W.bo)[r0 + 2 * wave], bo1 = gbl(W.bo)[r0 + 2 * wave + 1];
+    const float bd0 = gbl(W.bd)[r0 + 2 * wave], bd1 = gbl(W.bd)[r0 + 2 * wave + 1];
+
+    // ---- o projection + residual ----
+    gather<1>(ATT, E, tag, vs, a.err);
+    {
+      float acc = 0.0f;
+#pragma unroll
+      for (int c = 0; c < 3; c++) acc = fma8(acc, wo[c], vs + 8 * (ln + 32 * c));
+      const float s = sum16(acc);
+      const float o0 = readlane(s, 0) + readlane(s, 16), o1 = readlane(s, 32) + readlane(s, 48);
+      if (lane == 0) {
+        const float m0 = xown[2 * wave] + (o0 + bo0), m1 = xown[2 * wave + 1] + (o1 + bo1);
+        xmown[2 * wave] = m0;
+        xmown[2 * wave + 1] = m1;
+        put_word(XM + r0 + 2 * wave, m0, tag);
+        put_word(XM + r0 + 2 * wave + 1, m1, tag);
+      }
+    }
+
+    // ---- down projection + residual ----
+    gather<(F / 2 + kStepThreads - 1) / kStepThreads>(FFw, F, tag, vs, a.err);
+    {
+      float acc0 = 0.0f, acc1 = 0.0f;
+#pragma unroll
+      for (int c = 0; c < 6; c++) {
+        const float *h = vs + 8 * (lane + 64 * c);
+        acc0 = fma8(acc0, wd[0][c], h);
+        acc1 = fma8(acc1, wd[1][c], h);
+      }
+      const float s0 = sum16(acc0), s1 = sum16(acc1);
+      const float d0 = (readlane(s0, 0) + readlane(s0, 16)) + (readlane(s0, 32) + readlane(s0, 48));
+      const float d1 = (readlane(s1, 0) + readlane(s1, 16)) + (readlane(s1, 32) + readlane(s1, 48));
+      if (lane == 0) {
+        const float x0 = xmown[2 * wave] + (d0 + bd0), x1 = xmown[2 * wave + 1] + (d1 + bd1);
+        xown[2 * wave] = x0;
+        xown[2 * wave + 1] = x1;
+        put_word(Xo + r0 + 2 * wave, x0, tag);
+        put_word(Xo + r0 + 2 * wave + 1, x1, tag);
+        if (l + 1 == a.L) {
+          a.x_out[r0 + 2 * wave] = x0;
+          a.x_out[r0 + 2 * wave + 1] = x1;
+        }
+      }
+    }
+  }
+}
+
+// Wait for the 64 q, 64 k and 64 v words of head h (words h*64.., E + h*64..,
+// 2E + h*64.. of the q|k|v exchange) and put them into qkv_s[192] (LDS):
+// threads t < 96 take one pair each.  Ends with a barrier.
+__device__ void gather_head(const unsigned long long *QKV, int h, unsigned tag, float *qkv_s, int *err) {
+  const int t = threadIdx.x;
+  const __amdgpu_buffer_rsrc_t rs = xch_rsrc(QKV, 3 * E);
+  if (t < 96) {
+    const int r = t >> 5, w = r * E + h * HD + 2 * (t & 31);
+    for (int it = 0;; it++) {
+      const v4u v = get_pair(rs, w >> 1);
+      if (v.y == tag && v.w == tag) {
+        qkv_s[r * HD + 2 * (t & 31)] = __uint_as_float(v.x);
+        qkv_s[r * HD + 2 * (t & 31) + 1] = __uint_as_float(v.z);
+        break;
+      }
+      if (it >= kSpin) {
+        atomicOr(err, 1);
+        break;
+      }
+      if ((it & 63) == 63 && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) break;
+      __builtin_amdgcn_s_sleep(1);
+    }
+  }
+  // this wave's prefetched K / V rows have landed; the barrier publishes them
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+}
+
+// A blocks: head h, element slice s of the attention, every layer; the next
+// layer's K rows (up to the first K tile) and this slice's V rows are loaded
+// straight into the body's LDS tiles after each layer's attention.
+__device__ void attention_loop(const Step16Args &a, int head, int slice, unsigned tag, float *lds, float *qkv_s,
+                               const uint64_t *etab) {
+  __shared__ double2 cs_s[64];  // no rotation: cos 1, sin 0
+  if (threadIdx.x < 64) cs_s[threadIdx.x] = make_double2(1.0, 0.0);
+  const AttnPre pre{etab, cs_s};
+  const int hh = uniform_opaque(head), ss = uniform_opaque(slice);
+  attn_prefetch_k<HD, kStepSlices>(a.attn, 0, hh, lds, 0);
+  attn_prefetch_v<HD, kStepSlices>(a.attn, 0, hh, ss, lds, 0);
+  for (int l = 0; l < a.L; l++) {
+    const unsigned long long *QKV = a.xch + (size_t)l * kStep16Words + kOffQKV;
+    unsigned long long *att = a.xch + (size_t)l * kStep16Words + kOffATT;
+    gather_head(QKV, hh, tag, qkv_s, a.err);
+    const int o0 = hh * HD + 16 * ss;
+    attn_decode_block<HD, true, kStepSlices, false, true>(a.attn, 0, hh, ss, qkv_s, qkv_s + HD, qkv_s + 2 * HD, lds,
+                                                          [&](int i, float o) { put_word(att + o0 + i, o, tag); },
+                                                          a.kv_layer * l, NoMark{}, &pre);
+    __syncthreads();  // the body's LDS and qkv_s are reused by the next layer
+    if (l + 1 < a.L) {
+      attn_prefetch_k<HD, kStepSlices>(a.attn, 0, hh, lds, a.kv_layer * (l + 1));
+      attn_prefetch_v<HD, kStepSlices>(a.attn, 0, hh, ss, lds, a.kv_layer * (l + 1));
+    }
+  }
+}
+
+__global__ __launch_bounds__(kStepThreads) void decode_step_gpt2_kernel(Step16Args a) {
+  extern __shared__ __attribute__((aligned(16))) float lds[];
+  __shared__ __attribute__((aligned(16))) float qkv_s[3 * HD];
+  __shared__ float xown[kODRows], xmown[kODRows];
+  __shared__ double redd[2 * NW];
+  __shared__ uint64_t etab[32];
+  const int b = blockIdx.x, t = threadIdx.x;
+  const unsigned tag = ld_uniform(a.tag);
+  const int tok = ld_uniform(a.tok);
+  if (t < 32) etab[t] = ec_exp2_32[t];
+  // roles: attention blocks, head h < 8 on XCD h at slots j = b / 8 of 0-3,
+  // head 8 + x on XCD x at j 4-7; then, numbered gi in block order, the Q,
+  // O/D and F blocks; the rest have nothing to do
+  const int xcd = b & 7, j = b >> 3;
+  if (j < 4) {
+    attention_loop(a, xcd, j, tag, lds, qkv_s, etab);
+    return;
+  }
+  if (j < 8 && xcd < kHeads - 8) {
+    attention_loop(a, 8 + xcd, j - 4, tag, lds, qkv_s, etab);
+    return;
+  }
+  // attention blocks with a lower index: the 32 of j < 4, and of j 4-7 the
+  // kHeads - 8 of each earlier row (and of this row, whose XCDs below this
+  // one's all hold attention blocks)
+  const int before = 32 + (j < 8 ? (j - 3) * (kHeads - 8) : 4 * (kHeads - 8));
+  const int gi = b - before;
+  if (gi < kNQ) q_loop(a, gi, tag, tok, lds, redd);
+  else if (gi < kNQ + kNOD) od_loop(a, gi - kNQ, tag, tok, lds, xown, xmown);
+  else if (gi < kNQ + kNOD + kNF) f_loop(a, gi - kNQ - kNOD, tag, lds, redd);
+}
+
+}  // namespace
+
+size_t decode_step_gpt2_scratch_bytes() { return (size_t)(E + F) * sizeof(float) + 64; }
+
+hipError_t decode_step_gpt2(const Step16Args &a, size_t lds, bool cooperative, hipStream_t s) {
+  Step16Args args = a;
+  void *kargs[] = {&args};
+  const void *k = reinterpret_cast<const void *>(decode_step_gpt2_kernel);
+  if (cooperative)
+    return hipLaunchCooperativeKernel(k, dim3(kStepBlocks), dim3(kStepThreads), kargs, (unsigned)lds, s);
+  return hipLaunchKernel(k, dim3(kStepBlocks), dim3(kStepThreads), kargs, (unsigned)lds, s);
+}
+
+}  // namespace ec

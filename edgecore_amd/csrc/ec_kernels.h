@@ -298,6 +298,44 @@ size_t decode_step_scratch_bytes(int E, int F);
 // otherwise a plain launch of the same kStepBlocks blocks, one per CU, which the
 // step's bounded waits turn into a reported error if a block never ran
 hipError_t decode_step(const StepArgs &a, size_t lds, bool cooperative, hipStream_t s);
+
+// Persistent decode step of the fp16 GPT-2 forward (decode_step_gpt2.hip):
+// every layer for one token in one launch of kStepBlocks blocks of
+// kStepThreads threads, for the GPT-2 small shape (d_model kStep16E, head_dim
+// 64, FFN kStep16F).  Exchange words per layer (kStep16Words, tagged as in
+// the int8 step): [x: E][x_mid: E][attention output: E][q|k|v: 3 E][GELU
+// outputs: F].
+constexpr int kStep16E = 768, kStep16F = 3072;
+constexpr size_t kStep16Words = 6 * (size_t)kStep16E + kStep16F;
+struct Step16Layer {
+  const float *ln1_g, *ln1_b, *ln2_g, *ln2_b;
+  const uint16_t *wqkv;  // fp16 [3 E][E]: q | k | v rows
+  const float *bqkv;
+  const uint16_t *wo;
+  const float *bo;
+  const uint16_t *wfc;  // fp16 [F][E]
+  const float *bfc;
+  const uint16_t *wd;  // fp16 [E][F]
+  const float *bd;
+};
+struct Step16Args {
+  const Step16Layer *layers;   // device array [L]
+  const uint16_t *wte, *wpe;   // fp16 [V][E], [n_ctx][E]
+  int L;
+  double eps;
+  size_t kv_layer;             // elements per layer of one cache
+  const int *tok;              // the token's id (position and slot: attn.pos / attn.slot)
+  const unsigned *tag;         // this step's tag (> 0, new every launch)
+  unsigned long long *xch;     // [L][kStep16Words] tagged exchange words
+  float *x_out;                // x after the last layer [E]
+  int *err;                    // set when a wait timed out (results invalid)
+  // the attention body's arguments for layer 0 (no RoPE: cs null); layer l
+  // adds l * kv_layer to the caches
+  AttnArgs attn;
+};
+// dynamic LDS of the step's non-attention blocks
+size_t decode_step_gpt2_scratch_bytes();
+hipError_t decode_step_gpt2(const Step16Args &a, size_t lds, bool cooperative, hipStream_t s);
 // Prefill attention (attn_prefill.hip): the M tokens are one slot's run of
 // consecutive positions whose k / v are already in the cache (fuse_kv 0);
 // blocks of 16, 8 or 4 tokens per head.  _ok: head_dim 32/64/128, q rows

@@ -680,7 +680,11 @@ struct DevModel {
   int last_lm_rows = 0;  // rows of the LM-head chunk the last forward left in `logits`
   // persistent decode step (decode_step.hip), for int8 Qwen2 models of its shape
   bool step_ok = false;
+  // 0: the int8 Qwen2 step (decode_step.hip), 1: the fp16 GPT-2 step
+  // (decode_step_gpt2.hip)
+  int step_kind = 0;
   StepLayer *d_layers = nullptr;  // device copy of the layers' pointers
+  Step16Layer *d_layers16 = nullptr;
   unsigned long long *xch = nullptr;  // tagged exchange words
   float *ffv = nullptr;               // the step's FFN words, two halves of [L][F]
   size_t ffv_words = 0;
@@ -746,7 +750,8 @@ static void free_dev(DevModel *d) {
   if (!d) return;
   void *ps[] = {d->arena, d->rope, d->d_tok, d->d_pos, d->d_slot, d->d_amax, d->x, d->h, d->qkv,
                 d->att, d->ff, d->aq, d->as, d->ah, d->ahs, d->att_sc, d->logits, d->kc, d->vc, d->cand, d->tk_cand,
-                d->tk_nan, d->tk_vals, d->tk_idx, d->tk_status, d->d_layers, d->xch, d->ffv, d->d_step_io, d->d_trace,
+                d->tk_nan, d->tk_vals, d->tk_idx, d->tk_status, d->d_layers, d->d_layers16, d->xch, d->ffv,
+                d->d_step_io, d->d_trace,
                 d->d_gen, d->d_gen_t, d->pmax_att, d->pmax_ff};
   for (void *p : ps)
     if (p) (void)hipFree(p);
@@ -799,19 +804,27 @@ static DevModel *dev_detach(const GPT2 *g) {
 // words to tag 0, both FFN halves to kStepFfEmpty (not inside a capture).
 static hipError_t step_clear(DevModel *d, hipStream_t s) {
   hipError_t e = hipMemsetAsync(d->xch, 0, d->xch_bytes, s);
-  if (e == hipSuccess) e = hipMemsetD32Async((hipDeviceptr_t)d->ffv, (int)kStepFfEmpty, d->ffv_words, s);
+  if (e == hipSuccess && d->ffv) e = hipMemsetD32Async((hipDeviceptr_t)d->ffv, (int)kStepFfEmpty, d->ffv_words, s);
   return e;
 }
 
-static bool step_shape_ok(const GPT2 *g, const DevModel *d) {
+// The persistent step that applies to a model: 0 the int8 Qwen2 step, 1 the
+// fp16 GPT-2 step, -1 none (a kernel per operation).
+static int step_shape_kind(const GPT2 *g, const DevModel *d) {
   const char *env = getenv("EDGECORE_STEP");
-  if (env && !strcmp(env, "0")) return false;
+  if (env && !strcmp(env, "0")) return -1;
   int coop = 0;
-  if (hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, g_device) != hipSuccess || !coop) return false;
+  if (hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, g_device) != hipSuccess || !coop) return -1;
+  if (g_prop.multiProcessorCount != kStepBlocks) return -1;
   const int H = g->n_head, KVH = g->n_kv_head, E = g->n_embd, F = d->F;
-  return g->arch == ARCH_QWEN2 && g->precision == 0 && E == 896 && g->head_dim == 64 && KVH >= 1 && KVH <= 8 &&
-         H % KVH == 0 && (H / KVH) * kStepSlices <= kStepBlocks / 8 && F % 16 == 0 && F <= 5120 &&
-         H * kStepSlices + E / 16 + (F + 63) / 64 < kStepBlocks && g_prop.multiProcessorCount == kStepBlocks;
+  if (g->arch == ARCH_QWEN2 && g->precision == 0 && E == 896 && g->head_dim == 64 && KVH >= 1 && KVH <= 8 &&
+      H % KVH == 0 && (H / KVH) * kStepSlices <= kStepBlocks / 8 && F % 16 == 0 && F <= 5120 &&
+      H * kStepSlices + E / 16 + (F + 63) / 64 < kStepBlocks)
+    return 0;
+  if (g->arch != ARCH_QWEN2 && g->precision == 1 && E == kStep16E && g->head_dim == 64 && H == E / 64 &&
+      KVH == H && F == kStep16F && g->wpe && g->sliding_window == 0)
+    return 1;
+  return -1;
 }
 
 static int load_impl(GPT2 *g, const char *path, int batch_cap, int max_ctx) {
@@ -1098,19 +1111,40 @@ static int load_impl(GPT2 *g, const char *path, int batch_cap, int max_ctx) {
     EC_HIP(dev_malloc(&d->tk_idx, (size_t)d->lm_rows * n * sizeof(int)));
     EC_HIP(dev_malloc(&d->tk_status, (size_t)d->lm_rows * sizeof(int)));
   }
-  if (step_shape_ok(g, d)) {
-    std::vector<StepLayer> sl(Lc);
+  int kind = step_shape_kind(g, d);
+  if (kind == 1) {  // the GPT-2 step adds every bias
     for (int l = 0; l < Lc; l++) {
       const LayerDev &W = d->L[l];
-      sl[l] = StepLayer{W.ln1_g, W.ln2_g, (const int8_t *)W.wqkv, W.sqkv, (const int8_t *)W.wo, W.so,
-                        (const int8_t *)W.wg, (const int8_t *)W.wu, W.sg, W.su, (const int8_t *)W.wd, W.sd};
+      if (!W.ln1_b || !W.ln2_b || !W.bqkv || !W.bo || !W.bfc || !W.bd) kind = -1;
     }
-    EC_HIP(dev_malloc(&d->d_layers, sl.size() * sizeof(StepLayer)));
-    EC_HIP(hipMemcpy(d->d_layers, sl.data(), sl.size() * sizeof(StepLayer), hipMemcpyHostToDevice));
-    d->xch_bytes = (size_t)Lc * 3 * (size_t)E * sizeof(unsigned long long);
-    EC_HIP(dev_malloc(&d->xch, d->xch_bytes));
-    d->ffv_words = (size_t)2 * Lc * F;
-    EC_HIP(dev_malloc(&d->ffv, d->ffv_words * sizeof(float)));
+  }
+  if (kind >= 0) {
+    d->step_kind = kind;
+    if (kind == 0) {
+      std::vector<StepLayer> sl(Lc);
+      for (int l = 0; l < Lc; l++) {
+        const LayerDev &W = d->L[l];
+        sl[l] = StepLayer{W.ln1_g, W.ln2_g, (const int8_t *)W.wqkv, W.sqkv, (const int8_t *)W.wo, W.so,
+                          (const int8_t *)W.wg, (const int8_t *)W.wu, W.sg, W.su, (const int8_t *)W.wd, W.sd};
+      }
+      EC_HIP(dev_malloc(&d->d_layers, sl.size() * sizeof(StepLayer)));
+      EC_HIP(hipMemcpy(d->d_layers, sl.data(), sl.size() * sizeof(StepLayer), hipMemcpyHostToDevice));
+      d->xch_bytes = (size_t)Lc * 3 * (size_t)E * sizeof(unsigned long long);
+      EC_HIP(dev_malloc(&d->xch, d->xch_bytes));
+      d->ffv_words = (size_t)2 * Lc * F;
+      EC_HIP(dev_malloc(&d->ffv, d->ffv_words * sizeof(float)));
+    } else {
+      std::vector<Step16Layer> sl(Lc);
+      for (int l = 0; l < Lc; l++) {
+        const LayerDev &W = d->L[l];
+        sl[l] = Step16Layer{W.ln1_g, W.ln1_b, W.ln2_g, W.ln2_b, (const uint16_t *)W.wqkv, W.bqkv,
+                            (const uint16_t *)W.wo, W.bo, (const uint16_t *)W.wfc, W.bfc, (const uint16_t *)W.wd, W.bd};
+      }
+      EC_HIP(dev_malloc(&d->d_layers16, sl.size() * sizeof(Step16Layer)));
+      EC_HIP(hipMemcpy(d->d_layers16, sl.data(), sl.size() * sizeof(Step16Layer), hipMemcpyHostToDevice));
+      d->xch_bytes = (size_t)Lc * kStep16Words * sizeof(unsigned long long);
+      EC_HIP(dev_malloc(&d->xch, d->xch_bytes));
+    }
     EC_HIP(step_clear(d, nullptr));
     EC_HIP(hipDeviceSynchronize());
     EC_HIP(dev_malloc(&d->d_step_io, 8 * sizeof(int)));
@@ -1311,14 +1345,18 @@ static int step_vtile(int max_npos, int E, int kv) {
 
 static size_t step_lds(const GPT2 *g, const DevModel *d, int max_npos, int vtile) {
   const size_t a = step_attn_area(max_npos, vtile, g->n_kv_embd) + step_norm_bytes(g->n_embd),
-               b = decode_step_scratch_bytes(g->n_embd, d->F);
+               b = d->step_kind == 1 ? decode_step_gpt2_scratch_bytes() : decode_step_scratch_bytes(g->n_embd, d->F);
   return a > b ? a : b;
 }
 
-// algorithmic bytes of one persistent step: every layer's int8 weights and
-// row scales once, plus the K/V rows its attention reads
+// algorithmic bytes of one persistent step: every layer's weights and row
+// scales (int8) or biases (fp16) once, plus the K/V rows its attention reads
 static double step_bytes(const GPT2 *g, const DevModel *d, int npos) {
   const double E = g->n_embd, F = d->F, kv = g->n_kv_embd;
+  if (d->step_kind == 1) {
+    const double w = 3 * E * E + E * E + 2 * F * E, b = 3 * E + E + F + E + 4 * E;
+    return g->n_layer * (2 * w + 4 * b + (double)npos * kv * 4);
+  }
   const double rows = (E + 2 * kv) + E + 2 * F + E;
   const double w = E * (E + 2 * kv) + E * E + 2 * F * E + F * E;
   return g->n_layer * (w + 4 * rows + (double)npos * kv * 4);
@@ -1350,11 +1388,8 @@ static int enqueue_step(GPT2 *g, DevModel *d, int max_npos, hipStream_t s) {
   aa.max_npos = max_npos;
   aa.vtile = vtile;
   aa.fuse_kv = 1;
-  aa.cs = d->rope;
+  aa.cs = g->arch == ARCH_QWEN2 ? d->rope : nullptr;  // GPT-2: no rotation
   aa.half = d->half;
-  StepArgs sa{d->d_layers, g->wte, g->n_layer, g->n_embd, g->n_head, g->n_kv_head, d->F, g->eps, d->kv_layer,
-              io, reinterpret_cast<const unsigned *>(io + 3), d->xch, d->x, io + 4, d->d_trace, aa,
-              (int)(step_attn_area(max_npos, vtile, g->n_kv_embd) / sizeof(float)), d->ffv};
   const size_t lds = step_lds(g, d, max_npos, vtile);
   // decode_step is a cooperative launch (not through klaunch): its profiler
   // events are recorded on the stream around it
@@ -1362,7 +1397,17 @@ static int enqueue_step(GPT2 *g, DevModel *d, int max_npos, hipStream_t s) {
   hipEvent_t e0 = g_launch_ev[0], e1 = g_launch_ev[1];
   g_launch_ev[0] = g_launch_ev[1] = nullptr;
   if (e0) EC_HIP(hipEventRecord(e0, s));
-  const hipError_t e = decode_step(sa, lds, g_step_coop, s);
+  hipError_t e;
+  if (d->step_kind == 1) {
+    const Step16Args sa{d->d_layers16, g->wte, g->wpe, g->n_layer, g->eps, d->kv_layer, io,
+                        reinterpret_cast<const unsigned *>(io + 3), d->xch, d->x, io + 4, aa};
+    e = decode_step_gpt2(sa, lds, g_step_coop, s);
+  } else {
+    const StepArgs sa{d->d_layers, g->wte, g->n_layer, g->n_embd, g->n_head, g->n_kv_head, d->F, g->eps,
+                      d->kv_layer, io, reinterpret_cast<const unsigned *>(io + 3), d->xch, d->x, io + 4, d->d_trace,
+                      aa, (int)(step_attn_area(max_npos, vtile, g->n_kv_embd) / sizeof(float)), d->ffv};
+    e = decode_step(sa, lds, g_step_coop, s);
+  }
   if (e0 && e == hipSuccess) EC_HIP(hipEventRecord(e1, s));
   if (e != hipSuccess) {
     if (p_ >= 0) {

@@ -22,8 +22,15 @@
 //   D  (the o / down blocks, the same rows as O) -- wait for the GELU
 //      outputs; down rows + bias; x = x_mid + (d + bias); publish.
 //
-// Arithmetic: LayerNorm's mean and variance in double (a fixed tree over
-// the block) and the reference's float normalization; GELU is gelu_new
+// An exchange costs about 2 us whatever its size (the store's trip to the
+// device-coherent level, about 0.7 us, then the readers' next poll).  The
+// attention blocks computing the head's q|k|v rows themselves (one exchange
+// fewer) was slower: each slice block then does all 192 rows (2.3 us even on
+// the matrix cores, against 1 us for a Q block's 48 rows) and pulls 295 KB
+// of weights through its XCD's L2 every layer.
+//
+// Arithmetic: LayerNorm in two passes, each lane's sums in fp32 and the
+// wave's in double (a fixed tree), the normalization in fp32; GELU is gelu_new
 // (ec_device.h); the fp16 dots are fp32 fused multiply-adds in a fixed order
 // (the reference's AVX2 order is eight interleaved FMA chains: the fp16 path
 // is compared within a tolerance, not bit for bit).  The bias is added to the
@@ -42,7 +49,6 @@ namespace ec {
 namespace {
 
 constexpr int E = kStep16E, F = kStep16F, HD = 64;
-constexpr int NW = kStepThreads / 64;  // waves per block
 constexpr int kQRows = 48;             // q|k|v rows per Q block: 3 E / 48 = 48 blocks
 constexpr int kFRows = 64;             // fc rows per F block: F / 64 = 48 blocks
 constexpr int kODRows = 16;            // o / down rows per O/D block: E / 16 = 48 blocks
@@ -54,6 +60,45 @@ static_assert(kHeads <= 16, "heads 0-7 take j 0-3 of XCD h, heads 8-15 j 4-7 of 
 
 // exchange words per layer: X [E] | XM [E] | ATT [E] | QKV [3 E] | FF [F]
 constexpr size_t kOffXM = E, kOffATT = 2 * E, kOffQKV = 3 * E, kOffFF = 6 * E;
+
+// TRACE: thread 0 of every block records s_memrealtime (100 MHz) at each
+// phase boundary into a.trace[block][layer][kStepEvents]: Q blocks events
+// 0-3 (weights issued, x gathered, normalized, published), A blocks 4-6
+// (waiting, q|k|v gathered, published), O/D blocks 7-11 (weights issued, attention gathered, x_mid published, GELU
+// outputs gathered, x published), F blocks 12-15 (weights issued, x_mid
+// gathered, normalized, published)
+template <bool TRACE>
+__device__ __forceinline__ void mark(const Step16Args &a, int l, int e) {
+  if (TRACE && threadIdx.x == 0)
+    a.trace[((size_t)blockIdx.x * a.L + l) * kStepEvents + e] = __builtin_amdgcn_s_memrealtime();
+}
+
+// Layer l's pointers, read with scalar loads: a vector load of them would
+// make their first use wait for every earlier vector load of the block (the
+// weight and K / V loads still in flight).
+__device__ __forceinline__ Step16Layer layer_of(const Step16Args &a, int l) {
+  const Step16Layer *p = a.layers + l;
+  Step16Layer W;
+  W.ln1_g = ld_uniform(&p->ln1_g);
+  W.ln1_b = ld_uniform(&p->ln1_b);
+  W.ln2_g = ld_uniform(&p->ln2_g);
+  W.ln2_b = ld_uniform(&p->ln2_b);
+  W.wqkv = ld_uniform(&p->wqkv);
+  W.bqkv = ld_uniform(&p->bqkv);
+  W.wo = ld_uniform(&p->wo);
+  W.bo = ld_uniform(&p->bo);
+  W.wfc = ld_uniform(&p->wfc);
+  W.bfc = ld_uniform(&p->bfc);
+  W.wd = ld_uniform(&p->wd);
+  W.bd = ld_uniform(&p->bd);
+  return W;
+}
+
+// After a block's words are stored: wait until the stores have reached the
+// device-coherent level before the block issues more loads.  A store left
+// behind the next layer's weight loads (up to 120 KB a block) reached the
+// readers about 1.4 us later than one the block waited for.
+__device__ __forceinline__ void published() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // the 8 fp16 of a 16-byte chunk times the 8 floats at h (LDS), fused into acc
 __device__ __forceinline__ float fma8(float acc, v4u w, const float *h) {
@@ -77,25 +122,70 @@ __device__ __forceinline__ float sum16(float v) {
   return v;
 }
 
-// LayerNorm of xs[E] into hs[E] (both LDS; src/gpt2.c:398-414): the mean and
-// the variance in double, each a block sum in a fixed tree (thread t holds
-// elements t and t + 512); hs = (float)((x - mean) * rstd) * gamma + beta.
-// g / b: gamma and beta of the thread's elements.  Ends with a barrier.
-__device__ void layer_norm(const float *xs, const float (&g)[2], const float (&b)[2], double eps, float *hs,
-                           double *redd) {
-  const int t = threadIdx.x;
-  const bool two = t + kStepThreads < E;
-  const float x0 = xs[t], x1 = two ? xs[t + kStepThreads] : 0.0f;
-  double s = (double)x0 + (two ? (double)x1 : 0.0);
-  s = block_sum_1b<NW>(s, redd);
-  const double mean = s / E;
-  const double d0 = (double)x0 - mean, d1 = two ? (double)x1 - mean : 0.0;
-  double v = d0 * d0 + d1 * d1;
-  v = block_sum_1b<NW>(v, redd + NW);
-  const double rstd = 1.0 / sqrt(v / E + eps);
-  hs[t] = (float)(d0 * rstd) * g[0] + b[0];
-  if (two) hs[t + kStepThreads] = (float)(d1 * rstd) * g[1] + b[1];
-  __syncthreads();
+// The dots of 2 R rows of a wave (acc[i]: lanes 0-31 row 2 i, lanes 32-63 row
+// 2 i + 1, each a partial sum over the lane's chunks): each row's sum over its
+// 32 lanes (the two DPP rows of its half, then their sum); lane k < 2 R
+// receives the sum of row k.
+template <int R>
+__device__ __forceinline__ float finish_rows(const float (&acc)[R], int lane) {
+  float v = 0.0f;
+#pragma unroll
+  for (int i = 0; i < R; i++) {
+    const float s = sum16(acc[i]);
+    const float r0 = readlane(s, 0) + readlane(s, 16), r1 = readlane(s, 32) + readlane(s, 48);
+    v = lane == 2 * i ? r0 : v;
+    v = lane == 2 * i + 1 ? r1 : v;
+  }
+  return v;
+}
+
+// LayerNorm of xs[E] (LDS; src/gpt2.c:398-414) by one wave into its own
+// copy hw[E] (LDS), in two passes: lane l holds elements 4 l + 256 j, j < 3,
+// sums them in fp32 in a fixed order, and the wave sums the lanes' partial
+// sums in double (a fixed tree); mean, variance and 1 / sqrt(var + eps) in
+// double, the normalization hw = (x - mean) * rstd * gamma + beta in fp32.
+// Every wave computes the statistics itself, so the block passes no
+// barrier: the wave reads only what it wrote.  g / b: gamma and beta of the
+// lane's elements.  (The fp16 forward is compared within a tolerance.)
+__device__ __forceinline__ void wave_layer_norm(const float *xs, const float4 (&g)[3], const float4 (&b)[3],
+                                                double eps, float *hw) {
+  const int lane = threadIdx.x & 63;
+  float4 x[3];
+#pragma unroll
+  for (int j = 0; j < 3; j++) x[j] = *reinterpret_cast<const float4 *>(xs + 4 * lane + 256 * j);
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 3; j++) s += (x[j].x + x[j].y) + (x[j].z + x[j].w);
+  const double mean = wave_sum_dpp((double)s) / E;
+  const float mf = (float)mean;
+  float v = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 3; j++) {
+    const float d0 = x[j].x - mf, d1 = x[j].y - mf, d2 = x[j].z - mf, d3 = x[j].w - mf;
+    v += (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
+  }
+  const float rstd = (float)(1.0 / sqrt(wave_sum_dpp((double)v) / E + eps));
+#pragma unroll
+  for (int j = 0; j < 3; j++) {
+    float4 h;
+    h.x = ((x[j].x - mf) * rstd) * g[j].x + b[j].x;
+    h.y = ((x[j].y - mf) * rstd) * g[j].y + b[j].y;
+    h.z = ((x[j].z - mf) * rstd) * g[j].z + b[j].z;
+    h.w = ((x[j].w - mf) * rstd) * g[j].w + b[j].w;
+    *reinterpret_cast<float4 *>(hw + 4 * lane + 256 * j) = h;
+  }
+}
+
+// gamma and beta of lane l's LayerNorm elements (wave_layer_norm)
+__device__ __forceinline__ void ln_params(const float *gp, const float *bp, int lane, float4 (&g)[3],
+                                          float4 (&b)[3]) {
+  const gptr<v4u> g4 = (gptr<v4u>)gp, b4 = (gptr<v4u>)bp;
+#pragma unroll
+  for (int j = 0; j < 3; j++) {
+    const v4u gv = g4[lane + 64 * j], bv = b4[lane + 64 * j];
+    g[j] = make_float4(__uint_as_float(gv.x), __uint_as_float(gv.y), __uint_as_float(gv.z), __uint_as_float(gv.w));
+    b[j] = make_float4(__uint_as_float(bv.x), __uint_as_float(bv.y), __uint_as_float(bv.z), __uint_as_float(bv.w));
+  }
 }
 
 // x of the token at layer 0: fp32(wte[tok]) + fp32(wpe[pos]) (src/gpt2.c:489-499)
@@ -107,12 +197,13 @@ __device__ __forceinline__ float embed_x(const Step16Args &a, int tok, int pos, 
 // 6 w + 2 i + (lane >= 32), i < 3; a lane takes 16-byte chunks (lane & 31) +
 // 32 c, c < 3, of those rows, so that it reads each chunk of the normalized
 // row once for its three rows.
-__device__ void q_loop(const Step16Args &a, int gi, unsigned tag, int tok, float *lds, double *redd) {
-  float *xs = lds, *hs = lds + E;
+template <bool TRACE>
+__device__ void q_loop(const Step16Args &a, int gi, unsigned tag, int tok, float *lds) {
+  float *xs = lds;
   const int t = tid_opaque(), lane = t & 63, wave = t >> 6, half = lane >> 5, ln = lane & 31;
   const int pos = ld_uniform(a.attn.pos);
   for (int l = 0; l < a.L; l++) {
-    const Step16Layer &W = a.layers[l];
+    const Step16Layer W = layer_of(a, l);
     const unsigned long long *X = a.xch + (size_t)(l - 1) * kStep16Words;
     unsigned long long *QKV = a.xch + (size_t)l * kStep16Words + kOffQKV;
     // rows n0 + 2 i (lanes 0-31) and n0 + 2 i + 1 (lanes 32-63)
@@ -124,23 +215,20 @@ __device__ void q_loop(const Step16Args &a, int gi, unsigned tag, int tok, float
 #pragma unroll
       for (int c = 0; c < 3; c++) w[i][c] = __builtin_bit_cast(v4u, __builtin_nontemporal_load(src + ln + 32 * c));
     }
-    float bias[6];
-#pragma unroll
-    for (int i = 0; i < 6; i++) bias[i] = gbl(W.bqkv)[n0 + i];
-    float g[2], b[2];
-#pragma unroll
-    for (int j = 0; j < 2; j++) {
-      const int i = min(t + kStepThreads * j, E - 1);
-      g[j] = gbl(W.ln1_g)[i];
-      b[j] = gbl(W.ln1_b)[i];
-    }
+    const float bias = gbl(W.bqkv)[n0 + min(lane, 5)];  // lane k < 6 finishes row n0 + k
+    float4 g[3], b[3];
+    ln_params(W.ln1_g, W.ln1_b, lane, g, b);
+    mark<TRACE>(a, l, 0);
     if (l == 0) {
       for (int i = t; i < E; i += kStepThreads) xs[i] = embed_x(a, tok, pos, i);
       __syncthreads();
     } else {
       gather<1>(X, E, tag, xs, a.err);
     }
-    layer_norm(xs, g, b, a.eps, hs, redd);
+    mark<TRACE>(a, l, 1);
+    float *hs = lds + E * (1 + wave);  // this wave's normalized row
+    wave_layer_norm(xs, g, b, a.eps, hs);
+    mark<TRACE>(a, l, 2);
     float acc[3] = {0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int c = 0; c < 3; c++) {
@@ -148,26 +236,21 @@ __device__ void q_loop(const Step16Args &a, int gi, unsigned tag, int tok, float
 #pragma unroll
       for (int i = 0; i < 3; i++) acc[i] = fma8(acc[i], w[i][c], h);
     }
-#pragma unroll
-    for (int i = 0; i < 3; i++) {
-      const float s = sum16(acc[i]);
-      // the rows of lanes 0-31 and 32-63: the two DPP rows of each half
-      const float r0 = readlane(s, 0) + readlane(s, 16), r1 = readlane(s, 32) + readlane(s, 48);
-      if (lane == 0) {
-        put_word(QKV + n0 + 2 * i, r0 + bias[2 * i], tag);
-        put_word(QKV + n0 + 2 * i + 1, r1 + bias[2 * i + 1], tag);
-      }
-    }
+    const float v = finish_rows<3>(acc, lane);
+    if (lane < 6) put_word(QKV + n0 + lane, v + bias, tag);
+    published();
+    mark<TRACE>(a, l, 3);
   }
 }
 
 // F blocks (block gi): fc rows [64 gi, 64 gi + 64), as the Q blocks' rows
 // (wave w: rows 8 w + 2 i + (lane >= 32), i < 4).
-__device__ void f_loop(const Step16Args &a, int gi, unsigned tag, float *lds, double *redd) {
-  float *xs = lds, *hs = lds + E;
+template <bool TRACE>
+__device__ void f_loop(const Step16Args &a, int gi, unsigned tag, float *lds) {
+  float *xs = lds;
   const int t = tid_opaque(), lane = t & 63, wave = t >> 6, half = lane >> 5, ln = lane & 31;
   for (int l = 0; l < a.L; l++) {
-    const Step16Layer &W = a.layers[l];
+    const Step16Layer W = layer_of(a, l);
     const unsigned long long *XM = a.xch + (size_t)l * kStep16Words + kOffXM;
     unsigned long long *FF = a.xch + (size_t)l * kStep16Words + kOffFF;
     const int n0 = kFRows * uniform_opaque(gi) + 8 * wave;
@@ -178,18 +261,15 @@ __device__ void f_loop(const Step16Args &a, int gi, unsigned tag, float *lds, do
 #pragma unroll
       for (int c = 0; c < 3; c++) w[i][c] = __builtin_bit_cast(v4u, __builtin_nontemporal_load(src + ln + 32 * c));
     }
-    float bias[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) bias[i] = gbl(W.bfc)[n0 + i];
-    float g[2], b[2];
-#pragma unroll
-    for (int j = 0; j < 2; j++) {
-      const int i = min(t + kStepThreads * j, E - 1);
-      g[j] = gbl(W.ln2_g)[i];
-      b[j] = gbl(W.ln2_b)[i];
-    }
+    const float bias = gbl(W.bfc)[n0 + min(lane, 7)];  // lane k < 8 finishes row n0 + k
+    float4 g[3], b[3];
+    ln_params(W.ln2_g, W.ln2_b, lane, g, b);
+    mark<TRACE>(a, l, 12);
     gather<1>(XM, E, tag, xs, a.err);
-    layer_norm(xs, g, b, a.eps, hs, redd);
+    mark<TRACE>(a, l, 13);
+    float *hs = lds + E * (1 + wave);  // this wave's normalized row
+    wave_layer_norm(xs, g, b, a.eps, hs);
+    mark<TRACE>(a, l, 14);
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int c = 0; c < 3; c++) {
@@ -197,15 +277,11 @@ __device__ void f_loop(const Step16Args &a, int gi, unsigned tag, float *lds, do
 #pragma unroll
       for (int i = 0; i < 4; i++) acc[i] = fma8(acc[i], w[i][c], h);
     }
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const float s = sum16(acc[i]);
-      const float r0 = readlane(s, 0) + readlane(s, 16), r1 = readlane(s, 32) + readlane(s, 48);
-      if (lane == 0) {
-        put_word(FF + n0 + 2 * i, gelu_new(r0 + bias[2 * i]), tag);
-        put_word(FF + n0 + 2 * i + 1, gelu_new(r1 + bias[2 * i + 1]), tag);
-      }
-    }
+    // the eight GELUs (a double tanh each) on eight lanes at once
+    const float v = finish_rows<4>(acc, lane);
+    if (lane < 8) put_word(FF + n0 + lane, gelu_new(v + bias), tag);
+    published();
+    mark<TRACE>(a, l, 15);
   }
 }
 
@@ -213,6 +289,7 @@ __device__ void f_loop(const Step16Args &a, int gi, unsigned tag, float *lds, do
 // takes rows 2 w and 2 w + 1.  o: lanes 0-31 row 2 w, 32-63 row 2 w + 1, 3
 // chunks each; down (K = F): every lane both rows, 6 chunks, each GELU
 // chunk read once for the two rows.
+template <bool TRACE>
 __device__ void od_loop(const Step16Args &a, int gi, unsigned tag, int tok, float *lds, float *xown, float *xmown) {
   float *vs = lds;  // the attention output [E], then the GELU outputs [F]
   const int t = tid_opaque(), lane = t & 63, wave = t >> 6, half = lane >> 5, ln = lane & 31;
@@ -220,7 +297,7 @@ __device__ void od_loop(const Step16Args &a, int gi, unsigned tag, int tok, floa
   const int r0 = kODRows * uniform_opaque(gi);
   if (t < kODRows) xown[t] = embed_x(a, tok, pos, r0 + t);
   for (int l = 0; l < a.L; l++) {
-    const Step16Layer &W = a.layers[l];
+    const Step16Layer W = layer_of(a, l);
     unsigned long long *Xo = a.xch + (size_t)l * kStep16Words, *XM = Xo + kOffXM;
     const unsigned long long *ATT = Xo + kOffATT, *FFw = Xo + kOffFF;
     const int no = r0 + 2 * wave + half;
@@ -240,7 +317,9 @@ __device__ void od_loop(const Step16Args &a, int gi, unsigned tag, int tok, floa
     const float bd0 = gbl(W.bd)[r0 + 2 * wave], bd1 = gbl(W.bd)[r0 + 2 * wave + 1];
 
     // ---- o projection + residual ----
+    mark<TRACE>(a, l, 7);
     gather<1>(ATT, E, tag, vs, a.err);
+    mark<TRACE>(a, l, 8);
     {
       float acc = 0.0f;
 #pragma unroll
@@ -254,10 +333,13 @@ __device__ void od_loop(const Step16Args &a, int gi, unsigned tag, int tok, floa
         put_word(XM + r0 + 2 * wave, m0, tag);
         put_word(XM + r0 + 2 * wave + 1, m1, tag);
       }
+      published();
     }
 
     // ---- down projection + residual ----
+    mark<TRACE>(a, l, 9);
     gather<(F / 2 + kStepThreads - 1) / kStepThreads>(FFw, F, tag, vs, a.err);
+    mark<TRACE>(a, l, 10);
     {
       float acc0 = 0.0f, acc1 = 0.0f;
 #pragma unroll
@@ -281,6 +363,8 @@ __device__ void od_loop(const Step16Args &a, int gi, unsigned tag, int tok, floa
         }
       }
     }
+    published();
+    mark<TRACE>(a, l, 11);
   }
 }
 
@@ -315,6 +399,7 @@ __device__ void gather_head(const unsigned long long *QKV, int h, unsigned tag, 
 // A blocks: head h, element slice s of the attention, every layer; the next
 // layer's K rows (up to the first K tile) and this slice's V rows are loaded
 // straight into the body's LDS tiles after each layer's attention.
+template <bool TRACE>
 __device__ void attention_loop(const Step16Args &a, int head, int slice, unsigned tag, float *lds, float *qkv_s,
                                const uint64_t *etab) {
   __shared__ double2 cs_s[64];  // no rotation: cos 1, sin 0
@@ -326,12 +411,16 @@ __device__ void attention_loop(const Step16Args &a, int head, int slice, unsigne
   for (int l = 0; l < a.L; l++) {
     const unsigned long long *QKV = a.xch + (size_t)l * kStep16Words + kOffQKV;
     unsigned long long *att = a.xch + (size_t)l * kStep16Words + kOffATT;
+    mark<TRACE>(a, l, 4);
     gather_head(QKV, hh, tag, qkv_s, a.err);
+    mark<TRACE>(a, l, 5);
     const int o0 = hh * HD + 16 * ss;
     attn_decode_block<HD, true, kStepSlices, false, true>(a.attn, 0, hh, ss, qkv_s, qkv_s + HD, qkv_s + 2 * HD, lds,
                                                           [&](int i, float o) { put_word(att + o0 + i, o, tag); },
                                                           a.kv_layer * l, NoMark{}, &pre);
+    published();
     __syncthreads();  // the body's LDS and qkv_s are reused by the next layer
+    mark<TRACE>(a, l, 6);
     if (l + 1 < a.L) {
       attn_prefetch_k<HD, kStepSlices>(a.attn, 0, hh, lds, a.kv_layer * (l + 1));
       attn_prefetch_v<HD, kStepSlices>(a.attn, 0, hh, ss, lds, a.kv_layer * (l + 1));
@@ -339,11 +428,11 @@ __device__ void attention_loop(const Step16Args &a, int head, int slice, unsigne
   }
 }
 
+template <bool TRACE>
 __global__ __launch_bounds__(kStepThreads) void decode_step_gpt2_kernel(Step16Args a) {
   extern __shared__ __attribute__((aligned(16))) float lds[];
   __shared__ __attribute__((aligned(16))) float qkv_s[3 * HD];
   __shared__ float xown[kODRows], xmown[kODRows];
-  __shared__ double redd[2 * NW];
   __shared__ uint64_t etab[32];
   const int b = blockIdx.x, t = threadIdx.x;
   const unsigned tag = ld_uniform(a.tag);
@@ -354,11 +443,11 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_gpt2_kernel(Step16Ar
   // O/D and F blocks; the rest have nothing to do
   const int xcd = b & 7, j = b >> 3;
   if (j < 4) {
-    attention_loop(a, xcd, j, tag, lds, qkv_s, etab);
+    attention_loop<TRACE>(a, xcd, j, tag, lds, qkv_s, etab);
     return;
   }
   if (j < 8 && xcd < kHeads - 8) {
-    attention_loop(a, 8 + xcd, j - 4, tag, lds, qkv_s, etab);
+    attention_loop<TRACE>(a, 8 + xcd, j - 4, tag, lds, qkv_s, etab);
     return;
   }
   // attention blocks with a lower index: the 32 of j < 4, and of j 4-7 the
@@ -366,19 +455,22 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_gpt2_kernel(Step16Ar
   // one's all hold attention blocks)
   const int before = 32 + (j < 8 ? (j - 3) * (kHeads - 8) : 4 * (kHeads - 8));
   const int gi = b - before;
-  if (gi < kNQ) q_loop(a, gi, tag, tok, lds, redd);
-  else if (gi < kNQ + kNOD) od_loop(a, gi - kNQ, tag, tok, lds, xown, xmown);
-  else if (gi < kNQ + kNOD + kNF) f_loop(a, gi - kNQ - kNOD, tag, lds, redd);
+  if (gi < kNQ) q_loop<TRACE>(a, gi, tag, tok, lds);
+  else if (gi < kNQ + kNOD) od_loop<TRACE>(a, gi - kNQ, tag, tok, lds, xown, xmown);
+  else if (gi < kNQ + kNOD + kNF) f_loop<TRACE>(a, gi - kNQ - kNOD, tag, lds);
 }
 
 }  // namespace
 
-size_t decode_step_gpt2_scratch_bytes() { return (size_t)(E + F) * sizeof(float) + 64; }
+// Q and F blocks: x and the eight waves' normalized rows; O/D blocks: the
+// attention output or the GELU outputs
+size_t decode_step_gpt2_scratch_bytes() { return (size_t)(9 * E > F ? 9 * E : F) * sizeof(float); }
 
 hipError_t decode_step_gpt2(const Step16Args &a, size_t lds, bool cooperative, hipStream_t s) {
   Step16Args args = a;
   void *kargs[] = {&args};
-  const void *k = reinterpret_cast<const void *>(decode_step_gpt2_kernel);
+  const void *k = a.trace ? reinterpret_cast<const void *>(decode_step_gpt2_kernel<true>)
+                          : reinterpret_cast<const void *>(decode_step_gpt2_kernel<false>);
   if (cooperative)
     return hipLaunchCooperativeKernel(k, dim3(kStepBlocks), dim3(kStepThreads), kargs, (unsigned)lds, s);
   return hipLaunchKernel(k, dim3(kStepBlocks), dim3(kStepThreads), kargs, (unsigned)lds, s);

@@ -329,6 +329,7 @@ struct Step16Args {
   unsigned long long *xch;     // [L][kStep16Words] tagged exchange words
   float *x_out;                // x after the last layer [E]
   int *err;                    // set when a wait timed out (results invalid)
+  unsigned long long *trace;   // null, or [blocks][L][kStepEvents] phase timestamps
   // the attention body's arguments for layer 0 (no RoPE: cs null); layer l
   // adds l * kv_layer to the caches
   AttnArgs attn;

@@ -1328,11 +1328,19 @@ static size_t step_attn_area(int max_npos, int vtile, int kv) {
   return ((a > v ? a : v) + 15) & ~(size_t)15;
 }
 
+// LDS the persistent step uses past the attention area: the attention
+// blocks' norm row and codes (int8 Qwen2 step; the GPT-2 step's attention
+// blocks use the attention area only)
+static size_t step_row_bytes(const GPT2 *g, const DevModel *d) {
+  return d->step_kind == 1 ? 0 : step_norm_bytes(g->n_embd);
+}
+
 // the attention product tile of the persistent step for max_npos positions
-// (attn_vtile with the step's static LDS and the attention blocks' row set
+// (attn_vtile with the step's static LDS and the attention blocks' rows set
 // aside, and room for the V tile)
-static int step_vtile(int max_npos, int E, int kv) {
-  const size_t budget = (size_t)g_max_lds - kStepStaticLds - step_norm_bytes(E);
+static int step_vtile(const GPT2 *g, const DevModel *d, int max_npos) {
+  const int kv = g->n_kv_embd;
+  const size_t budget = (size_t)g_max_lds - kStepStaticLds - step_row_bytes(g, d);
   const size_t lds_fixed = attention_lds_bytes(max_npos, 64, 0);
   if (lds_fixed >= budget) return 0;
   const size_t room = (budget - lds_fixed) / ((size_t)attn_pitch(64, 0) * sizeof(float));
@@ -1344,7 +1352,7 @@ static int step_vtile(int max_npos, int E, int kv) {
 }
 
 static size_t step_lds(const GPT2 *g, const DevModel *d, int max_npos, int vtile) {
-  const size_t a = step_attn_area(max_npos, vtile, g->n_kv_embd) + step_norm_bytes(g->n_embd),
+  const size_t a = step_attn_area(max_npos, vtile, g->n_kv_embd) + step_row_bytes(g, d),
                b = d->step_kind == 1 ? decode_step_gpt2_scratch_bytes() : decode_step_scratch_bytes(g->n_embd, d->F);
   return a > b ? a : b;
 }
@@ -1365,7 +1373,7 @@ static double step_bytes(const GPT2 *g, const DevModel *d, int npos) {
 // The layers of a one-token forward as one persistent launch (decode_step.hip);
 // x after the last layer lands in d->x.
 static int enqueue_step(GPT2 *g, DevModel *d, int max_npos, hipStream_t s) {
-  const int vtile = step_vtile(max_npos, g->n_embd, g->n_kv_embd);
+  const int vtile = step_vtile(g, d, max_npos);
   if (vtile < 4) return set_err(-1, "decode step: position %d does not fit the LDS", max_npos - 1);
   if (!d->chaining)  // a chained step's inputs were written by the previous step
     EC_HIP(hipMemcpyAsync(d->d_step_io, d->h_step_io, 4 * sizeof(int), hipMemcpyHostToDevice, s));
@@ -1400,7 +1408,7 @@ static int enqueue_step(GPT2 *g, DevModel *d, int max_npos, hipStream_t s) {
   hipError_t e;
   if (d->step_kind == 1) {
     const Step16Args sa{d->d_layers16, g->wte, g->wpe, g->n_layer, g->eps, d->kv_layer, io,
-                        reinterpret_cast<const unsigned *>(io + 3), d->xch, d->x, io + 4, aa};
+                        reinterpret_cast<const unsigned *>(io + 3), d->xch, d->x, io + 4, d->d_trace, aa};
     e = decode_step_gpt2(sa, lds, g_step_coop, s);
   } else {
     const StepArgs sa{d->d_layers, g->wte, g->n_layer, g->n_embd, g->n_head, g->n_kv_head, d->F, g->eps,
@@ -1702,7 +1710,7 @@ static int forward_impl(GPT2 *g, const int *tokens, const int *positions, const 
   if (bucket > d->eff_ctx) bucket = d->eff_ctx;
   if (tk && !topk_ok(V, tk->top_k))
     return set_err(-1, "top_k=%d outside (0, %d) or above %d", tk->top_k, V, kTopkMax);
-  const bool step = M == 1 && lm_from == 0 && d->step_ok && step_vtile(max_npos, g->n_embd, g->n_kv_embd) >= 4;
+  const bool step = M == 1 && lm_from == 0 && d->step_ok && step_vtile(g, d, max_npos) >= 4;
   if (step) {
     // one token through the persistent step: its inputs and the step's tag
     // into the pinned I/O block, then -- for a greedy step without logits --
@@ -1721,7 +1729,7 @@ static int forward_impl(GPT2 *g, const int *tokens, const int *positions, const 
     io[3] = (int)d->step_tag;
     io[4] = io[5] = 0;
     bool graph = argmax && !logits && !tk && !g_prof_on && g_use_graphs && !d->step_nograph &&
-                 step_vtile(bucket, g->n_embd, g->n_kv_embd) >= 4;
+                 step_vtile(g, d, bucket) >= 4;
     if (graph && (!d->step_graph || d->step_bucket != bucket)) {
       if (d->step_graph) {
         EC_HIP(hipGraphExecDestroy(d->step_graph));
@@ -1932,7 +1940,7 @@ extern "C" int ec_generate_greedy_timed(GPT2 *g, int token, int pos, int slot, i
     return set_err(-1, "ec_generate_greedy: positions %d..%d outside [0, %d)", pos, pos + n - 1, d->eff_ctx);
   if (slot < 0) return set_err(-1, "ec_generate_greedy: negative slot %d", slot);
   if (slot >= g->batch_cap) slot = g->batch_cap - 1;  // as the forward (src/gpt2.c:512-513)
-  if (!d->step_ok || g_prof_on || step_vtile(pos + n, g->n_embd, g->n_kv_embd) < 4) {
+  if (!d->step_ok || g_prof_on || step_vtile(g, d, pos + n) < 4) {
     int t = token;
     for (int k = 0; k < n; k++) {
       const int p = pos + k;
@@ -1975,7 +1983,7 @@ extern "C" int ec_generate_greedy_timed(GPT2 *g, int token, int pos, int slot, i
     // kChainBurst steps in one graph when their positions stay in the bucket
     const int len = (n - k >= kChainBurst && bucket - (pos + k) >= kChainBurst) ? kChainBurst : 1;
     const int gi = len == 1 ? 0 : 1;
-    bool graph = g_use_graphs && !d->step_nograph && step_vtile(bucket, g->n_embd, g->n_kv_embd) >= 4;
+    bool graph = g_use_graphs && !d->step_nograph && step_vtile(g, d, bucket) >= 4;
     if (graph && (!d->chain_graph[gi] || d->chain_bucket[gi] != bucket)) {
       if (d->chain_graph[gi]) {
         const hipError_t ed = hipGraphExecDestroy(d->chain_graph[gi]);

@@ -58,8 +58,9 @@ constexpr int kNA = 4 * kHeads;  // attention blocks (4 slices per head)
 static_assert(kNA + kNQ + kNOD + kNF <= kStepBlocks, "roles");
 static_assert(kHeads <= 16, "heads 0-7 take j 0-3 of XCD h, heads 8-15 j 4-7 of XCD h - 8");
 
-// exchange words per layer: X [E] | XM [E] | ATT [E] | QKV [3 E] | FF [F]
-constexpr size_t kOffXM = E, kOffATT = 2 * E, kOffQKV = 3 * E, kOffFF = 6 * E;
+// exchange words per layer: X [E] | XM [E] | ATT [E] | QKV [3 E]; the GELU
+// outputs are plain fp32 words in a.ffv
+constexpr size_t kOffXM = E, kOffATT = 2 * E, kOffQKV = 3 * E;
 
 // TRACE: thread 0 of every block records s_memrealtime (100 MHz) at each
 // phase boundary into a.trace[block][layer][kStepEvents]: Q blocks events
@@ -252,7 +253,7 @@ __device__ void f_loop(const Step16Args &a, int gi, unsigned tag, float *lds) {
   for (int l = 0; l < a.L; l++) {
     const Step16Layer W = layer_of(a, l);
     const unsigned long long *XM = a.xch + (size_t)l * kStep16Words + kOffXM;
-    unsigned long long *FF = a.xch + (size_t)l * kStep16Words + kOffFF;
+    float *FF = a.ffv + ((size_t)(tag & 1u) * a.L + l) * F;
     const int n0 = kFRows * uniform_opaque(gi) + 8 * wave;
     v4u w[4][3];
 #pragma unroll
@@ -279,7 +280,7 @@ __device__ void f_loop(const Step16Args &a, int gi, unsigned tag, float *lds) {
     }
     // the eight GELUs (a double tanh each) on eight lanes at once
     const float v = finish_rows<4>(acc, lane);
-    if (lane < 8) put_word(FF + n0 + lane, gelu_new(v + bias), tag);
+    if (lane < 8) put_plain(FF + n0 + lane, gelu_new(v + bias));
     published();
     mark<TRACE>(a, l, 15);
   }
@@ -299,7 +300,8 @@ __device__ void od_loop(const Step16Args &a, int gi, unsigned tag, int tok, floa
   for (int l = 0; l < a.L; l++) {
     const Step16Layer W = layer_of(a, l);
     unsigned long long *Xo = a.xch + (size_t)l * kStep16Words, *XM = Xo + kOffXM;
-    const unsigned long long *ATT = Xo + kOffATT, *FFw = Xo + kOffFF;
+    const unsigned long long *ATT = Xo + kOffATT;
+    const float *FFw = a.ffv + ((size_t)(tag & 1u) * a.L + l) * F;
     const int no = r0 + 2 * wave + half;
     v4u wo[3], wd[2][6];
     {
@@ -338,7 +340,7 @@ __device__ void od_loop(const Step16Args &a, int gi, unsigned tag, int tok, floa
 
     // ---- down projection + residual ----
     mark<TRACE>(a, l, 9);
-    gather<(F / 2 + kStepThreads - 1) / kStepThreads>(FFw, F, tag, vs, a.err);
+    gather_plain<(F / 4 + kStepThreads - 1) / kStepThreads>(FFw, F, vs, a.err);
     mark<TRACE>(a, l, 10);
     {
       float acc0 = 0.0f, acc1 = 0.0f;
@@ -428,6 +430,16 @@ __device__ void attention_loop(const Step16Args &a, int head, int slice, unsigne
   }
 }
 
+// The blocks with no role fill the half of ffv that the next step writes
+// (tag + 1) with kStepFfEmpty: this step's half was filled during the step
+// before, which has ended; the next step starts after this launch ends.
+__device__ void ff_rearm(const Step16Args &a, int ib, int nb, unsigned tag) {
+  const size_t nq = (size_t)a.L * F / 4;
+  v4u *q = reinterpret_cast<v4u *>(a.ffv + (size_t)((tag + 1u) & 1u) * a.L * F);
+  const v4u e = {kStepFfEmpty, kStepFfEmpty, kStepFfEmpty, kStepFfEmpty};
+  for (size_t i = (size_t)ib * kStepThreads + threadIdx.x; i < nq; i += (size_t)nb * kStepThreads) q[i] = e;
+}
+
 template <bool TRACE>
 __global__ __launch_bounds__(kStepThreads) void decode_step_gpt2_kernel(Step16Args a) {
   extern __shared__ __attribute__((aligned(16))) float lds[];
@@ -458,6 +470,7 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_gpt2_kernel(Step16Ar
   if (gi < kNQ) q_loop<TRACE>(a, gi, tag, tok, lds);
   else if (gi < kNQ + kNOD) od_loop<TRACE>(a, gi - kNQ, tag, tok, lds, xown, xmown);
   else if (gi < kNQ + kNOD + kNF) f_loop<TRACE>(a, gi - kNQ - kNOD, tag, lds);
+  else ff_rearm(a, gi - kNQ - kNOD - kNF, kStepBlocks - kNA - kNQ - kNOD - kNF, tag);
 }
 
 }  // namespace

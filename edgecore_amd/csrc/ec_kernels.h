@@ -303,10 +303,10 @@ hipError_t decode_step(const StepArgs &a, size_t lds, bool cooperative, hipStrea
 // every layer for one token in one launch of kStepBlocks blocks of
 // kStepThreads threads, for the GPT-2 small shape (d_model kStep16E, head_dim
 // 64, FFN kStep16F).  Exchange words per layer (kStep16Words, tagged as in
-// the int8 step): [x: E][x_mid: E][attention output: E][q|k|v: 3 E][GELU
-// outputs: F].
+// the int8 step): [x: E][x_mid: E][attention output: E][q|k|v: 3 E]; the GELU
+// outputs go through ffv as the int8 step's FFN words do.
 constexpr int kStep16E = 768, kStep16F = 3072;
-constexpr size_t kStep16Words = 6 * (size_t)kStep16E + kStep16F;
+constexpr size_t kStep16Words = 6 * (size_t)kStep16E;
 struct Step16Layer {
   const float *ln1_g, *ln1_b, *ln2_g, *ln2_b;
   const uint16_t *wqkv;  // fp16 [3 E][E]: q | k | v rows
@@ -330,6 +330,7 @@ struct Step16Args {
   float *x_out;                // x after the last layer [E]
   int *err;                    // set when a wait timed out (results invalid)
   unsigned long long *trace;   // null, or [blocks][L][kStepEvents] phase timestamps
+  float *ffv;                  // GELU outputs [2][L][kStep16F]: half tag & 1, re-arming the other
   // the attention body's arguments for layer 0 (no RoPE: cs null); layer l
   // adds l * kv_layer to the caches
   AttnArgs attn;

@@ -1144,6 +1144,8 @@ static int load_impl(GPT2 *g, const char *path, int batch_cap, int max_ctx) {
       EC_HIP(hipMemcpy(d->d_layers16, sl.data(), sl.size() * sizeof(Step16Layer), hipMemcpyHostToDevice));
       d->xch_bytes = (size_t)Lc * kStep16Words * sizeof(unsigned long long);
       EC_HIP(dev_malloc(&d->xch, d->xch_bytes));
+      d->ffv_words = (size_t)2 * Lc * F;
+      EC_HIP(dev_malloc(&d->ffv, d->ffv_words * sizeof(float)));
     }
     EC_HIP(step_clear(d, nullptr));
     EC_HIP(hipDeviceSynchronize());
@@ -1408,7 +1410,7 @@ static int enqueue_step(GPT2 *g, DevModel *d, int max_npos, hipStream_t s) {
   hipError_t e;
   if (d->step_kind == 1) {
     const Step16Args sa{d->d_layers16, g->wte, g->wpe, g->n_layer, g->eps, d->kv_layer, io,
-                        reinterpret_cast<const unsigned *>(io + 3), d->xch, d->x, io + 4, d->d_trace, aa};
+                        reinterpret_cast<const unsigned *>(io + 3), d->xch, d->x, io + 4, d->d_trace, d->ffv, aa};
     e = decode_step_gpt2(sa, lds, g_step_coop, s);
   } else {
     const StepArgs sa{d->d_layers, g->wte, g->n_layer, g->n_embd, g->n_head, g->n_kv_head, d->F, g->eps,

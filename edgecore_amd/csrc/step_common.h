@@ -108,6 +108,53 @@ __device__ void gather(const unsigned long long *buf, int n, unsigned tag, float
   __syncthreads();
 }
 
+// Plain fp32 words, kStepFfEmpty until written (each word by one 4-byte
+// store): wait until words [0, n) of buf (n % 4 == 0, buf 16-byte aligned)
+// are all written and put them into dst (LDS).  Thread t owns the quads t +
+// kStepThreads * j (j < WQ), one 16-byte device-coherent load each, reissued
+// only for the quads still incomplete; a 16-byte load brings 4 values where
+// a tagged pair brings 2.  Every thread of the block calls it; it starts and
+// ends with a barrier, as gather does.
+template <int WQ>
+__device__ void gather_plain(const float *buf, int n, float *dst, int *err) {
+  const int t = threadIdx.x;
+  __syncthreads();
+  const uint64_t bp = (uint64_t)(uintptr_t)buf;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)bp), hi = __builtin_amdgcn_readfirstlane((uint32_t)(bp >> 32));
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)(uintptr_t)(((uint64_t)hi << 32) | lo), 0, __builtin_amdgcn_readfirstlane(n * 4), 0x00020000);
+  unsigned pending = 0;
+#pragma unroll
+  for (int j = 0; j < WQ; j++)
+    if (t + kStepThreads * j < (n >> 2)) pending |= 1u << j;
+  v4u v[WQ];
+  for (int it = 0; pending; it++) {
+#pragma unroll
+    for (int j = 0; j < WQ; j++)
+      if ((pending >> j) & 1u)
+        v[j] = __builtin_amdgcn_raw_buffer_load_b128(rs, (t + kStepThreads * j) * 16, 0, 16 /* sc1 */);
+#pragma unroll
+    for (int j = 0; j < WQ; j++) {
+      if (((pending >> j) & 1u) && v[j].x != kStepFfEmpty && v[j].y != kStepFfEmpty && v[j].z != kStepFfEmpty &&
+          v[j].w != kStepFfEmpty) {
+        *reinterpret_cast<v4u *>(dst + 4 * (t + kStepThreads * j)) = v[j];
+        pending &= ~(1u << j);
+      }
+    }
+    if (!pending) break;
+    if (it >= kSpin) {
+      atomicOr(err, 1);
+      break;
+    }
+    if ((it & 63) == 63 && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) break;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  __syncthreads();
+}
+
+__device__ __forceinline__ void put_plain(float *p, float v) {
+  __hip_atomic_store(reinterpret_cast<uint32_t *>(p), __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 }  // namespace
 

@@ -12,9 +12,10 @@
 //      (ln_1); 48 rows of fp16 weights against the normalized row (fp32
 //      products and sums); + bias; publish.
 //   A  (48 attention blocks: head h, element slice s; the 4 slices of a head
-//      on one XCD) -- wait for the head's 64 q, 64 k and 64 v words; the
-//      decode attention body (attn_decode.h: fp16 KV append, scores,
-//      softmax, p*v sums, no RoPE); publish the slice of the output.
+//      on one XCD) -- wait for the head's 64 q, 64 k and 64 v words (with
+//      the K and V rows already in registers); fp16 KV append, scores,
+//      softmax, p*v sums (gpt2_attn, no RoPE); publish the slice of the
+//      output.
 //   O  (48 o / down blocks, 16 rows each) -- wait for the attention output;
 //      o rows + bias; x_mid = x + (o + bias); publish.
 //   F  (48 fc blocks, 64 rows each) -- wait for x_mid; LayerNorm (ln_2); fc
@@ -95,11 +96,17 @@ __device__ __forceinline__ Step16Layer layer_of(const Step16Args &a, int l) {
   return W;
 }
 
-// After a block's words are stored: wait until the stores have reached the
-// device-coherent level before the block issues more loads.  A store left
-// behind the next layer's weight loads (up to 120 KB a block) reached the
-// readers about 1.4 us later than one the block waited for.
-__device__ __forceinline__ void published() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// A block's words for an exchange are staged in LDS and stored by one wave,
+// one store instruction per 128-byte line: lines written piecewise by
+// several instructions (each wave its own few words) reached the readers
+// about 0.7 us later.  published(): then that wave waits until the stores
+// have reached the device-coherent level, and the block waits for it, before
+// it issues more loads -- a store left behind the next layer's weight loads
+// (up to 120 KB a block) reached the readers about 1.4 us later still.
+__device__ __forceinline__ void published() {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+}
 
 // the 8 fp16 of a 16-byte chunk times the 8 floats at h (LDS), fused into acc
 __device__ __forceinline__ float fma8(float acc, v4u w, const float *h) {
@@ -238,7 +245,10 @@ __device__ void q_loop(const Step16Args &a, int gi, unsigned tag, int tok, float
       for (int i = 0; i < 3; i++) acc[i] = fma8(acc[i], w[i][c], h);
     }
     const float v = finish_rows<3>(acc, lane);
-    if (lane < 6) put_word(QKV + n0 + lane, v + bias, tag);
+    float *stage = lds + 9 * E;  // the block's 48 rows
+    if (lane < 6) stage[6 * wave + lane] = v + bias;
+    __syncthreads();
+    if (t < kQRows) put_word(QKV + kQRows * uniform_opaque(gi) + t, stage[t], tag);
     published();
     mark<TRACE>(a, l, 3);
   }
@@ -280,7 +290,10 @@ __device__ void f_loop(const Step16Args &a, int gi, unsigned tag, float *lds) {
     }
     // the eight GELUs (a double tanh each) on eight lanes at once
     const float v = finish_rows<4>(acc, lane);
-    if (lane < 8) put_plain(FF + n0 + lane, gelu_new(v + bias));
+    float *stage = lds + 9 * E;  // the block's 64 rows
+    if (lane < 8) stage[8 * wave + lane] = gelu_new(v + bias);
+    __syncthreads();
+    if (t < kFRows) put_plain(FF + kFRows * uniform_opaque(gi) + t, stage[t]);
     published();
     mark<TRACE>(a, l, 15);
   }
@@ -329,12 +342,11 @@ __device__ void od_loop(const Step16Args &a, int gi, unsigned tag, int tok, floa
       const float s = sum16(acc);
       const float o0 = readlane(s, 0) + readlane(s, 16), o1 = readlane(s, 32) + readlane(s, 48);
       if (lane == 0) {
-        const float m0 = xown[2 * wave] + (o0 + bo0), m1 = xown[2 * wave + 1] + (o1 + bo1);
-        xmown[2 * wave] = m0;
-        xmown[2 * wave + 1] = m1;
-        put_word(XM + r0 + 2 * wave, m0, tag);
-        put_word(XM + r0 + 2 * wave + 1, m1, tag);
+        xmown[2 * wave] = xown[2 * wave] + (o0 + bo0);
+        xmown[2 * wave + 1] = xown[2 * wave + 1] + (o1 + bo1);
       }
+      __syncthreads();
+      if (t < kODRows) put_word(XM + r0 + t, xmown[t], tag);
       published();
     }
 
@@ -354,16 +366,14 @@ __device__ void od_loop(const Step16Args &a, int gi, unsigned tag, int tok, floa
       const float d0 = (readlane(s0, 0) + readlane(s0, 16)) + (readlane(s0, 32) + readlane(s0, 48));
       const float d1 = (readlane(s1, 0) + readlane(s1, 16)) + (readlane(s1, 32) + readlane(s1, 48));
       if (lane == 0) {
-        const float x0 = xmown[2 * wave] + (d0 + bd0), x1 = xmown[2 * wave + 1] + (d1 + bd1);
-        xown[2 * wave] = x0;
-        xown[2 * wave + 1] = x1;
-        put_word(Xo + r0 + 2 * wave, x0, tag);
-        put_word(Xo + r0 + 2 * wave + 1, x1, tag);
-        if (l + 1 == a.L) {
-          a.x_out[r0 + 2 * wave] = x0;
-          a.x_out[r0 + 2 * wave + 1] = x1;
-        }
+        xown[2 * wave] = xmown[2 * wave] + (d0 + bd0);
+        xown[2 * wave + 1] = xmown[2 * wave + 1] + (d1 + bd1);
       }
+    }
+    __syncthreads();
+    if (t < kODRows) {
+      put_word(Xo + r0 + t, xown[t], tag);
+      if (l + 1 == a.L) a.x_out[r0 + t] = xown[t];
     }
     published();
     mark<TRACE>(a, l, 11);
@@ -393,23 +403,157 @@ __device__ void gather_head(const unsigned long long *QKV, int h, unsigned tag, 
       __builtin_amdgcn_s_sleep(1);
     }
   }
-  // this wave's prefetched K / V rows have landed; the barrier publishes them
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
 }
 
+// Attention of one head for the element slice s (16 of head_dim 64), fp16
+// forward (src/gpt2.c:520-556 at M = 1): every position i < n = pos + 1 on
+// thread i % 512 (at most kStep16MaxPos positions: two per thread), its K
+// row and the slice's 16 V elements in registers, loaded by
+// gpt2_attn_prefetch before the q|k|v words arrive (rows [0, pos) are final
+// cache rows; the token's own row comes from the new k / v, rounded to fp16
+// as the cache stores it).  The softmax's maximum and sum and the products'
+// sums over positions are block reductions (fixed trees), not the
+// reference's sequential sums: the fp16 forward is compared within a
+// tolerance.  The slice-0 block appends the new k / v to the cache.
+struct AttnRegs {
+  v4u k[2][HD / 8];  // K rows t and t + 512
+  v4u v[2][2];       // the slice's 16 V elements of those rows
+};
+
+__device__ __forceinline__ void gpt2_attn_prefetch(const AttnArgs &aa, size_t coff, int h, int slice, AttnRegs &r) {
+  const int t = threadIdx.x;
+  const int pos = ld_uniform(aa.pos), slot = ld_uniform(aa.slot);
+  const size_t base = coff + (size_t)slot * aa.C * aa.kv + (size_t)h * HD;
+  const auto K = gbl16(aa.kc + base), V = gbl16(aa.vc + base);
+  const int last = pos > 0 ? pos - 1 : 0;  // the last cache row (clamp target of the unconditional loads)
+  const int rc = aa.kv / 8;                // 16-byte chunks per cache row
+#pragma unroll
+  for (int q = 0; q < 2; q++) {
+    const int i = min(t + kStepThreads * q, last);
+#pragma unroll
+    for (int c = 0; c < HD / 8; c++) r.k[q][c] = __builtin_bit_cast(v4u, K[(size_t)i * rc + c]);
+#pragma unroll
+    for (int c = 0; c < 2; c++) r.v[q][c] = __builtin_bit_cast(v4u, V[(size_t)i * rc + 2 * slice + c]);
+  }
+}
+
+// block reductions over the 8 waves (fixed trees); red: 8 floats of LDS,
+// free until every thread has passed the next barrier
+__device__ __forceinline__ float block_max8(float v, float *red) {
+  v = wave_max_dpp(v);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return fmaxf(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])), fmaxf(fmaxf(red[4], red[5]), fmaxf(red[6], red[7])));
+}
+__device__ __forceinline__ float wave_sum_f(float v) {
+  v = sum16(v);
+  return (readlane(v, 0) + readlane(v, 16)) + (readlane(v, 32) + readlane(v, 48));
+}
+__device__ __forceinline__ float block_sum8(float v, float *red) {
+  v = wave_sum_f(v);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return ((red[0] + red[1]) + (red[2] + red[3])) + ((red[4] + red[5]) + (red[6] + red[7]));
+}
+
+// qkv: q [64] | new k [64] | new v [64] (LDS); out(i, o) for the slice's 16
+// outputs (threads t < 16, i = t); red: 16 + 16 x 512 floats of LDS.  What the next call writes to qkv and red is written after barriers
+// that every thread passes only after this call's last reads.
+template <class Out>
+__device__ void gpt2_attn(const AttnArgs &aa, size_t coff, int h, int slice, const AttnRegs &r, const float *qkv,
+                          float *red, Out &&out) {
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int pos = ld_uniform(aa.pos), slot = ld_uniform(aa.slot), n = pos + 1;
+  const float *q = qkv, *kn = qkv + HD, *vn = qkv + 2 * HD;
+  if (slice == 0 && t < HD) {  // append the new k / v (fp16) to the cache
+    const size_t w = coff + ((size_t)slot * aa.C + pos) * aa.kv + (size_t)h * HD + t;
+    aa.kc_w[w] = f2h(kn[t]);
+    aa.vc_w[w] = f2h(vn[t]);
+  }
+  // scores; the token's own row (the new k, rounded to fp16) is scored by the
+  // wave that holds its position, one element a lane
+  const int il = n - 1, wl = (il % kStepThreads) >> 6;
+  float dn = 0.0f;
+  if (wave == wl) dn = wave_sum_f(q[lane] * h2f(f2h(kn[lane])));
+  float sc[2], mx = -FLT_MAX;
+#pragma unroll
+  for (int k = 0; k < 2; k++) {
+    const int i = t + kStepThreads * k;
+    float d = dn;
+    if (i < il) {
+      float d0 = 0.0f, d1 = 0.0f;  // two chains: even and odd chunks
+#pragma unroll
+      for (int c = 0; c < HD / 8; c += 2) {
+        d0 = fma8(d0, r.k[k][c], q + 8 * c);
+        d1 = fma8(d1, r.k[k][c + 1], q + 8 * c + 8);
+      }
+      d = d0 + d1;
+    }
+    sc[k] = (float)((double)d * aa.inv_hd);
+    if (i < n) mx = fmaxf(mx, sc[k]);
+  }
+  mx = block_max8(mx, red);
+  float e[2], es = 0.0f;
+#pragma unroll
+  for (int k = 0; k < 2; k++) {
+    e[k] = t + kStepThreads * k < n ? expf(sc[k] - mx) : 0.0f;
+    es += e[k];
+  }
+  const float inv = 1.0f / block_sum8(es, red + 8);
+  // products: the slice's 16 elements of p_i v_i for this thread's positions
+  float o[16];
+#pragma unroll
+  for (int d = 0; d < 16; d++) o[d] = 0.0f;
+#pragma unroll
+  for (int k = 0; k < 2; k++) {
+    const int i = t + kStepThreads * k;
+    const float p = e[k] * inv;
+    if (i < il) {
+#pragma unroll
+      for (int c = 0; c < 2; c++) {
+        const uint32_t ww[4] = {r.v[k][c].x, r.v[k][c].y, r.v[k][c].z, r.v[k][c].w};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          o[8 * c + 2 * j] = __builtin_fmaf(p, h2f((uint16_t)(ww[j] & 0xffffu)), o[8 * c + 2 * j]);
+          o[8 * c + 2 * j + 1] = __builtin_fmaf(p, h2f((uint16_t)(ww[j] >> 16)), o[8 * c + 2 * j + 1]);
+        }
+      }
+    } else if (i == il) {
+#pragma unroll
+      for (int d = 0; d < 16; d++) o[d] = __builtin_fmaf(p, h2f(f2h(vn[16 * slice + d])), o[d]);
+    }
+  }
+  // sums over the block through LDS: part[d][t], then thread t sums element
+  // d = t / 32 over the threads j = t % 32 + 32 k, and the 32 lanes of its
+  // half-wave add up (fixed trees throughout)
+  float *part = red + 16;
+#pragma unroll
+  for (int d = 0; d < 16; d++) part[d * kStepThreads + t] = o[d];
+  __syncthreads();
+  float v = 0.0f;
+#pragma unroll
+  for (int k = 0; k < kStepThreads / 32; k++) v += part[(t >> 5) * kStepThreads + (t & 31) + 32 * k];
+  v = sum16(v);
+  const float v0 = readlane(v, 0) + readlane(v, 16), v1 = readlane(v, 32) + readlane(v, 48);
+  // the 16 outputs leave through one store instruction (one 128-byte line):
+  // stores to one line from several instructions reach the readers later
+  if (lane == 0) {
+    red[2 * wave] = v0;
+    red[2 * wave + 1] = v1;
+  }
+  __syncthreads();
+  if (t < 16) out(t, red[t]);
+}
+
 // A blocks: head h, element slice s of the attention, every layer; the next
-// layer's K rows (up to the first K tile) and this slice's V rows are loaded
-// straight into the body's LDS tiles after each layer's attention.
+// layer's K and V rows go into registers after each layer's attention, while
+// the block waits for that layer's q|k|v words.
 template <bool TRACE>
-__device__ void attention_loop(const Step16Args &a, int head, int slice, unsigned tag, float *lds, float *qkv_s,
-                               const uint64_t *etab) {
-  __shared__ double2 cs_s[64];  // no rotation: cos 1, sin 0
-  if (threadIdx.x < 64) cs_s[threadIdx.x] = make_double2(1.0, 0.0);
-  const AttnPre pre{etab, cs_s};
+__device__ void attention_loop(const Step16Args &a, int head, int slice, unsigned tag, float *lds, float *qkv_s) {
   const int hh = uniform_opaque(head), ss = uniform_opaque(slice);
-  attn_prefetch_k<HD, kStepSlices>(a.attn, 0, hh, lds, 0);
-  attn_prefetch_v<HD, kStepSlices>(a.attn, 0, hh, ss, lds, 0);
+  AttnRegs r;
+  gpt2_attn_prefetch(a.attn, 0, hh, ss, r);
   for (int l = 0; l < a.L; l++) {
     const unsigned long long *QKV = a.xch + (size_t)l * kStep16Words + kOffQKV;
     unsigned long long *att = a.xch + (size_t)l * kStep16Words + kOffATT;
@@ -417,16 +561,10 @@ __device__ void attention_loop(const Step16Args &a, int head, int slice, unsigne
     gather_head(QKV, hh, tag, qkv_s, a.err);
     mark<TRACE>(a, l, 5);
     const int o0 = hh * HD + 16 * ss;
-    attn_decode_block<HD, true, kStepSlices, false, true>(a.attn, 0, hh, ss, qkv_s, qkv_s + HD, qkv_s + 2 * HD, lds,
-                                                          [&](int i, float o) { put_word(att + o0 + i, o, tag); },
-                                                          a.kv_layer * l, NoMark{}, &pre);
+    gpt2_attn(a.attn, a.kv_layer * l, hh, ss, r, qkv_s, lds, [&](int i, float o) { put_word(att + o0 + i, o, tag); });
     published();
-    __syncthreads();  // the body's LDS and qkv_s are reused by the next layer
     mark<TRACE>(a, l, 6);
-    if (l + 1 < a.L) {
-      attn_prefetch_k<HD, kStepSlices>(a.attn, 0, hh, lds, a.kv_layer * (l + 1));
-      attn_prefetch_v<HD, kStepSlices>(a.attn, 0, hh, ss, lds, a.kv_layer * (l + 1));
-    }
+    if (l + 1 < a.L) gpt2_attn_prefetch(a.attn, a.kv_layer * (l + 1), hh, ss, r);
   }
 }
 
@@ -445,21 +583,19 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_gpt2_kernel(Step16Ar
   extern __shared__ __attribute__((aligned(16))) float lds[];
   __shared__ __attribute__((aligned(16))) float qkv_s[3 * HD];
   __shared__ float xown[kODRows], xmown[kODRows];
-  __shared__ uint64_t etab[32];
-  const int b = blockIdx.x, t = threadIdx.x;
+  const int b = blockIdx.x;
   const unsigned tag = ld_uniform(a.tag);
   const int tok = ld_uniform(a.tok);
-  if (t < 32) etab[t] = ec_exp2_32[t];
   // roles: attention blocks, head h < 8 on XCD h at slots j = b / 8 of 0-3,
   // head 8 + x on XCD x at j 4-7; then, numbered gi in block order, the Q,
   // O/D and F blocks; the rest have nothing to do
   const int xcd = b & 7, j = b >> 3;
   if (j < 4) {
-    attention_loop<TRACE>(a, xcd, j, tag, lds, qkv_s, etab);
+    attention_loop<TRACE>(a, xcd, j, tag, lds, qkv_s);
     return;
   }
   if (j < 8 && xcd < kHeads - 8) {
-    attention_loop<TRACE>(a, 8 + xcd, j - 4, tag, lds, qkv_s, etab);
+    attention_loop<TRACE>(a, 8 + xcd, j - 4, tag, lds, qkv_s);
     return;
   }
   // attention blocks with a lower index: the 32 of j < 4, and of j 4-7 the
@@ -475,9 +611,13 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_gpt2_kernel(Step16Ar
 
 }  // namespace
 
-// Q and F blocks: x and the eight waves' normalized rows; O/D blocks: the
-// attention output or the GELU outputs
-size_t decode_step_gpt2_scratch_bytes() { return (size_t)(9 * E > F ? 9 * E : F) * sizeof(float); }
+// Q and F blocks: x, the eight waves' normalized rows and the staged rows;
+// O/D blocks: the attention output or the GELU outputs; A blocks: the
+// reductions' slots and the products' partial sums
+size_t decode_step_gpt2_scratch_bytes() {
+  const size_t a = (size_t)(9 * E + kFRows > F ? 9 * E + kFRows : F), b = 16 + 16 * (size_t)kStepThreads;
+  return (a > b ? a : b) * sizeof(float);
+}
 
 hipError_t decode_step_gpt2(const Step16Args &a, size_t lds, bool cooperative, hipStream_t s) {
   Step16Args args = a;

@@ -306,6 +306,7 @@ hipError_t decode_step(const StepArgs &a, size_t lds, bool cooperative, hipStrea
 // the int8 step): [x: E][x_mid: E][attention output: E][q|k|v: 3 E]; the GELU
 // outputs go through ffv as the int8 step's FFN words do.
 constexpr int kStep16E = 768, kStep16F = 3072;
+constexpr int kStep16MaxPos = 2 * kStepThreads;  // positions the step's attention holds (two per thread)
 constexpr size_t kStep16Words = 6 * (size_t)kStep16E;
 struct Step16Layer {
   const float *ln1_g, *ln1_b, *ln2_g, *ln2_b;

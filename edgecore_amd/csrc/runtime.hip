@@ -1330,17 +1330,18 @@ static size_t step_attn_area(int max_npos, int vtile, int kv) {
   return ((a > v ? a : v) + 15) & ~(size_t)15;
 }
 
-// LDS the persistent step uses past the attention area: the attention
-// blocks' norm row and codes (int8 Qwen2 step; the GPT-2 step's attention
-// blocks use the attention area only)
+// LDS the int8 Qwen2 step uses past the attention area: the attention
+// blocks' norm row and codes
 static size_t step_row_bytes(const GPT2 *g, const DevModel *d) {
-  return d->step_kind == 1 ? 0 : step_norm_bytes(g->n_embd);
+  (void)d;
+  return step_norm_bytes(g->n_embd);
 }
 
 // the attention product tile of the persistent step for max_npos positions
 // (attn_vtile with the step's static LDS and the attention blocks' rows set
 // aside, and room for the V tile)
 static int step_vtile(const GPT2 *g, const DevModel *d, int max_npos) {
+  if (d->step_kind == 1) return max_npos <= kStep16MaxPos ? 4 : 0;  // no LDS tile: any value >= 4 means it fits
   const int kv = g->n_kv_embd;
   const size_t budget = (size_t)g_max_lds - kStepStaticLds - step_row_bytes(g, d);
   const size_t lds_fixed = attention_lds_bytes(max_npos, 64, 0);
@@ -1354,6 +1355,7 @@ static int step_vtile(const GPT2 *g, const DevModel *d, int max_npos) {
 }
 
 static size_t step_lds(const GPT2 *g, const DevModel *d, int max_npos, int vtile) {
+  if (d->step_kind == 1) return decode_step_gpt2_scratch_bytes();  // its attention keeps K / V in registers
   const size_t a = step_attn_area(max_npos, vtile, g->n_kv_embd) + step_row_bytes(g, d),
                b = d->step_kind == 1 ? decode_step_gpt2_scratch_bytes() : decode_step_scratch_bytes(g->n_embd, d->F);
   return a > b ? a : b;

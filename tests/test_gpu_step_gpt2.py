@@ -7,8 +7,9 @@ FFN 3072, LayerNorm, biases, learned positions) at 3 layers, fp16 weights.
 The step's fp16 dots are fp32 sums in an order of their own, so its logits
 equal the kernel-per-op path's within a small tolerance (2e-3) rather than
 bit for bit; both must give the oracle's greedy tokens and stay within the
-fp16 bar (max-abs 1e-2) of its logits.  The decode crosses position 512 (the
-attention's first K tile and a 512-position graph bucket)."""
+fp16 bar (max-abs 1e-2) of its logits.  The decode crosses position 512 (a
+512-position graph bucket, and the step's attention's second position per
+thread) and runs up to position 1009 of the 1024 the step holds."""
 import ctypes as C
 import json
 import os
@@ -75,7 +76,7 @@ def _decode(path, prompt, steps, step_on):
     return np.stack(out), ids, fams
 
 
-@pytest.mark.parametrize("n,steps", [(500, 24), (1, 12)])
+@pytest.mark.parametrize("n,steps", [(500, 24), (1, 12), (990, 20)])
 def test_gpt2_step_against_kernel_per_op_and_oracle(g2_model, n, steps):
     prompt = prompt_ids(n, V, seed=21)
     lg_s, ids_s, fam_s = _decode(g2_model, prompt, steps, True)

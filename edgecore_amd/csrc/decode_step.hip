@@ -60,6 +60,17 @@ __device__ __forceinline__ void mark(const StepArgs &a, int b, int l, int e) {
   if (TRACE && threadIdx.x == 0) a.trace[((size_t)b * a.L + l) * kStepEvents + e] = __builtin_amdgcn_s_memrealtime();
 }
 
+// A block's words for an exchange are stored by one wave, one store
+// instruction per 128-byte line (lines written piecewise by several waves
+// reached the readers about 0.7 us later); published(): that wave waits until
+// its stores have reached the device-coherent level and the block waits for
+// it, before any wave issues more loads (a store left behind the next
+// layer's weight loads reached the readers later still).
+__device__ __forceinline__ void published() {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+}
+
 // gather's wait, then the int8 quantization of the words (src/gpt2.c:446-461)
 // straight from the registers that received them: the row maximum over the
 // block, then each thread's codes into codes[] (LDS).  Returns the scale.
@@ -350,7 +361,7 @@ __device__ void attention_loop(const StepArgs &a, int head, int slice, unsigned 
     attn_decode_block<64, true, kStepSlices, false, true>(a.attn, 0, hh, ss, qkv_s, qkv_s + 64, qkv_s + 128, lds,
                                              [&](int i, float o) { put_word(att + o0 + i, o, tag); },
                                              a.kv_layer * l, [&](int e) { mark<TRACE>(a, b, l, 15 + e); }, &pre);
-    __syncthreads();  // the body's LDS is reused by the next layer
+    published();  // (threads t < 16 stored the slice's words; the body's LDS is reused by the next layer)
     mark<TRACE>(a, b, l, 3);
     if (l + 1 < a.L) {
       load_layer(l + 1);
@@ -410,11 +421,10 @@ __device__ void od_loop(const StepArgs &a, int gi, unsigned tag, int tok, float 
 #pragma unroll
       for (int c = 0; c < 7; c++) acc = dot16(acc, wo[c], codes + 16 * (sub + 8 * c));
       acc = sum8(acc);
-      if (on_o && sub == 0) {
-        const float v = xown[grp] + i8_epilogue(acc, sa, wso, 0.0f);
-        xmown[grp] = v;
-        put_word(XM + no, v, tag);
-      }
+      if (on_o && sub == 0) xmown[grp] = xown[grp] + i8_epilogue(acc, sa, wso, 0.0f);
+      __syncthreads();
+      if ((int)threadIdx.x < kODRows) put_word(XM + r0 + threadIdx.x, xmown[threadIdx.x], tag);
+      published();
       mark<TRACE>(a, b, l, 5);
     }
 
@@ -435,18 +445,15 @@ __device__ void od_loop(const StepArgs &a, int gi, unsigned tag, int tok, float 
       acc0 = sum64(acc0);
       acc1 = sum64(acc1);
       if (lane == 0) {
-        const float v0 = xmown[wave] + i8_epilogue(acc0, sf, wsd0, 0.0f);
-        const float v1 = xmown[wave + 8] + i8_epilogue(acc1, sf, wsd1, 0.0f);
-        xown[wave] = v0;
-        xown[wave + 8] = v1;
-        put_word(X + r0 + wave, v0, tag);
-        put_word(X + r0 + wave + 8, v1, tag);
-        if (l + 1 == a.L) {
-          a.x_out[r0 + wave] = v0;
-          a.x_out[r0 + wave + 8] = v1;
-        }
+        xown[wave] = xmown[wave] + i8_epilogue(acc0, sf, wsd0, 0.0f);
+        xown[wave + 8] = xmown[wave + 8] + i8_epilogue(acc1, sf, wsd1, 0.0f);
       }
-      __syncthreads();  // xown / codes reused by the next layer
+      __syncthreads();
+      if ((int)threadIdx.x < kODRows) {
+        put_word(X + r0 + threadIdx.x, xown[threadIdx.x], tag);
+        if (l + 1 == a.L) a.x_out[r0 + threadIdx.x] = xown[threadIdx.x];
+      }
+      published();  // (xown / codes are reused by the next layer)
       mark<TRACE>(a, b, l, 9);
     }
   }
@@ -500,12 +507,16 @@ __device__ void gu_loop(const StepArgs &a, int gi, int ng, unsigned tag, float *
     }
     ag = sum8(ag);
     au = sum8(au);
+    __shared__ float stage[64];  // the block's FFN words
     if (on_g && sub == 0) {
       const float gv = i8_epilogue(ag, sx, bsg, 0.0f), u = i8_epilogue(au, sx, bsu, 0.0f);
-      __hip_atomic_store(reinterpret_cast<uint32_t *>(FV + ngt), __float_as_uint(silu(gv, etab) * u), __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
+      stage[grp] = silu(gv, etab) * u;
     }
-    if constexpr (TRACE) __syncthreads();  // the mark follows every wave's stores
+    __syncthreads();
+    if ((int)threadIdx.x < g1 - g0)
+      __hip_atomic_store(reinterpret_cast<uint32_t *>(FV + g0 + threadIdx.x), __float_as_uint(stage[threadIdx.x]),
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    published();
     mark<TRACE>(a, b, l, 7);
   }
 }

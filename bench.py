@@ -130,6 +130,9 @@ def prefill_c4(ec, np, model: Path, cache: Path):
     decode(C4_DECODE)
     L.ec_sync()
     t_decode = time.perf_counter() - t0
+    # four more M=4 steps with per-launch timestamps (launched directly, not
+    # as the graph: the per-family table of a decode step)
+    dec_kernels = _prof(L, lambda: decode(4))
 
     # one more prefill of slot 0 with per-launch timestamps
     L.ec_prof_start(b"")
@@ -162,6 +165,7 @@ def prefill_c4(ec, np, model: Path, cache: Path):
             "unit": "TOP/s (int8)", "frac": dom["int8_mfma_frac"], "avg_us": dom["avg_us"]},
         "gemm_all_tops": round(gflop / (gus * 1e6), 1) if gus else None,
         "kernels": kernels,
+        "decode_kernels": dec_kernels,
     }
 
 

@@ -836,9 +836,14 @@ hipError_t launch_skinny_nj(const GemvArgs &a, int wpb, int ksplit, hipStream_t 
     ksplit = 1;
   ksplit = min(ksplit, ksteps);
   const int kper = (ksteps + ksplit - 1) / ksplit;
-  // waves per block: two or more K steps each, 4 to 16 waves, and at least
-  // 4 TI NO (the epilogue takes one thread per output of 16 TI rows x 16 NO)
-  if (wpb <= 0) wpb = min(16, max(4, kper / 2));
+  // waves per block: two or more K steps each (SwiGLU: six), 4 to 16 waves,
+  // and at least 4 TI NO (the epilogue takes one thread per output of 16 TI
+  // rows x 16 NO).  At batch 16 with weights from HBM (a microbenchmark
+  // cycling through more weight copies than the last-level cache holds),
+  // gate/up (K = 1536, 24 steps) took 11.0 us with 4 waves against 12.9 us
+  // with 12; in the decode 14.1 -> 11.7 us.  The o projection with its fused
+  // quantization went the other way (8.5 -> 10.8 us with 4 waves).
+  if (wpb <= 0) wpb = min(16, max(4, kper / (EPI == EPI_SWIGLU ? 6 : 2)));
   wpb = max(min(wpb, 16), 4 * TI * NO);
   if (a.pmax_out && groups > a.np_out) return hipErrorInvalidValue;
   klaunch((gemm_skinny_kernel<OP, TI, NJ, EPI, QA>), dim3(groups, ksplit), dim3(64 * wpb), 0, s, a);

@@ -453,21 +453,23 @@ __device__ __forceinline__ void attn_decode_block(const AttnArgs &a, int m, int 
   static_assert(HD == 0 || NPT % CPRV == 0, "product threads cover whole quads");
   const int pt = t - 64 * SWV;  // product thread index (negative in the summing waves)
   v4u vr[NSTG * UPS][4];
-  auto load_v = [&](int t0) {  // this product thread's V units of the tile at t0
+  // this product thread's V units of stage s of the tile at t0
+  auto load_v_stage = [&](int t0, int s) {
     if (HD > 0 && pt >= 0) {
       const int qd0 = pt / CPRV, cd = pt - qd0 * CPRV;
 #pragma unroll
-      for (int s = 0; s < NSTG; s++) {
+      for (int u = 0; u < UPS; u++) {
 #pragma unroll
-        for (int u = 0; u < UPS; u++) {
-#pragma unroll
-          for (int e = 0; e < 4; e++) {
-            const int i = min(t0 + 4 * (stage_lo(s) + QPU * u + qd0) + e, last);
-            vr[s * UPS + u][e] = *reinterpret_cast<const v4u *>(V + (size_t)i * a.kv + 8 * (CPRV * slice + cd));
-          }
+        for (int e = 0; e < 4; e++) {
+          const int i = min(t0 + 4 * (stage_lo(s) + QPU * u + qd0) + e, last);
+          vr[s * UPS + u][e] = *reinterpret_cast<const v4u *>(V + (size_t)i * a.kv + 8 * (CPRV * slice + cd));
         }
       }
     }
+  };
+  auto load_v = [&](int t0) {  // ... of every stage
+#pragma unroll
+    for (int s = 0; s < NSTG; s++) load_v_stage(t0, s);
   };
   // PREK with the whole context in one product tile: the product threads read
   // V from the V tile in LDS (attn_prefetch_v) instead of loading registers
@@ -758,8 +760,12 @@ __device__ __forceinline__ void attn_decode_block(const AttnArgs &a, int m, int 
                     make_float4(pr[k][0], pr[k][1], pr[k][2], pr[k][3]);
             }
           }
-          // the next tile's V into the registers this tile has used up
-          if (s == nst - 1 && t0 + T < n) load_v(t0 + T);
+          // the next tile's V of this stage into the registers the stage
+          // has used up, so that its loads have the tile's later stages to
+          // arrive in (loaded at the tile's end, each next tile began by
+          // waiting for its V: about 1 us of the 2.4 us a 256-position tile
+          // took at head_dim 128)
+          if (s < nst && t0 + T < n) load_v_stage(t0 + T, min(s, NSTG - 1));
         } else if (t < hs && s > 0) {
           sum_quads(stage_lo(s - 1), min(stage_lo(s), nq));
           if (s == nst) sum_tail(nq, cnt);

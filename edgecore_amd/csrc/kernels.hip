@@ -850,20 +850,22 @@ static void launch_attn_scored(AttnArgs a, hipStream_t st) {
   // blocks running in more rounds; one block per (token, KV group, 16
   // elements) for all six heads of a group, V read once per group, took 25
   // us: each block recomputes the six heads' softmax (six times the
-  // exponentials of a per-head block)
-  constexpr int NS = 1;
+  // exponentials of a per-head block).  head_dim 64 keeps the fused
+  // kernel's four element slices of 16 (512 threads each).
+  constexpr int NS = HD == 64 ? 4 : 1;
   const dim3 grid((a.xcd_r ? 8 * r : a.H) * NS, a.M);
   klaunch((attn_kernel<HD, false, NS, true>), grid, dim3(attn_threads(HD, NS, true)),
           attention_lds_bytes(a.max_npos, HD, a.vtile), st, a);
 }
 
 // the scores pass applies: a workspace, a long context, head_dim 128 (the
-// one-block-per-head body, which re-scores nothing), whole KV groups of at
-// most kScMaxHeads heads.  head_dim 64 keeps its element slices in one
-// launch: the split measured no faster there (C4, 2048 positions, M = 4).
+// one-block-per-head body, which re-scores nothing) or 64 (its four element
+// slices, which otherwise each score every position again: C4's M = 4 steps
+// at 2080 positions, 24.4 -> 5.3 + 17.2 us per layer), whole KV groups of at
+// most kScMaxHeads heads.
 bool attention_split_ok(const AttnArgs &a) {
   return a.scores && a.sc_ld >= a.max_npos && a.max_npos >= kAttnSplitMinPos && attn_vec(a.hd, a.kv) &&
-         a.hd == 128 && a.H % a.KVH == 0 && a.H / a.KVH <= kScMaxHeads;
+         (a.hd == 128 || a.hd == 64) && a.H % a.KVH == 0 && a.H / a.KVH <= kScMaxHeads;
 }
 
 hipError_t attention(const AttnArgs &a, hipStream_t st) {
@@ -871,10 +873,12 @@ hipError_t attention(const AttnArgs &a, hipStream_t st) {
     return hipErrorInvalidValue;
   const size_t lds = attention_lds_bytes(a.max_npos, a.hd, a.vtile);
   if (attention_split_ok(a)) {
-    launch_attn_scores<128>(a, st);
+    if (a.hd == 64) launch_attn_scores<64>(a, st);
+    else launch_attn_scores<128>(a, st);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    launch_attn_scored<128>(a, st);
+    if (a.hd == 64) launch_attn_scored<64>(a, st);
+    else launch_attn_scored<128>(a, st);
     return hipGetLastError();
   }
   if (attn_vec(a.hd, a.kv) && a.hd == 64) launch_attn<64>(a, lds, st);
@@ -886,14 +890,16 @@ hipError_t attention(const AttnArgs &a, hipStream_t st) {
 
 hipError_t attention_scores(const AttnArgs &a, hipStream_t st) {
   if (!attention_split_ok(a)) return hipErrorInvalidValue;
-  launch_attn_scores<128>(a, st);
+  if (a.hd == 64) launch_attn_scores<64>(a, st);
+  else launch_attn_scores<128>(a, st);
   return hipGetLastError();
 }
 
 hipError_t attention_after_scores(const AttnArgs &a, hipStream_t st) {
   if (!attention_split_ok(a) || a.vtile < 4 || (a.vtile & 3) || a.vtile > attention_max_vtile(a.hd, a.kv))
     return hipErrorInvalidValue;
-  launch_attn_scored<128>(a, st);
+  if (a.hd == 64) launch_attn_scored<64>(a, st);
+  else launch_attn_scored<128>(a, st);
   return hipGetLastError();
 }
 

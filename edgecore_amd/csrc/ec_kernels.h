@@ -129,11 +129,13 @@ int gemv_max_blocks();
 int gemv_pick_shape(int wt, int K);
 int gemv_pick_mt(int M);
 // prologue computed by every wave alone (activation rows of at most 1024
-// fp32 elements, quantized or normalized): for one row, no block barrier and
-// one LDS copy of the row per wave; for an M tile of up to 4 rows, one row
-// per wave and one barrier
+// fp32 elements, quantized or normalized; quantized rows of an M tile up to
+// 5120): for one row, no block barrier and one LDS copy of the row per wave;
+// for an M tile of up to 4 rows, one row per wave and one barrier
 inline bool gemv_wave_pro(int pro, int MT, int K) {
-  return MT <= 4 && K <= 1024 && (pro == PRO_QUANT || pro == PRO_RMS || pro == PRO_LN);
+  if (MT > 4) return false;
+  if (pro == PRO_QUANT && MT > 1 && K <= 5120) return true;
+  return K <= 1024 && (pro == PRO_QUANT || pro == PRO_RMS || pro == PRO_LN);
 }
 // LDS budget per block (device limit), checked by gemv_vector_ok
 void gemv_set_max_lds(int bytes);

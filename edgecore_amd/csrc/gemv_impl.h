@@ -90,7 +90,7 @@ __device__ __forceinline__ T group_sum(T v) {
   return v;
 }
 
-template <int WT, int SHAPE, int MT, int EPI, int PRO, bool WL>
+template <int WT, int SHAPE, int MT, int EPI, int PRO, int WL>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   constexpr bool Q8 = WT == WT_I8;
   constexpr int LPR = GemvShape<WT, SHAPE>::LPR, CPL = GemvShape<WT, SHAPE>::CPL;
@@ -103,9 +103,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   constexpr bool NORM = PRO == PRO_RMS || PRO == PRO_LN;
   constexpr int NS = ProStrips<PRO>::NS;
   static_assert(!WL || (MT <= 4 && (PRO == PRO_QUANT || NORM)), "wave-local prologue: up to 4 rows, fp32 input");
+  static_assert(WL != 2 || (MT > 1 && PRO == PRO_QUANT), "wide wave-local prologue: quantized M tiles only");
   // WL with MT > 1: wave w computes row min(w, mc - 1) of the tile into LDS
   // slot w, and one block barrier precedes the dot
-  constexpr bool WL1 = WL && MT == 1;
+  constexpr bool WL1 = WL != 0 && MT == 1;
 
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
   __shared__ double redd[2][4];
@@ -157,16 +158,21 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
       }
     }
   };
-  // WL: every wave holds a whole row (K <= 1024), lane l elements
-  // 4l + 256j, and computes the prologue alone: for one row (WL1) no block
-  // barrier, each wave writing its own copy of the quantized / normalized
-  // row to LDS; for an M tile of up to 4 rows, wave w takes row w
-  float4 xw[WL ? 4 : 1], gw[WL && NORM ? 4 : 1], bw[WL && PRO == PRO_LN ? 4 : 1];
+  // WL: every wave holds a whole row, lane l elements 4l + 256j, and
+  // computes the prologue alone: for one row (WL1) no block barrier, each
+  // wave writing its own copy of the quantized / normalized row to LDS; for
+  // an M tile of up to 4 rows, wave w takes row w.  WL 1: rows up to 1024;
+  // WL 2: quantized rows of an M tile up to 5120 (all rows' loads in flight
+  // at once and one block barrier, instead of one row after another through
+  // block reductions).  The loads are unconditional (clamped into the row),
+  // so the prologue's wait still leaves the weight loads in flight.
+  constexpr int WLS = WL == 2 ? 20 : WL ? 4 : 1;
+  float4 xw[WLS], gw[WL && NORM ? WLS : 1], bw[WL && PRO == PRO_LN ? WLS : 1];
   if constexpr (WL) {
     const int wr = MT > 1 ? min(wave, mc - 1) : 0;
     const float *row = reinterpret_cast<const float *>(a.A) + (size_t)(m0 + wr) * a.lda;
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
+    for (int j = 0; j < WLS; j++) {
       const int i = min(4 * lane + 256 * j, K - 4);
       xw[j] = *reinterpret_cast<const float4 *>(row + i);
       if constexpr (NORM) gw[j] = *reinterpret_cast<const float4 *>(a.gamma + i);
@@ -231,13 +237,13 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   float xsw = 1.0f;  // WL: the row's scale (int8 path)
   if constexpr (WL) {
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
+    for (int j = 0; j < WLS; j++) {
       if (4 * lane + 256 * j >= K) xw[j] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
     if constexpr (NORM) {
       double s1 = 0.0;
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
+      for (int j = 0; j < WLS; j++) {
         const double d0 = xw[j].x, d1 = xw[j].y, d2 = xw[j].z, d3 = xw[j].w;
         if constexpr (PRO == PRO_LN) s1 += ((d0 + d1) + d2) + d3;
         else s1 += ((d0 * d0 + d1 * d1) + d2 * d2) + d3 * d3;
@@ -248,7 +254,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
         mean = s1 / K;
         double s2 = 0.0;
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
+        for (int j = 0; j < WLS; j++) {
           if (4 * lane + 256 * j < K) {
             const double d0 = xw[j].x - mean, d1 = xw[j].y - mean, d2 = xw[j].z - mean, d3 = xw[j].w - mean;
             s2 += ((d0 * d0 + d1 * d1) + d2 * d2) + d3 * d3;
@@ -269,7 +275,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
         }
       };
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
+      for (int j = 0; j < WLS; j++) {
         const float4 b = PRO == PRO_LN ? bw[j] : make_float4(0.f, 0.f, 0.f, 0.f);
         xw[j].x = nrm(xw[j].x, gw[j].x, b.x);
         xw[j].y = nrm(xw[j].y, gw[j].y, b.y);
@@ -281,7 +287,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     if constexpr (Q8) {
       float mx = 0.0f;
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
+      for (int j = 0; j < WLS; j++) {
         mx = fmaxf(mx, fabsf(xw[j].x));
         mx = fmaxf(mx, fabsf(xw[j].y));
         mx = fmaxf(mx, fabsf(xw[j].z));
@@ -293,7 +299,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
       const bool fast = ec_quant_rcp_ok(sc);
       const float rcp = 1.0f / sc;
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
+      for (int j = 0; j < WLS; j++) {
         const int i = 4 * lane + 256 * j;
         if (i < K) {
           uint32_t b0, b1, b2, b3;
@@ -318,7 +324,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     } else {
       float *f = xf + (size_t)wave * Kp;
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
+      for (int j = 0; j < WLS; j++) {
         const int i = 4 * lane + 256 * j;
         if (i < K) *reinterpret_cast<float4 *>(f + i) = xw[j];
       }
@@ -604,7 +610,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
 // host-side launch helpers (instantiated per weight type in gemv_*.hip)
 // ---------------------------------------------------------------------------
 
-template <int WT, int SHAPE, int MT, int EPI, int PRO, bool WL = false>
+template <int WT, int SHAPE, int MT, int EPI, int PRO, int WL = 0>
 hipError_t gemv_launch(const GemvArgs &a, hipStream_t s) {
   constexpr int RPB = 4 * (kWave / GemvShape<WT, SHAPE>::LPR);
   const int ngroups = (a.N + RPB - 1) / RPB;
@@ -616,6 +622,15 @@ hipError_t gemv_launch(const GemvArgs &a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// wave-local prologue of an M tile: rows up to 1024, or quantized rows up
+// to 5120 (the wide form)
+template <int WT, int SHAPE, int MT, int EPI, int PRO>
+hipError_t gemv_wave_launch(const GemvArgs &a, hipStream_t s) {
+  if constexpr (PRO == PRO_QUANT)
+    if (a.K > 1024) return gemv_launch<WT, SHAPE, MT, EPI, PRO, 2>(a, s);
+  return gemv_launch<WT, SHAPE, MT, EPI, PRO, 1>(a, s);
+}
+
 template <int WT, int EPI, int PRO>
 hipError_t gemv_launch_shape(const GemvArgs &a, hipStream_t s) {
   const int shape = gemv_pick_shape(WT, a.K);
@@ -624,15 +639,15 @@ hipError_t gemv_launch_shape(const GemvArgs &a, hipStream_t s) {
   switch (mt) {                                                     \
   case 1:                                                           \
     if constexpr (PRO == PRO_QUANT || PRO == PRO_RMS || PRO == PRO_LN) \
-      if (gemv_wave_pro(PRO, 1, a.K)) return gemv_launch<WT, SH, 1, EPI, PRO, true>(a, s); \
+      if (gemv_wave_pro(PRO, 1, a.K)) return gemv_launch<WT, SH, 1, EPI, PRO, 1>(a, s);    \
     return gemv_launch<WT, SH, 1, EPI, PRO>(a, s);                  \
   case 2:                                                           \
     if constexpr (PRO == PRO_QUANT || PRO == PRO_RMS || PRO == PRO_LN) \
-      if (gemv_wave_pro(PRO, 2, a.K)) return gemv_launch<WT, SH, 2, EPI, PRO, true>(a, s); \
+      if (gemv_wave_pro(PRO, 2, a.K)) return gemv_wave_launch<WT, SH, 2, EPI, PRO>(a, s);  \
     return gemv_launch<WT, SH, 2, EPI, PRO>(a, s);                  \
   case 4:                                                           \
     if constexpr (PRO == PRO_QUANT || PRO == PRO_RMS || PRO == PRO_LN) \
-      if (gemv_wave_pro(PRO, 4, a.K)) return gemv_launch<WT, SH, 4, EPI, PRO, true>(a, s); \
+      if (gemv_wave_pro(PRO, 4, a.K)) return gemv_wave_launch<WT, SH, 4, EPI, PRO>(a, s);  \
     return gemv_launch<WT, SH, 4, EPI, PRO>(a, s);                  \
   default: return gemv_launch<WT, SH, 8, EPI, PRO>(a, s);           \
   }

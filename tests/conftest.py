@@ -31,6 +31,12 @@ MODEL_SPECS = {
                                    ctx=256, vocab=1000, precision="int8", sliding_window=48,
                                    rope_type="yarn", yarn_factor=4.0, yarn_orig_max=64,
                                    yarn_attention_factor=1.1),
+    # intermediate sizes past 1024: the batched down GEMV's wide quantizing
+    # prologue (one wave per row up to 5120) and its clamped strips
+    "qwen2-ffn5120-int8": dict(arch="qwen2", layers=2, embd=256, heads=4, kv_heads=2, ffn=5120,
+                               ctx=128, vocab=1000, precision="int8"),
+    "qwen2-ffn1040-int8": dict(arch="qwen2", layers=2, embd=256, heads=4, kv_heads=2, ffn=1040,
+                               ctx=128, vocab=1000, precision="int8"),
     # long context: decode crosses 512-position boundaries
     "qwen2-long-int8": dict(arch="qwen2", layers=2, embd=128, heads=4, kv_heads=2, ffn=256,
                             ctx=1536, vocab=1000, precision="int8"),

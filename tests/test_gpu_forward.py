@@ -90,11 +90,14 @@ def test_sliding_window_and_yarn(make_model):
         assert np.abs(got - want).max() <= 1e-4
 
 
-@pytest.mark.parametrize("name,B", [("tiny-qwen2-int8", 4), ("tiny-gpt2-int8", 3), ("qwen2-hd128-int8", 2)])
+@pytest.mark.parametrize("name,B", [("tiny-qwen2-int8", 4), ("tiny-gpt2-int8", 3), ("qwen2-hd128-int8", 2),
+                                    ("qwen2-ffn5120-int8", 3), ("qwen2-ffn5120-int8", 4),
+                                    ("qwen2-ffn1040-int8", 2)])
 def test_batched_decode_slots(make_model, name, B):
     """Per-slot prefill (seqs=b), then M=B decode with seqs=NULL
     (src/runtime_main.c:325-352): the decode GEMVs' M tiles of 2 and 4 rows
-    (3 rows: a clamped fourth), RMSNorm and LayerNorm prologues."""
+    (3 rows: a clamped fourth), RMSNorm and LayerNorm prologues, and the down
+    projection's quantizing prologue over rows of 1040 and 5120."""
     path = make_model(name)
     with ec.Model(path, B, 64) as m:
         om = oracle.OracleModel(path, B, 64)

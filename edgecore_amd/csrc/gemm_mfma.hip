@@ -92,9 +92,22 @@ constexpr size_t gemm_lds_bytes() {
   return (size_t)NB * (MfmaOp<OP>::NP * BM + kBN) * (DL ? kBK : kPitch);
 }
 
+// Split K of the tiled kernel: gridDim.y blocks share a tile, each taking a
+// contiguous range of K stages; each stores its 32-bit accumulators to
+// gm_part, and the tile's last block to arrive (a counter per tile, reset by
+// that block, so every launch finds it at zero) adds the gridDim.y partial
+// tiles in y order and applies the epilogue.  For int8 the sums are exact;
+// for 16-bit weights the fp32 sums take a fixed order, the same class of
+// rounding as the one-block tile.  One workspace per device: launches that
+// use it must not overlap (the forward issues its linears on one stream).
+constexpr int kGmMaxTiles = 1024;         // tiles of a split launch
+constexpr int kGmPartInts = 1024 * 1024;  // 32-bit partial tiles of a split launch
+__device__ int gm_part[kGmPartInts];
+__device__ unsigned gm_cnt[kGmMaxTiles];
+
 // A: [M * NP][lda] elements (row m's part p at row m * NP + p), as: per-row
 // scale (int8 quantization scale, or the split's 2^e; 1 for bf16)
-template <int OP, int BM, int EPI, bool DL, int NB = 2>
+template <int OP, int BM, int EPI, bool DL, int NB = 2, bool SPLIT = false>
 __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemvArgs a) {
   using Op = MfmaOp<OP>;
   using Acc = typename Op::Acc;
@@ -239,15 +252,17 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemvArgs a) {
 #pragma unroll
     for (int j = 0; j < TJ; j++) acc[i][j] = Acc{0, 0, 0, 0};
 
-  const int ns = (KB + kBK - 1) / kBK;
+  // this block's K stages: [sb, sb + ns) of the row's, all of them unless split
+  const int ns_all = (KB + kBK - 1) / kBK, kper = (ns_all + (int)gridDim.y - 1) / (int)gridDim.y;
+  const int sb = (int)blockIdx.y * kper, ns = min(ns_all - sb, kper);
+  const int kb0 = sb * kBK;
   if constexpr (!DL) {
-    const int ns = (KB + kBK - 1) / kBK;
-    load(0);
+    load(kb0);
     store(0);
     __syncthreads();
     for (int s = 0; s < ns; s++) {
       const int buf = s & 1;
-      if (s + 1 < ns) load((s + 1) * kBK);
+      if (s + 1 < ns) load(kb0 + (s + 1) * kBK);
       const int8_t *ta = la + buf * NP * BM * kPitch + (wm * WM + lr) * kPitch + 16 * lq;
       const int8_t *tb = lb + buf * kBN * kPitch + lr * kPitch + 16 * lq;
   #pragma unroll
@@ -320,12 +335,12 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemvArgs a) {
     // linears with NB 2 took ~1 us per stage.)
 #pragma unroll
     for (int p = 0; p < NB - 1; p++)
-      if (p < ns) dload(p * kBK, p);
+      if (p < ns) dload(kb0 + p * kBK, p);
     for (int s = 0; s < ns; s++) {
       if (NB > 2 && s + NB - 2 < ns) asm volatile("s_waitcnt vmcnt(%0)" ::"i"((NB - 2) * UPW) : "memory");
       else __builtin_amdgcn_s_waitcnt(0);
       asm volatile("s_barrier" ::: "memory");
-      if (s + NB - 1 < ns) dload((s + NB - 1) * kBK, (s + NB - 1) % NB);
+      if (s + NB - 1 < ns) dload(kb0 + (s + NB - 1) * kBK, (s + NB - 1) % NB);
       const int buf = s % NB;
       const int8_t *ta = lds + (size_t)buf * RT * kBK + (size_t)(wm * WM + lr) * kBK;
       const int8_t *tb = lds + (size_t)buf * RT * kBK + (size_t)(NP * BM + lr) * kBK;
@@ -348,6 +363,73 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemvArgs a) {
             for (int j = 0; j < TJ; j++) acc[i][j] = Op::mma(fa[p][i], fb[j], acc[i][j]);
       }
     }
+  }
+
+  if constexpr (SPLIT) {
+    // split K: publish this block's partial tile; the tile's last block adds
+    // them.  Device-coherent buffer stores and loads (sc1: they bypass the
+    // XCD's L2), a thread's accumulators 16 bytes at a time, and a wait for
+    // the stores' completion before the counter, instead of a device-scope
+    // fence (which writes back the whole L2).  The last block issues all its
+    // loads at once (at most 256 / BM splits, so 128 values per thread):
+    // atomic loads came out one round trip each.
+    constexpr int NQ = TI * TJ;        // 16-byte accumulator vectors per thread
+    constexpr int KSM = 256 / BM;      // splits a launch may use
+    const int ks = (int)gridDim.y;
+    // the address's halves as unsigned words (readfirstlane returns int: an
+    // int low half would sign-extend into the high half)
+    const uint64_t pv = (uint64_t)(uintptr_t)(gm_part + (size_t)tl * ks * 256 * NQ * 4);
+    const uint32_t plo = __builtin_amdgcn_readfirstlane((uint32_t)pv),
+                   phi = __builtin_amdgcn_readfirstlane((uint32_t)(pv >> 32));
+    void *pu = (void *)(uintptr_t)(((uint64_t)phi << 32) | plo);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(pu, 0, ks * 256 * NQ * 16, 0x00020000);
+#pragma unroll
+    for (int i = 0; i < TI; i++)
+#pragma unroll
+      for (int j = 0; j < TJ; j++)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, acc[i][j]), rs,
+                                               (((int)blockIdx.y * 256 + t) * NQ + i * TJ + j) * 16, 0,
+                                               16 /* sc1 */);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __shared__ int s_last;
+    __syncthreads();
+    if (t == 0)
+      s_last = __hip_atomic_fetch_add(&gm_cnt[tl], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == ks - 1;
+    __syncthreads();
+    if (!s_last) return;
+    // unconditional loads (splits past ks read the last one again and are
+    // not added): behind a branch per split, each split's loads waited for
+    // the previous ones
+    v4u part[KSM][NQ];
+#pragma unroll
+    for (int y = 0; y < KSM; y++)
+#pragma unroll
+      for (int q = 0; q < NQ; q++)
+        part[y][q] =
+            __builtin_amdgcn_raw_buffer_load_b128(rs, ((min(y, ks - 1) * 256 + t) * NQ + q) * 16, 0, 16 /* sc1 */);
+    typedef typename std::conditional<I8, int, float>::type El;
+#pragma unroll
+    for (int i = 0; i < TI; i++)
+#pragma unroll
+      for (int j = 0; j < TJ; j++) {
+        El v[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int y = 0; y < KSM; y++) {
+          // the whole vector cast, then its elements read: a bit cast of an
+          // element expression (w.y) read element 0
+          const Acc w = __builtin_bit_cast(Acc, part[y][i * TJ + j]);
+          if (y < ks) {
+            v[0] += w[0];
+            v[1] += w[1];
+            v[2] += w[2];
+            v[3] += w[3];
+          }
+        }
+        // whole-vector assignment: element-wise writes of acc[i][j][r] kept
+        // only element 0 of the sums live
+        acc[i][j] = Acc{v[0], v[1], v[2], v[3]};
+      }
+    if (t == 0) __hip_atomic_store(&gm_cnt[tl], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 
   // ---- epilogue: lane holds D[4*lq + r][lr] of each tile ----
@@ -413,18 +495,46 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemvArgs a) {
 #ifndef EC_GEMM_DL
 #define EC_GEMM_DL 1
 #endif
+// K splits of a launch of T tiles over ns K stages: none when the tiles
+// already fill the CUs or the rows are short (under 16 stages: C2's q|k|v,
+// o and fc at 12 stages ran 8.6 -> 11.9, 8.6 -> 10.3 and 14.6 -> 18.7 us
+// split in 2-3); otherwise up to 256 blocks of 6 stages or more, within the
+// partial workspace, and no split left empty.  Only 32-row tiles split (few
+// tiles over long rows: a prefill of a few hundred tokens); such a launch
+// holds one block per CU and 4 stage buffers.
+int gemm_ksplit(int T, int ns, int BM) {
+  if (BM != 32 || T >= 128 || ns < 16 || T > kGmMaxTiles) return 1;
+  int ks = min(min(ns / 6, 256 / T), 256 / BM);
+  ks = min(ks, kGmPartInts / (T * BM * kBN));
+  if (ks < 2) return 1;
+  const int kper = (ns + ks - 1) / ks;
+  return (ns + kper - 1) / kper;
+}
+
 template <int OP, int BM, int EPI>
 hipError_t launch_bm(const GemvArgs &a, hipStream_t s) {
   constexpr int NOUT = EPI == EPI_SWIGLU ? kBN / 2 : kBN;
   const int T = ((a.N + NOUT - 1) / NOUT) * ((a.M + BM - 1) / BM);
-  const dim3 grid(8 * ((T + 7) / 8));
+  // split K for few tiles over long rows: C2's 128-token down projection
+  // (24 tiles of 32 x 128 over 48 stages of K) ran each tile's whole K on
+  // one CU while 232 CUs idled
   const bool dl = EC_GEMM_DL && (a.K * MfmaOp<OP>::EB) % kBK == 0 && (a.lda * MfmaOp<OP>::EB) % kBK == 0;
+  const int ks = dl ? gemm_ksplit(T, (a.K * MfmaOp<OP>::EB + kBK - 1) / kBK, BM) : 1;
+  const dim3 grid(8 * ((T + 7) / 8), ks);
+  if constexpr (BM == 32) {
+    static_assert(gemm_lds_bytes<OP, 32, true, 4>() <= 158 * 1024, "split K: 4 stage buffers per CU");
+    if (ks > 1) {
+      klaunch((gemm_mfma_kernel<OP, 32, EPI, true, 4, true>), grid, dim3(256), gemm_lds_bytes<OP, 32, true, 4>(), s,
+              a);
+      return hipGetLastError();
+    }
+  }
   // grids of at most two tiles per CU: the most stage buffers (up to 4) with
   // which the tiles a CU holds at once still fit its LDS, so that 2-3
   // stages' loads are in flight.  C2's 128-token linears (24-96 tiles):
   // down 40.3 -> 23.6 us, q|k|v and o 11.9 -> 8.4 us; C4's down (448
   // tiles) 23.6 -> 21.7 us.
-  const int bpc = T <= 256 ? 1 : 2;
+  const int bpc = T * ks <= 256 ? 1 : 2;
   const size_t budget = (size_t)(158 * 1024) / bpc;
   constexpr size_t l4 = gemm_lds_bytes<OP, BM, true, 4>(), l3 = gemm_lds_bytes<OP, BM, true, 3>();
   if (dl && T <= 512 && l4 <= budget)

@@ -264,7 +264,8 @@ def test_gemm_w16_matrix_core_within_bound(M, K, N, bf16):
 
 @pytest.mark.parametrize("bf16", [False, True])
 @pytest.mark.parametrize("bm,M,K,N", [(bm, M, K, N) for bm in (0, 32, 64, 128)
-                                      for M, K, N in ((200, 768, 300), (130, 3072, 129), (64, 896, 128))]
+                                      for M, K, N in ((200, 768, 300), (130, 3072, 129), (64, 896, 128),
+                                                      (128, 3072, 768))]
                          + [(bm, M, K, N) for bm in (0, 16)
                             for M, K, N in ((16, 1536, 600), (32, 768, 129), (20, 3072, 200), (1, 8, 17),
                                             (16, 768, 16500))])
@@ -288,6 +289,23 @@ def test_gemm_w16_tiles_and_epilogues(bm, M, K, N, bf16):
     want = _silu64(v) * u
     tol = 1.1 * (np.abs(u) * bv + np.abs(_silu64(v)) * bu) + 1e-6 * np.abs(want)
     check(ec.gemm_w16_epi(wt, 3, bm, A, B, B2=B2), want, tol)
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("M,K,N", [(128, 3072, 768), (130, 3072, 129), (40, 3072, 768)])
+def test_gemm_w16_split_k_repeatable(M, K, N, bf16):
+    """Few tiles over long rows run split K (the tile's K stages over
+    several blocks, the partial tiles added in a fixed order by the last
+    block): the same call gives the same bits every time, with the
+    residual epilogue reading C0 while other blocks of the tile still run."""
+    wt = 2 if bf16 else 1
+    A, B, _, bias, C0 = _w16_inputs(M, K, N, bf16, seed=K + N + bf16)
+    first = ec.gemm_w16_epi(wt, 5, 32, A, B, bias=bias, C0=C0)
+    for _ in range(3):
+        assert np.array_equal(_bits(ec.gemm_w16_epi(wt, 5, 32, A, B, bias=bias, C0=C0)), _bits(first))
+    v, bv = _exact_and_bound(A, B, bf16)
+    want = C0.astype(np.float64) + (v + bias.astype(np.float64))
+    assert np.all(np.abs(first - want) <= bv + 2 * 2.0 ** -23 * np.abs(want) + 1e-30)
 
 
 @pytest.mark.parametrize("scale", [1e-30, 1e-8, 1e4, 3e5, 1e30])

@@ -25,7 +25,7 @@ HIPFLAGS := --offload-arch=$(ARCH) -O3 -std=c++17 -fPIC -ffp-contract=off \
             -Xclang -target-feature -Xclang -packed-fp32-ops -Iinclude -I$(SRC) -Wall
 CFLAGS   := -O2 -std=c11 -Wall -Wextra -fPIC -Iinclude -ffp-contract=off
 
-HIPSRC := $(SRC)/kernels.hip $(SRC)/decode_step.hip $(SRC)/decode_step_gpt2.hip $(SRC)/gemm_mfma.hip $(SRC)/attn_prefill.hip $(SRC)/topk.hip $(SRC)/gemv_i8.hip $(SRC)/gemv_f16.hip $(SRC)/gemv_bf16.hip $(SRC)/runtime.hip
+HIPSRC := $(SRC)/kernels.hip $(SRC)/decode_step.hip $(SRC)/decode_step_gpt2.hip $(SRC)/decode_tail.hip $(SRC)/gemm_mfma.hip $(SRC)/attn_prefill.hip $(SRC)/topk.hip $(SRC)/gemv_i8.hip $(SRC)/gemv_f16.hip $(SRC)/gemv_bf16.hip $(SRC)/runtime.hip
 HIPOBJ := $(HIPSRC:$(SRC)/%.hip=$(OBJ)/%.o)
 
 all: $(LIB) $(RUNTIME) $(SYNTH) oracle

@@ -1,0 +1,524 @@
+// The layer tail of a batched int8 Qwen2 decode (M <= kTailMaxM tokens, one
+// slot each): everything of layer l after its attention, and the start of
+// layer l + 1 before its attention, in one co-resident launch
+// (src/gpt2.c:744-797 at M = batch, then :702-743 of the next layer):
+//
+//   o projection + residual     x_mid = x + o(quant(att))      :744-784
+//   RMSNorm, gate/up, SiLU      h = silu(g(n)) * u(n)          :785-791
+//   down projection + residual  x = x_mid + d(quant(h))        :792-796
+//   next layer: RMSNorm, q|k|v  qkv = Wqkv n(x) + b            :702-713
+//
+// Why: the batched decode otherwise runs these as four GEMV launches per
+// layer (q|k|v, o, gate/up, down) of 1-9 MB each, each starting from a cold
+// weight stream behind a full kernel boundary; at C4's four tokens they took
+// ~25 us per layer against ~10 us for the same phases inside the one-token
+// persistent step.  The attention (two launches at long contexts) stays
+// separate: this kernel runs between layer l's attention and layer l + 1's.
+//
+// Grid: kStepBlocks blocks of kStepThreads threads, all resident (a plain
+// launch on an idle device, or a cooperative one).  Roles, by block index:
+//
+//   OD (E / 16 blocks, 16 rows each) -- o rows for every token (64 groups of
+//      8 lanes: row r0 + g % 16, token g / 16), x_mid = x + o, publish
+//      x_mid; then wait for the FFN words, quantize each token's row, down
+//      rows (two per wave, every token), x = x_mid + d: store x and publish.
+//   G  (ceil(F / 64) blocks, 64 gate/up row pairs each) -- wait for x_mid,
+//      RMSNorm + quantize (wave m: token m), gate and up rows for every
+//      token, silu(g) * u, publish.
+//   Q  (ceil(NQ / 16) blocks, 16 rows each; none after the last layer) --
+//      wait for x, the next layer's RMSNorm + quantize, q|k|v rows, store.
+//
+// Every block issues its weight loads before it waits, so the weight stream
+// overlaps the wait.  Results go from block to block through tagged 64-bit
+// words (step_common.h; the FFN activation as plain fp32 words, below),
+// polled by every thread of a waiting block (a
+// counter of finished producers polled by one thread instead took 2.5-5 us
+// to be seen, against 0.6-2 us for the words themselves); the tag is one
+// counter for every launch, read at the start and advanced by the launch's
+// last block to finish, so a graph replay needs nothing from the host and no
+// buffer is ever cleared.
+//
+// The arithmetic is the batched GEMVs' (gemv_impl.h at M tiles of up to 4
+// rows): the norms sum in double in the wave order (lane l holds elements
+// 4l + 256j, then the DPP tree), the codes depend only on the row maximum,
+// int8 dots are exact int32, and the epilogues are the same device
+// functions, so the logits equal the kernel-per-op path's bit for bit.
+//
+// Waits are bounded (kSpin polls); a timed-out wait sets *err, the other
+// waiting blocks see it within 64 polls and give up, and the host redoes the
+// forward through the separate kernels.
+#include "ec_device.h"
+#include "ec_kernels.h"
+#include "ec_quant.h"
+#include "step_common.h"
+
+namespace ec {
+
+namespace {
+
+constexpr int kTW = kStepThreads / 64;                             // waves per block
+constexpr int kTailRows = 16;                                      // rows of an OD or Q block
+constexpr int kTailPairs = 64;                                     // row pairs of a G block
+constexpr int kTailWP = (kTailMaxM * kTailMaxE / 2 + kStepThreads - 1) / kStepThreads;  // x words
+constexpr int kTailQT = (kTailMaxF / 4 + kStepThreads - 1) / kStepThreads;  // FFN quads per thread and token
+
+// sum over the 8 lanes of each row group (exact int32)
+__device__ __forceinline__ int tsum8(int v) {
+  v = v + dpp_mov<0xB1>(v);
+  v = v + dpp_mov<0x4E>(v);
+  v = v + dpp_mov<0x141>(v);
+  return v;
+}
+
+// sum over the wave (exact int32)
+__device__ __forceinline__ int tsum64(int v) {
+  v = v + dpp_mov<0xB1>(v);
+  v = v + dpp_mov<0x4E>(v);
+  v = v + dpp_mov<0x141>(v);
+  v = v + dpp_mov<0x140>(v);
+  return (readlane(v, 0) + readlane(v, 16)) + (readlane(v, 32) + readlane(v, 48));
+}
+
+__device__ __forceinline__ int tdot16(int s, v4i w, v4i x) {
+  s = __builtin_amdgcn_sdot4(x.x, w.x, s, false);
+  s = __builtin_amdgcn_sdot4(x.y, w.y, s, false);
+  s = __builtin_amdgcn_sdot4(x.z, w.z, s, false);
+  s = __builtin_amdgcn_sdot4(x.w, w.w, s, false);
+  return s;
+}
+
+// A block's words for an exchange: stored, then waited for (the stores
+// complete) before the block goes on, as the persistent steps do
+__device__ __forceinline__ void published() {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+}
+
+// One row of K <= 1024 fp32 values (K % 4 == 0) into int8 codes by one wave,
+// as the GEMV's wave-local prologue does: lane l holds elements 4l + 256j
+// (x, loaded by load_row; gamma g of the same elements, loaded by the
+// caller, for the RMSNorm); NORM: RMSNorm first.  Returns the row scale.
+__device__ __forceinline__ void load_row(const float *row, int K, float4 (&x)[4]) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int j = 0; j < 4; j++) x[j] = *reinterpret_cast<const float4 *>(row + min(4 * lane + 256 * j, K - 4));
+}
+template <bool NORM>
+__device__ float wave_codes(float4 (&x)[4], const float4 (&g)[4], int K, double eps, int8_t *q) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int j = 0; j < 4; j++)
+    if (4 * lane + 256 * j >= K) x[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+  if constexpr (NORM) {
+    double s1 = 0.0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const double d0 = x[j].x, d1 = x[j].y, d2 = x[j].z, d3 = x[j].w;
+      s1 += ((d0 * d0 + d1 * d1) + d2 * d2) + d3 * d3;
+    }
+    s1 = wave_sum_dpp(s1);
+    const double rstd = 1.0 / sqrt(s1 / K + eps);
+    auto nrm = [&](float v, float gv) -> float {
+      v = (float)((double)v * rstd);
+      return v * gv;
+    };
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      x[j].x = nrm(x[j].x, g[j].x);
+      x[j].y = nrm(x[j].y, g[j].y);
+      x[j].z = nrm(x[j].z, g[j].z);
+      x[j].w = nrm(x[j].w, g[j].w);
+      if (4 * lane + 256 * j >= K) x[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+  float mx = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 4; j++)
+    mx = fmaxf(fmaxf(mx, fmaxf(fabsf(x[j].x), fabsf(x[j].y))), fmaxf(fabsf(x[j].z), fabsf(x[j].w)));
+  mx = wave_max_dpp(mx);
+  const float sc = quant_scale(mx);
+  auto put = [&](auto q1) {
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int i = 4 * lane + 256 * j;
+      if (i < K) {
+        const uint32_t b0 = (uint8_t)q1(x[j].x), b1 = (uint8_t)q1(x[j].y), b2 = (uint8_t)q1(x[j].z),
+                       b3 = (uint8_t)q1(x[j].w);
+        *reinterpret_cast<uint32_t *>(q + i) = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+      }
+    }
+  };
+  if (ec_quant_rcp_ok(sc)) {
+    const float rcp = 1.0f / sc;
+    put([&](float v) { return ec_quant1_rcp(v, sc, rcp); });
+  } else {
+    put([&](float v) { return quant1(v, sc); });
+  }
+  return sc;
+}
+
+// gamma of a lane's elements of the wave-local row (loaded ahead of a wait)
+__device__ __forceinline__ void load_gamma(const float *g, int K, float4 (&gv)[4]) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int j = 0; j < 4; j++) gv[j] = *reinterpret_cast<const float4 *>(g + min(4 * lane + 256 * j, K - 4));
+}
+
+// o / down rows [r0, r0 + 16) for every token
+__device__ void tail_od(const BatchTailArgs &a, int gi, unsigned tag, int8_t *codes, float *red) {
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int grp = t >> 3, sub = t & 7;
+  const int E = a.E, F = a.F, M = a.M, ce = E >> 7, nch = F >> 4;
+  const int r0 = gi * kTailRows;
+  const int ro = r0 + (grp & 15), mo = grp >> 4;
+  const bool on_o = mo < M;
+  unsigned long long *XM = a.xch, *X = a.xch + kTailMaxM * E;
+  const float *FV = a.ffv + (size_t)(tag & 1u) * kTailMaxM * F;
+  __shared__ float xm_own[kTailMaxM * kTailRows], x_own[kTailMaxM * kTailRows], s_sc[kTailMaxM];
+
+  // the attention rows first (on the critical path), then the weights: this
+  // group's o row, this wave's two down rows
+  float4 ax[4];
+  if (wave < M) load_row(a.att + (size_t)wave * E, E, ax);
+  v4i wo[8], wd[2][5];
+  {
+    const auto so = gbl16(a.wo + (size_t)ro * E);
+#pragma unroll
+    for (int c = 0; c < 8; c++)
+      if (c < ce) wo[c] = __builtin_nontemporal_load(so + sub + 8 * c);
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      const auto sd = gbl16(a.wd + (size_t)(r0 + wave + 8 * h) * F);
+#pragma unroll
+      for (int c = 0; c < 5; c++) wd[h][c] = __builtin_nontemporal_load(sd + min(lane + 64 * c, nch - 1));
+    }
+  }
+  const float wso = gbl(a.so)[ro], wsd0 = gbl(a.sd)[r0 + wave], wsd1 = gbl(a.sd)[r0 + wave + 8];
+  const float bo = a.bo ? gbl(a.bo)[ro] : 0.0f, bd0 = a.bd ? gbl(a.bd)[r0 + wave] : 0.0f,
+              bd1 = a.bd ? gbl(a.bd)[r0 + wave + 8] : 0.0f;
+  const float xin = on_o && sub == 0 ? a.x[(size_t)mo * E + ro] : 0.0f;
+
+  // ---- O: each token's attention row quantized by wave m ----
+  if (wave < M) {
+    const float4 none[4] = {};
+    const float s = wave_codes<false>(ax, none, E, 0.0, codes + (size_t)wave * E);
+    if (lane == 0) s_sc[wave] = s;
+  }
+  __syncthreads();
+  if (on_o) {
+    int acc = 0;
+#pragma unroll
+    for (int c = 0; c < 8; c++)
+      if (c < ce) acc = tdot16(acc, wo[c], *reinterpret_cast<const v4i *>(codes + (size_t)mo * E + 16 * (sub + 8 * c)));
+    acc = tsum8(acc);
+    if (sub == 0) xm_own[mo * kTailRows + (grp & 15)] = xin + i8_epilogue(acc, s_sc[mo], wso, bo);
+  }
+  __syncthreads();
+  // one wave stores the words, one instruction per 128-byte line (token m's 16 rows)
+  if (t < M * kTailRows) put_word(XM + (size_t)(t >> 4) * E + r0 + (t & 15), xm_own[t], tag);
+  published();
+
+  // ---- D: wait for the FFN words, quantize each token's row ----
+  // the FFN activation: plain fp32 words, kStepFfEmpty until written, in
+  // the half of a double buffer picked by the tag's parity (tagged words
+  // carry 4 bytes of value in 8).  Token m's quads m * F / 4 + t +
+  // kStepThreads * j (j < kTailQT) per thread, one 16-byte device-coherent
+  // load each, reissued only while incomplete; each value's token, scale and
+  // quantization branch are known per j (per-element selections of the token
+  // took ~9 us).
+  const int nq4 = F >> 2;
+  const uint64_t fp = (uint64_t)(uintptr_t)FV;
+  const uint32_t flo = __builtin_amdgcn_readfirstlane((uint32_t)fp),
+                 fhi = __builtin_amdgcn_readfirstlane((uint32_t)(fp >> 32));
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)(uintptr_t)(((uint64_t)fhi << 32) | flo), 0, __builtin_amdgcn_readfirstlane(M * F * 4), 0x00020000);
+  float v[kTailMaxM][kTailQT][4];
+  unsigned pending = 0;
+#pragma unroll
+  for (int m = 0; m < kTailMaxM; m++)
+#pragma unroll
+    for (int j = 0; j < kTailQT; j++) {
+      v[m][j][0] = v[m][j][1] = v[m][j][2] = v[m][j][3] = 0.0f;
+      if (m < M && t + kStepThreads * j < nq4) pending |= 1u << (m * kTailQT + j);
+    }
+  for (int it = 0; pending; it++) {
+    v4u w[kTailMaxM][kTailQT];
+#pragma unroll
+    for (int m = 0; m < kTailMaxM; m++)
+#pragma unroll
+      for (int j = 0; j < kTailQT; j++)
+        if ((pending >> (m * kTailQT + j)) & 1u)
+          w[m][j] = __builtin_amdgcn_raw_buffer_load_b128(rs, (m * nq4 + t + kStepThreads * j) * 16, 0, 16 /* sc1 */);
+#pragma unroll
+    for (int m = 0; m < kTailMaxM; m++)
+#pragma unroll
+      for (int j = 0; j < kTailQT; j++) {
+        const unsigned bit = 1u << (m * kTailQT + j);
+        const v4u q = w[m][j];
+        if ((pending & bit) && q.x != kStepFfEmpty && q.y != kStepFfEmpty && q.z != kStepFfEmpty &&
+            q.w != kStepFfEmpty) {
+          v[m][j][0] = __uint_as_float(q.x);
+          v[m][j][1] = __uint_as_float(q.y);
+          v[m][j][2] = __uint_as_float(q.z);
+          v[m][j][3] = __uint_as_float(q.w);
+          pending &= ~bit;
+        }
+      }
+    if (!pending) break;
+    if (it >= kSpin) {
+      atomicOr(a.err, 1);
+      break;
+    }
+    if ((it & 63) == 63 && __hip_atomic_load(a.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) break;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  // each token's row maximum (quads past the row hold zeros), then its codes
+#pragma unroll
+  for (int m = 0; m < kTailMaxM; m++) {
+    float mx = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kTailQT; j++)
+      mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[m][j][0]), fabsf(v[m][j][1])), fmaxf(fabsf(v[m][j][2]), fabsf(v[m][j][3]))));
+    mx = wave_max_dpp(mx);
+    if (lane == 0) red[m * kTW + wave] = mx;
+  }
+  __syncthreads();
+  float sc[kTailMaxM];
+#pragma unroll
+  for (int m = 0; m < kTailMaxM; m++) {
+    float m8 = red[m * kTW];
+#pragma unroll
+    for (int w = 1; w < kTW; w++) m8 = fmaxf(m8, red[m * kTW + w]);
+    sc[m] = quant_scale(m8);
+  }
+#pragma unroll
+  for (int m = 0; m < kTailMaxM; m++) {
+    if (m < M) {
+      auto put = [&](auto q1) {
+#pragma unroll
+        for (int j = 0; j < kTailQT; j++) {
+          const int q = t + kStepThreads * j;
+          if (q < nq4) {
+            uint32_t c = 0;
+#pragma unroll
+            for (int e = 0; e < 4; e++) c |= (uint32_t)(uint8_t)q1(v[m][j][e]) << (8 * e);
+            *reinterpret_cast<uint32_t *>(codes + (size_t)m * F + 4 * q) = c;
+          }
+        }
+      };
+      // one branch per token (sc[m] is uniform), not a select per element
+      if (ec_quant_rcp_ok(sc[m])) {
+        const float rcp = 1.0f / sc[m];
+        put([&](float x) { return ec_quant1_rcp(x, sc[m], rcp); });
+      } else {
+        put([&](float x) { return quant1(x, sc[m]); });
+      }
+    }
+  }
+  __syncthreads();
+  // down rows r0 + wave and r0 + wave + 8, every token
+  int acc[2][kTailMaxM] = {};
+#pragma unroll
+  for (int c = 0; c < 5; c++) {
+    if (lane + 64 * c < nch) {
+#pragma unroll
+      for (int m = 0; m < kTailMaxM; m++) {
+        if (m < M) {
+          const v4i xq = *reinterpret_cast<const v4i *>(codes + (size_t)m * F + 16 * (lane + 64 * c));
+          acc[0][m] = tdot16(acc[0][m], wd[0][c], xq);
+          acc[1][m] = tdot16(acc[1][m], wd[1][c], xq);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < kTailMaxM; m++) {
+    if (m < M) {
+      const int d0 = tsum64(acc[0][m]), d1 = tsum64(acc[1][m]);
+      if (lane == 0) {
+        x_own[m * kTailRows + wave] = xm_own[m * kTailRows + wave] + i8_epilogue(d0, sc[m], wsd0, bd0);
+        x_own[m * kTailRows + wave + 8] = xm_own[m * kTailRows + wave + 8] + i8_epilogue(d1, sc[m], wsd1, bd1);
+      }
+    }
+  }
+  __syncthreads();
+  if (t < M * kTailRows) {
+    const size_t i = (size_t)(t >> 4) * E + r0 + (t & 15);
+    a.x[i] = x_own[t];
+    if (a.wqkv) put_word(X + i, x_own[t], tag);
+  }
+}
+
+// gate/up row pairs [g0, g0 + 64) for every token
+__device__ void tail_gu(const BatchTailArgs &a, int gi, unsigned tag, float *xs, int8_t *codes) {
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int grp = t >> 3, sub = t & 7;
+  const int E = a.E, F = a.F, M = a.M, ce = E >> 7;
+  const int g0 = gi * kTailPairs;
+  const int pg = min(g0 + grp, F - 1);
+  const unsigned long long *XM = a.xch;
+  float *FV = a.ffv + (size_t)(tag & 1u) * kTailMaxM * F;
+  __shared__ float s_sc[kTailMaxM], stage[kTailMaxM * kTailPairs];
+  __shared__ uint64_t etab[32];  // the SiLU's 2^(i/32) table
+  if (t < 32) etab[t] = ec_exp2_32[t];
+
+  v4i wg[8], wu[8];
+  {
+    const auto sg = gbl16(a.wg + (size_t)pg * E), su = gbl16(a.wu + (size_t)pg * E);
+#pragma unroll
+    for (int c = 0; c < 8; c++)
+      if (c < ce) {
+        wg[c] = __builtin_nontemporal_load(sg + sub + 8 * c);
+        wu[c] = __builtin_nontemporal_load(su + sub + 8 * c);
+      }
+  }
+  const float bsg = gbl(a.sg)[pg], bsu = gbl(a.su)[pg];
+  float4 gam[4];
+  load_gamma(a.ln2_g, E, gam);
+
+  gather<kTailWP>(XM, M * E, tag, xs, a.err);
+  if (wave < M) {
+    float4 xr[4];
+    load_row(xs + (size_t)wave * E, E, xr);
+    const float s = wave_codes<true>(xr, gam, E, a.eps, codes + (size_t)wave * E);
+    if (lane == 0) s_sc[wave] = s;
+  }
+  __syncthreads();
+  int ag[kTailMaxM] = {}, au[kTailMaxM] = {};
+#pragma unroll
+  for (int c = 0; c < 8; c++) {
+    if (c < ce) {
+#pragma unroll
+      for (int m = 0; m < kTailMaxM; m++) {
+        if (m < M) {
+          const v4i xq = *reinterpret_cast<const v4i *>(codes + (size_t)m * E + 16 * (sub + 8 * c));
+          ag[m] = tdot16(ag[m], wg[c], xq);
+          au[m] = tdot16(au[m], wu[c], xq);
+        }
+      }
+    }
+  }
+  // every lane of the group holds the sums; lane m takes token m's epilogue
+  int dg = 0, du = 0;
+#pragma unroll
+  for (int m = 0; m < kTailMaxM; m++) {
+    if (m < M) {
+      const int sg = tsum8(ag[m]), su = tsum8(au[m]);
+      if (sub == m) {
+        dg = sg;
+        du = su;
+      }
+    }
+  }
+  if (sub < M) {
+    const float gv = i8_epilogue(dg, s_sc[sub], bsg, 0.0f), u = i8_epilogue(du, s_sc[sub], bsu, 0.0f);
+    stage[sub * kTailPairs + grp] = silu(gv, etab) * u;
+  }
+  __syncthreads();
+  // wave m stores token m's 64 words: one instruction per four 128-byte lines
+  if (wave < M && g0 + lane < F)
+    __hip_atomic_store(reinterpret_cast<uint32_t *>(FV + (size_t)wave * F + g0 + lane),
+                       __float_as_uint(stage[wave * kTailPairs + lane]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// the next layer's q|k|v rows [q0, q0 + 16) for every token
+__device__ void tail_qkv(const BatchTailArgs &a, int qi, unsigned tag, float *xs, int8_t *codes) {
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int grp = t >> 3, sub = t & 7;
+  const int E = a.E, M = a.M, ce = E >> 7;
+  const int rq = min(qi * kTailRows + (grp & 15), a.NQ - 1), mq = grp >> 4;
+  const bool on_q = mq < M && qi * kTailRows + (grp & 15) < a.NQ;
+  const unsigned long long *X = a.xch + kTailMaxM * E;
+  __shared__ float s_sc[kTailMaxM];
+
+  v4i wq[8];
+  {
+    const auto sq = gbl16(a.wqkv + (size_t)rq * E);
+#pragma unroll
+    for (int c = 0; c < 8; c++)
+      if (c < ce) wq[c] = __builtin_nontemporal_load(sq + sub + 8 * c);
+  }
+  const float wsq = gbl(a.sqkv)[rq], bq = a.bqkv ? gbl(a.bqkv)[rq] : 0.0f;
+  float4 gam[4];
+  load_gamma(a.ln1n_g, E, gam);
+
+  gather<kTailWP>(X, M * E, tag, xs, a.err);
+  if (wave < M) {
+    float4 xr[4];
+    load_row(xs + (size_t)wave * E, E, xr);
+    const float s = wave_codes<true>(xr, gam, E, a.eps, codes + (size_t)wave * E);
+    if (lane == 0) s_sc[wave] = s;
+  }
+  __syncthreads();
+  if (on_q) {
+    int acc = 0;
+#pragma unroll
+    for (int c = 0; c < 8; c++)
+      if (c < ce) acc = tdot16(acc, wq[c], *reinterpret_cast<const v4i *>(codes + (size_t)mq * E + 16 * (sub + 8 * c)));
+    acc = tsum8(acc);
+    if (sub == 0) a.qkv[(size_t)mq * a.ldq + rq] = i8_epilogue(acc, s_sc[mq], wsq, bq);
+  }
+}
+
+__global__ __launch_bounds__(kStepThreads) void batch_tail_kernel(BatchTailArgs a) {
+  extern __shared__ __attribute__((aligned(16))) float lds[];
+  __shared__ float red[kTailMaxM * kTW];
+  const int b = blockIdx.x;
+  const unsigned tag = ld_uniform(a.tag);
+  const int nod = a.E / kTailRows, ngu = (a.F + kTailPairs - 1) / kTailPairs;
+  const int nq = a.wqkv ? (a.NQ + kTailRows - 1) / kTailRows : 0;
+  float *xs = lds;                                                      // [M][E] gathered rows
+  int8_t *codes = reinterpret_cast<int8_t *>(lds + kTailMaxM * a.E);  // [M][max(E, F)]
+  if (b < nod)
+    tail_od(a, b, tag, codes, red);
+  else if (b < nod + ngu)
+    tail_gu(a, b - nod, tag, xs, codes);
+  else if (b < nod + ngu + nq)
+    tail_qkv(a, b - nod - ngu, tag, xs, codes);
+  else {
+    // no role: fill the FFN half that the next launch (tag + 1) uses with
+    // kStepFfEmpty (the previous launch used it and has ended; the next
+    // starts when this one has)
+    const int ib = b - nod - ngu - nq, nb = (int)gridDim.x - nod - ngu - nq;
+    v4u *q = reinterpret_cast<v4u *>(a.ffv + (size_t)((tag + 1u) & 1u) * kTailMaxM * a.F);
+    const v4u e = {kStepFfEmpty, kStepFfEmpty, kStepFfEmpty, kStepFfEmpty};
+    for (int i = ib * kStepThreads + (int)threadIdx.x; i < kTailMaxM * a.F / 4; i += nb * kStepThreads) q[i] = e;
+  }
+  // the last block to finish advances the tag for the next launch (every
+  // block read it at its start) and resets the counter
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    if (__hip_atomic_fetch_add(a.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1) {
+      __hip_atomic_store(a.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_fetch_add(a.tag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
+}  // namespace
+
+size_t batch_tail_lds(int E, int F) {
+  return (size_t)kTailMaxM * E * sizeof(float) + (size_t)kTailMaxM * (E > F ? E : F) + 16;
+}
+
+bool batch_tail_shape_ok(int E, int F, int NQ) {
+  // at least one block with no role, which re-arms the FFN words
+  return E % 128 == 0 && E <= kTailMaxE && F % 16 == 0 && F >= 64 && F <= kTailMaxF && NQ >= 1 &&
+         E / kTailRows + (F + kTailPairs - 1) / kTailPairs + (NQ + kTailRows - 1) / kTailRows < kStepBlocks;
+}
+
+hipError_t batch_tail(const BatchTailArgs &a, bool cooperative, hipStream_t s) {
+  if (a.M < 1 || a.M > kTailMaxM || !batch_tail_shape_ok(a.E, a.F, a.NQ)) return hipErrorInvalidValue;
+  const size_t lds = batch_tail_lds(a.E, a.F);
+  if (cooperative) {
+    BatchTailArgs args = a;
+    void *kargs[] = {&args};
+    return hipLaunchCooperativeKernel(reinterpret_cast<const void *>(batch_tail_kernel), dim3(kStepBlocks),
+                                      dim3(kStepThreads), kargs, (unsigned)lds, s);
+  }
+  klaunch(batch_tail_kernel, dim3(kStepBlocks), dim3(kStepThreads), (uint32_t)lds, s, a);
+  return hipGetLastError();
+}
+
+}  // namespace ec

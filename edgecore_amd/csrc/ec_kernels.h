@@ -293,6 +293,39 @@ struct StepArgs {
 // the FFN words' "not written" pattern: a signaling NaN, which arithmetic never
 // produces (its NaN results are quiet)
 constexpr uint32_t kStepFfEmpty = 0x7FA5A5A5u;
+
+// The batched decode's layer tail (decode_tail.hip): layer l's o projection,
+// RMSNorm, gate/up + SiLU and down (with their residuals), then layer l + 1's
+// RMSNorm and q|k|v, for M <= kTailMaxM int8 Qwen2 tokens in one co-resident
+// launch of kStepBlocks blocks of kStepThreads threads, between two
+// attentions.  Shapes: E % 128 == 0, E <= kTailMaxE, F % 16 == 0,
+// 64 <= F <= kTailMaxF, and E/16 + ceil(F/64) + ceil(NQ/16) blocks, fewer
+// than kStepBlocks.
+constexpr int kTailMaxM = 4, kTailMaxE = 1024, kTailMaxF = 5120;
+struct BatchTailArgs {
+  const int8_t *wo;                   // layer l: o [E][E], scales, bias (or null)
+  const float *so, *bo;
+  const float *ln2_g;                 // RMSNorm gamma before the MLP
+  const int8_t *wg, *wu;              // gate / up [F][E] and their scales
+  const float *sg, *su;
+  const int8_t *wd;                   // down [E][F], scales, bias (or null)
+  const float *sd, *bd;
+  const float *ln1n_g;                // layer l + 1: RMSNorm gamma, q|k|v [NQ][E],
+  const int8_t *wqkv;                 //   scales, bias (or null); wqkv null after
+  const float *sqkv, *bqkv;           //   the last layer
+  const float *att;                   // [M][E] layer l's attention output
+  float *x;                           // [M][E] residual stream (in: x, out: x after layer l)
+  float *qkv;                         // [M][ldq] layer l + 1's q|k|v
+  int ldq, M, E, F, NQ;
+  double eps;
+  unsigned long long *xch;            // exchange words: x_mid, x ([kTailMaxM][E] each)
+  float *ffv;                         // FFN words, two halves of [kTailMaxM][F] (kStepFfEmpty until written)
+  unsigned *tag, *done;               // launch tag, blocks finished
+  int *err;                           // set when a wait times out
+};
+size_t batch_tail_lds(int E, int F);
+bool batch_tail_shape_ok(int E, int F, int NQ);
+hipError_t batch_tail(const BatchTailArgs &a, bool cooperative, hipStream_t s);
 // dynamic LDS of the attention blocks' row and codes (d_model E)
 constexpr inline size_t step_norm_bytes(int E) { return ((size_t)E * 5 + 15) & ~(size_t)15; }
 size_t decode_step_scratch_bytes(int E, int F);

@@ -53,6 +53,9 @@ static bool g_touch = true;
 // plain step report a timeout (tests of the switch).
 static bool g_step_coop = false;
 static bool g_step_test_fail = false;
+// EDGECORE_TAIL_TEST_FAIL=1 makes the first forward through the batched
+// layer tail report a timed-out wait (tests of the fallback to the GEMVs)
+static bool g_tail_test_fail = false;
 static int g_touch_blocks = 8;  // one per XCD; a multiple of 8 (EDGECORE_TOUCH_BLOCKS)
 constexpr int kTouchMinRows = 1024;  // prompts at least this long
 static hipDeviceProp_t g_prop;
@@ -137,6 +140,8 @@ static int init_device(void) {
   g_step_coop = sc && !strcmp(sc, "1");
   const char *sf = getenv("EDGECORE_STEP_TEST_FAIL");
   g_step_test_fail = sf && !strcmp(sf, "1");
+  const char *tf = getenv("EDGECORE_TAIL_TEST_FAIL");
+  g_tail_test_fail = tf && !strcmp(tf, "1");
   const char *tb = getenv("EDGECORE_TOUCH_BLOCKS");
   if (tb && atoi(tb) >= 8) g_touch_blocks = atoi(tb) / 8 * 8;
   const char *gr = getenv("EDGECORE_GRAPHS");
@@ -696,6 +701,12 @@ struct DevModel {
   unsigned step_tag = 0;          // last tag used
   bool step_nograph = false;      // capturing the step failed once: launch it directly
   unsigned long long *d_trace = nullptr;  // EDGECORE_STEP_TRACE=1: phase timestamps of the last step
+  // batched decode's layer tail (decode_tail.hip), int8 Qwen2 of its shapes
+  bool tail_ok = false;
+  unsigned long long *tail_xch = nullptr;  // its exchange words
+  float *tail_ffv = nullptr;               // its FFN words, two halves
+  int *d_tail_io = nullptr;  // [0] launch tag, [1] blocks finished, [2] a wait timed out
+  int *h_tail_err = nullptr;  // pinned copy of [2] after each forward that used it
 };
 
 // host outputs of a forward that selects the top-k logits of its LM-head rows
@@ -752,12 +763,13 @@ static void free_dev(DevModel *d) {
                 d->att, d->ff, d->aq, d->as, d->ah, d->ahs, d->att_sc, d->logits, d->kc, d->vc, d->cand, d->tk_cand,
                 d->tk_nan, d->tk_vals, d->tk_idx, d->tk_status, d->d_layers, d->d_layers16, d->xch, d->ffv,
                 d->d_step_io, d->d_trace,
-                d->d_gen, d->d_gen_t, d->pmax_att, d->pmax_ff};
+                d->d_gen, d->d_gen_t, d->pmax_att, d->pmax_ff, d->tail_xch, d->tail_ffv, d->d_tail_io};
   for (void *p : ps)
     if (p) (void)hipFree(p);
   if (d->h_stage) (void)hipHostFree(d->h_stage);
   if (d->h_amax) (void)hipHostFree(d->h_amax);
   if (d->h_step_io) (void)hipHostFree(d->h_step_io);
+  if (d->h_tail_err) (void)hipHostFree(d->h_tail_err);
   if (d->step_graph) (void)hipGraphExecDestroy(d->step_graph);
   for (hipGraphExec_t ge : d->chain_graph)
     if (ge) (void)hipGraphExecDestroy(ge);
@@ -825,6 +837,20 @@ static int step_shape_kind(const GPT2 *g, const DevModel *d) {
       KVH == H && F == kStep16F && g->wpe && g->sliding_window == 0)
     return 1;
   return -1;
+}
+
+// The batched decode's layer tail (decode_tail.hip) applies to int8 Qwen2
+// models of its shapes on a device with kStepBlocks CUs and cooperative
+// launch.  EDGECORE_TAIL=0 turns it off (the batched decode then runs a GEMV
+// per linear).
+static bool tail_shape_ok(const GPT2 *g, const DevModel *d) {
+  const char *env = getenv("EDGECORE_TAIL");
+  if (env && !strcmp(env, "0")) return false;
+  int coop = 0;
+  if (hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, g_device) != hipSuccess || !coop) return false;
+  if (g_prop.multiProcessorCount != kStepBlocks) return false;
+  return g->arch == ARCH_QWEN2 && g->precision == 0 &&
+         batch_tail_shape_ok(g->n_embd, d->F, g->n_embd + 2 * g->n_kv_embd);
 }
 
 static int load_impl(GPT2 *g, const char *path, int batch_cap, int max_ctx) {
@@ -1110,6 +1136,20 @@ static int load_impl(GPT2 *g, const char *path, int batch_cap, int max_ctx) {
     EC_HIP(dev_malloc(&d->tk_vals, (size_t)d->lm_rows * n * sizeof(float)));
     EC_HIP(dev_malloc(&d->tk_idx, (size_t)d->lm_rows * n * sizeof(int)));
     EC_HIP(dev_malloc(&d->tk_status, (size_t)d->lm_rows * sizeof(int)));
+  }
+  if (tail_shape_ok(g, d)) {
+    const int E = g->n_embd;
+    const size_t words = (size_t)2 * kTailMaxM * E, fw = (size_t)2 * kTailMaxM * d->F;
+    EC_HIP(dev_malloc(&d->tail_xch, words * sizeof(unsigned long long)));
+    EC_HIP(hipMemset(d->tail_xch, 0, words * sizeof(unsigned long long)));
+    EC_HIP(dev_malloc(&d->tail_ffv, fw * sizeof(float)));
+    EC_HIP(hipMemsetD32((hipDeviceptr_t)d->tail_ffv, (int)kStepFfEmpty, fw));
+    EC_HIP(dev_malloc(&d->d_tail_io, 8 * sizeof(int)));
+    const int io0[8] = {1, 0, 0, 0, 0, 0, 0, 0};  // tag 1: the cleared words (tag 0) never match
+    EC_HIP(hipMemcpy(d->d_tail_io, io0, sizeof io0, hipMemcpyHostToDevice));
+    EC_HIP(host_malloc((void **)&d->h_tail_err, sizeof(int), hipHostMallocDefault));
+    *d->h_tail_err = 0;
+    d->tail_ok = true;
   }
   int kind = step_shape_kind(g, d);
   if (kind == 1) {  // the GPT-2 step adds every bias
@@ -1431,6 +1471,32 @@ static int enqueue_step(GPT2 *g, DevModel *d, int max_npos, hipStream_t s) {
   return 0;
 }
 
+// The batched layer tail applies: up to kTailMaxM tokens, each in its own
+// slot (the attention appends each token's k / v itself), not a prefill
+static bool use_tail(const DevModel *d, int M, bool run, bool distinct) {
+  return d->tail_ok && !run && distinct && M <= kTailMaxM;
+}
+
+// After a forward through the layer tail: 1 if one of its waits timed out (a
+// block that never became resident) -- the flag is cleared, the tail turned
+// off and the captured graphs dropped, and the forward is to be redone
+// through the separate kernels; -1 if clearing failed; 0 otherwise
+static int tail_timed_out(DevModel *d) {
+  bool fail = *d->h_tail_err != 0;
+  if (g_tail_test_fail) {
+    g_tail_test_fail = false;
+    fail = true;
+  }
+  if (!fail) return 0;
+  *d->h_tail_err = 0;
+  if (hipMemset(d->d_tail_io + 2, 0, sizeof(int)) != hipSuccess || hipDeviceSynchronize() != hipSuccess) return -1;
+  d->tail_ok = false;
+  for (auto &dg : d->dec_graphs) (void)hipGraphExecDestroy(dg.exec);
+  d->dec_graphs.clear();
+  fprintf(stderr, "edgecore: a batched layer tail's blocks were not all resident; separate kernels from now on\n");
+  return 1;
+}
+
 static int enqueue_forward(GPT2 *g, DevModel *d, int M, int lm_from, bool distinct, bool run, int max_npos,
                            double abytes, float *logits, int *argmax, const TopkReq *tk, hipStream_t s,
                            bool step = false) {
@@ -1459,12 +1525,16 @@ static int enqueue_forward(GPT2 *g, DevModel *d, int M, int lm_from, bool distin
   const int nqkv = qwen ? E + 2 * kv : 3 * E;
   // batched decode of 16-32 tokens: o and down quantize inside their GEMMs
   const bool fq = d->fuse_quant && i8 && g_use_mfma && !run && M >= kGemmMinM && M <= 32;
+  // a decode of up to 4 tokens: each layer's o, MLP and the next layer's
+  // q|k|v in one launch (decode_tail.hip)
+  const bool tail = !step && use_tail(d, M, run, distinct);
   bool touched = false;
   for (int l = 0; l < (step ? 0 : g->n_layer); l++) {
     const LayerDev &W = d->L[l];
     uint16_t *kcl = d->kc + d->kv_layer * l, *vcl = d->vc + d->kv_layer * l;
-    // norm -> q|k|v projection (GPT-2 bias: inside the int8 epilogue, a bias pass for 16-bit)
-    {
+    // norm -> q|k|v projection (GPT-2 bias: inside the int8 epilogue, a bias pass for 16-bit);
+    // after the first layer the layer tail has computed it
+    if (!tail || l == 0) {
       GemvArgs a{d->x, E, nullptr, W.ln1_g, W.ln1_b, g->eps, W.wqkv, nullptr, W.sqkv, nullptr, W.bqkv,
                  d->qkv, ldq, M, E, nqkv, nullptr};
       const int epi = (!i8 && W.bqkv) ? EPI_BIAS : EPI_STORE;
@@ -1525,6 +1595,19 @@ static int enqueue_forward(GPT2 *g, DevModel *d, int M, int lm_from, bool distin
     } else {
       EC_LAUNCH("attention", abytes, attention(aa, s));
     }
+    if (tail) {
+      const bool nx = l + 1 < g->n_layer;
+      const LayerDev &Wn = d->L[nx ? l + 1 : l];
+      const BatchTailArgs ta{(const int8_t *)W.wo, W.so, W.bo, W.ln2_g, (const int8_t *)W.wg, (const int8_t *)W.wu,
+                             W.sg, W.su, (const int8_t *)W.wd, W.sd, W.bd, nx ? Wn.ln1_g : nullptr,
+                             nx ? (const int8_t *)Wn.wqkv : nullptr, nx ? Wn.sqkv : nullptr, nx ? Wn.bqkv : nullptr,
+                             d->att, d->x, d->qkv, ldq, M, E, F, nqkv, g->eps, d->tail_xch, d->tail_ffv,
+                             reinterpret_cast<unsigned *>(d->d_tail_io), reinterpret_cast<unsigned *>(d->d_tail_io + 1),
+                             d->d_tail_io + 2};
+      const double tb = (double)E * E + 3.0 * F * E + (nx ? (double)nqkv * E : 0.0) + 8.0 * M * E;
+      EC_LAUNCH("decode_tail", tb, batch_tail(ta, g_step_coop, s));
+      continue;
+    }
     // output projection + residual
     {
       GemvArgs a{d->att, E, nullptr, nullptr, nullptr, 0.0, W.wo, nullptr, W.so, nullptr, W.bo, d->x, E, M, E, E,
@@ -1566,6 +1649,7 @@ static int enqueue_forward(GPT2 *g, DevModel *d, int M, int lm_from, bool distin
       if ((r = linear(g, d, "gemv_down", a, wt, epi, i8 ? PRO_QUANT : PRO_F32, s))) return r;
     }
   }
+  if (tail) EC_HIP(hipMemcpyAsync(d->h_tail_err, d->d_tail_io + 2, sizeof(int), hipMemcpyDeviceToHost, s));
   if (touched) {  // the side stream's reads end before anything after this forward
     hipEvent_t ev = g_touch_ev[g_touch_i++ & 3];
     EC_HIP(hipEventRecord(ev, g_side));
@@ -1806,12 +1890,23 @@ static int forward_impl(GPT2 *g, const int *tokens, const int *positions, const 
     }
     EC_HIP(hipGraphLaunch(ex, s));
     EC_HIP(hipStreamSynchronize(s));
+    if (use_tail(d, M, run, distinct)) {
+      const int tr = tail_timed_out(d);
+      if (tr > 0) return forward_impl(g, tokens, positions, seqs, M, lm_from, logits, argmax, tk);
+      if (tr < 0) return set_err(-3, "batched decode: clearing a timed-out layer tail failed");
+    }
     memcpy(argmax, d->h_amax, (size_t)M * sizeof(int));
     return 0;
   }
+  const bool tail = use_tail(d, M, run, distinct);
   const int r = enqueue_forward(g, d, M, lm_from, distinct, run, max_npos, abytes, logits, argmax, tk, s);
   if (r) return r;
   EC_HIP(hipStreamSynchronize(s));
+  if (tail) {
+    const int tr = tail_timed_out(d);
+    if (tr > 0) return forward_impl(g, tokens, positions, seqs, M, lm_from, logits, argmax, tk);
+    if (tr < 0) return set_err(-3, "batched decode: clearing a timed-out layer tail failed");
+  }
   return 0;
 }
 

@@ -157,6 +157,29 @@ __device__ float wave_codes(float4 (&x)[4], const float4 (&g)[4], int K, double 
   return sc;
 }
 
+// A row's 16-byte chunks sub + 8 c (c < 8) of a weight row of E int8: chunks
+// past the row (c >= E / 128) load a clamped address and are zeroed, so the
+// dot loops run all eight chunks without branches (a branch per chunk made
+// each chunk's LDS read wait before its dot)
+__device__ __forceinline__ void load_chunks(gptr<v4i> src, int sub, int ce, v4i (&w)[8]) {
+#pragma unroll
+  for (int c = 0; c < 8; c++) {
+    const v4i v = __builtin_nontemporal_load(src + min(sub + 8 * c, 8 * ce - 1));
+    w[c] = c < ce ? v : v4i{0, 0, 0, 0};
+  }
+}
+// a dot of the eight chunks against the row's codes (LDS; the reads of the
+// zeroed chunks past the row stay inside the codes area's padding)
+__device__ __forceinline__ int dot_chunks(const v4i (&w)[8], const int8_t *q, int sub) {
+  v4i x[8];
+#pragma unroll
+  for (int c = 0; c < 8; c++) x[c] = *reinterpret_cast<const v4i *>(q + 16 * (sub + 8 * c));
+  int acc = 0;
+#pragma unroll
+  for (int c = 0; c < 8; c++) acc = tdot16(acc, w[c], x[c]);
+  return acc;
+}
+
 // gamma of a lane's elements of the wave-local row (loaded ahead of a wait)
 __device__ __forceinline__ void load_gamma(const float *g, int K, float4 (&gv)[4]) {
   const int lane = threadIdx.x & 63;
@@ -182,10 +205,7 @@ __device__ void tail_od(const BatchTailArgs &a, int gi, unsigned tag, int8_t *co
   if (wave < M) load_row(a.att + (size_t)wave * E, E, ax);
   v4i wo[8], wd[2][5];
   {
-    const auto so = gbl16(a.wo + (size_t)ro * E);
-#pragma unroll
-    for (int c = 0; c < 8; c++)
-      if (c < ce) wo[c] = __builtin_nontemporal_load(so + sub + 8 * c);
+    load_chunks(gbl16(a.wo + (size_t)ro * E), sub, ce, wo);
 #pragma unroll
     for (int h = 0; h < 2; h++) {
       const auto sd = gbl16(a.wd + (size_t)(r0 + wave + 8 * h) * F);
@@ -206,11 +226,7 @@ __device__ void tail_od(const BatchTailArgs &a, int gi, unsigned tag, int8_t *co
   }
   __syncthreads();
   if (on_o) {
-    int acc = 0;
-#pragma unroll
-    for (int c = 0; c < 8; c++)
-      if (c < ce) acc = tdot16(acc, wo[c], *reinterpret_cast<const v4i *>(codes + (size_t)mo * E + 16 * (sub + 8 * c)));
-    acc = tsum8(acc);
+    const int acc = tsum8(dot_chunks(wo, codes + (size_t)mo * E, sub));
     if (sub == 0) xm_own[mo * kTailRows + (grp & 15)] = xin + i8_epilogue(acc, s_sc[mo], wso, bo);
   }
   __syncthreads();
@@ -364,13 +380,8 @@ __device__ void tail_gu(const BatchTailArgs &a, int gi, unsigned tag, float *xs,
 
   v4i wg[8], wu[8];
   {
-    const auto sg = gbl16(a.wg + (size_t)pg * E), su = gbl16(a.wu + (size_t)pg * E);
-#pragma unroll
-    for (int c = 0; c < 8; c++)
-      if (c < ce) {
-        wg[c] = __builtin_nontemporal_load(sg + sub + 8 * c);
-        wu[c] = __builtin_nontemporal_load(su + sub + 8 * c);
-      }
+    load_chunks(gbl16(a.wg + (size_t)pg * E), sub, ce, wg);
+    load_chunks(gbl16(a.wu + (size_t)pg * E), sub, ce, wu);
   }
   const float bsg = gbl(a.sg)[pg], bsu = gbl(a.su)[pg];
   float4 gam[4];
@@ -386,15 +397,15 @@ __device__ void tail_gu(const BatchTailArgs &a, int gi, unsigned tag, float *xs,
   __syncthreads();
   int ag[kTailMaxM] = {}, au[kTailMaxM] = {};
 #pragma unroll
-  for (int c = 0; c < 8; c++) {
-    if (c < ce) {
+  for (int m = 0; m < kTailMaxM; m++) {
+    if (m < M) {
+      v4i x[8];
 #pragma unroll
-      for (int m = 0; m < kTailMaxM; m++) {
-        if (m < M) {
-          const v4i xq = *reinterpret_cast<const v4i *>(codes + (size_t)m * E + 16 * (sub + 8 * c));
-          ag[m] = tdot16(ag[m], wg[c], xq);
-          au[m] = tdot16(au[m], wu[c], xq);
-        }
+      for (int c = 0; c < 8; c++) x[c] = *reinterpret_cast<const v4i *>(codes + (size_t)m * E + 16 * (sub + 8 * c));
+#pragma unroll
+      for (int c = 0; c < 8; c++) {
+        ag[m] = tdot16(ag[m], wg[c], x[c]);
+        au[m] = tdot16(au[m], wu[c], x[c]);
       }
     }
   }
@@ -433,10 +444,7 @@ __device__ void tail_qkv(const BatchTailArgs &a, int qi, unsigned tag, float *xs
 
   v4i wq[8];
   {
-    const auto sq = gbl16(a.wqkv + (size_t)rq * E);
-#pragma unroll
-    for (int c = 0; c < 8; c++)
-      if (c < ce) wq[c] = __builtin_nontemporal_load(sq + sub + 8 * c);
+    load_chunks(gbl16(a.wqkv + (size_t)rq * E), sub, ce, wq);
   }
   const float wsq = gbl(a.sqkv)[rq], bq = a.bqkv ? gbl(a.bqkv)[rq] : 0.0f;
   float4 gam[4];
@@ -451,11 +459,7 @@ __device__ void tail_qkv(const BatchTailArgs &a, int qi, unsigned tag, float *xs
   }
   __syncthreads();
   if (on_q) {
-    int acc = 0;
-#pragma unroll
-    for (int c = 0; c < 8; c++)
-      if (c < ce) acc = tdot16(acc, wq[c], *reinterpret_cast<const v4i *>(codes + (size_t)mq * E + 16 * (sub + 8 * c)));
-    acc = tsum8(acc);
+    const int acc = tsum8(dot_chunks(wq, codes + (size_t)mq * E, sub));
     if (sub == 0) a.qkv[(size_t)mq * a.ldq + rq] = i8_epilogue(acc, s_sc[mq], wsq, bq);
   }
 }
@@ -499,7 +503,9 @@ __global__ __launch_bounds__(kStepThreads) void batch_tail_kernel(BatchTailArgs 
 }  // namespace
 
 size_t batch_tail_lds(int E, int F) {
-  return (size_t)kTailMaxM * E * sizeof(float) + (size_t)kTailMaxM * (E > F ? E : F) + 16;
+  // the codes area padded by the 1024 - E bytes that the dots' zeroed
+  // chunks read past the last row
+  return (size_t)kTailMaxM * E * sizeof(float) + (size_t)kTailMaxM * (E > F ? E : F) + kTailMaxE;
 }
 
 bool batch_tail_shape_ok(int E, int F, int NQ) {

@@ -20,18 +20,21 @@
 //
 //   OD (E / 16 blocks, 16 rows each) -- o rows for every token (64 groups of
 //      8 lanes: row r0 + g % 16, token g / 16), x_mid = x + o, publish
-//      x_mid; then wait for the FFN words, quantize each token's row, down
-//      rows (two per wave, every token), x = x_mid + d: store x and publish.
+//      x_mid; then wait for the FFN rows' scales and codes, down rows (two
+//      per wave, every token), x = x_mid + d: store x and publish.
 //   G  (ceil(F / 64) blocks, 64 gate/up row pairs each) -- wait for x_mid,
 //      RMSNorm + quantize (wave m: token m), gate and up rows for every
-//      token, silu(g) * u, publish.
+//      token, silu(g) * u; publish each token's maximum over the block's
+//      values, wait for every block's, and quantize and publish the block's
+//      values with the row scale (each FFN value is quantized once, by its
+//      producer, instead of by every o/down block: that took 2.7 us there,
+//      and codes cross the exchange in a quarter of the bytes).
 //   Q  (ceil(NQ / 16) blocks, 16 rows each; none after the last layer) --
 //      wait for x, the next layer's RMSNorm + quantize, q|k|v rows, store.
 //
 // Every block issues its weight loads before it waits, so the weight stream
 // overlaps the wait.  Results go from block to block through tagged 64-bit
-// words (step_common.h; the FFN activation as plain fp32 words, below),
-// polled by every thread of a waiting block (a
+// words (step_common.h), polled by every thread of a waiting block (a
 // counter of finished producers polled by one thread instead took 2.5-5 us
 // to be seen, against 0.6-2 us for the words themselves); the tag is one
 // counter for every launch, read at the start and advanced by the launch's
@@ -60,7 +63,72 @@ constexpr int kTW = kStepThreads / 64;                             // waves per 
 constexpr int kTailRows = 16;                                      // rows of an OD or Q block
 constexpr int kTailPairs = 64;                                     // row pairs of a G block
 constexpr int kTailWP = (kTailMaxM * kTailMaxE / 2 + kStepThreads - 1) / kStepThreads;  // x words
-constexpr int kTailQT = (kTailMaxF / 4 + kStepThreads - 1) / kStepThreads;  // FFN quads per thread and token
+constexpr int kTailMaxG = kTailMaxF / kTailPairs;                  // gate/up blocks at most
+constexpr int kTailWQ = (kTailMaxM * kTailMaxF / 8 + kStepThreads - 1) / kStepThreads;  // FFN code pairs
+// exchange areas (tagged words): x_mid [kTailMaxM][E], x [kTailMaxM][E],
+// the gate/up blocks' per-token maxima (block gi's words for tokens m at
+// 16 gi + m: one 128-byte line per block), the FFN codes four per word
+// [kTailMaxM][kTailMaxF / 4]
+constexpr int kMxLine = 16;  // words per 128-byte line
+__device__ __forceinline__ unsigned long long *tail_mx(const BatchTailArgs &a) { return a.xch + 2 * kTailMaxM * a.E; }
+__device__ __forceinline__ unsigned long long *tail_fq(const BatchTailArgs &a) {
+  return a.xch + 2 * kTailMaxM * a.E + kMxLine * kTailMaxG;
+}
+
+// Wait for every gate/up block's maxima and form each token's row scale
+// (quant_scale of the maximum over the whole FFN row: a maximum is exact in
+// any order) into s_sf[m].  One wave polls, lane l the lines of blocks l
+// and l + 64 (every thread of 132 blocks polling 19 shared lines took ~3 us
+// to see them); every thread of the block calls it.
+__device__ void wait_row_scales(const BatchTailArgs &a, int ngu, unsigned tag, float *s_sf) {
+  const int t = threadIdx.x;
+  if (t < 64) {
+    const int M = a.M;
+    const __amdgpu_buffer_rsrc_t rs = xch_rsrc(tail_mx(a), ngu * kMxLine);
+    float mx[kTailMaxM] = {0.f, 0.f, 0.f, 0.f};
+    unsigned pending = 0;
+#pragma unroll
+    for (int h = 0; h < 2; h++)
+      if (t + 64 * h < ngu) pending |= 1u << h;
+    for (int it = 0; pending; it++) {
+      v4u w[2][2];
+#pragma unroll
+      for (int h = 0; h < 2; h++)
+        if ((pending >> h) & 1u) {
+          w[h][0] = get_pair(rs, (t + 64 * h) * (kMxLine / 2));
+          w[h][1] = M > 2 ? get_pair(rs, (t + 64 * h) * (kMxLine / 2) + 1) : w[h][0];
+        }
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        if (!((pending >> h) & 1u)) continue;
+        const unsigned tg[4] = {w[h][0].y, w[h][0].w, w[h][1].y, w[h][1].w};
+        bool ok = true;
+#pragma unroll
+        for (int m = 0; m < kTailMaxM; m++) ok = ok && (m >= M || tg[m] == tag);
+        if (ok) {
+          const uint32_t vv[4] = {w[h][0].x, w[h][0].z, w[h][1].x, w[h][1].z};
+#pragma unroll
+          for (int m = 0; m < kTailMaxM; m++)
+            if (m < M) mx[m] = fmaxf(mx[m], __uint_as_float(vv[m]));
+          pending &= ~(1u << h);
+        }
+      }
+      if (!pending) break;
+      if (it >= kSpin) {
+        atomicOr(a.err, 1);
+        break;
+      }
+      if ((it & 63) == 63 && __hip_atomic_load(a.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) break;
+      __builtin_amdgcn_s_sleep(1);
+    }
+#pragma unroll
+    for (int m = 0; m < kTailMaxM; m++) {
+      const float r = wave_max_dpp(mx[m]);
+      if (t == 0) s_sf[m] = quant_scale(r);
+    }
+  }
+  __syncthreads();
+}
 
 // sum over the 8 lanes of each row group (exact int32)
 __device__ __forceinline__ int tsum8(int v) {
@@ -196,8 +264,7 @@ __device__ void tail_od(const BatchTailArgs &a, int gi, unsigned tag, int8_t *co
   const int ro = r0 + (grp & 15), mo = grp >> 4;
   const bool on_o = mo < M;
   unsigned long long *XM = a.xch, *X = a.xch + kTailMaxM * E;
-  const float *FV = a.ffv + (size_t)(tag & 1u) * kTailMaxM * F;
-  __shared__ float xm_own[kTailMaxM * kTailRows], x_own[kTailMaxM * kTailRows], s_sc[kTailMaxM];
+  __shared__ float xm_own[kTailMaxM * kTailRows], x_own[kTailMaxM * kTailRows], s_sc[kTailMaxM], s_sf[kTailMaxM];
 
   // the attention rows first (on the critical path), then the weights: this
   // group's o row, this wave's two down rows
@@ -234,104 +301,23 @@ __device__ void tail_od(const BatchTailArgs &a, int gi, unsigned tag, int8_t *co
   if (t < M * kTailRows) put_word(XM + (size_t)(t >> 4) * E + r0 + (t & 15), xm_own[t], tag);
   published();
 
-  // ---- D: wait for the FFN words, quantize each token's row ----
-  // the FFN activation: plain fp32 words, kStepFfEmpty until written, in
-  // the half of a double buffer picked by the tag's parity (tagged words
-  // carry 4 bytes of value in 8).  Token m's quads m * F / 4 + t +
-  // kStepThreads * j (j < kTailQT) per thread, one 16-byte device-coherent
-  // load each, reissued only while incomplete; each value's token, scale and
-  // quantization branch are known per j (per-element selections of the token
-  // took ~9 us).
-  const int nq4 = F >> 2;
-  const uint64_t fp = (uint64_t)(uintptr_t)FV;
-  const uint32_t flo = __builtin_amdgcn_readfirstlane((uint32_t)fp),
-                 fhi = __builtin_amdgcn_readfirstlane((uint32_t)(fp >> 32));
-  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-      (void *)(uintptr_t)(((uint64_t)fhi << 32) | flo), 0, __builtin_amdgcn_readfirstlane(M * F * 4), 0x00020000);
-  float v[kTailMaxM][kTailQT][4];
-  unsigned pending = 0;
+  // ---- D: the rows' scales from the gate/up blocks' maxima, then the FFN
+  // codes (quantized by the gate/up blocks, four per word) into LDS ----
+  const int ngu = (F + kTailPairs - 1) / kTailPairs;
+  wait_row_scales(a, ngu, tag, s_sf);
+  {
+    float v[kTailWQ][2];
+    const unsigned own = wait_pairs<kTailWQ>(tail_fq(a), M * F / 4, tag, v, a.err);
 #pragma unroll
-  for (int m = 0; m < kTailMaxM; m++)
-#pragma unroll
-    for (int j = 0; j < kTailQT; j++) {
-      v[m][j][0] = v[m][j][1] = v[m][j][2] = v[m][j][3] = 0.0f;
-      if (m < M && t + kStepThreads * j < nq4) pending |= 1u << (m * kTailQT + j);
-    }
-  for (int it = 0; pending; it++) {
-    v4u w[kTailMaxM][kTailQT];
-#pragma unroll
-    for (int m = 0; m < kTailMaxM; m++)
-#pragma unroll
-      for (int j = 0; j < kTailQT; j++)
-        if ((pending >> (m * kTailQT + j)) & 1u)
-          w[m][j] = __builtin_amdgcn_raw_buffer_load_b128(rs, (m * nq4 + t + kStepThreads * j) * 16, 0, 16 /* sc1 */);
-#pragma unroll
-    for (int m = 0; m < kTailMaxM; m++)
-#pragma unroll
-      for (int j = 0; j < kTailQT; j++) {
-        const unsigned bit = 1u << (m * kTailQT + j);
-        const v4u q = w[m][j];
-        if ((pending & bit) && q.x != kStepFfEmpty && q.y != kStepFfEmpty && q.z != kStepFfEmpty &&
-            q.w != kStepFfEmpty) {
-          v[m][j][0] = __uint_as_float(q.x);
-          v[m][j][1] = __uint_as_float(q.y);
-          v[m][j][2] = __uint_as_float(q.z);
-          v[m][j][3] = __uint_as_float(q.w);
-          pending &= ~bit;
-        }
-      }
-    if (!pending) break;
-    if (it >= kSpin) {
-      atomicOr(a.err, 1);
-      break;
-    }
-    if ((it & 63) == 63 && __hip_atomic_load(a.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) break;
-    __builtin_amdgcn_s_sleep(1);
-  }
-  // each token's row maximum (quads past the row hold zeros), then its codes
-#pragma unroll
-  for (int m = 0; m < kTailMaxM; m++) {
-    float mx = 0.0f;
-#pragma unroll
-    for (int j = 0; j < kTailQT; j++)
-      mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[m][j][0]), fabsf(v[m][j][1])), fmaxf(fabsf(v[m][j][2]), fabsf(v[m][j][3]))));
-    mx = wave_max_dpp(mx);
-    if (lane == 0) red[m * kTW + wave] = mx;
+    for (int j = 0; j < kTailWQ; j++)
+      if ((own >> j) & 1u)
+        *reinterpret_cast<uint2 *>(codes + 8 * (t + kStepThreads * j)) =
+            make_uint2(__float_as_uint(v[j][0]), __float_as_uint(v[j][1]));
   }
   __syncthreads();
   float sc[kTailMaxM];
 #pragma unroll
-  for (int m = 0; m < kTailMaxM; m++) {
-    float m8 = red[m * kTW];
-#pragma unroll
-    for (int w = 1; w < kTW; w++) m8 = fmaxf(m8, red[m * kTW + w]);
-    sc[m] = quant_scale(m8);
-  }
-#pragma unroll
-  for (int m = 0; m < kTailMaxM; m++) {
-    if (m < M) {
-      auto put = [&](auto q1) {
-#pragma unroll
-        for (int j = 0; j < kTailQT; j++) {
-          const int q = t + kStepThreads * j;
-          if (q < nq4) {
-            uint32_t c = 0;
-#pragma unroll
-            for (int e = 0; e < 4; e++) c |= (uint32_t)(uint8_t)q1(v[m][j][e]) << (8 * e);
-            *reinterpret_cast<uint32_t *>(codes + (size_t)m * F + 4 * q) = c;
-          }
-        }
-      };
-      // one branch per token (sc[m] is uniform), not a select per element
-      if (ec_quant_rcp_ok(sc[m])) {
-        const float rcp = 1.0f / sc[m];
-        put([&](float x) { return ec_quant1_rcp(x, sc[m], rcp); });
-      } else {
-        put([&](float x) { return quant1(x, sc[m]); });
-      }
-    }
-  }
-  __syncthreads();
+  for (int m = 0; m < kTailMaxM; m++) sc[m] = s_sf[m];
   // down rows r0 + wave and r0 + wave + 8, every token
   int acc[2][kTailMaxM] = {};
 #pragma unroll
@@ -373,8 +359,8 @@ __device__ void tail_gu(const BatchTailArgs &a, int gi, unsigned tag, float *xs,
   const int g0 = gi * kTailPairs;
   const int pg = min(g0 + grp, F - 1);
   const unsigned long long *XM = a.xch;
-  float *FV = a.ffv + (size_t)(tag & 1u) * kTailMaxM * F;
-  __shared__ float s_sc[kTailMaxM], stage[kTailMaxM * kTailPairs];
+  __shared__ float s_sc[kTailMaxM], stage[kTailMaxM * kTailPairs], s_sf[kTailMaxM], s_mx[kTailMaxM];
+  __shared__ uint32_t qstage[kTailMaxM * kTailPairs / 4];  // the block's codes, four per word
   __shared__ uint64_t etab[32];  // the SiLU's 2^(i/32) table
   if (t < 32) etab[t] = ec_exp2_32[t];
 
@@ -426,10 +412,31 @@ __device__ void tail_gu(const BatchTailArgs &a, int gi, unsigned tag, float *xs,
     stage[sub * kTailPairs + grp] = silu(gv, etab) * u;
   }
   __syncthreads();
-  // wave m stores token m's 64 words: one instruction per four 128-byte lines
-  if (wave < M && g0 + lane < F)
-    __hip_atomic_store(reinterpret_cast<uint32_t *>(FV + (size_t)wave * F + g0 + lane),
-                       __float_as_uint(stage[wave * kTailPairs + lane]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // wave m: token m's maximum over this block's values, published; then,
+  // with every block's maxima, the row scale and this block's codes
+  const int ngu = (F + kTailPairs - 1) / kTailPairs;
+  unsigned long long *MX = tail_mx(a), *FQ = tail_fq(a);
+  const float hv = wave < M && g0 + lane < F ? stage[wave * kTailPairs + lane] : 0.0f;
+  if (wave < M) {
+    const float mx = wave_max_dpp(fabsf(hv));
+    if (lane == 0) s_mx[wave] = mx;
+  }
+  __syncthreads();
+  // the block's line of maxima, by one store instruction
+  if (t < M) put_word(MX + (size_t)gi * kMxLine + t, s_mx[t], tag);
+  wait_row_scales(a, ngu, tag, s_sf);
+  if (wave < M) {
+    const float sf = s_sf[wave];
+    const int8_t c = ec_quant_rcp_ok(sf) ? ec_quant1_rcp(hv, sf, 1.0f / sf) : quant1(hv, sf);
+    reinterpret_cast<int8_t *>(qstage)[wave * kTailPairs + lane] = c;
+  }
+  __syncthreads();
+  // 16 words (64 codes) per token, stored by one wave
+  if (t < 16 * M) {
+    const int m = t >> 4, k = t & 15;
+    if (g0 + 4 * k < F)
+      put_word(FQ + (size_t)m * (F / 4) + g0 / 4 + k, __uint_as_float(qstage[m * 16 + k]), tag);
+  }
 }
 
 // the next layer's q|k|v rows [q0, q0 + 16) for every token
@@ -479,15 +486,6 @@ __global__ __launch_bounds__(kStepThreads) void batch_tail_kernel(BatchTailArgs 
     tail_gu(a, b - nod, tag, xs, codes);
   else if (b < nod + ngu + nq)
     tail_qkv(a, b - nod - ngu, tag, xs, codes);
-  else {
-    // no role: fill the FFN half that the next launch (tag + 1) uses with
-    // kStepFfEmpty (the previous launch used it and has ended; the next
-    // starts when this one has)
-    const int ib = b - nod - ngu - nq, nb = (int)gridDim.x - nod - ngu - nq;
-    v4u *q = reinterpret_cast<v4u *>(a.ffv + (size_t)((tag + 1u) & 1u) * kTailMaxM * a.F);
-    const v4u e = {kStepFfEmpty, kStepFfEmpty, kStepFfEmpty, kStepFfEmpty};
-    for (int i = ib * kStepThreads + (int)threadIdx.x; i < kTailMaxM * a.F / 4; i += nb * kStepThreads) q[i] = e;
-  }
   // the last block to finish advances the tag for the next launch (every
   // block read it at its start) and resets the counter
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -508,10 +506,13 @@ size_t batch_tail_lds(int E, int F) {
   return (size_t)kTailMaxM * E * sizeof(float) + (size_t)kTailMaxM * (E > F ? E : F) + kTailMaxE;
 }
 
+size_t batch_tail_xch_words(int E) {
+  return (size_t)2 * kTailMaxM * E + (size_t)kMxLine * kTailMaxG + (size_t)kTailMaxM * kTailMaxF / 4;
+}
+
 bool batch_tail_shape_ok(int E, int F, int NQ) {
-  // at least one block with no role, which re-arms the FFN words
   return E % 128 == 0 && E <= kTailMaxE && F % 16 == 0 && F >= 64 && F <= kTailMaxF && NQ >= 1 &&
-         E / kTailRows + (F + kTailPairs - 1) / kTailPairs + (NQ + kTailRows - 1) / kTailRows < kStepBlocks;
+         E / kTailRows + (F + kTailPairs - 1) / kTailPairs + (NQ + kTailRows - 1) / kTailRows <= kStepBlocks;
 }
 
 hipError_t batch_tail(const BatchTailArgs &a, bool cooperative, hipStream_t s) {

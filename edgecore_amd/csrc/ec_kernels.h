@@ -299,8 +299,7 @@ constexpr uint32_t kStepFfEmpty = 0x7FA5A5A5u;
 // RMSNorm and q|k|v, for M <= kTailMaxM int8 Qwen2 tokens in one co-resident
 // launch of kStepBlocks blocks of kStepThreads threads, between two
 // attentions.  Shapes: E % 128 == 0, E <= kTailMaxE, F % 16 == 0,
-// 64 <= F <= kTailMaxF, and E/16 + ceil(F/64) + ceil(NQ/16) blocks, fewer
-// than kStepBlocks.
+// 64 <= F <= kTailMaxF, and E/16 + ceil(F/64) + ceil(NQ/16) blocks at most.
 constexpr int kTailMaxM = 4, kTailMaxE = 1024, kTailMaxF = 5120;
 struct BatchTailArgs {
   const int8_t *wo;                   // layer l: o [E][E], scales, bias (or null)
@@ -318,12 +317,12 @@ struct BatchTailArgs {
   float *qkv;                         // [M][ldq] layer l + 1's q|k|v
   int ldq, M, E, F, NQ;
   double eps;
-  unsigned long long *xch;            // exchange words: x_mid, x ([kTailMaxM][E] each)
-  float *ffv;                         // FFN words, two halves of [kTailMaxM][F] (kStepFfEmpty until written)
+  unsigned long long *xch;            // exchange words (batch_tail_xch_words of them)
   unsigned *tag, *done;               // launch tag, blocks finished
   int *err;                           // set when a wait times out
 };
 size_t batch_tail_lds(int E, int F);
+size_t batch_tail_xch_words(int E);
 bool batch_tail_shape_ok(int E, int F, int NQ);
 hipError_t batch_tail(const BatchTailArgs &a, bool cooperative, hipStream_t s);
 // dynamic LDS of the attention blocks' row and codes (d_model E)

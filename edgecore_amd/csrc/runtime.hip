@@ -704,7 +704,6 @@ struct DevModel {
   // batched decode's layer tail (decode_tail.hip), int8 Qwen2 of its shapes
   bool tail_ok = false;
   unsigned long long *tail_xch = nullptr;  // its exchange words
-  float *tail_ffv = nullptr;               // its FFN words, two halves
   int *d_tail_io = nullptr;  // [0] launch tag, [1] blocks finished, [2] a wait timed out
   int *h_tail_err = nullptr;  // pinned copy of [2] after each forward that used it
 };
@@ -763,7 +762,7 @@ static void free_dev(DevModel *d) {
                 d->att, d->ff, d->aq, d->as, d->ah, d->ahs, d->att_sc, d->logits, d->kc, d->vc, d->cand, d->tk_cand,
                 d->tk_nan, d->tk_vals, d->tk_idx, d->tk_status, d->d_layers, d->d_layers16, d->xch, d->ffv,
                 d->d_step_io, d->d_trace,
-                d->d_gen, d->d_gen_t, d->pmax_att, d->pmax_ff, d->tail_xch, d->tail_ffv, d->d_tail_io};
+                d->d_gen, d->d_gen_t, d->pmax_att, d->pmax_ff, d->tail_xch, d->d_tail_io};
   for (void *p : ps)
     if (p) (void)hipFree(p);
   if (d->h_stage) (void)hipHostFree(d->h_stage);
@@ -1139,11 +1138,9 @@ static int load_impl(GPT2 *g, const char *path, int batch_cap, int max_ctx) {
   }
   if (tail_shape_ok(g, d)) {
     const int E = g->n_embd;
-    const size_t words = (size_t)2 * kTailMaxM * E, fw = (size_t)2 * kTailMaxM * d->F;
+    const size_t words = batch_tail_xch_words(E);
     EC_HIP(dev_malloc(&d->tail_xch, words * sizeof(unsigned long long)));
     EC_HIP(hipMemset(d->tail_xch, 0, words * sizeof(unsigned long long)));
-    EC_HIP(dev_malloc(&d->tail_ffv, fw * sizeof(float)));
-    EC_HIP(hipMemsetD32((hipDeviceptr_t)d->tail_ffv, (int)kStepFfEmpty, fw));
     EC_HIP(dev_malloc(&d->d_tail_io, 8 * sizeof(int)));
     const int io0[8] = {1, 0, 0, 0, 0, 0, 0, 0};  // tag 1: the cleared words (tag 0) never match
     EC_HIP(hipMemcpy(d->d_tail_io, io0, sizeof io0, hipMemcpyHostToDevice));
@@ -1601,7 +1598,7 @@ static int enqueue_forward(GPT2 *g, DevModel *d, int M, int lm_from, bool distin
       const BatchTailArgs ta{(const int8_t *)W.wo, W.so, W.bo, W.ln2_g, (const int8_t *)W.wg, (const int8_t *)W.wu,
                              W.sg, W.su, (const int8_t *)W.wd, W.sd, W.bd, nx ? Wn.ln1_g : nullptr,
                              nx ? (const int8_t *)Wn.wqkv : nullptr, nx ? Wn.sqkv : nullptr, nx ? Wn.bqkv : nullptr,
-                             d->att, d->x, d->qkv, ldq, M, E, F, nqkv, g->eps, d->tail_xch, d->tail_ffv,
+                             d->att, d->x, d->qkv, ldq, M, E, F, nqkv, g->eps, d->tail_xch,
                              reinterpret_cast<unsigned *>(d->d_tail_io), reinterpret_cast<unsigned *>(d->d_tail_io + 1),
                              d->d_tail_io + 2};
       const double tb = (double)E * E + 3.0 * F * E + (nx ? (double)nqkv * E : 0.0) + 8.0 * M * E;

@@ -59,16 +59,15 @@ namespace ec {
 
 namespace {
 
-constexpr int kTW = kStepThreads / 64;                             // waves per block
 constexpr int kTailRows = 16;                                      // rows of an OD or Q block
 constexpr int kTailPairs = 64;                                     // row pairs of a G block
 constexpr int kTailWP = (kTailMaxM * kTailMaxE / 2 + kStepThreads - 1) / kStepThreads;  // x words
 constexpr int kTailMaxG = kTailMaxF / kTailPairs;                  // gate/up blocks at most
-constexpr int kTailWQ = (kTailMaxM * kTailMaxF / 8 + kStepThreads - 1) / kStepThreads;  // FFN code pairs
+constexpr int kTailWQ = (kTailMaxM * kTailMaxF / 8 + 2 + kStepThreads - 1) / kStepThreads;  // FFN code pairs
 // exchange areas (tagged words): x_mid [kTailMaxM][E], x [kTailMaxM][E],
 // the gate/up blocks' per-token maxima (block gi's words for tokens m at
 // 16 gi + m: one 128-byte line per block), the FFN codes four per word
-// [kTailMaxM][kTailMaxF / 4]
+// [M][F / 4] followed by the M rows' scales (kTailMaxM words)
 constexpr int kMxLine = 16;  // words per 128-byte line
 __device__ __forceinline__ unsigned long long *tail_mx(const BatchTailArgs &a) { return a.xch + 2 * kTailMaxM * a.E; }
 __device__ __forceinline__ unsigned long long *tail_fq(const BatchTailArgs &a) {
@@ -79,7 +78,7 @@ __device__ __forceinline__ unsigned long long *tail_fq(const BatchTailArgs &a) {
 // (quant_scale of the maximum over the whole FFN row: a maximum is exact in
 // any order) into s_sf[m].  One wave polls, lane l the lines of blocks l
 // and l + 64 (every thread of 132 blocks polling 19 shared lines took ~3 us
-// to see them); every thread of the block calls it.
+// to see them); every thread of a gate/up block calls it.
 __device__ void wait_row_scales(const BatchTailArgs &a, int ngu, unsigned tag, float *s_sf) {
   const int t = threadIdx.x;
   if (t < 64) {
@@ -256,7 +255,7 @@ __device__ __forceinline__ void load_gamma(const float *g, int K, float4 (&gv)[4
 }
 
 // o / down rows [r0, r0 + 16) for every token
-__device__ void tail_od(const BatchTailArgs &a, int gi, unsigned tag, int8_t *codes, float *red) {
+__device__ void tail_od(const BatchTailArgs &a, int gi, unsigned tag, int8_t *codes) {
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int grp = t >> 3, sub = t & 7;
   const int E = a.E, F = a.F, M = a.M, ce = E >> 7, nch = F >> 4;
@@ -303,16 +302,24 @@ __device__ void tail_od(const BatchTailArgs &a, int gi, unsigned tag, int8_t *co
 
   // ---- D: the rows' scales from the gate/up blocks' maxima, then the FFN
   // codes (quantized by the gate/up blocks, four per word) into LDS ----
-  const int ngu = (F + kTailPairs - 1) / kTailPairs;
-  wait_row_scales(a, ngu, tag, s_sf);
+  // (the scales follow the codes, written by gate/up block 0: the o/down
+  // blocks do not poll the maxima lines)
   {
+    const int ncp = M * F / 8;  // code pairs
     float v[kTailWQ][2];
-    const unsigned own = wait_pairs<kTailWQ>(tail_fq(a), M * F / 4, tag, v, a.err);
+    const unsigned own = wait_pairs<kTailWQ>(tail_fq(a), M * F / 4 + kTailMaxM, tag, v, a.err);
 #pragma unroll
-    for (int j = 0; j < kTailWQ; j++)
-      if ((own >> j) & 1u)
-        *reinterpret_cast<uint2 *>(codes + 8 * (t + kStepThreads * j)) =
-            make_uint2(__float_as_uint(v[j][0]), __float_as_uint(v[j][1]));
+    for (int j = 0; j < kTailWQ; j++) {
+      const int p = t + kStepThreads * j;
+      if ((own >> j) & 1u) {
+        if (p < ncp) {
+          *reinterpret_cast<uint2 *>(codes + 8 * p) = make_uint2(__float_as_uint(v[j][0]), __float_as_uint(v[j][1]));
+        } else {
+          s_sf[2 * (p - ncp)] = v[j][0];
+          s_sf[2 * (p - ncp) + 1] = v[j][1];
+        }
+      }
+    }
   }
   __syncthreads();
   float sc[kTailMaxM];
@@ -431,12 +438,15 @@ __device__ void tail_gu(const BatchTailArgs &a, int gi, unsigned tag, float *xs,
     reinterpret_cast<int8_t *>(qstage)[wave * kTailPairs + lane] = c;
   }
   __syncthreads();
-  // 16 words (64 codes) per token, stored by one wave
+  // 16 words (64 codes) per token, stored by one wave; block 0 also stores
+  // the rows' scales after the codes
   if (t < 16 * M) {
     const int m = t >> 4, k = t & 15;
     if (g0 + 4 * k < F)
       put_word(FQ + (size_t)m * (F / 4) + g0 / 4 + k, __uint_as_float(qstage[m * 16 + k]), tag);
   }
+  if (gi == 0 && t >= 64 && t < 64 + kTailMaxM)
+    put_word(FQ + (size_t)M * (F / 4) + (t - 64), t - 64 < M ? s_sf[t - 64] : 1.0f, tag);
 }
 
 // the next layer's q|k|v rows [q0, q0 + 16) for every token
@@ -473,7 +483,6 @@ __device__ void tail_qkv(const BatchTailArgs &a, int qi, unsigned tag, float *xs
 
 __global__ __launch_bounds__(kStepThreads) void batch_tail_kernel(BatchTailArgs a) {
   extern __shared__ __attribute__((aligned(16))) float lds[];
-  __shared__ float red[kTailMaxM * kTW];
   const int b = blockIdx.x;
   const unsigned tag = ld_uniform(a.tag);
   const int nod = a.E / kTailRows, ngu = (a.F + kTailPairs - 1) / kTailPairs;
@@ -481,7 +490,7 @@ __global__ __launch_bounds__(kStepThreads) void batch_tail_kernel(BatchTailArgs 
   float *xs = lds;                                                      // [M][E] gathered rows
   int8_t *codes = reinterpret_cast<int8_t *>(lds + kTailMaxM * a.E);  // [M][max(E, F)]
   if (b < nod)
-    tail_od(a, b, tag, codes, red);
+    tail_od(a, b, tag, codes);
   else if (b < nod + ngu)
     tail_gu(a, b - nod, tag, xs, codes);
   else if (b < nod + ngu + nq)
@@ -507,7 +516,7 @@ size_t batch_tail_lds(int E, int F) {
 }
 
 size_t batch_tail_xch_words(int E) {
-  return (size_t)2 * kTailMaxM * E + (size_t)kMxLine * kTailMaxG + (size_t)kTailMaxM * kTailMaxF / 4;
+  return (size_t)2 * kTailMaxM * E + (size_t)kMxLine * kTailMaxG + (size_t)kTailMaxM * kTailMaxF / 4 + kTailMaxM;
 }
 
 bool batch_tail_shape_ok(int E, int F, int NQ) {

@@ -711,7 +711,6 @@ int attention_max_vtile(int hd, int kv) {
 // holding the token's position appends them to the cache and scores that
 // position from the rounded k.  The softmax / sums pass (attn_kernel with
 // SCORED) runs after it.
-constexpr int kScChunk = 256;
 constexpr int kScMaxHeads = 16;  // query heads per KV group
 
 // element tt of a head row after RoPE (rotate-half, the (cos, sin) pair of
@@ -730,15 +729,19 @@ __device__ __forceinline__ float rope_elem(const float *row, int tt, int rot, co
   return (float)(t3 + t4);
 }
 
-// kScThreads threads: two per position of the chunk, thread t scoring
-// position t % kScChunk for the group's heads r = t / kScChunk, + 2, ...
-// (two waves per SIMD instead of one, each thread's sequential dots half as
-// many): C5's scores pass 10.3 -> 8.9 us per layer; three per position took
-// 9.4 us, chunks of 128 positions 9.6 us.
-constexpr int kScThreads = 2 * kScChunk;
-template <int HD, bool FUSED>
+// kScThreads threads over a chunk of CH positions: NT / CH per position,
+// thread t scoring position t % CH for the group's heads r = t / CH, +
+// NT / CH, ...  At 256 positions (two threads per position, two waves per
+// SIMD instead of one, each thread's sequential dots half as many) C5's
+// scores pass went 10.3 -> 8.9 us per layer (three per position 9.4 us,
+// chunks of 128 positions 9.6 us: 320 blocks, more than one round).  Small
+// grids take chunks of 128 (four threads per position, twice the blocks):
+// C4's 4 tokens x 2 KV groups at 2080 positions are 72 blocks of 256.
+constexpr int kScThreads = 512;
+template <int HD, bool FUSED, int CH>
 __global__ __launch_bounds__(kScThreads) void attn_scores_kernel(AttnArgs a) {
   constexpr int NT = kScThreads;
+  constexpr int kScChunk = CH;
   constexpr int CPR = HD / 8;         // 16-byte chunks per K row
   constexpr int KP = CPR + 1;         // LDS row pitch in chunks (odd: a thread's row reads spread over the banks)
   constexpr int RPL = NT / CPR;       // rows per load instruction over the block
@@ -830,11 +833,18 @@ static void launch_attn(AttnArgs a, size_t lds, hipStream_t st) {
   else klaunch((attn_kernel<HD, false, NS>), grid, block, lds, st, a);
 }
 
+template <int HD, int CH>
+static void launch_attn_scores_ch(const AttnArgs &a, hipStream_t st) {
+  const dim3 g1((a.max_npos + CH - 1) / CH, a.KVH, a.M);
+  if (a.fuse_kv) klaunch((attn_scores_kernel<HD, true, CH>), g1, dim3(kScThreads), 0, st, a);
+  else klaunch((attn_scores_kernel<HD, false, CH>), g1, dim3(kScThreads), 0, st, a);
+}
 template <int HD>
 static void launch_attn_scores(const AttnArgs &a, hipStream_t st) {
-  const dim3 g1((a.max_npos + kScChunk - 1) / kScChunk, a.KVH, a.M);
-  if (a.fuse_kv) klaunch((attn_scores_kernel<HD, true>), g1, dim3(kScThreads), 0, st, a);
-  else klaunch((attn_scores_kernel<HD, false>), g1, dim3(kScThreads), 0, st, a);
+  // chunks of 256 positions, or of 128 when that grid would fill half the CUs or less
+  const long b256 = (long)((a.max_npos + 255) / 256) * a.KVH * a.M;
+  if (b256 * 2 <= kStepBlocks) launch_attn_scores_ch<HD, 128>(a, st);
+  else launch_attn_scores_ch<HD, 256>(a, st);
 }
 
 // the body on the scores pass's scores (the cache holds the new k / v)

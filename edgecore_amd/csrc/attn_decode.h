@@ -342,7 +342,8 @@ __host__ __device__ constexpr inline int attn_sswz(int hs) { return hs <= 16 ? 0
 // before its last barrier); the body loads and writes only the rest.
 // mk(e) (optional) is called by every thread at phase boundaries, for a
 // caller's timestamps: 0 the scores start, 1 the softmax starts, 2 the
-// products and sums start.
+// products and sums start, 3 and 4 the first tile's second and third stages
+// start.
 struct NoMark {
   __device__ void operator()(int) const {}
 };
@@ -741,6 +742,7 @@ __device__ __forceinline__ void attn_decode_block(const AttnArgs &a, int m, int 
 #pragma unroll
       for (int s = 0; s <= NSTG; s++) {
         if (s > nst) continue;  // uniform
+        if (s == 1 || s == 2) mk(2 + s);
         if (pt >= 0) {
 #pragma unroll
           for (int u = 0; u < UPS; u++) {

@@ -360,7 +360,8 @@ __device__ void attention_loop(const StepArgs &a, int head, int slice, unsigned 
     const int o0 = hh * 64 + 16 * ss;
     attn_decode_block<64, true, kStepSlices, false, true>(a.attn, 0, hh, ss, qkv_s, qkv_s + 64, qkv_s + 128, lds,
                                              [&](int i, float o) { put_word(att + o0 + i, o, tag); },
-                                             a.kv_layer * l, [&](int e) { mark<TRACE>(a, b, l, 15 + e); }, &pre);
+                                             a.kv_layer * l, [&](int e) { mark<TRACE>(a, b, l, e < 3 ? 15 + e : 1 + e); }, &pre);
+    mark<TRACE>(a, b, l, 8);
     published();  // (threads t < 16 stored the slice's words; the body's LDS is reused by the next layer)
     mark<TRACE>(a, b, l, 3);
     if (l + 1 < a.L) {

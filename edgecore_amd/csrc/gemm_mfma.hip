@@ -658,6 +658,7 @@ __global__ __launch_bounds__(256) void split_kernel(const float *x, int ldx, int
 namespace {
 
 constexpr int kSkMaxGroups = 256;              // column groups of a split launch
+constexpr int kSkMaxSplit = 8;                 // blocks per column group of a split launch
 constexpr int kSkPartInts = 256 * 1024;        // int32 partial tiles of a split launch
 __device__ int sk_part[kSkPartInts];
 __device__ unsigned sk_cnt[kSkMaxGroups];
@@ -850,16 +851,23 @@ __global__ __launch_bounds__(1024) void gemm_skinny_kernel(GemvArgs a) {
     if (gridDim.y > 1) {
       // split K: publish this block's tile; the group's last block adds them
       constexpr int TS = 256 * TI * NO * NS;  // ints per tile
-      int *wp = sk_part + (size_t)blockIdx.x * gridDim.y * TS;
-      // Device-coherent stores and loads (they bypass the XCD's L2) and a
-      // wait for the stores' completion before the counter, instead of
-      // fences: a device-scope fence writes back the whole L2 (about 50 us
-      // per launch measured)
+      const int ks = (int)gridDim.y;
+      // Device-coherent buffer stores and loads (sc1: they bypass the XCD's
+      // L2) and a wait for the stores' completion before the counter,
+      // instead of fences: a device-scope fence writes back the whole L2
+      // (about 50 us per launch measured).  The address's halves as unsigned
+      // words (readfirstlane returns int: an int low half would sign-extend
+      // into the high half).
+      const uint64_t pv = (uint64_t)(uintptr_t)(sk_part + (size_t)blockIdx.x * ks * TS);
+      const uint32_t plo = __builtin_amdgcn_readfirstlane((uint32_t)pv),
+                     phi = __builtin_amdgcn_readfirstlane((uint32_t)(pv >> 32));
+      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+          (void *)(uintptr_t)(((uint64_t)phi << 32) | plo), 0, ks * TS * 4, 0x00020000);
       if (outt) {
 #pragma unroll
         for (int k = 0; k < NS; k++)
-          __hip_atomic_store(wp + (size_t)blockIdx.y * TS + 256 * TI * NO * k + t, sum[k], __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
+          __builtin_amdgcn_raw_buffer_store_b32((uint32_t)sum[k], rs, ((int)blockIdx.y * TS + 256 * TI * NO * k + t) * 4,
+                                                0, 16 /* sc1 */);
       }
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __shared__ int s_last;
@@ -870,11 +878,22 @@ __global__ __launch_bounds__(1024) void gemm_skinny_kernel(GemvArgs a) {
       __syncthreads();
       if (!s_last) return;
       if (outt) {
+        // every split's value loaded at once, unconditionally (splits past
+        // ks read the last one again and are not added): atomic loads in a
+        // loop came out one round trip each
+        uint32_t w[NS][kSkMaxSplit];
+#pragma unroll
+        for (int k = 0; k < NS; k++)
+#pragma unroll
+          for (int y = 0; y < kSkMaxSplit; y++)
+            w[k][y] = __builtin_amdgcn_raw_buffer_load_b32(rs, (min(y, ks - 1) * TS + 256 * TI * NO * k + t) * 4, 0,
+                                                           16 /* sc1 */);
 #pragma unroll
         for (int k = 0; k < NS; k++) {
           int v = 0;
-          for (int y = 0; y < (int)gridDim.y; y++) v += __hip_atomic_load(wp + (size_t)y * TS + 256 * TI * NO * k + t,
-                                                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+          for (int y = 0; y < kSkMaxSplit; y++)
+            if (y < ks) v += (int)w[k][y];
           sum[k] = v;
         }
       }
@@ -944,7 +963,7 @@ hipError_t launch_skinny_nj(const GemvArgs &a, int wpb, int ksplit, hipStream_t 
   if (ksplit < 1 || OP != OP_I8 || groups > kSkMaxGroups ||
       (size_t)groups * ksplit * 256 * TI * NO * (EPI == EPI_SWIGLU ? 2 : 1) > (size_t)kSkPartInts)
     ksplit = 1;
-  ksplit = min(ksplit, ksteps);
+  ksplit = min(min(ksplit, ksteps), kSkMaxSplit);
   const int kper = (ksteps + ksplit - 1) / ksplit;
   // waves per block: two or more K steps each (SwiGLU: six), 4 to 16 waves,
   // and at least 4 TI NO (the epilogue takes one thread per output of 16 TI

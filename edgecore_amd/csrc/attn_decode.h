@@ -727,76 +727,97 @@ __device__ __forceinline__ void attn_decode_block(const AttnArgs &a, int m, int 
     const float *tail = reinterpret_cast<const float *>(pp + (size_t)nq * P);
     for (int e = 0; e < (cnt & 3); e++) o = o + tail[e];
   };
+  // the products of stage s (s < NSTG) of the tile at tt0 (tcnt positions):
+  // this product thread's UPS units
+  auto form = [&](int tt0, int tcnt, int s) {
+#pragma unroll
+    for (int u = 0; u < UPS; u++) {
+      const int qd = stage_lo(s) + QPU * u + pt / CPRV, cd = pt % CPRV;
+      v4u *vu = vr[s * UPS + u];
+      if (4 * qd < tcnt && qd < stage_lo(s + 1)) {
+        if (vpre) {
+#pragma unroll
+          for (int e = 0; e < 4; e++) vu[e] = vtl[(e * (T / 4) + qd) * CPRV + cd];
+        }
+        if (FUSED) {
+          // the token's own position takes the fp16-rounded new v (one lane)
+          const int en = n - 1 - tt0 - 4 * qd;
+          if (en >= 0 && en < 4) {
+            uint32_t w[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+              w[j] = (uint32_t)f2h(vn[HS * slice + 8 * cd + 2 * j]) |
+                     ((uint32_t)f2h(vn[HS * slice + 8 * cd + 2 * j + 1]) << 16);
+            const v4u nv = {w[0], w[1], w[2], w[3]};
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+              if (e == en) vu[e] = nv;
+          }
+        }
+        const float4 eq = *reinterpret_cast<const float4 *>(sc + tt0 + 4 * qd);
+        const float pe[4] = {(float)((double)eq.x * isum), (float)((double)eq.y * isum),
+                             (float)((double)eq.z * isum), (float)((double)eq.w * isum)};
+        float pr[8][4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          float r8[8];
+          mul8h(r8, pe[e], vu[e]);
+#pragma unroll
+          for (int k = 0; k < 8; k++) pr[k][e] = r8[k];
+        }
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+          *reinterpret_cast<float4 *>(prod + ((size_t)qd * P + ((8 * cd + k) ^ (((8 * cd + k) >> 4) & sw))) * 4) =
+              make_float4(pr[k][0], pr[k][1], pr[k][2], pr[k][3]);
+      }
+    }
+  };
+  bool pre0 = false;  // this tile's stage-0 products were formed in the previous tile's last stage
   for (int t0 = 0; t0 < n; t0 += T) {
     const int cnt = min(T, n - t0);
     const int nq = cnt >> 2;  // complete quads
-    if (t0 > 0) __syncthreads();  // the previous tile's sums are done (the first tile: the sum's barrier)
+    if (t0 > 0) __syncthreads();  // the previous tile's last stage is done (the first tile: the sum's barrier)
     if constexpr (HD > 0) {
       // Stage s: the product threads form the products of their UPS units of
       // stage s (quads [stage_lo(s), stage_lo(s+1))) while the summing lanes
       // add the quads of stage s - 1; a barrier separates the stages.
       // (the V of tiles after the first is loaded during the previous tile's
-      // last stage)
+      // stages)
       const int nqt = (cnt + 3) / 4;  // quads holding positions
       const int nst = nqt <= Q0 ? 1 : 1 + (nqt - Q0 + SQ - 1) / SQ;  // stages holding positions
+      // The next tile's stage-0 products are formed during this tile's last
+      // stage, beside its last sums, when that stage reads none of the quads
+      // they overwrite (two stages or more): the next tile then starts with
+      // its first sums instead of a stage of products alone.
+      // (not in the persistent step, whose contexts mostly fit one tile:
+      // there the extra code costs registers)
+      const int cnt1 = min(T, n - t0 - T);  // the next tile's positions (<= 0: none)
+      const bool pipe = !PREK && cnt1 > 0 && nst >= 2;
 #pragma unroll
       for (int s = 0; s <= NSTG; s++) {
-        if (s > nst) continue;  // uniform
+        if (s > nst || (s == 0 && pre0)) continue;  // uniform
         if (s == 1 || s == 2) mk(2 + s);
         if (pt >= 0) {
-#pragma unroll
-          for (int u = 0; u < UPS; u++) {
-            const int qd = stage_lo(s) + QPU * u + pt / CPRV, cd = pt % CPRV;
-            v4u *vu = vr[min(s, NSTG - 1) * UPS + u];
-            if (s < nst && 4 * qd < cnt && qd < stage_lo(s + 1)) {
-              if (vpre) {
-#pragma unroll
-                for (int e = 0; e < 4; e++) vu[e] = vtl[(e * (T / 4) + qd) * CPRV + cd];
-              }
-              if (FUSED) {
-                // the token's own position takes the fp16-rounded new v (one lane)
-                const int en = n - 1 - t0 - 4 * qd;
-                if (en >= 0 && en < 4) {
-                  uint32_t w[4];
-#pragma unroll
-                  for (int j = 0; j < 4; j++)
-                    w[j] = (uint32_t)f2h(vn[HS * slice + 8 * cd + 2 * j]) |
-                           ((uint32_t)f2h(vn[HS * slice + 8 * cd + 2 * j + 1]) << 16);
-                  const v4u nv = {w[0], w[1], w[2], w[3]};
-#pragma unroll
-                  for (int e = 0; e < 4; e++)
-                    if (e == en) vu[e] = nv;
-                }
-              }
-              const float4 eq = *reinterpret_cast<const float4 *>(sc + t0 + 4 * qd);
-              const float pe[4] = {(float)((double)eq.x * isum), (float)((double)eq.y * isum),
-                                   (float)((double)eq.z * isum), (float)((double)eq.w * isum)};
-              float pr[8][4];
-#pragma unroll
-              for (int e = 0; e < 4; e++) {
-                float r8[8];
-                mul8h(r8, pe[e], vu[e]);
-#pragma unroll
-                for (int k = 0; k < 8; k++) pr[k][e] = r8[k];
-              }
-#pragma unroll
-              for (int k = 0; k < 8; k++)
-                *reinterpret_cast<float4 *>(prod + ((size_t)qd * P + ((8 * cd + k) ^ (((8 * cd + k) >> 4) & sw))) * 4) =
-                    make_float4(pr[k][0], pr[k][1], pr[k][2], pr[k][3]);
-            }
+          if (s < nst) {
+            form(t0, cnt, min(s, NSTG - 1));
+            // the next tile's V of this stage into the registers the stage
+            // has used up, so that its loads have the tile's later stages to
+            // arrive in (loaded at the tile's end, each next tile began by
+            // waiting for its V: about 1 us of the 2.4 us a 256-position tile
+            // took at head_dim 128)
+            if (t0 + T < n) load_v_stage(t0 + T, min(s, NSTG - 1));
           }
-          // the next tile's V of this stage into the registers the stage
-          // has used up, so that its loads have the tile's later stages to
-          // arrive in (loaded at the tile's end, each next tile began by
-          // waiting for its V: about 1 us of the 2.4 us a 256-position tile
-          // took at head_dim 128)
-          if (s < nst && t0 + T < n) load_v_stage(t0 + T, min(s, NSTG - 1));
         } else if (t < hs && s > 0) {
           sum_quads(stage_lo(s - 1), min(stage_lo(s), nq));
           if (s == nst) sum_tail(nq, cnt);
         }
         if (s < nst) __syncthreads();
       }
+      if (pipe && pt >= 0) {
+        form(t0 + T, cnt1, 0);
+        if (t0 + 2 * T < n) load_v_stage(t0 + 2 * T, 0);  // the V of the tile after next, stage 0
+      }
+      pre0 = pipe;
     } else {
       for (int e = t; e < cnt * hd; e += NT) {
         const int i = e / hd, d = e - i * hd;

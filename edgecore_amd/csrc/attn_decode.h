@@ -681,13 +681,19 @@ __device__ __forceinline__ void attn_decode_block(const AttnArgs &a, int m, int 
 
   mk(2);
   // ---- 5. products p*v, and the sequential sums ----
-  // element d of quad q sits in 16-byte slot q*P + (d ^ ((d >> 4) & sw)); with
-  // P and sw from attn_pitch/attn_swz every 16 consecutive lanes of the
-  // product writes (units of 4 positions x 8 elements) and of the sums' reads
-  // (consecutive d) touch 16 distinct bank slots
+  // element d of quad q sits in 16-byte slot q*P + swz(d) (below), P from
+  // attn_pitch / attn_spitch
   const int sw = NS > 1 ? attn_sswz(HS) : attn_swz(hd, a.kv);
   const int hs = NS > 1 ? HS : hd;  // output elements of this block (summing lanes)
-  const float4 *pp = reinterpret_cast<const float4 *>(prod) + (t ^ ((t >> 4) & sw));
+  // slot of element d within a quad: 16 consecutive lanes of the product
+  // writes (units of 4 positions x 8 elements) and of the sums' reads
+  // (consecutive d) touch 16 distinct bank slots; for head_dim 128 also each
+  // 8 of them 8 distinct slots mod 8
+  auto swz = [&](int d) {
+    if constexpr (HD == 128 && NS == 1) return d ^ (((d >> 3) & 7) | (((d >> 6) & 1) << 3));
+    else return d ^ ((d >> 4) & sw);
+  };
+  const float4 *pp = reinterpret_cast<const float4 *>(prod) + swz(t);
   float o = 0.0f;
   // sequential sum of the complete quads [qa, qe) of the tile into o
   auto sum_quads = [&](int qa, int qe) {
@@ -767,7 +773,7 @@ __device__ __forceinline__ void attn_decode_block(const AttnArgs &a, int m, int 
         }
 #pragma unroll
         for (int k = 0; k < 8; k++)
-          *reinterpret_cast<float4 *>(prod + ((size_t)qd * P + ((8 * cd + k) ^ (((8 * cd + k) >> 4) & sw))) * 4) =
+          *reinterpret_cast<float4 *>(prod + ((size_t)qd * P + swz(8 * cd + k)) * 4) =
               make_float4(pr[k][0], pr[k][1], pr[k][2], pr[k][3]);
       }
     }

@@ -419,10 +419,11 @@ __device__ __forceinline__ void pf_tile2(float &o0, float &o1, uint32_t p0, uint
 }
 
 // V tiles are staged transposed: element d of the tile's position r at
-// tile[pf_vrow(d) + r].  Rows are 68 floats apart plus 8 more every 16 rows,
-// so that the staging writes (per wave 8 positions x 8 chunks of 8 elements)
-// and the 16-byte reads of 16 consecutive rows both hit distinct banks.
-constexpr int pf_vrow(int d) { return d * (kPfTile + 4) + 8 * (d >> 4); }
+// tile[pf_vrow(d) + r].  Rows are 68 floats apart plus 4 more every 8 rows,
+// so that the 4-byte staging writes (32 lanes: 4 positions x 8 chunks of 8
+// elements) and the 16-byte reads of 8 consecutive rows (served 8 lanes at a
+// time) both hit distinct banks.
+constexpr int pf_vrow(int d) { return d * (kPfTile + 4) + 4 * (d >> 3); }
 
 // NW waves per block, QW tokens per wave (consecutive), NW * QW tokens per block
 template <int HD, int NW, int QW>
@@ -509,9 +510,15 @@ __global__ __launch_bounds__(NW * 64) void attn_prefill_kernel(AttnArgs a, int n
           f[2 * i] = h2f((uint16_t)(hv[i] & 0xffffu));
           f[2 * i + 1] = h2f((uint16_t)(hv[i] >> 16));
         }
+        // the row's two halves in the opposite order for chunks 4-7: the 8
+        // lanes of one row then write 8 distinct slots mod 8 per instruction
+        // (16-byte accesses are served 8 lanes at a time)
         float *dst = tile + r * KP + 8 * cc;
-        *reinterpret_cast<float4 *>(dst) = make_float4(f[0], f[1], f[2], f[3]);
-        *reinterpret_cast<float4 *>(dst + 4) = make_float4(f[4], f[5], f[6], f[7]);
+        const bool sw = cc & 4;
+        *reinterpret_cast<float4 *>(dst + (sw ? 4 : 0)) =
+            sw ? make_float4(f[4], f[5], f[6], f[7]) : make_float4(f[0], f[1], f[2], f[3]);
+        *reinterpret_cast<float4 *>(dst + (sw ? 0 : 4)) =
+            sw ? make_float4(f[0], f[1], f[2], f[3]) : make_float4(f[4], f[5], f[6], f[7]);
       }
     }
   };
@@ -522,7 +529,7 @@ __global__ __launch_bounds__(NW * 64) void attn_prefill_kernel(AttnArgs a, int n
       if (TCH % NT == 0 || c < TCH) {
         const int r = c / CPR, cc = c - r * CPR;
         const uint32_t hv[4] = {pre[j].x, pre[j].y, pre[j].z, pre[j].w};
-        // elements 8cc .. 8cc+7 share d >> 4: rows kPfTile + 4 floats apart
+        // elements 8cc .. 8cc+7 share d >> 3: rows kPfTile + 4 floats apart
         float *dst = tile + pf_vrow(8 * cc) + r;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
